@@ -1,0 +1,225 @@
+"""ctypes bindings for the CPU oracle (oracle/liboracle.so) and the reference build
+(oracle/_ref/libbeglin_ref.so).  Test infrastructure: only tests/, __graft_entry__.smoke()
+and bench.py's cpu_baseline leg use this module."""
+import ctypes as C
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libbeglin_ref.so")
+
+_P = C.c_void_p
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "array must be C-contiguous"
+    return a.ctypes.data_as(_P)
+
+
+def load_oracle():
+    if not os.path.exists(ORACLE_SO):
+        raise FileNotFoundError(f"{ORACLE_SO} missing: run `make -C oracle` (or __graft_entry__.build())")
+    lib = C.CDLL(ORACLE_SO)
+    lib.or_f32_to_f16.restype = C.c_uint16
+    lib.or_f32_to_f16.argtypes = [C.c_float]
+    lib.or_f16_to_f32.restype = C.c_float
+    lib.or_f16_to_f32.argtypes = [C.c_uint16]
+    lib.or_quantize_qng64_dense.restype = C.c_int
+    lib.or_moe_row.restype = C.c_double
+    lib.or_qng64_decode_code.restype = C.c_float
+    lib.or_qng64_decode_code.argtypes = [_P, C.c_int, C.c_int]
+    lib.or_pool_create.restype = _P
+    lib.or_pool_create.argtypes = [C.c_int, C.c_int]
+    lib.or_pool_destroy.argtypes = [_P]
+    lib.or_pool_threads.argtypes = [_P]
+    lib.or_pool_gemv_g256sf_sdot.argtypes = [_P] * 7 + [C.c_int, C.c_int]
+    lib.or_pool_gemv_q4g64_sdot.argtypes = [_P] * 6 + [C.c_int, C.c_int]
+    lib.or_pool_gemv_f32.argtypes = [_P, C.c_int, C.c_int] + [_P] * 5 + [C.c_int, C.c_int]
+    return lib
+
+
+def load_ref():
+    """The reference's own C sources for this path, compiled in place by oracle/Makefile.
+    Returns None where it was not built (e.g. a box without the reference tree and no
+    prebuilt copy)."""
+    if not os.path.exists(REF_SO):
+        return None
+    lib = C.CDLL(REF_SO)
+    lib.qng64_group_bytes.restype = C.c_size_t
+    lib.qng64_group_bytes.argtypes = [C.c_int]
+    lib.qng64_packed_bytes.restype = C.c_size_t
+    lib.qng64_packed_bytes.argtypes = [C.c_int, C.c_int, C.c_int]
+    lib.qng64_quantize_f32.restype = C.c_int
+    lib.qng64_quantize_f32.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P]
+    lib.qng64_decode_code.restype = C.c_float
+    lib.qng64_decode_code.argtypes = [_P, C.c_int, C.c_int]
+    lib.qng64_matvec_f32.argtypes = [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int]
+    lib.qng64_matmul_f32.argtypes = [_P, _P, C.c_int, _P, _P, _P, C.c_int, C.c_int, C.c_int]
+    lib.gguf_quantize_q4g64_error_feedback.argtypes = [_P, C.c_int, C.c_int, _P, _P]
+    lib.gguf_quantize_q8g64.argtypes = [_P, C.c_int, C.c_int, _P, _P]
+    lib.gguf_quantize_qNg64.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P]
+    lib.gguf_w_quantize_q4_0.argtypes = [_P, C.c_int64, _P]
+    lib.gguf_dequant_row.argtypes = [C.c_int, _P, _P, C.c_int64]
+    return lib
+
+
+class Oracle:
+    """numpy-facing wrappers over liboracle.so."""
+
+    def __init__(self):
+        self.lib = load_oracle()
+
+    # ---- fp16 ----
+    def f32_to_f16(self, f):
+        return self.lib.or_f32_to_f16(C.c_float(f))
+
+    # ---- packers (weights w: float32 [out][in]) ----
+    def quantize_q4g64(self, w):
+        out, inn = w.shape
+        packed = np.zeros((out, inn // 2), np.uint8)
+        scales = np.zeros((out, inn // 64), np.float32)
+        self.lib.or_quantize_q4g64_ef(_ptr(w), out, inn, _ptr(packed), _ptr(scales))
+        return packed, scales
+
+    def quantize_q8g64(self, w):
+        out, inn = w.shape
+        codes = np.zeros((out, inn), np.int8)
+        scales = np.zeros((out, inn // 64), np.float32)
+        self.lib.or_quantize_q8g64(_ptr(w), out, inn, _ptr(codes), _ptr(scales))
+        return codes, scales
+
+    def quantize_qng64_gguf(self, w, n):
+        out, inn = w.shape
+        planes = np.zeros((out, inn // 64 * n * 8), np.uint8)
+        scales = np.zeros((out, inn // 64), np.float32)
+        self.lib.or_quantize_qng64_gguf(_ptr(w), out, inn, n, _ptr(planes), _ptr(scales))
+        return planes, scales
+
+    def quantize_qng64_dense(self, w, n):
+        out, inn = w.shape
+        planes = np.zeros((out, inn // 64 * n * 8), np.uint8)
+        scales = np.zeros((out, inn // 64), np.float32)
+        rc = self.lib.or_quantize_qng64_dense(_ptr(w), out, inn, n, _ptr(planes), _ptr(scales))
+        if rc != 0:
+            raise ValueError(f"qng64_quantize_f32 rejects n={n}")
+        return planes, scales
+
+    def quantize_qng64(self, w, n):
+        """The config's 'reference qng64 encoder' (qng64_quantize_f32); n=4, which it rejects,
+        goes through gguf_quantize_qNg64 (no n gate)."""
+        return self.quantize_qng64_gguf(w, 4) if n == 4 else self.quantize_qng64_dense(w, n)
+
+    def quantize_q4_0(self, w):
+        n = w.size
+        blocks = np.zeros(n // 32 * 18, np.uint8)
+        self.lib.or_quantize_q4_0(_ptr(np.ascontiguousarray(w, np.float32)), C.c_int64(n), _ptr(blocks))
+        return blocks
+
+    def quantize_q4g32h(self, w):
+        out, inn = w.shape
+        packed = np.zeros((out, inn // 2), np.uint8)
+        s16 = np.zeros((out, inn // 32), np.uint16)
+        self.lib.or_quantize_q4g32h(_ptr(w), out, inn, _ptr(packed), _ptr(s16))
+        return packed, s16
+
+    def q4_0_to_q4g32h(self, blocks, out, inn):
+        packed = np.zeros((out, inn // 2), np.uint8)
+        s16 = np.zeros((out, inn // 32), np.uint16)
+        self.lib.or_q4_0_to_q4g32h(_ptr(blocks), out, inn, _ptr(packed), _ptr(s16))
+        return packed, s16
+
+    def quantize_g256sf(self, w):
+        out, inn = w.shape
+        packed = np.zeros((out, inn // 2), np.uint8)
+        wsuper = np.zeros((out, inn // 256), np.float32)
+        sub = np.zeros((out, inn // 64), np.uint8)
+        self.lib.or_quantize_g256sf(_ptr(w), out, inn, _ptr(packed), _ptr(wsuper), _ptr(sub))
+        return packed, wsuper, sub
+
+    # ---- decoders ----
+    def decode(self, kind, packed, scales, out, inn, bits=0, sub=None):
+        w = np.zeros((out, inn), np.float32)
+        if kind == 1:
+            self.lib.or_decode_q4g64(_ptr(packed), _ptr(scales), out, inn, _ptr(w))
+        elif kind == 2:
+            self.lib.or_decode_q8g64(_ptr(packed), _ptr(scales), out, inn, _ptr(w))
+        elif kind == 3:
+            self.lib.or_decode_g256sf(_ptr(packed), _ptr(scales), _ptr(sub), out, inn, _ptr(w))
+        elif kind == 4:
+            self.lib.or_decode_qng64(_ptr(packed), _ptr(scales), bits, out, inn, _ptr(w))
+        elif kind == 5:
+            self.lib.or_decode_q4g32h(_ptr(packed), _ptr(scales), out, inn, _ptr(w))
+        else:
+            raise ValueError(kind)
+        return w
+
+    def decode_q4_0(self, blocks, n):
+        w = np.zeros(n, np.float32)
+        self.lib.or_decode_q4_0(_ptr(blocks), C.c_int64(n), _ptr(w))
+        return w
+
+    # ---- GEMV ----
+    def gemm_f32(self, kind, packed, scales, x, bias=None, bits=0):
+        x = np.ascontiguousarray(x, np.float32)
+        M = 1 if x.ndim == 1 else x.shape[0]
+        inn = x.shape[-1]
+        out = packed.shape[0]
+        y = np.zeros((M, out), np.float32)
+        self.lib.or_gemm_f32(kind, bits, _ptr(packed), _ptr(scales), _ptr(x), _ptr(bias), _ptr(y), out, inn, M)
+        return y if x.ndim == 2 else y[0]
+
+    def quant_act_i8(self, x, gsize):
+        x = np.ascontiguousarray(x, np.float32)
+        xq = np.zeros(x.shape, np.int8)
+        a = np.zeros(x.shape[:-1] + (x.shape[-1] // gsize,), np.float32)
+        rows = 1 if x.ndim == 1 else x.shape[0]
+        inn = x.shape[-1]
+        for m in range(rows):
+            xs = x if x.ndim == 1 else x[m]
+            xqs = xq if x.ndim == 1 else xq[m]
+            as_ = a if x.ndim == 1 else a[m]
+            self.lib.or_quant_act_i8(_ptr(xs), inn, gsize, _ptr(xqs), _ptr(as_))
+        return xq, a
+
+    def matmul_sdot(self, kind, packed, scales, x, bias=None, sub=None):
+        x = np.ascontiguousarray(x, np.float32)
+        M = 1 if x.ndim == 1 else x.shape[0]
+        inn = x.shape[-1]
+        out = packed.shape[0]
+        y = np.zeros((M, out), np.float32)
+        self.lib.or_matmul_sdot(kind, _ptr(packed), _ptr(scales), _ptr(sub), _ptr(x), _ptr(bias), _ptr(y), out, inn, M)
+        return y if x.ndim == 2 else y[0]
+
+    def gemm_sdot(self, kind, packed, scales, xq, ascale, bias=None, sub=None):
+        M = 1 if xq.ndim == 1 else xq.shape[0]
+        inn = xq.shape[-1]
+        out = packed.shape[0]
+        y = np.zeros((M, out), np.float32)
+        if kind == 1:
+            self.lib.or_gemm_q4g64_sdot(_ptr(packed), _ptr(scales), _ptr(xq), _ptr(ascale), _ptr(bias), _ptr(y), out, inn, M)
+        elif kind == 2:
+            self.lib.or_gemm_q8g64_sdot(_ptr(packed), _ptr(scales), _ptr(xq), _ptr(ascale), _ptr(bias), _ptr(y), out, inn, M)
+        else:
+            self.lib.or_gemm_g256sf_sdot(_ptr(packed), _ptr(scales), _ptr(sub), _ptr(xq), _ptr(ascale), _ptr(bias), _ptr(y), out, inn, M)
+        return y if xq.ndim == 2 else y[0]
+
+    # ---- MoE ----
+    def route(self, logits, K, renorm=False):
+        logits = np.ascontiguousarray(logits, np.float32)
+        T, E = logits.shape
+        idx = np.zeros((T, K), np.int32)
+        w = np.zeros((T, K), np.float32)
+        self.lib.or_moe_route(_ptr(logits), T, E, K, int(renorm), _ptr(idx), _ptr(w))
+        return idx, w
+
+
+class OrExpert(C.Structure):
+    _fields_ = [("kind", C.c_int), ("bits", C.c_int), ("packed", C.c_void_p), ("scales", C.c_void_p)]
+
+
+def expert_struct(kind, bits, packed, scales):
+    return OrExpert(kind, bits, packed.ctypes.data, scales.ctypes.data)
