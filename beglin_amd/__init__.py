@@ -1,0 +1,166 @@
+"""beglin_amd -- MI355X (gfx950) backend for beglin's quantized GEMV / MoE-gather hot path.
+
+The product is the C-ABI library libbeglin_hip.so (include/beglin_qgemv.h).  This package is a
+thin Python veneer over it for tests and benchmarks: PyTorch only supplies device memory and the
+stream.  Every call goes through the HIP library; if it is not built, importing `Context` fails.
+"""
+import ctypes as C
+
+from . import capi
+from .capi import ACT_F32, ACT_W4A8, K_Q4G32H, K_Q4G64, K_Q4G256SF, K_Q8G64, K_QNG64  # noqa: F401
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = capi.load()
+    return _lib
+
+
+class BglError(RuntimeError):
+    pass
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise BglError(f"{what} failed ({rc}): {lib().bgl_last_error().decode(errors='replace')}")
+
+
+def _p(t):
+    """Device (or host numpy) pointer of a torch tensor / numpy array, None passes through."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        assert t.is_contiguous(), "tensor must be contiguous"
+        return C.c_void_p(t.data_ptr())
+    return C.c_void_p(t.ctypes.data)
+
+
+class Tensor:
+    """A weight tensor bound on the device (bgl_tensor*)."""
+
+    def __init__(self, handle):
+        self.h = C.c_void_p(handle) if not isinstance(handle, C.c_void_p) else handle
+
+    def info(self):
+        k, b, o, i = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        nb = C.c_size_t()
+        _check(lib().bgl_tensor_info(self.h, C.byref(k), C.byref(b), C.byref(o), C.byref(i), C.byref(nb)), "bgl_tensor_info")
+        return dict(kind=k.value, bits=b.value, out=o.value, inn=i.value, device_bytes=nb.value)
+
+    def free(self):
+        if self.h:
+            lib().bgl_tensor_free(self.h)
+            self.h = None
+
+
+class Context:
+    """One bgl_ctx on one device and one HIP stream (torch's current stream by default)."""
+
+    def __init__(self, device=0, stream=None):
+        import torch
+        L = lib()
+        if stream is None:
+            stream = torch.cuda.current_stream(device).cuda_stream
+        h = C.c_void_p()
+        _check(L.bgl_ctx_create(device, C.c_void_p(stream), C.byref(h)), "bgl_ctx_create")
+        self.h = h
+        self.device = device
+
+    def close(self):
+        if self.h:
+            lib().bgl_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sync(self):
+        _check(lib().bgl_synchronize(self.h), "bgl_synchronize")
+
+    # ---- binding ----
+    def bind(self, kind, packed, scales, out, inn, bits=0, sub=None):
+        """Bind host (numpy) buffers in the reference layout."""
+        w = capi.bgl_wt(kind, bits if kind == K_QNG64 else (8 if kind == K_Q8G64 else 4), out, inn,
+                        packed.ctypes.data, scales.ctypes.data, sub.ctypes.data if sub is not None else None)
+        h = C.c_void_p()
+        _check(lib().bgl_bind(self.h, C.byref(w), C.byref(h)), "bgl_bind")
+        return Tensor(h)
+
+    def quantize(self, kind, w_dev, bits=0, qng64_encoder=1, want_ref=False):
+        """Quantize fp32 weights already on the device (torch tensor [out][in]).  With want_ref the
+        reference-layout bytes come back as numpy arrays."""
+        import numpy as np
+        out, inn = w_dev.shape
+        ref = None
+        args = [None, None, None]
+        if want_ref:
+            if kind in (K_Q4G64, K_Q4G256SF, K_Q4G32H):
+                pk = np.zeros((out, inn // 2), np.uint8)
+            elif kind == K_Q8G64:
+                pk = np.zeros((out, inn), np.int8)
+            else:
+                pk = np.zeros((out, inn // 64 * bits * 8), np.uint8)
+            if kind == K_Q4G32H:
+                sc = np.zeros((out, inn // 32), np.uint16)
+            elif kind == K_Q4G256SF:
+                sc = np.zeros((out, inn // 256), np.float32)
+            else:
+                sc = np.zeros((out, inn // 64), np.float32)
+            sub = np.zeros((out, inn // 64), np.uint8) if kind == K_Q4G256SF else None
+            ref = (pk, sc, sub)
+            args = [_p(pk), _p(sc), _p(sub)]
+        h = C.c_void_p()
+        _check(lib().bgl_quantize_dev(self.h, kind, bits, int(qng64_encoder), _p(w_dev), out, inn, C.byref(h), *args),
+               "bgl_quantize_dev")
+        return (Tensor(h), ref) if want_ref else Tensor(h)
+
+    def dequant(self, t, row0, nrows, out_dev):
+        _check(lib().bgl_dequant_dev(self.h, t.h, row0, nrows, _p(out_dev)), "bgl_dequant_dev")
+
+    # ---- compute (device pointers) ----
+    def matmul(self, t, x_dev, y_dev, act=ACT_F32, bias_dev=None):
+        M = 1 if x_dev.dim() == 1 else x_dev.shape[0]
+        _check(lib().bgl_matmul_dev(self.h, t.h, act, _p(x_dev), _p(bias_dev), _p(y_dev), M), "bgl_matmul_dev")
+
+    def matmul_group(self, ts, x_dev, ys, act=ACT_F32, biases=None):
+        n = len(ts)
+        M = 1 if x_dev.dim() == 1 else x_dev.shape[0]
+        W = (C.c_void_p * n)(*[t.h.value for t in ts])
+        Y = (C.c_void_p * n)(*[y.data_ptr() for y in ys])
+        B = (C.c_void_p * n)(*[(b.data_ptr() if b is not None else None) for b in (biases or [None] * n)])
+        _check(lib().bgl_matmul_group_dev(self.h, n, W, act, _p(x_dev), B, Y, M), "bgl_matmul_group_dev")
+
+    def quant_act_i8(self, x_dev, gsize, xq_dev, ascale_dev):
+        M = 1 if x_dev.dim() == 1 else x_dev.shape[0]
+        _check(lib().bgl_quant_act_i8_dev(self.h, _p(x_dev), M, x_dev.shape[-1], gsize, _p(xq_dev), _p(ascale_dev)),
+               "bgl_quant_act_i8_dev")
+
+    # ---- MoE ----
+    def bind_experts(self, descs):
+        """descs: list of (kind, bits, packed, scales) numpy tuples, one per expert."""
+        E = len(descs)
+        arr = (capi.bgl_wt * E)()
+        for e, (kind, bits, pk, sc) in enumerate(descs):
+            out = pk.shape[0]
+            inn = sc.shape[1] * (32 if kind == K_Q4G32H else 64)
+            arr[e] = capi.bgl_wt(kind, bits, out, inn, pk.ctypes.data, sc.ctypes.data, None)
+        h = C.c_void_p()
+        _check(lib().bgl_bind_experts(self.h, E, arr, C.byref(h)), "bgl_bind_experts")
+        return Tensor(h)
+
+    def gather_matvec(self, experts, x_dev, idx_dev, y_dev):
+        _check(lib().bgl_gather_matvec_dev(self.h, experts.h, _p(x_dev), _p(idx_dev), x_dev.shape[0], _p(y_dev)),
+               "bgl_gather_matvec_dev")
+
+    def moe_ffn(self, gate, up, down, shared, x_dev, idx_dev, w_dev, out_dev):
+        sg, su, sd = (shared or (None, None, None))
+        T, K = idx_dev.shape
+        _check(lib().bgl_moe_ffn_dev(self.h, gate.h, up.h, down.h, sg.h if sg else None, su.h if su else None,
+                                     sd.h if sd else None, _p(x_dev), _p(idx_dev), _p(w_dev), T, K, _p(out_dev)),
+               "bgl_moe_ffn_dev")

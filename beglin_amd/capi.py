@@ -1,0 +1,75 @@
+"""ctypes binding of include/beglin_qgemv.h (libbeglin_hip.so).
+
+The library is the product; this module only declares its C signatures.  Importing it fails
+loudly when the shared library is missing -- there is no CPU fallback anywhere in the package."""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbeglin_hip.so")
+
+# mirrors of the header's enums
+K_Q4G64, K_Q8G64, K_Q4G256SF, K_QNG64, K_Q4G32H = 1, 2, 3, 4, 5
+ACT_F32, ACT_W4A8 = 0, 1
+
+_P = C.c_void_p
+_I = C.c_int
+
+
+class bgl_wt(C.Structure):
+    _fields_ = [("kind", C.c_int), ("bits", C.c_int), ("out", C.c_int), ("in_", C.c_int),
+                ("packed", C.c_void_p), ("scales", C.c_void_p), ("sub", C.c_void_p)]
+
+
+# (name, restype, argtypes) for every entry point declared in include/beglin_qgemv.h
+SIGNATURES = [
+    ("bgl_available", _I, []),
+    ("bgl_last_error", C.c_char_p, []),
+    ("bgl_ctx_create", _I, [_I, _P, C.POINTER(_P)]),
+    ("bgl_ctx_destroy", None, [_P]),
+    ("bgl_synchronize", _I, [_P]),
+    ("bgl_ctx_stream", _P, [_P]),
+    ("bgl_bind", _I, [_P, C.POINTER(bgl_wt), C.POINTER(_P)]),
+    ("bgl_quantize_dev", _I, [_P, _I, _I, _I, _P, _I, _I, C.POINTER(_P), _P, _P, _P]),
+    ("bgl_tensor_free", None, [_P]),
+    ("bgl_tensor_info", _I, [_P, C.POINTER(_I), C.POINTER(_I), C.POINTER(_I), C.POINTER(_I), C.POINTER(C.c_size_t)]),
+    ("bgl_dequant_dev", _I, [_P, _P, _I, _I, _P]),
+    ("bgl_matmul_dev", _I, [_P, _P, _I, _P, _P, _P, _I]),
+    ("bgl_matmul_group_dev", _I, [_P, _I, C.POINTER(_P), _I, _P, C.POINTER(_P), C.POINTER(_P), _I]),
+    ("bgl_quant_act_i8_dev", _I, [_P, _P, _I, _I, _I, _P, _P]),
+    ("bgl_gemv_q4g64_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+    ("bgl_gemv_q4g64_sdot_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+    ("bgl_gemv_q8g64_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+    ("bgl_gemv_q8g64_sdot_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+    ("bgl_gemm_qXg64_mt", _I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _I]),
+    ("bgl_gemv_q4g256sf_sdot_mt", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I]),
+    ("bgl_gemm_q4g256sf_mt", _I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
+    ("bgl_qng64_matvec_f32", _I, [_P, _P, _P, _I, _P, _P, _P, _I, _I]),
+    ("bgl_qng64_matmul_f32", _I, [_P, _P, _P, _I, _P, _P, _P, _I, _I, _I]),
+    ("bgl_gemv_q4g32h_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+    ("bgl_forget", _I, [_P, _P]),
+    ("bgl_bind_experts", _I, [_P, _I, C.POINTER(bgl_wt), C.POINTER(_P)]),
+    ("bgl_experts_from_tensors", _I, [_P, _I, C.POINTER(_P), C.POINTER(_P)]),
+    ("bgl_gather_matvec_dev", _I, [_P, _P, _P, _P, _I, _P]),
+    ("bgl_moe_ffn_dev", _I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
+]
+
+
+def header_symbols():
+    """Function names declared in include/beglin_qgemv.h (parsed from the header text)."""
+    import re
+    hdr = os.path.join(os.path.dirname(HERE), "include", "beglin_qgemv.h")
+    txt = open(hdr).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(bgl_[A-Za-z0-9_]+)\s*\(", txt)))
+
+
+def load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built: run __graft_entry__.build() (python -m beglin_amd.build)")
+    lib = C.CDLL(LIB_PATH)
+    for name, res, args in SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib

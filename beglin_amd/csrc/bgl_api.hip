@@ -1,0 +1,527 @@
+// bgl_api.hip -- the C-ABI (include/beglin_qgemv.h): contexts, binding/repack, GEMV dispatch.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/beglin_qgemv.h"
+#include "bgl_kernels.h"
+#include "bgl_internal.h"
+
+static thread_local char g_err[512];
+
+int bgl_fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+#define HIPCHK(expr)                                                                             \
+    do {                                                                                         \
+        hipError_t e_ = (expr);                                                                  \
+        if (e_ != hipSuccess) return bgl_fail(BGL_E_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+extern "C" const char *bgl_last_error(void) { return g_err; }
+
+extern "C" int bgl_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, 0) != hipSuccess) return 0;
+    return strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+// ------------------------------------------------------------------ device buffers
+int dbuf_reserve(bgl_ctx *c, DevBuf &b, size_t bytes, bool zero) {
+    if (b.bytes >= bytes) return 0;
+    if (b.p) {
+        HIPCHK(hipStreamSynchronize(c->stream));
+        HIPCHK(hipFree(b.p));
+        b.p = nullptr; b.bytes = 0;
+    }
+    size_t want = bytes + bytes / 4 + 4096;
+    HIPCHK(hipMalloc(&b.p, want));
+    b.bytes = want;
+    if (zero) {
+        HIPCHK(hipMemsetAsync(b.p, 0, want, c->stream));
+        HIPCHK(hipStreamSynchronize(c->stream));
+    }
+    return 0;
+}
+
+static void dbuf_free(DevBuf &b) {
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr; b.bytes = 0;
+}
+
+extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
+    if (!out) return bgl_fail(BGL_E_ARG, "bgl_ctx_create: out is NULL");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
+        return bgl_fail(BGL_E_NODEV, "bgl_ctx_create: no HIP device %d", device);
+    HIPCHK(hipSetDevice(device));
+    bgl_ctx *c = new bgl_ctx();
+    c->device = device;
+    if (hip_stream) { c->stream = (hipStream_t)hip_stream; c->own_stream = false; }
+    else {
+        hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) { delete c; return bgl_fail(BGL_E_HIP, "hipStreamCreate: %s", hipGetErrorString(e)); }
+        c->own_stream = true;
+    }
+    const char *tb = getenv("BGL_TARGET_BLOCKS");
+    c->target_blocks = tb ? atoi(tb) : 1024;
+    if (c->target_blocks < 1) c->target_blocks = 1024;
+    *out = c;
+    return 0;
+}
+
+extern "C" void bgl_ctx_destroy(bgl_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (auto &kv : c->host_cache) bgl_tensor_free(kv.second);
+    c->host_cache.clear();
+    DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->tbuf, &c->ctr, &c->hx, &c->hy, &c->hb,
+                      &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_meta};
+    for (DevBuf *b : bufs) dbuf_free(*b);
+    if (c->own_stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+extern "C" int bgl_synchronize(bgl_ctx *c) {
+    if (!c) return bgl_fail(BGL_E_ARG, "bgl_synchronize: NULL context");
+    HIPCHK(hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+extern "C" void *bgl_ctx_stream(bgl_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+// ------------------------------------------------------------------ tensors
+static int units_of(int kind, int in) {
+    switch (kind) {
+    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q8G64: return in / 64;
+    case BGL_Q4G256SF: return in / 256;
+    case BGL_QNG64: return (in / 64 + 1) / 2;
+    default: return 0;
+    }
+}
+
+int check_wt(int kind, int bits, int out, int in) {
+    if (out <= 0 || in <= 0) return bgl_fail(BGL_E_ARG, "bad shape out=%d in=%d", out, in);
+    switch (kind) {
+    case BGL_Q4G64: case BGL_Q8G64: case BGL_QNG64:
+        if (in % 64) return bgl_fail(BGL_E_ARG, "in=%d %% 64 != 0", in);
+        if (kind == BGL_QNG64 && (bits < 2 || bits > 15)) return bgl_fail(BGL_E_ARG, "qNg64 n=%d outside 2..15", bits);
+        return 0;
+    case BGL_Q4G32H:
+        if (in % 64) return bgl_fail(BGL_E_ARG, "Q4G32H in=%d %% 64 != 0", in);
+        return 0;
+    case BGL_Q4G256SF:
+        if (in % 256) return bgl_fail(BGL_E_ARG, "g256sf in=%d %% 256 != 0", in);
+        return 0;
+    default: return bgl_fail(BGL_E_UNSUPPORTED, "unknown weight kind %d", kind);
+    }
+}
+
+static size_t ref_packed_bytes(int kind, int bits, int out, int in) {
+    switch (kind) {
+    case BGL_Q4G64: case BGL_Q4G256SF: case BGL_Q4G32H: return (size_t)out * in / 2;
+    case BGL_Q8G64: return (size_t)out * in;
+    case BGL_QNG64: return (size_t)out * (in / 64) * bits * 8;
+    default: return 0;
+    }
+}
+static size_t ref_scale_bytes(int kind, int out, int in) {
+    switch (kind) {
+    case BGL_Q4G64: case BGL_Q8G64: case BGL_QNG64: return (size_t)out * (in / 64) * 4;
+    case BGL_Q4G256SF: return (size_t)out * (in / 256) * 4;
+    case BGL_Q4G32H: return (size_t)out * (in / 32) * 2;
+    default: return 0;
+    }
+}
+
+static inline unsigned nblk(long n, int bs = 256) { return (unsigned)((n + bs - 1) / bs); }
+
+// Repack reference-layout device buffers into a new tensor.
+static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const void *dpk, const void *dsc,
+                       const uint8_t *dsub, bgl_tensor **res) {
+    bgl_tensor *t = new bgl_tensor();
+    BglDevTensor &T = t->T;
+    T.fmt = kind; T.bits = kind == BGL_QNG64 ? bits : (kind == BGL_Q8G64 ? 8 : 4);
+    T.N = out; T.K = in; T.ntiles = (out + BGL_TILE - 1) / BGL_TILE;
+    T.nunits = units_of(kind, in);
+    T.cpu = kind == BGL_Q4G256SF ? 8 : kind == BGL_Q8G64 ? 4 : kind == BGL_QNG64 ? bits : 2;
+    T.cpr = T.nunits * T.cpu;
+    long rows = (long)T.ntiles * BGL_TILE;
+    size_t wbytes = (size_t)rows * T.cpr * 16;
+    size_t s0bytes = (size_t)rows * T.nunits * (kind == BGL_QNG64 ? 8 : 4);
+    void *w = nullptr, *s0 = nullptr, *s1 = nullptr;
+    hipError_t e = hipMalloc(&w, wbytes);
+    if (e == hipSuccess) e = hipMalloc(&s0, s0bytes);
+    if (e == hipSuccess && kind == BGL_Q4G256SF) e = hipMalloc(&s1, (size_t)rows * T.nunits * 4);
+    if (e != hipSuccess) {
+        if (w) (void)hipFree(w);
+        if (s0) (void)hipFree(s0);
+        delete t;
+        return bgl_fail(BGL_E_NOMEM, "hipMalloc for tensor (%zu B): %s", wbytes, hipGetErrorString(e));
+    }
+    t->owned = {w, s0, s1};
+    T.w = (const uint8_t *)w; T.s0 = s0; T.s1 = (const uint32_t *)s1;
+    t->device_bytes = wbytes + s0bytes + (s1 ? (size_t)rows * T.nunits * 4 : 0);
+    long nch = rows * T.cpr;
+    switch (kind) {
+    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q4G256SF:
+        hipLaunchKernelGGL(k_repack_nib, dim3(nblk(nch)), dim3(256), 0, c->stream, (const uint8_t *)dpk, out, in, (uint8_t *)w);
+        break;
+    case BGL_Q8G64:
+        hipLaunchKernelGGL(k_repack_q8, dim3(nblk(nch)), dim3(256), 0, c->stream, (const int8_t *)dpk, out, in, (uint8_t *)w);
+        break;
+    case BGL_QNG64:
+        hipLaunchKernelGGL(k_repack_qng, dim3(nblk(rows * T.nunits, 64)), dim3(64), 0, c->stream, (const uint8_t *)dpk, out, in, bits, (uint8_t *)w);
+        break;
+    }
+    long nu = rows * T.nunits;
+    switch (kind) {
+    case BGL_Q4G64: case BGL_Q8G64: case BGL_Q4G32H: case BGL_Q4G256SF:
+        // Q4G32H: two fp16 per unit read as one u32; the others one fp32 per unit.
+        hipLaunchKernelGGL(k_repack_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsc, out, T.nunits, (uint32_t *)s0);
+        if (kind == BGL_Q4G256SF)
+            hipLaunchKernelGGL(k_repack_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsub, out, T.nunits, (uint32_t *)s1);
+        break;
+    case BGL_QNG64:
+        hipLaunchKernelGGL(k_repack_qng_scales, dim3(nblk(nu)), dim3(256), 0, c->stream, (const float *)dsc, out, in / 64, (float2 *)s0);
+        break;
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) { bgl_tensor_free(t); return bgl_fail(BGL_E_HIP, "repack launch: %s", hipGetErrorString(e)); }
+    *res = t;
+    return 0;
+}
+
+extern "C" int bgl_bind(bgl_ctx *c, const bgl_wt *w, bgl_tensor **out) {
+    if (!c || !w || !out || !w->packed || !w->scales) return bgl_fail(BGL_E_ARG, "bgl_bind: NULL argument");
+    int rc = check_wt(w->kind, w->bits, w->out, w->in);
+    if (rc) return rc;
+    if (w->kind == BGL_Q4G256SF && !w->sub) return bgl_fail(BGL_E_ARG, "bgl_bind: g256sf needs sub-codes");
+    HIPCHK(hipSetDevice(c->device));
+    size_t pb = ref_packed_bytes(w->kind, w->bits, w->out, w->in), sb = ref_scale_bytes(w->kind, w->out, w->in);
+    size_t subb = w->kind == BGL_Q4G256SF ? (size_t)w->out * (w->in / 64) : 0;
+    void *dpk = nullptr, *dsc = nullptr, *dsub = nullptr;
+    HIPCHK(hipMalloc(&dpk, pb));
+    HIPCHK(hipMalloc(&dsc, sb));
+    if (subb) HIPCHK(hipMalloc(&dsub, subb));
+    HIPCHK(hipMemcpyAsync(dpk, w->packed, pb, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(hipMemcpyAsync(dsc, w->scales, sb, hipMemcpyHostToDevice, c->stream));
+    if (subb) HIPCHK(hipMemcpyAsync(dsub, w->sub, subb, hipMemcpyHostToDevice, c->stream));
+    rc = repack_into(c, w->kind, w->bits, w->out, w->in, dpk, dsc, (const uint8_t *)dsub, out);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    (void)hipFree(dpk); (void)hipFree(dsc);
+    if (dsub) (void)hipFree(dsub);
+    if (rc) return rc;
+    if (e != hipSuccess) return bgl_fail(BGL_E_HIP, "bind sync: %s", hipGetErrorString(e));
+    return 0;
+}
+
+extern "C" int bgl_quantize_dev(bgl_ctx *c, int kind, int bits, int qng64_encoder, const float *w_dev, int out, int in,
+                                bgl_tensor **t, void *ref_packed, void *ref_scales, uint8_t *ref_sub) {
+    if (!c || !w_dev || !t) return bgl_fail(BGL_E_ARG, "bgl_quantize_dev: NULL argument");
+    int rc = check_wt(kind, bits, out, in);
+    if (rc) return rc;
+    if (kind == BGL_QNG64 && qng64_encoder && bits == 4)
+        return bgl_fail(BGL_E_ARG, "qng64_quantize_f32 rejects n=4 (qng64_dense.c:9)");
+    HIPCHK(hipSetDevice(c->device));
+    size_t pb = ref_packed_bytes(kind, bits, out, in), sb = ref_scale_bytes(kind, out, in);
+    size_t subb = kind == BGL_Q4G256SF ? (size_t)out * (in / 64) : 0;
+    void *dpk = nullptr, *dsc = nullptr, *dsub = nullptr;
+    HIPCHK(hipMalloc(&dpk, pb));
+    HIPCHK(hipMalloc(&dsc, sb));
+    if (subb) HIPCHK(hipMalloc(&dsub, subb));
+    long units;
+    switch (kind) {
+    case BGL_Q4G64:
+        units = (long)out * (in / 64);
+        hipLaunchKernelGGL(k_quant_q4g64, dim3(nblk(units)), dim3(256), 0, c->stream, w_dev, out, in, (uint8_t *)dpk, (float *)dsc);
+        break;
+    case BGL_Q8G64:
+        units = (long)out * (in / 64);
+        hipLaunchKernelGGL(k_quant_q8g64, dim3(nblk(units)), dim3(256), 0, c->stream, w_dev, out, in, (int8_t *)dpk, (float *)dsc);
+        break;
+    case BGL_QNG64:
+        units = (long)out * (in / 64);
+        hipLaunchKernelGGL(k_quant_qng64, dim3(nblk(units, 64)), dim3(64), 0, c->stream, w_dev, out, in, bits, qng64_encoder ? 1 : 0,
+                           (uint8_t *)dpk, (float *)dsc);
+        break;
+    case BGL_Q4G32H:
+        units = (long)out * (in / 32);
+        hipLaunchKernelGGL(k_quant_q4g32h, dim3(nblk(units)), dim3(256), 0, c->stream, w_dev, out, in, (uint8_t *)dpk, (uint16_t *)dsc);
+        break;
+    case BGL_Q4G256SF:
+        units = (long)out * (in / 256);
+        hipLaunchKernelGGL(k_quant_g256sf, dim3(nblk(units, 64)), dim3(64), 0, c->stream, w_dev, out, in, (uint8_t *)dpk, (float *)dsc,
+                           (uint8_t *)dsub);
+        break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) rc = bgl_fail(BGL_E_HIP, "quantize launch: %s", hipGetErrorString(e));
+    if (!rc) rc = repack_into(c, kind, bits, out, in, dpk, dsc, (const uint8_t *)dsub, t);
+    if (!rc && ref_packed) rc = hipMemcpyAsync(ref_packed, dpk, pb, hipMemcpyDeviceToHost, c->stream) ? BGL_E_HIP : 0;
+    if (!rc && ref_scales) rc = hipMemcpyAsync(ref_scales, dsc, sb, hipMemcpyDeviceToHost, c->stream) ? BGL_E_HIP : 0;
+    if (!rc && ref_sub && subb) rc = hipMemcpyAsync(ref_sub, dsub, subb, hipMemcpyDeviceToHost, c->stream) ? BGL_E_HIP : 0;
+    e = hipStreamSynchronize(c->stream);
+    (void)hipFree(dpk); (void)hipFree(dsc);
+    if (dsub) (void)hipFree(dsub);
+    if (rc) return rc == BGL_E_HIP ? bgl_fail(BGL_E_HIP, "quantize copy-back failed") : rc;
+    if (e != hipSuccess) return bgl_fail(BGL_E_HIP, "quantize sync: %s", hipGetErrorString(e));
+    return 0;
+}
+
+extern "C" void bgl_tensor_free(bgl_tensor *t) {
+    if (!t) return;
+    for (void *p : t->owned) if (p) (void)hipFree(p);
+    for (bgl_tensor *e : t->experts) bgl_tensor_free(e);
+    delete t;
+}
+
+extern "C" int bgl_tensor_info(const bgl_tensor *t, int *kind, int *bits, int *out, int *in, size_t *device_bytes) {
+    if (!t) return bgl_fail(BGL_E_ARG, "bgl_tensor_info: NULL tensor");
+    if (!t->experts.empty()) {
+        if (kind) *kind = 0;
+        if (bits) *bits = 0;
+        if (out) *out = t->experts[0]->T.N;
+        if (in) *in = t->experts[0]->T.K;
+        if (device_bytes) { size_t s = 0; for (auto *e : t->experts) s += e->device_bytes; *device_bytes = s; }
+        return 0;
+    }
+    if (kind) *kind = t->T.fmt;
+    if (bits) *bits = t->T.bits;
+    if (out) *out = t->T.N;
+    if (in) *in = t->T.K;
+    if (device_bytes) *device_bytes = t->device_bytes;
+    return 0;
+}
+
+extern "C" int bgl_dequant_dev(bgl_ctx *c, const bgl_tensor *t, int row0, int nrows, float *out_dev) {
+    if (!c || !t || !out_dev || !t->experts.empty()) return bgl_fail(BGL_E_ARG, "bgl_dequant_dev: bad argument");
+    if (row0 < 0 || nrows <= 0 || row0 + nrows > t->T.N) return bgl_fail(BGL_E_ARG, "bgl_dequant_dev: rows out of range");
+    hipLaunchKernelGGL(k_dequant, dim3(nblk((long)nrows * t->T.K)), dim3(256), 0, c->stream, t->T, row0, nrows, out_dev);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+// ------------------------------------------------------------------ activation prep
+int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, GemvAct &A) {
+    memset(&A, 0, sizeof A);
+    if (act == BGL_ACT_F32) {
+        int ng = K / 64;
+        if (dbuf_reserve(c, c->act_w, (size_t)M * ng * 192, false) || dbuf_reserve(c, c->act_s, (size_t)M * ng * 4, false) ||
+            dbuf_reserve(c, c->act_sum, (size_t)M * (K / 32) * 16, false))
+            return BGL_E_NOMEM;
+        hipLaunchKernelGGL(k_act_x24, dim3(nblk((long)M * ng * 64)), dim3(256), 0, c->stream, x_dev, M, K,
+                           (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
+    } else {
+        if (dbuf_reserve(c, c->act_w, (size_t)M * K, false) || dbuf_reserve(c, c->act_s, (size_t)M * (K / gq) * 4, false) ||
+            dbuf_reserve(c, c->act_sum, (size_t)M * (K / 64) * 4, false))
+            return BGL_E_NOMEM;
+        hipLaunchKernelGGL(k_act_w4a8, dim3(nblk((long)M * (K / gq) * 64)), dim3(256), 0, c->stream, x_dev, M, K, gq,
+                           (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
+    }
+    HIPCHK(hipGetLastError());
+    A.xw = (const int *)c->act_w.p;
+    A.xs = (const float *)c->act_s.p;
+    A.xsum = (const int *)c->act_sum.p;
+    A.gq = gq;
+    return 0;
+}
+
+extern "C" int bgl_quant_act_i8_dev(bgl_ctx *c, const float *x_dev, int M, int in, int gsize, int8_t *xq_dev, float *ascale_dev) {
+    if (!c || !x_dev || !xq_dev || !ascale_dev || M <= 0) return bgl_fail(BGL_E_ARG, "bgl_quant_act_i8_dev: bad argument");
+    if ((gsize != 64 && gsize != 256) || in % gsize) return bgl_fail(BGL_E_ARG, "bgl_quant_act_i8_dev: in=%d gsize=%d", in, gsize);
+    if (dbuf_reserve(c, c->act_sum, (size_t)M * (in / 64) * 4, false)) return BGL_E_NOMEM;
+    hipLaunchKernelGGL(k_act_w4a8, dim3(nblk((long)M * (in / gsize) * 64)), dim3(256), 0, c->stream, x_dev, M, in, gsize, xq_dev,
+                       ascale_dev, (int *)c->act_sum.p);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+// ------------------------------------------------------------------ GEMV planning + launch
+// Split K across workgroups so the whole launch has about target_blocks workgroups (4 waves each).
+void plan_task(bgl_ctx *c, const BglDevTensor &T, int total_tiles, int &ks, int &gpb) {
+    int want = (c->target_blocks + total_tiles - 1) / total_tiles;
+    if (want < 1) want = 1;
+    if (want > T.nunits) want = T.nunits;
+    gpb = (T.nunits + want - 1) / want;
+    ks = (T.nunits + gpb - 1) / gpb;
+}
+
+int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &A, int M,
+             const float *const *bias, float *const *y, const int *ystride) {
+    int total_tiles = 0;
+    for (int i = 0; i < n; i++) total_tiles += Ts[i].ntiles;
+    GemvLaunch L;
+    memset(&L, 0, sizeof L);
+    L.ntasks = n;
+    L.a = A;
+    int blocks = 0, tb = 0, ct = 0;
+    for (int i = 0; i < n; i++) {
+        GemvTask &t = L.t[i];
+        t.T = Ts[i];
+        t.y = y[i];
+        t.bias = bias ? bias[i] : nullptr;
+        t.ystride = ystride ? ystride[i] : Ts[i].N;
+        plan_task(c, Ts[i], total_tiles, t.ks, t.gpb);
+        t.blk0 = blocks;
+        blocks += Ts[i].ntiles * t.ks;
+        t.tb_off = tb;
+        t.ctr_off = ct;
+        if (t.ks > 1) { tb += Ts[i].ntiles * t.ks * 8 * BGL_TILE; ct += Ts[i].ntiles; }
+    }
+    if (dbuf_reserve(c, c->tbuf, (size_t)(tb ? tb : 1) * 4, false) || dbuf_reserve(c, c->ctr, (size_t)(ct ? ct : 1) * 4, true))
+        return BGL_E_NOMEM;
+    L.tbuf = (float *)c->tbuf.p;
+    L.ctr = (unsigned *)c->ctr.p;
+    for (int m0 = 0; m0 < M;) {
+        int r = M - m0, MB, mc;
+        if (r >= 5) { MB = 8; mc = r < 8 ? r : 8; }
+        else if (r >= 2) { MB = 4; mc = r; }
+        else { MB = 1; mc = 1; }
+        L.m0 = m0;
+        L.mcols = mc;
+        int rc = bgl_launch_gemv(act, MB, L, blocks, c->stream);
+        if (rc == -2) return bgl_fail(BGL_E_UNSUPPORTED, "kind %d does not support activation mode %d", Ts[0].fmt, act);
+        if (rc) return bgl_fail(BGL_E_ARG, "gemv launch: bad column block");
+        HIPCHK(hipGetLastError());
+        m0 += mc;
+    }
+    return 0;
+}
+
+static int act_group(int kind) { return kind == BGL_Q4G256SF ? 256 : 64; }
+
+extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *w, int act, const float *x_dev,
+                                    const float *const *bias_dev, float *const *y_dev, int M) {
+    if (!c || n < 1 || n > BGL_MAX_TASKS || !w || !x_dev || !y_dev || M < 1) return bgl_fail(BGL_E_ARG, "bgl_matmul_group_dev: bad argument");
+    if (act != BGL_ACT_F32 && act != BGL_ACT_W4A8) return bgl_fail(BGL_E_ARG, "unknown activation mode %d", act);
+    BglDevTensor Ts[BGL_MAX_TASKS];
+    for (int i = 0; i < n; i++) {
+        if (!w[i] || !w[i]->experts.empty() || !y_dev[i]) return bgl_fail(BGL_E_ARG, "bgl_matmul_group_dev: tensor %d invalid", i);
+        Ts[i] = w[i]->T;
+        if (Ts[i].K != Ts[0].K || Ts[i].fmt != Ts[0].fmt || Ts[i].bits != Ts[0].bits)
+            return bgl_fail(BGL_E_ARG, "bgl_matmul_group_dev: fused tensors must share kind, bits and in");
+    }
+    const int kind = Ts[0].fmt;
+    if (kind == BGL_Q4G256SF && act != BGL_ACT_W4A8)
+        return bgl_fail(BGL_E_UNSUPPORTED, "K_Q4G256SF requires W4A8 activations -- no fp32-activation path exists for g256sf");
+    if ((kind == BGL_Q4G32H || kind == BGL_QNG64) && act != BGL_ACT_F32)
+        return bgl_fail(BGL_E_UNSUPPORTED, "kind %d has fp32-activation kernels only", kind);
+    HIPCHK(hipSetDevice(c->device));
+    GemvAct A;
+    int rc = prep_act(c, act, act_group(kind), x_dev, M, Ts[0].K, A);
+    if (rc) return rc;
+    return run_gemv(c, n, Ts, act, A, M, bias_dev, y_dev, nullptr);
+}
+
+extern "C" int bgl_matmul_dev(bgl_ctx *c, const bgl_tensor *w, int act, const float *x_dev, const float *bias_dev,
+                              float *y_dev, int M) {
+    const float *b[1] = {bias_dev};
+    float *y[1] = {y_dev};
+    return bgl_matmul_group_dev(c, 1, &w, act, x_dev, b, y, M);
+}
+
+// ------------------------------------------------------------------ host-pointer drop-ins
+static int host_call(bgl_ctx *c, const bgl_wt &wt, int act, const float *x, const float *bias, float *y, int M) {
+    if (!c || !x || !y || M < 1) return bgl_fail(BGL_E_ARG, "NULL argument");
+    int rc = check_wt(wt.kind, wt.bits, wt.out, wt.in);
+    if (rc) return rc;
+    HIPCHK(hipSetDevice(c->device));
+    bgl_tensor *t = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(c->mu);
+        auto it = c->host_cache.find(wt.packed);
+        if (it != c->host_cache.end()) {
+            t = it->second;
+            if (t->T.fmt != wt.kind || t->T.N != wt.out || t->T.K != wt.in || (wt.kind == BGL_QNG64 && t->T.bits != wt.bits))
+                return bgl_fail(BGL_E_ARG, "cached tensor for %p has a different shape/kind (call bgl_forget first)", wt.packed);
+        }
+    }
+    if (!t) {
+        rc = bgl_bind(c, &wt, &t);
+        if (rc) return rc;
+        std::lock_guard<std::mutex> lk(c->mu);
+        c->host_cache[wt.packed] = t;
+    }
+    size_t xb = (size_t)M * wt.in * 4, yb = (size_t)M * wt.out * 4;
+    if (dbuf_reserve(c, c->hx, xb, false) || dbuf_reserve(c, c->hy, yb, false) || dbuf_reserve(c, c->hb, (size_t)wt.out * 4, false))
+        return BGL_E_NOMEM;
+    HIPCHK(hipMemcpyAsync(c->hx.p, x, xb, hipMemcpyHostToDevice, c->stream));
+    if (bias) HIPCHK(hipMemcpyAsync(c->hb.p, bias, (size_t)wt.out * 4, hipMemcpyHostToDevice, c->stream));
+    rc = bgl_matmul_dev(c, t, act, (const float *)c->hx.p, bias ? (const float *)c->hb.p : nullptr, (float *)c->hy.p, M);
+    if (rc) return rc;
+    HIPCHK(hipMemcpyAsync(y, c->hy.p, yb, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+static bgl_wt mkwt(int kind, int bits, int out, int in, const void *packed, const void *scales, const uint8_t *sub) {
+    bgl_wt w;
+    w.kind = kind; w.bits = bits; w.out = out; w.in = in; w.packed = packed; w.scales = scales; w.sub = sub;
+    return w;
+}
+
+extern "C" int bgl_gemv_q4g64_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x, const float *bias,
+                                 float *y, int out, int in) {
+    return host_call(p, mkwt(BGL_Q4G64, 4, out, in, packed, scales, nullptr), BGL_ACT_F32, x, bias, y, 1);
+}
+extern "C" int bgl_gemv_q4g64_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x, const float *bias,
+                                      float *y, int out, int in) {
+    return host_call(p, mkwt(BGL_Q4G64, 4, out, in, packed, scales, nullptr), BGL_ACT_W4A8, x, bias, y, 1);
+}
+extern "C" int bgl_gemv_q8g64_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x, const float *bias,
+                                 float *y, int out, int in) {
+    return host_call(p, mkwt(BGL_Q8G64, 8, out, in, packed, scales, nullptr), BGL_ACT_F32, x, bias, y, 1);
+}
+extern "C" int bgl_gemv_q8g64_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x, const float *bias,
+                                      float *y, int out, int in) {
+    return host_call(p, mkwt(BGL_Q8G64, 8, out, in, packed, scales, nullptr), BGL_ACT_W4A8, x, bias, y, 1);
+}
+extern "C" int bgl_gemm_qXg64_mt(bgl_ctx *p, int bits, const uint8_t *packed, const float *scales, const float *x,
+                                 const float *bias, float *y, int out, int in, int M) {
+    if (bits != 4 && bits != 8) return bgl_fail(BGL_E_ARG, "gemm_qXg64_mt: bits=%d (4 or 8)", bits);
+    return host_call(p, mkwt(bits == 8 ? BGL_Q8G64 : BGL_Q4G64, bits, out, in, packed, scales, nullptr), BGL_ACT_F32, x, bias, y, M);
+}
+extern "C" int bgl_gemv_q4g256sf_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *wsuper, const uint8_t *subcode,
+                                         const float *x, const float *bias, float *y, int out, int in) {
+    return host_call(p, mkwt(BGL_Q4G256SF, 4, out, in, packed, wsuper, subcode), BGL_ACT_W4A8, x, bias, y, 1);
+}
+extern "C" int bgl_gemm_q4g256sf_mt(bgl_ctx *p, const uint8_t *packed, const float *wsuper, const uint8_t *subcode,
+                                    const float *x, const float *bias, float *y, int out, int in, int M) {
+    return host_call(p, mkwt(BGL_Q4G256SF, 4, out, in, packed, wsuper, subcode), BGL_ACT_W4A8, x, bias, y, M);
+}
+extern "C" int bgl_qng64_matvec_f32(bgl_ctx *p, const uint8_t *packed, const float *scales, int n, const float *x,
+                                    const float *bias, float *y, int out, int in) {
+    return host_call(p, mkwt(BGL_QNG64, n, out, in, packed, scales, nullptr), BGL_ACT_F32, x, bias, y, 1);
+}
+extern "C" int bgl_qng64_matmul_f32(bgl_ctx *p, const uint8_t *packed, const float *scales, int n, const float *x,
+                                    const float *bias, float *y, int out, int in, int M) {
+    return host_call(p, mkwt(BGL_QNG64, n, out, in, packed, scales, nullptr), BGL_ACT_F32, x, bias, y, M);
+}
+extern "C" int bgl_gemv_q4g32h_mt(bgl_ctx *p, const uint8_t *packed, const uint16_t *scales16, const float *x,
+                                  const float *bias, float *y, int out, int in) {
+    return host_call(p, mkwt(BGL_Q4G32H, 4, out, in, packed, scales16, nullptr), BGL_ACT_F32, x, bias, y, 1);
+}
+extern "C" int bgl_forget(bgl_ctx *c, const void *packed) {
+    if (!c) return bgl_fail(BGL_E_ARG, "bgl_forget: NULL context");
+    std::lock_guard<std::mutex> lk(c->mu);
+    auto it = c->host_cache.find(packed);
+    if (it == c->host_cache.end()) return 0;
+    (void)hipStreamSynchronize(c->stream);
+    bgl_tensor_free(it->second);
+    c->host_cache.erase(it);
+    return 0;
+}

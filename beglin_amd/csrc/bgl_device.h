@@ -1,0 +1,63 @@
+// bgl_device.h -- device-side layout constants and helpers shared by the HIP kernels.
+//
+// Device weight layout ("row-interleaved tiles"): rows are grouped in tiles of 64 (one row per
+// lane of a wavefront).  A row's packed bytes are cut into 16-byte chunks in K order; the tile
+// stores chunk c of all 64 rows contiguously: byte offset ((tile*cpr + c)*64 + lane)*16.  Every
+// wave-wide load is one contiguous 1 KB run, and all lanes of a wave work on the same K range,
+// so the activation values they need are wave-uniform (scalar loads, SGPR operands).
+// Per-group scales are stored the same way: [tile][group][lane].
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define BGL_TILE 64            // rows per tile == lanes per wavefront
+#define BGL_WAVES 4            // wavefronts per workgroup in the GEMV kernels
+
+#include "../../include/beglin_qgemv.h"
+
+// Format ids: 1..4 are the reference engine's WT kinds (qwen_infer.c:207); 5 is the
+// build-defined int4 group-32 fp16-scale format.  Activation modes BGL_ACT_F32 (fp32 activations,
+// exact fixed-point digits) and BGL_ACT_W4A8 (the reference's dynamic int8 quantization,
+// QWEN_W4A8=1, qwen_infer.c:625-629) come from the public header.
+#define BGL_Q4G64 BGL_K_Q4G64
+#define BGL_Q8G64 BGL_K_Q8G64
+#define BGL_Q4G256SF BGL_K_Q4G256SF
+#define BGL_QNG64 BGL_K_QNG64
+#define BGL_Q4G32H BGL_K_Q4G32H
+
+// fp32 activations are represented exactly enough for the 1e-5 bar as X = rint(x * 2^(21-e)) per
+// 64-group (e = exponent of the group's max |x|, so |X| <= 2^21), split into three balanced
+// base-256 int8 digits X = d0 + 256*d1 + 65536*d2.  Per column the prep kernel writes
+// [group][digit][64 bytes] (48 dwords per group), the power-of-two scale 2^(e-21) per group and
+// the exact integer sum of X per 32-element half-group.
+#define BGL_XD_DW 48
+
+// Wave-uniform read-only operands (activations, column maps) are read through the constant address
+// space so the compiler emits scalar loads (s_load_dwordx16) and feeds v_dot4 from SGPRs.
+typedef const int __attribute__((address_space(4))) *ucint;
+typedef const float __attribute__((address_space(4))) *ucfloat;
+__device__ __forceinline__ ucint uni(const int *p) { return (ucint)p; }
+__device__ __forceinline__ ucfloat uni(const float *p) { return (ucfloat)p; }
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// int4 chunk dword -> two dwords of 4 unsigned nibble bytes (device nibble order: byte i of the
+// dword holds element i in its low nibble and element 4+i in its high nibble).
+__device__ __forceinline__ int nib_lo(uint32_t w) { return (int)(w & 0x0F0F0F0Fu); }
+__device__ __forceinline__ int nib_hi(uint32_t w) { return (int)((w >> 4) & 0x0F0F0F0Fu); }
+
+__device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// qNg64 field decomposition: n = 8a + 4b + 2c + d; field widths in descending order occupy
+// consecutive bits of the biased code u = code + 2^(n-1) from bit 0 upwards.
+struct QngFields {
+    int has8, has4, has2, has1;
+    int sh4, sh2, sh1;         // bit offsets of the 4-, 2-, 1-bit fields inside u
+};
+__host__ __device__ inline QngFields qng_fields(int n) {
+    QngFields f;
+    f.has8 = (n >> 3) & 1; f.has4 = (n >> 2) & 1; f.has2 = (n >> 1) & 1; f.has1 = n & 1;
+    f.sh4 = 8 * f.has8; f.sh2 = f.sh4 + 4 * f.has4; f.sh1 = f.sh2 + 2 * f.has2;
+    return f;
+}

@@ -1,0 +1,66 @@
+// bgl_kernels.h -- device tensor descriptor and kernel entry points (internal to the library).
+#pragma once
+#include "bgl_device.h"
+
+// A bound tensor in the tiled device layout.  Work unit per format (one wave iteration):
+//   Q4G64   64 elements, 2 chunks, s0 = fp32 scale
+//   Q4G32H  64 elements, 2 chunks, s0 = u32 holding the two fp16 group-32 scales (low = first)
+//   G256SF  256 elements, 8 chunks, s0 = fp32 wsuper, s1 = u32 of the 4 sub-codes (byte s = sub s)
+//   Q8G64   64 elements, 4 chunks, s0 = fp32 scale
+//   QNG64   128 elements (a pair of 64-groups), n chunks, s0 = float2 (the two group scales)
+struct BglDevTensor {
+    int fmt, bits, N, K, ntiles, cpr, nunits, cpu;   // cpu: chunks per unit
+    const uint8_t *w;
+    const void *s0;
+    const uint32_t *s1;
+};
+
+#define BGL_MAX_TASKS 4
+
+// One GEMV "task" = one tensor of a (possibly fused) launch.  Blocks [blk0, blk0 + ntiles*ks) of
+// the grid belong to it; block b covers tile (b-blk0)/ks and unit range [s*gpb, (s+1)*gpb).
+struct GemvTask {
+    BglDevTensor T;
+    float *y;                 // [M][N] (row stride ystride)
+    const float *bias;        // [N] or null
+    int ystride;
+    int ks, gpb, blk0;
+    int tb_off, ctr_off;      // partial-sum buffer / counter offsets (in floats / counters)
+};
+
+// Activation operands (shared by every task of a launch; all tasks have the same K).
+struct GemvAct {
+    const int *xw;            // W4A8: xq dwords [M][K/4];       F32: digits [M][K/64][48]
+    const float *xs;          // W4A8: ascale [M][K/gq];          F32: 2^(e-21) [M][K/64]
+    const int *xsum;          // W4A8: sum xq per 64 [M][K/64];   F32: digit sums [M][K/32][4]
+    const int *colmap;        // optional: column m of this launch reads activation row colmap[m]
+    int gq;                   // W4A8 activation group (64 or 256)
+};
+
+struct GemvLaunch {
+    GemvTask t[BGL_MAX_TASKS];
+    int ntasks;
+    GemvAct a;
+    int m0, mcols;            // columns [m0, m0+mcols) of the activation (mcols <= MB)
+    float *tbuf;
+    unsigned *ctr;
+};
+
+// ---- kernels (bgl_prep.hip) ----
+__global__ void k_act_w4a8(const float *x, int M, int K, int gsize, int8_t *xq, float *ascale, int *xqsum64);
+__global__ void k_act_x24(const float *x, int M, int K, int8_t *xd, float *xs, int *dsum);
+__global__ void k_quant_q4g64(const float *w, int N, int K, uint8_t *packed, float *scales);
+__global__ void k_quant_q8g64(const float *w, int N, int K, int8_t *codes, float *scales);
+__global__ void k_quant_qng64(const float *w, int N, int K, int n, int dense_floor, uint8_t *planes, float *scales);
+__global__ void k_quant_q4g32h(const float *w, int N, int K, uint8_t *packed, uint16_t *scales16);
+__global__ void k_quant_g256sf(const float *w, int N, int K, uint8_t *packed, float *wsuper, uint8_t *sub);
+__global__ void k_repack_nib(const uint8_t *src, int N, int K, uint8_t *dst);
+__global__ void k_repack_q8(const int8_t *src, int N, int K, uint8_t *dst);
+__global__ void k_repack_qng(const uint8_t *src, int N, int K, int n, uint8_t *dst);
+__global__ void k_repack_u32(const uint32_t *src, int N, int U, uint32_t *dst);
+__global__ void k_repack_u64(const uint64_t *src, int N, int U, uint64_t *dst);
+__global__ void k_repack_qng_scales(const float *src, int N, int ng, float2 *dst);
+__global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *out);
+
+// ---- host-side launchers (bgl_gemv.hip) ----
+int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, hipStream_t st);

@@ -1,0 +1,142 @@
+/* beglin_qgemv.h -- C-ABI of the MI355X (gfx950) quantized GEMV / MoE-gather backend.
+ *
+ * Plain C: pointers, sizes and ints only.  Implemented by beglin_amd/libbeglin_hip.so (HIP).
+ * Each entry point names the reference interface it replaces (paths relative to the reference
+ * repository root).  Conventions:
+ *   - return 0 on success, a negative BGL_E_* code on failure (bgl_last_error() has the text).
+ *     The reference's GEMV entries FATAL+exit(1) on misuse (q4gemv.h:675, :704, :783;
+ *     q4gemv_g256.h:342-343); the engine-side shim in INTEGRATION.md turns a non-zero return into
+ *     that same FATAL, so behaviour at the engine boundary is unchanged.
+ *   - weights: "kind" ids 1..4 are the engine's WT kinds (qwen_infer.c:207): 1 K_Q4G64, 2 K_Q8G64,
+ *     3 K_Q4G256SF, 4 K_QNG64; 5 is BGL_K_Q4G32H (int4 group-32, fp16 scale, q4gemv nibble pairing).
+ *   - *_dev entry points take DEVICE pointers and are asynchronous on the context's stream;
+ *     host-pointer entry points (the drop-ins with the reference's exact argument lists) copy
+ *     x in and y out and return after y is on the host.
+ *   - one context = one HIP stream; calls on one context are serialised by that stream.  Two
+ *     threads must not use the same context concurrently (the q4pool contract, q4gemv.h:721).
+ */
+#ifndef BEGLIN_QGEMV_H
+#define BEGLIN_QGEMV_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { BGL_K_Q4G64 = 1, BGL_K_Q8G64 = 2, BGL_K_Q4G256SF = 3, BGL_K_QNG64 = 4, BGL_K_Q4G32H = 5 };
+enum { BGL_ACT_F32 = 0, BGL_ACT_W4A8 = 1 };
+enum { BGL_OK = 0, BGL_E_ARG = -1, BGL_E_UNSUPPORTED = -2, BGL_E_HIP = -3, BGL_E_NODEV = -4, BGL_E_NOMEM = -5 };
+
+typedef struct bgl_ctx bgl_ctx;
+typedef struct bgl_tensor bgl_tensor;
+
+/* Weight descriptor: the fields of the engine's WT (qwen_infer.c:208-222).
+ *   packed: K_Q4G64/K_Q4G256SF/Q4G32H nibbles [out][in/2] (low nibble = even column);
+ *           K_Q8G64 int8 codes [out][in]; K_QNG64 bit planes [out][in/64][n][8].
+ *   scales: fp32 [out][in/64] (K_Q4G64, K_Q8G64, K_QNG64); fp32 wsuper [out][in/256] (K_Q4G256SF);
+ *           fp16 bits [out][in/32] (Q4G32H).
+ *   sub:    K_Q4G256SF only: sub-codes u8 [out][in/64].
+ *   bits:   K_QNG64 only: n in 2..15. */
+typedef struct {
+    int kind, bits, out, in;
+    const void *packed;
+    const void *scales;
+    const uint8_t *sub;
+} bgl_wt;
+
+/* ---------------- runtime (mlx_moe.h:24-36 analogues) ---------------- */
+int  bgl_available(void);                                   /* mlx_gpu_available (mlx_moe.h:24) */
+const char *bgl_last_error(void);
+int  bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out);   /* q4pool_init+start (q4gemv.h:580-620); stream NULL = own stream */
+void bgl_ctx_destroy(bgl_ctx *ctx);                         /* q4pool_destroy (q4gemv.h:623-637) */
+int  bgl_synchronize(bgl_ctx *ctx);                         /* mlx_gpu_synchronize (mlx_moe.h:29) */
+void *bgl_ctx_stream(bgl_ctx *ctx);                          /* the hipStream_t work is queued on */
+
+/* ---------------- weight binding: upload + repack into the tiled device layout ----------------
+ * mlx_gpu_bind_af (mlx_moe.h:48-50) / kai_repack_one_lazy (qwen_infer.c:473-487).  Host buffers
+ * are read once; the device copy is owned by the returned tensor. */
+int  bgl_bind(bgl_ctx *ctx, const bgl_wt *w, bgl_tensor **out);
+/* Quantize fp32 weights already on the device with the reference packer of `kind`, straight into
+ * the device layout (load-time transcode: gguf_quantize_q4g64_error_feedback / gguf_quantize_q8g64 /
+ * gguf_quantize_qNg64 (gguf_transcode.c:24-162), qng64_quantize_f32 (qng64_dense.c:29-68,
+ * qng64_encoder=1), gguf_w_quantize_q4_0 re-paired (gguf_write_quants.c:34-62), g256sf build packer).
+ * If ref_packed/ref_scales/ref_sub are non-NULL the reference-layout bytes are copied back there
+ * (host pointers) for byte-exact checks or caching. */
+int  bgl_quantize_dev(bgl_ctx *ctx, int kind, int bits, int qng64_encoder, const float *w_dev, int out, int in,
+                      bgl_tensor **t, void *ref_packed, void *ref_scales, uint8_t *ref_sub);
+void bgl_tensor_free(bgl_tensor *t);
+int  bgl_tensor_info(const bgl_tensor *t, int *kind, int *bits, int *out, int *in, size_t *device_bytes);
+/* mlx_gpu_dequant_probe (mlx_moe.h:78-79): decode rows [row0,row0+nrows) from the device layout. */
+int  bgl_dequant_dev(bgl_ctx *ctx, const bgl_tensor *t, int row0, int nrows, float *out_dev);
+
+/* ---------------- GEMV / small-M GEMM on device pointers ----------------
+ * y[m][r] = bias[r] + sum_c W[r][c] x[m][c], m < M.
+ *   act = BGL_ACT_F32: fp32 activations (gemv_q4g64_mt / gemv_q8g64_mt / gemm_qXg64_mt,
+ *         q4gemv.h:672-769; qng64_matvec_f32 / qng64_matmul_f32, qng64_dense.c:70-100).
+ *   act = BGL_ACT_W4A8: the reference's dynamic int8 activations (gemv_q4g64_sdot_mt,
+ *         gemv_q8g64_sdot_mt, gemm_qXg64_sdot_mt, q4gemv.h:701-791; gemv/gemm_q4g256sf_sdot_mt,
+ *         q4gemv_g256.h:339-383).  K_Q4G256SF accepts only this mode (qwen_infer.c:697-702).
+ * This is the matvec_t / matmul_t / matmul_sdot backend switch (qwen_infer.c:687-708,
+ * :1608-1655, :1852-1900) with the format taken from the bound tensor. */
+int  bgl_matmul_dev(bgl_ctx *ctx, const bgl_tensor *w, int act, const float *x_dev, const float *bias_dev,
+                    float *y_dev, int M);
+/* Several tensors that share one activation (fused q/k/v or gate+up, QWEN_FUSED_DISPATCH,
+ * qwen_infer.c:1276-1306) in ONE launch.  All must have the same `in` and kind; n <= 4. */
+int  bgl_matmul_group_dev(bgl_ctx *ctx, int n, const bgl_tensor *const *w, int act, const float *x_dev,
+                          const float *const *bias_dev, float *const *y_dev, int M);
+/* W4A8 activation quantizer on device (q4_quant_act_i8, q4gemv.h:177-213; _g256,
+ * q4gemv_g256.h:72-99): xq [M][in] int8, ascale [M][in/gsize]. */
+int  bgl_quant_act_i8_dev(bgl_ctx *ctx, const float *x_dev, int M, int in, int gsize, int8_t *xq_dev, float *ascale_dev);
+
+/* ---------------- host-pointer drop-ins with the reference's argument lists ----------------
+ * The q4pool* argument becomes the context.  The weight pointer identifies the tensor: the first
+ * call binds it (lazy repack), later calls reuse the device copy (keyed by the packed pointer).
+ * Synchronous: y is valid on return. */
+int bgl_gemv_q4g64_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
+                      const float *bias, float *y, int out, int in);                     /* q4gemv.h:672 */
+int bgl_gemv_q4g64_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
+                           const float *bias, float *y, int out, int in);                /* q4gemv.h:701 */
+int bgl_gemv_q8g64_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
+                      const float *bias, float *y, int out, int in);                     /* q4gemv.h:748 */
+int bgl_gemv_q8g64_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
+                           const float *bias, float *y, int out, int in);                /* q4gemv.h:726 */
+int bgl_gemm_qXg64_mt(bgl_ctx *p, int bits, const uint8_t *packed, const float *scales, const float *x,
+                      const float *bias, float *y, int out, int in, int M);              /* q4gemv.h:761 */
+int bgl_gemv_q4g256sf_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *wsuper, const uint8_t *subcode,
+                              const float *x, const float *bias, float *y, int out, int in);   /* q4gemv_g256.h:339 */
+int bgl_gemm_q4g256sf_mt(bgl_ctx *p, const uint8_t *packed, const float *wsuper, const uint8_t *subcode,
+                         const float *x, const float *bias, float *y, int out, int in, int M); /* matmul_sdot g256sf arm, qwen_infer.c:1880-1898 */
+int bgl_qng64_matvec_f32(bgl_ctx *p, const uint8_t *packed, const float *scales, int n, const float *x,
+                         const float *bias, float *y, int out, int in);                  /* qng64_dense.c:81 */
+int bgl_qng64_matmul_f32(bgl_ctx *p, const uint8_t *packed, const float *scales, int n, const float *x,
+                         const float *bias, float *y, int out, int in, int M);           /* qng64_dense.c:70 */
+int bgl_gemv_q4g32h_mt(bgl_ctx *p, const uint8_t *packed, const uint16_t *scales16, const float *x,
+                       const float *bias, float *y, int out, int in);                    /* no reference kernel: Q4_0 values (gguf_quants.c:118-130) */
+/* Drop the cached device copy bound to `packed` (rebind after the caller changes the bytes). */
+int bgl_forget(bgl_ctx *p, const void *packed);
+
+/* ---------------- MoE: expert-sorted gather ----------------
+ * An E-stacked expert tensor (MoeAFTensor, qwen_infer.c:2358-2444; per-expert widths like
+ * st_register_moe_experts_mixed_as, :16439-16564): E descriptors, each expert with its own kind.
+ * All experts share out/in. */
+int bgl_bind_experts(bgl_ctx *ctx, int E, const bgl_wt *experts, bgl_tensor **out);
+int bgl_experts_from_tensors(bgl_ctx *ctx, int E, bgl_tensor *const *experts, bgl_tensor **out);  /* takes ownership */
+/* Explicit pairs: y[z] = W[expert_idx[z]] x[z] for z < N (mlx_gpu_qng64_gather_probe, mlx_moe.h:89-91;
+ * ffn_gather canonical form, mlx_moe.cpp:1577-1589, :1901-1916).  Pairs are sorted by expert on
+ * the device so each expert's weights stream once per call.  fp32 activations. */
+int bgl_gather_matvec_dev(bgl_ctx *ctx, const bgl_tensor *experts, const float *x_dev, const int32_t *expert_idx_dev,
+                          int N, float *y_dev);
+/* Routed SwiGLU FFN for T tokens with top-K routing given (moe_ffn_batched, qwen_infer.c:5238-5350):
+ * out[t] = sum_k w[t][k] * down_e(silu(gate_e x_t) * up_e x_t) + shared(x_t), e = idx[t][k];
+ * the weighted sum runs in ascending expert order per token like the reference's bucket loop.
+ * shared_* may be NULL (no shared experts). x_dev [T][in], idx/w [T][K] on device, out [T][in]. */
+int bgl_moe_ffn_dev(bgl_ctx *ctx, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down,
+                    const bgl_tensor *shared_gate, const bgl_tensor *shared_up, const bgl_tensor *shared_down,
+                    const float *x_dev, const int32_t *topk_idx_dev, const float *topk_w_dev, int T, int K,
+                    float *out_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,252 @@
+"""GPU parity: the HIP library (through the C-ABI) against the CPU oracle on the same inputs.
+
+Bar: packed bytes, decoded weights and int8 activation codes bit-exact; GEMV outputs within
+max|y - ref| / max|ref| <= 1e-5 (fp32 accumulation, order-of-summation differences only)."""
+import sys
+
+import numpy as np
+import pytest
+
+from golden.fixtures import seeded_normal
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "gpu tests need a GPU"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ctx(torch_dev):
+    import beglin_amd
+    c = beglin_amd.Context(0)
+    yield c
+    c.sync()
+    c.close()
+
+
+def relerr(y, r):
+    y = np.asarray(y, np.float64); r = np.asarray(r, np.float64)
+    return float(np.max(np.abs(y - r)) / max(np.max(np.abs(r)), 1e-30))
+
+
+def weights(seed, out, inn, edge=True):
+    w = seeded_normal(seed, (out, inn), 0.02)
+    rng = np.random.default_rng(seed + 1)
+    w[rng.random(w.shape) < 0.01] *= 8
+    if edge and out > 3:
+        w[1, :] = 0.0
+        w[2, :64] = 5e-12
+    return w
+
+
+def ref_quant(oracle, kind, w, bits=0):
+    if kind == 1:
+        p, s = oracle.quantize_q4g64(w); return p, s, None
+    if kind == 2:
+        p, s = oracle.quantize_q8g64(w); return p, s, None
+    if kind == 3:
+        return oracle.quantize_g256sf(w)
+    if kind == 4:
+        p, s = oracle.quantize_qng64(w, bits); return p, s, None
+    p, s = oracle.quantize_q4g32h(w); return p, s, None
+
+
+CASES = [(1, 0), (2, 0), (3, 0), (5, 0)] + [(4, n) for n in range(2, 16)]
+
+
+@pytest.mark.parametrize("kind,bits", CASES)
+def test_device_packer_bytes_and_decode(ctx, torch_dev, oracle, kind, bits):
+    torch = torch_dev
+    out, inn = 77, 512
+    say("packer", kind, bits, out, inn)
+    w = weights(100 + kind * 20 + bits, out, inn)
+    pk, sc, sub = ref_quant(oracle, kind, w, bits)
+    t, (gpk, gsc, gsub) = ctx.quantize(kind, torch.from_numpy(w).cuda(), bits=bits, qng64_encoder=(bits != 4), want_ref=True)
+    assert np.array_equal(gpk, pk), "device packer bytes differ"
+    assert np.array_equal(gsc.view(np.uint8), sc.view(np.uint8)), "device packer scales differ"
+    if sub is not None:
+        assert np.array_equal(gsub, sub)
+    want = oracle.decode(kind, pk, sc, out, inn, bits=bits, sub=sub)
+    got = torch.empty((out, inn), dtype=torch.float32, device="cuda")
+    ctx.dequant(t, 0, out, got)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32)), "tiled-layout decode not bit-exact"
+    # host-side bind of the same reference bytes decodes identically
+    t2 = ctx.bind(kind, pk, sc, out, inn, bits=bits, sub=sub)
+    got2 = torch.empty_like(got)
+    ctx.dequant(t2, 0, out, got2)
+    torch.cuda.synchronize()
+    assert torch.equal(got, got2)
+    t.free(); t2.free()
+
+
+@pytest.mark.parametrize("gsize", [64, 256])
+def test_w4a8_activation_codes_bit_exact(ctx, torch_dev, oracle, gsize):
+    torch = torch_dev
+    say("quant_act", gsize)
+    x = seeded_normal(7, (5, 2048))
+    x[0, :gsize] = 0.0                                     # 1e-8 floor
+    x[1, :4] = [127.0, 2.5 * 127 / 127, -0.5, 0.5]         # ties go away from zero
+    xq, a = oracle.quant_act_i8(x, gsize)
+    xd = torch.from_numpy(x).cuda()
+    gq = torch.empty((5, 2048), dtype=torch.int8, device="cuda")
+    ga = torch.empty((5, 2048 // gsize), dtype=torch.float32, device="cuda")
+    ctx.quant_act_i8(xd, gsize, gq, ga)
+    torch.cuda.synchronize()
+    assert np.array_equal(gq.cpu().numpy(), xq)
+    assert np.array_equal(ga.cpu().numpy().view(np.uint32), a.view(np.uint32))
+
+
+GEMV_CASES = [
+    (1, 0, 0, 1536), (1, 0, 1, 1536), (2, 0, 0, 1024), (2, 0, 1, 1024), (3, 0, 1, 1536), (5, 0, 0, 1536),
+    (4, 2, 0, 1024), (4, 3, 0, 1024), (4, 4, 0, 1024), (4, 5, 0, 1408), (4, 7, 0, 1024), (4, 8, 0, 1024),
+    (4, 12, 0, 1024), (4, 15, 0, 1024), (4, 9, 0, 192),
+]
+
+
+@pytest.mark.parametrize("kind,bits,act,inn", GEMV_CASES)
+@pytest.mark.parametrize("M", [1, 3, 8, 13])
+def test_gemv_parity(ctx, torch_dev, oracle, kind, bits, act, inn, M):
+    torch = torch_dev
+    out = 200
+    say("gemv", kind, bits, act, inn, M)
+    w = weights(300 + kind * 20 + bits, out, inn)
+    pk, sc, sub = ref_quant(oracle, kind, w, bits)
+    x = seeded_normal(400 + M, (M, inn))
+    bias = seeded_normal(500, (out,))
+    if act == 0:
+        ref = oracle.gemm_f32(kind, pk, sc, x, bias=bias, bits=bits)
+    else:
+        ref = oracle.matmul_sdot(kind, pk, sc, x, bias=bias, sub=sub)
+    t = ctx.bind(kind, pk, sc, out, inn, bits=bits, sub=sub)
+    xd = torch.from_numpy(x).cuda()
+    bd = torch.from_numpy(bias).cuda()
+    y = torch.full((M, out), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.matmul(t, xd, y, act=act, bias_dev=bd)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    e = relerr(got, ref)
+    print(f"  max-rel {e:.3e}")
+    assert np.all(np.isfinite(got))
+    assert e <= TOL, e
+    t.free()
+
+
+def test_fused_group_equals_separate(ctx, torch_dev, oracle):
+    """q/k/v in one launch == three launches (QWEN_FUSED_DISPATCH)."""
+    torch = torch_dev
+    say("fused group")
+    shapes = [(1536, 1536), (256, 1536), (256, 1536)]
+    ts, ys1, ys2 = [], [], []
+    x = torch.from_numpy(seeded_normal(9, (1536,))).cuda()
+    for i, (o, k) in enumerate(shapes):
+        pk, ws, sub = oracle.quantize_g256sf(weights(600 + i, o, k, edge=False))
+        ts.append(ctx.bind(3, pk, ws, o, k, sub=sub))
+        ys1.append(torch.empty(o, device="cuda")); ys2.append(torch.empty(o, device="cuda"))
+    ctx.matmul_group(ts, x, ys1, act=1)
+    for t, y in zip(ts, ys2):
+        ctx.matmul(t, x, y, act=1)
+    torch.cuda.synchronize()
+    for a, b in zip(ys1, ys2):
+        assert torch.equal(a, b)
+    for t in ts:
+        t.free()
+
+
+def test_host_pointer_dropins(ctx, torch_dev, oracle):
+    """The reference-signature entry points (q4gemv.h:672-791, q4gemv_g256.h:339, qng64_dense.c:70-100)."""
+    import ctypes as C
+    import beglin_amd
+    L = beglin_amd.lib()
+    say("host drop-ins")
+    out, inn = 130, 1024
+    w = weights(700, out, inn)
+    x = seeded_normal(701, (4, inn))
+    bias = seeded_normal(702, (out,))
+    P = lambda a: C.c_void_p(a.ctypes.data) if a is not None else None
+    y = np.zeros((4, out), np.float32)
+    pk, sc = oracle.quantize_q4g64(w)
+    assert L.bgl_gemv_q4g64_mt(ctx.h, P(pk), P(sc), P(x[0]), P(bias), P(y[0]), out, inn) == 0
+    assert relerr(y[0], oracle.gemm_f32(1, pk, sc, x[0], bias=bias)) <= TOL
+    assert L.bgl_gemv_q4g64_sdot_mt(ctx.h, P(pk), P(sc), P(x[0]), P(bias), P(y[0]), out, inn) == 0
+    assert relerr(y[0], oracle.matmul_sdot(1, pk, sc, x[0], bias=bias)) <= TOL
+    assert L.bgl_gemm_qXg64_mt(ctx.h, 4, P(pk), P(sc), P(x), None, P(y), out, inn, 4) == 0
+    assert relerr(y, oracle.gemm_f32(1, pk, sc, x)) <= TOL
+    c8, s8 = oracle.quantize_q8g64(w)
+    assert L.bgl_gemv_q8g64_mt(ctx.h, P(c8), P(s8), P(x[1]), None, P(y[1]), out, inn) == 0
+    assert relerr(y[1], oracle.gemm_f32(2, c8, s8, x[1])) <= TOL
+    assert L.bgl_gemv_q8g64_sdot_mt(ctx.h, P(c8), P(s8), P(x[1]), P(bias), P(y[1]), out, inn) == 0
+    assert relerr(y[1], oracle.matmul_sdot(2, c8, s8, x[1], bias=bias)) <= TOL
+    pg, wsu, sub = oracle.quantize_g256sf(w)
+    assert L.bgl_gemv_q4g256sf_sdot_mt(ctx.h, P(pg), P(wsu), P(sub), P(x[2]), P(bias), P(y[2]), out, inn) == 0
+    assert relerr(y[2], oracle.matmul_sdot(3, pg, wsu, x[2], bias=bias, sub=sub)) <= TOL
+    assert L.bgl_gemm_q4g256sf_mt(ctx.h, P(pg), P(wsu), P(sub), P(x), P(bias), P(y), out, inn, 4) == 0
+    assert relerr(y, oracle.matmul_sdot(3, pg, wsu, x, bias=bias, sub=sub)) <= TOL
+    pq, sq = oracle.quantize_qng64(w, 5)
+    assert L.bgl_qng64_matvec_f32(ctx.h, P(pq), P(sq), 5, P(x[3]), P(bias), P(y[3]), out, inn) == 0
+    assert relerr(y[3], oracle.gemm_f32(4, pq, sq, x[3], bias=bias, bits=5)) <= TOL
+    assert L.bgl_qng64_matmul_f32(ctx.h, P(pq), P(sq), 5, P(x), P(bias), P(y), out, inn, 4) == 0
+    assert relerr(y, oracle.gemm_f32(4, pq, sq, x, bias=bias, bits=5)) <= TOL
+    ph, sh = oracle.quantize_q4g32h(w)
+    assert L.bgl_gemv_q4g32h_mt(ctx.h, P(ph), P(sh), P(x[0]), P(bias), P(y[0]), out, inn) == 0
+    assert relerr(y[0], oracle.gemm_f32(5, ph, sh, x[0], bias=bias)) <= TOL
+    for a in (pk, c8, pg, pq, ph):
+        assert L.bgl_forget(ctx.h, P(a)) == 0
+
+
+def test_error_paths(ctx, torch_dev, oracle):
+    import ctypes as C
+    import beglin_amd
+    L = beglin_amd.lib()
+    say("error paths")
+    out, inn = 64, 512
+    pg, wsu, sub = oracle.quantize_g256sf(weights(800, out, inn, edge=False))
+    t = ctx.bind(3, pg, wsu, out, inn, sub=sub)
+    x = __import__("torch").zeros(inn, device="cuda")
+    y = __import__("torch").zeros(out, device="cuda")
+    with pytest.raises(beglin_amd.BglError, match="requires W4A8"):
+        ctx.matmul(t, x, y, act=0)                       # qwen_infer.c:697-702 FATAL -> error code
+    t.free()
+    P = lambda a: C.c_void_p(a.ctypes.data)
+    z = np.zeros(100, np.float32)
+    assert L.bgl_gemv_q4g64_mt(ctx.h, P(z), P(z), P(z), None, P(z), 10, 100) == -1     # in % 64
+    assert L.bgl_qng64_matvec_f32(ctx.h, P(z), P(z), 16, P(z), None, P(z), 1, 64) == -1  # n out of range
+
+
+FULL = [
+    ("cfg1 int4 g32 fp16 gate_proj", 5, 0, 0, 8960, 1536),
+    ("cfg2 g256sf W4A8 down_proj", 3, 0, 1, 1536, 8960),
+    ("cfg3 qNg64 n=2 gate", 4, 2, 0, 14336, 4096),
+    ("cfg3 qNg64 n=15 down", 4, 15, 0, 4096, 14336),
+]
+
+
+@pytest.mark.parametrize("name,kind,bits,act,out,inn", FULL)
+def test_full_size_configs(ctx, torch_dev, oracle, name, kind, bits, act, out, inn):
+    """BASELINE shapes at full size, weights quantized on the device and checked byte-exact
+    against the oracle packer, output against the oracle GEMV."""
+    torch = torch_dev
+    say("full", name)
+    w = seeded_normal(900 + kind + bits, (out, inn), 0.02)
+    t, (gpk, gsc, gsub) = ctx.quantize(kind, torch.from_numpy(w).cuda(), bits=bits, want_ref=True)
+    pk, sc, sub = ref_quant(oracle, kind, w, bits)
+    assert np.array_equal(gpk, pk) and np.array_equal(gsc.view(np.uint8), sc.view(np.uint8))
+    x = seeded_normal(901, (inn,))
+    y = torch.empty(out, device="cuda")
+    ctx.matmul(t, torch.from_numpy(x).cuda(), y, act=act)
+    torch.cuda.synchronize()
+    ref = oracle.gemm_f32(kind, pk, sc, x, bits=bits) if act == 0 else oracle.matmul_sdot(kind, pk, sc, x, sub=sub)
+    e = relerr(y.cpu().numpy(), ref)
+    print(f"  max-rel {e:.3e}")
+    assert e <= TOL
+    t.free()
