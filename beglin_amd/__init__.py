@@ -83,6 +83,17 @@ class Context:
     def sync(self):
         _check(lib().bgl_synchronize(self.h), "bgl_synchronize")
 
+    # ---- profiling (QWEN_PROF analogue) ----
+    def prof_enable(self, on=True):
+        _check(lib().bgl_prof_enable(self.h, int(on)), "bgl_prof_enable")
+
+    def prof_read(self):
+        """{phase: (ms, launches)} for phases prep/gemv/other, summed since the last read."""
+        ms = (C.c_double * 3)()
+        n = (C.c_int * 3)()
+        _check(lib().bgl_prof_read(self.h, ms, n, 3), "bgl_prof_read")
+        return {"prep": (ms[0], n[0]), "gemv": (ms[1], n[1]), "other": (ms[2], n[2])}
+
     # ---- binding ----
     def bind(self, kind, packed, scales, out, inn, bits=0, sub=None):
         """Bind host (numpy) buffers in the reference layout."""

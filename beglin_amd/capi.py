@@ -29,6 +29,8 @@ SIGNATURES = [
     ("bgl_ctx_destroy", None, [_P]),
     ("bgl_synchronize", _I, [_P]),
     ("bgl_ctx_stream", _P, [_P]),
+    ("bgl_prof_enable", _I, [_P, _I]),
+    ("bgl_prof_read", _I, [_P, C.POINTER(C.c_double), C.POINTER(_I), _I]),
     ("bgl_bind", _I, [_P, C.POINTER(bgl_wt), C.POINTER(_P)]),
     ("bgl_quantize_dev", _I, [_P, _I, _I, _I, _P, _I, _I, C.POINTER(_P), _P, _P, _P]),
     ("bgl_tensor_free", None, [_P]),

@@ -75,10 +75,62 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
         if (e != hipSuccess) { delete c; return bgl_fail(BGL_E_HIP, "hipStreamCreate: %s", hipGetErrorString(e)); }
         c->own_stream = true;
     }
-    const char *tb = getenv("BGL_TARGET_BLOCKS");
-    c->target_blocks = tb ? atoi(tb) : 1024;
-    if (c->target_blocks < 1) c->target_blocks = 1024;
+    const char *mw = getenv("BGL_MAX_WAVES");
+    c->max_waves = mw ? atoi(mw) : 16;
+    if (c->max_waves < 1 || c->max_waves > 16) c->max_waves = 16;
+    const char *mb = getenv("BGL_MIN_BLOCKS");
+    c->min_blocks = mb ? atoi(mb) : 256;
+    const char *ft = getenv("BGL_FORCE_TR");
+    c->force_tr = ft ? atoi(ft) : 0;
+    if (c->force_tr != 0 && c->force_tr != 8 && c->force_tr != 16 && c->force_tr != 32 && c->force_tr != 64) c->force_tr = 0;
+    const char *nf = getenv("BGL_NO_FUSED_Q");
+    c->no_fused = nf && atoi(nf) != 0;
     *out = c;
+    return 0;
+}
+
+// ------------------------------------------------------------------ profiling
+static hipEvent_t ev_get(bgl_ctx *c) {
+    if (!c->ev_pool.empty()) { hipEvent_t e = c->ev_pool.back(); c->ev_pool.pop_back(); return e; }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+int prof_begin(bgl_ctx *c, int phase) {
+    if (!c->prof) return -1;
+    hipEvent_t a = ev_get(c), b = ev_get(c);
+    if (!a || !b) return -1;
+    (void)hipEventRecord(a, c->stream);
+    c->prof_ev.push_back({phase, {a, b}});
+    return (int)c->prof_ev.size() - 1;
+}
+
+void prof_end(bgl_ctx *c, int token) {
+    if (token < 0) return;
+    (void)hipEventRecord(c->prof_ev[token].second.second, c->stream);
+}
+
+extern "C" int bgl_prof_enable(bgl_ctx *c, int on) {
+    if (!c) return bgl_fail(BGL_E_ARG, "bgl_prof_enable: NULL context");
+    c->prof = on != 0;
+    return 0;
+}
+
+extern "C" int bgl_prof_read(bgl_ctx *c, double *ms, int *cnt, int nphase) {
+    if (!c) return bgl_fail(BGL_E_ARG, "bgl_prof_read: NULL context");
+    HIPCHK(hipStreamSynchronize(c->stream));
+    for (int i = 0; i < nphase; i++) { if (ms) ms[i] = 0.0; if (cnt) cnt[i] = 0; }
+    for (auto &r : c->prof_ev) {
+        float t = 0.0f;
+        if (hipEventElapsedTime(&t, r.second.first, r.second.second) == hipSuccess && r.first < nphase) {
+            if (ms) ms[r.first] += t;
+            if (cnt) cnt[r.first] += 1;
+        }
+        c->ev_pool.push_back(r.second.first);
+        c->ev_pool.push_back(r.second.second);
+    }
+    c->prof_ev.clear();
     return 0;
 }
 
@@ -86,9 +138,11 @@ extern "C" void bgl_ctx_destroy(bgl_ctx *c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    for (auto &r : c->prof_ev) { c->ev_pool.push_back(r.second.first); c->ev_pool.push_back(r.second.second); }
+    for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
     for (auto &kv : c->host_cache) bgl_tensor_free(kv.second);
     c->host_cache.clear();
-    DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->tbuf, &c->ctr, &c->hx, &c->hy, &c->hb,
+    DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->hx, &c->hy, &c->hb,
                       &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_meta};
     for (DevBuf *b : bufs) dbuf_free(*b);
     if (c->own_stream) (void)hipStreamDestroy(c->stream);
@@ -323,14 +377,18 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
         if (dbuf_reserve(c, c->act_w, (size_t)M * ng * 192, false) || dbuf_reserve(c, c->act_s, (size_t)M * ng * 4, false) ||
             dbuf_reserve(c, c->act_sum, (size_t)M * (K / 32) * 16, false))
             return BGL_E_NOMEM;
+        int tok = prof_begin(c, 0);
         hipLaunchKernelGGL(k_act_x24, dim3(nblk((long)M * ng * 64)), dim3(256), 0, c->stream, x_dev, M, K,
                            (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
+        prof_end(c, tok);
     } else {
         if (dbuf_reserve(c, c->act_w, (size_t)M * K, false) || dbuf_reserve(c, c->act_s, (size_t)M * (K / gq) * 4, false) ||
             dbuf_reserve(c, c->act_sum, (size_t)M * (K / 64) * 4, false))
             return BGL_E_NOMEM;
+        int tok = prof_begin(c, 0);
         hipLaunchKernelGGL(k_act_w4a8, dim3(nblk((long)M * (K / gq) * 64)), dim3(256), 0, c->stream, x_dev, M, K, gq,
                            (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
+        prof_end(c, tok);
     }
     HIPCHK(hipGetLastError());
     A.xw = (const int *)c->act_w.p;
@@ -351,41 +409,35 @@ extern "C" int bgl_quant_act_i8_dev(bgl_ctx *c, const float *x_dev, int M, int i
 }
 
 // ------------------------------------------------------------------ GEMV planning + launch
-// Split K across workgroups so the whole launch has about target_blocks workgroups (4 waves each).
-void plan_task(bgl_ctx *c, const BglDevTensor &T, int total_tiles, int &ks, int &gpb) {
-    int want = (c->target_blocks + total_tiles - 1) / total_tiles;
-    if (want < 1) want = 1;
-    if (want > T.nunits) want = T.nunits;
-    gpb = (T.nunits + want - 1) / want;
-    ks = (T.nunits + gpb - 1) / gpb;
+// Waves per workgroup: one per work unit up to 16 (BGL_MAX_WAVES overrides the cap).
+int pick_waves(bgl_ctx *c, int nunits) {
+    int cap = c->max_waves;
+    return nunits < cap ? (nunits < 1 ? 1 : nunits) : cap;
 }
 
-int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &A, int M,
-             const float *const *bias, float *const *y, const int *ystride) {
-    int total_tiles = 0;
-    for (int i = 0; i < n; i++) total_tiles += Ts[i].ntiles;
-    GemvLaunch L;
-    memset(&L, 0, sizeof L);
+static void fill_tasks(GemvLaunch &L, int n, const BglDevTensor *Ts, const float *const *bias, float *const *y,
+                       const int *ystride, int &blocks) {
     L.ntasks = n;
-    L.a = A;
-    int blocks = 0, tb = 0, ct = 0;
+    blocks = 0;
     for (int i = 0; i < n; i++) {
         GemvTask &t = L.t[i];
         t.T = Ts[i];
         t.y = y[i];
         t.bias = bias ? bias[i] : nullptr;
         t.ystride = ystride ? ystride[i] : Ts[i].N;
-        plan_task(c, Ts[i], total_tiles, t.ks, t.gpb);
         t.blk0 = blocks;
-        blocks += Ts[i].ntiles * t.ks;
-        t.tb_off = tb;
-        t.ctr_off = ct;
-        if (t.ks > 1) { tb += Ts[i].ntiles * t.ks * 8 * BGL_TILE; ct += Ts[i].ntiles; }
+        blocks += Ts[i].ntiles;
     }
-    if (dbuf_reserve(c, c->tbuf, (size_t)(tb ? tb : 1) * 4, false) || dbuf_reserve(c, c->ctr, (size_t)(ct ? ct : 1) * 4, true))
-        return BGL_E_NOMEM;
-    L.tbuf = (float *)c->tbuf.p;
-    L.ctr = (unsigned *)c->ctr.p;
+}
+
+int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &A, int M,
+             const float *const *bias, float *const *y, const int *ystride) {
+    GemvLaunch L;
+    memset(&L, 0, sizeof L);
+    int blocks = 0;
+    fill_tasks(L, n, Ts, bias, y, ystride, blocks);
+    L.a = A;
+    const int nw = pick_waves(c, Ts[0].nunits);
     for (int m0 = 0; m0 < M;) {
         int r = M - m0, MB, mc;
         if (r >= 5) { MB = 8; mc = r < 8 ? r : 8; }
@@ -393,13 +445,51 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
         else { MB = 1; mc = 1; }
         L.m0 = m0;
         L.mcols = mc;
-        int rc = bgl_launch_gemv(act, MB, L, blocks, c->stream);
+        int tok = prof_begin(c, 1);
+        int rc = bgl_launch_gemv(act, MB, L, blocks, nw, c->stream);
+        prof_end(c, tok);
         if (rc == -2) return bgl_fail(BGL_E_UNSUPPORTED, "kind %d does not support activation mode %d", Ts[0].fmt, act);
         if (rc) return bgl_fail(BGL_E_ARG, "gemv launch: bad column block");
         HIPCHK(hipGetLastError());
         m0 += mc;
     }
     return 0;
+}
+
+// W4A8 with one activation column: quantization fused into the GEMV workgroups (one launch).
+static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, const float *const *bias,
+                      float *const *y) {
+    GemvLaunch L;
+    memset(&L, 0, sizeof L);
+    int blocks = 0;
+    fill_tasks(L, n, Ts, bias, y, nullptr, blocks);
+    L.x = x_dev;
+    L.m0 = 0;
+    L.mcols = 1;
+    // Rows per workgroup: split 64-row tiles until the launch has enough workgroups to spread
+    // over the CUs (each workgroup still reads >= 128-byte runs per row group).
+    // (measured: K=1536 projections are fastest unsplit, K=8960 at 16 rows per workgroup)
+    int TR = 64;
+    if (Ts[0].K >= 4096)
+        while (TR > 16 && (long)blocks * (BGL_TILE / TR) < c->min_blocks) TR >>= 1;
+    if (c->force_tr) TR = c->force_tr;
+    const int KQ = BGL_TILE / TR, U = Ts[0].nunits;
+    int nw = (U + KQ - 1) / KQ;
+    if (nw > c->max_waves) nw = c->max_waves;
+    // every task block of the launch uses the same TR; remap blk0 to workgroup units
+    for (int i = 0; i < n; i++) L.t[i].blk0 *= KQ;
+    int tok = prof_begin(c, 1);
+    int rc = bgl_launch_gemv_q(L, blocks, TR, nw, c->stream);
+    prof_end(c, tok);
+    if (rc) return bgl_fail(BGL_E_UNSUPPORTED, "fused W4A8 path: kind %d", Ts[0].fmt);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+static bool fused_q_ok(bgl_ctx *c, int kind, int K, int M) {
+    if (M != 1 || c->no_fused) return false;
+    if (kind != BGL_Q4G256SF && kind != BGL_Q4G64 && kind != BGL_Q8G64) return false;
+    return bgl_gemv_q_lds(kind, K, 64) <= 64 * 1024;
 }
 
 static int act_group(int kind) { return kind == BGL_Q4G256SF ? 256 : 64; }
@@ -421,6 +511,7 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
     if ((kind == BGL_Q4G32H || kind == BGL_QNG64) && act != BGL_ACT_F32)
         return bgl_fail(BGL_E_UNSUPPORTED, "kind %d has fp32-activation kernels only", kind);
     HIPCHK(hipSetDevice(c->device));
+    if (act == BGL_ACT_W4A8 && fused_q_ok(c, kind, Ts[0].K, M)) return run_gemv_q(c, n, Ts, x_dev, bias_dev, y_dev);
     GemvAct A;
     int rc = prep_act(c, act, act_group(kind), x_dev, M, Ts[0].K, A);
     if (rc) return rc;

@@ -40,6 +40,41 @@ typedef const float __attribute__((address_space(4))) *ucfloat;
 __device__ __forceinline__ ucint uni(const int *p) { return (ucint)p; }
 __device__ __forceinline__ ucfloat uni(const float *p) { return (ucfloat)p; }
 
+// Wavefront reductions through DPP (quad_perm 1032 / 2301, row_half_mirror, row_mirror reduce each
+// 16-lane row), then readlane of the four row results.  Every lane gets the (uniform) result.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __int_as_float(dpp_i<CTRL>(__float_as_int(v))); }
+__device__ __forceinline__ float rlane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(rlane_f(v, 0), rlane_f(v, 16)), fmaxf(rlane_f(v, 32), rlane_f(v, 48)));
+}
+// returns the per-row (16-lane) sums in every lane of that row
+__device__ __forceinline__ int row_sum_i32(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    v += dpp_i<0x141>(v);
+    v += dpp_i<0x140>(v);
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+    v = row_sum_i32(v);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+// sums over lanes 0..31 and 32..63
+__device__ __forceinline__ int2 half_sums_i32(int v) {
+    v = row_sum_i32(v);
+    return make_int2(__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16),
+                     __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // int4 chunk dword -> two dwords of 4 unsigned nibble bytes (device nibble order: byte i of the

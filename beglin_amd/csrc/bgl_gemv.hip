@@ -1,20 +1,26 @@
 // bgl_gemv.hip -- the quantized GEMV / small-M GEMM kernel family (one kernel template per format).
 //
-// Work decomposition: a workgroup of 4 wavefronts owns one 64-row tile and a contiguous range of
-// work units along K; lane = row, so every wave-wide weight load is a contiguous 1 KB run and the
-// activation operands are wave-uniform (scalar loads, SGPR operands of v_dot4).  Each wave walks
-// units w, w+4, ... of the range, folding each unit's contribution into per-column fp32
-// accumulators; the 4 waves are combined in LDS in fixed order.  When K is split over several
-// workgroups (ks > 1) each writes its partial to a scratch buffer and the last one to arrive
-// (device-scope counter, reset by that same block) sums them in block order, so results are
-// deterministic run to run.
+// Work decomposition: one workgroup owns one 64-row tile and the whole K range (no cross-workgroup
+// reduction); its nw wavefronts (1..16) split the work units along K.  lane = row, so every
+// wave-wide weight load is a contiguous 1 KB run and every lane needs the same activation bytes.
+// Each wave prefetches its next unit's chunks before consuming the current one.
 //
-// Arithmetic: weight codes are exact integers.  fp32 activations arrive as three int8 digits of an
-// exact fixed-point value (see bgl_device.h), W4A8 activations as the reference's int8 codes; all
-// products are exact int32 dot4 sums, and fp32 only enters in the per-unit scale fold.
+// Two activation paths:
+//   k_gemv   (fp32 activations, and batched W4A8): the activation operands were prepared by a
+//            separate kernel (bgl_prep.hip) and are read with scalar loads straight into SGPRs,
+//            which feed v_dot4 directly.  Waves' fp32 partials are combined in LDS in fixed order.
+//   k_gemv_q (W4A8, one column): the workgroup quantizes x itself into LDS (the reference's
+//            q4_quant_act_i8 / _g256 arithmetic, bit for bit), so one call is one launch, and the
+//            per-group fp32 terms are folded in group order exactly as the reference's row loop
+//            does (q4gemv.h:241, q4gemv_g256.h:154): the result is bit-identical to the oracle.
+//
+// Arithmetic: weight codes are exact integers; fp32 activations arrive as three int8 digits of an
+// exact fixed-point value (bgl_device.h), W4A8 activations as the reference's int8 codes; every
+// product is an exact int32 dot4 sum and fp32 only enters in the per-unit scale fold.
 #include "bgl_kernels.h"
 
 #define C63 (1.0f / 63.0f)
+#define MAXW 16
 
 template <int MB>
 struct Cols {
@@ -42,22 +48,46 @@ __device__ __forceinline__ float fold_digits(int t0, int t1, int t2) {
     return (float)t0 + 256.0f * (float)t1 + 65536.0f * (float)t2;
 }
 
-// ---------------------------------------------------------------------------------- Q4G64
-template <int ACT, int MB>
-__device__ __forceinline__ void unit_q4g64(const BglDevTensor &T, int tile, int lane, int u, const GemvAct &A,
+// ================================================================================== raw unit loads
+template <int FMT, int NB> struct Raw;
+template <int NB> struct Raw<BGL_Q4G64, NB> { uint4 c[2]; float s; };
+template <int NB> struct Raw<BGL_Q4G32H, NB> { uint4 c[2]; uint32_t s; };
+template <int NB> struct Raw<BGL_Q4G256SF, NB> { uint4 c[8]; float s; uint32_t sub; };
+template <int NB> struct Raw<BGL_Q8G64, NB> { uint4 c[4]; float s; };
+template <int NB> struct Raw<BGL_QNG64, NB> { uint4 c[NB]; float2 s; };
+
+template <int FMT> constexpr int chunks_per_unit(int nb) {
+    return FMT == BGL_Q4G256SF ? 8 : FMT == BGL_Q8G64 ? 4 : FMT == BGL_QNG64 ? nb : 2;
+}
+
+template <int FMT, int NB>
+__device__ __forceinline__ void load_raw(Raw<FMT, NB> &r, const BglDevTensor &T, int tile, int lane, int u) {
+    constexpr int CPU = chunks_per_unit<FMT>(NB);
+    const uint4 *cp = reinterpret_cast<const uint4 *>(T.w) + ((size_t)tile * T.cpr + (size_t)u * CPU) * BGL_TILE + lane;
+#pragma unroll
+    for (int k = 0; k < CPU; k++) r.c[k] = cp[k * BGL_TILE];
+    const size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + lane;
+    if constexpr (FMT == BGL_QNG64) r.s = reinterpret_cast<const float2 *>(T.s0)[so];
+    else if constexpr (FMT == BGL_Q4G32H) r.s = reinterpret_cast<const uint32_t *>(T.s0)[so];
+    else r.s = reinterpret_cast<const float *>(T.s0)[so];
+    if constexpr (FMT == BGL_Q4G256SF) r.sub = T.s1[so];
+}
+
+// ================================================================================== path A compute
+// x operands: ucint (scalar-loaded) pointers into the prepared activation buffers.
+
+template <int ACT, int MB, int NB>
+__device__ __forceinline__ void comp_q4g64(const Raw<BGL_Q4G64, NB> &r, int K, int u, const GemvAct &A,
                                            const Cols<MB> &C, float (&acc)[MB]) {
-    const uint4 *cp = reinterpret_cast<const uint4 *>(T.w) + ((size_t)tile * T.cpr + (size_t)u * 2) * BGL_TILE + lane;
-    uint4 c0 = cp[0], c1 = cp[BGL_TILE];
-    float s = reinterpret_cast<const float *>(T.s0)[((size_t)tile * T.nunits + u) * BGL_TILE + lane];
     int lo[8], hi[8];
-    uint32_t raw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    uint32_t raw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w};
 #pragma unroll
     for (int q = 0; q < 8; q++) { lo[q] = nib_lo(raw[q]); hi[q] = nib_hi(raw[q]); }
-    const int K = T.K, ng = K >> 6;
+    const int ng = K >> 6;
 #pragma unroll
     for (int m = 0; m < MB; m++) {
-        int am = C.am[m];
-        if (ACT == BGL_ACT_F32) {
+        const int am = C.am[m];
+        if constexpr (ACT == BGL_ACT_F32) {
             ucint xg = uni(A.xw) + ((size_t)am * ng + u) * BGL_XD_DW;
             int t0 = 0, t1 = 0, t2 = 0;
 #pragma unroll
@@ -68,37 +98,31 @@ __device__ __forceinline__ void unit_q4g64(const BglDevTensor &T, int tile, int 
             }
             int4 d0 = ld_dsum(A, am, K, 2 * u), d1 = ld_dsum(A, am, K, 2 * u + 1);
             t0 -= 8 * (d0.x + d1.x); t1 -= 8 * (d0.y + d1.y); t2 -= 8 * (d0.z + d1.z);
-            float V = fold_digits(t0, t1, t2);
-            acc[m] += s * (V * uni(A.xs)[(size_t)am * ng + u]);
+            acc[m] += r.s * (fold_digits(t0, t1, t2) * uni(A.xs)[(size_t)am * ng + u]);
         } else {
             ucint xq = uni(A.xw) + (size_t)am * (K >> 2) + (size_t)u * 16;
             int isum = 0;
 #pragma unroll
             for (int q = 0; q < 8; q++) { isum = dot4(lo[q], xq[2 * q], isum); isum = dot4(hi[q], xq[2 * q + 1], isum); }
             isum -= 8 * uni(A.xsum)[(size_t)am * ng + u];
-            float t = __fmul_rn(__fmul_rn((float)isum, s), uni(A.xs)[(size_t)am * ng + u]);
-            acc[m] = __fadd_rn(acc[m], t);
+            acc[m] = __fadd_rn(acc[m], __fmul_rn(__fmul_rn((float)isum, r.s), uni(A.xs)[(size_t)am * ng + u]));
         }
     }
 }
 
-// ---------------------------------------------------------------------------------- Q4G32H (fp32 act)
-template <int MB>
-__device__ __forceinline__ void unit_q4g32h(const BglDevTensor &T, int tile, int lane, int u, const GemvAct &A,
+template <int MB, int NB>
+__device__ __forceinline__ void comp_q4g32h(const Raw<BGL_Q4G32H, NB> &r, int K, int u, const GemvAct &A,
                                             const Cols<MB> &C, float (&acc)[MB]) {
-    const uint4 *cp = reinterpret_cast<const uint4 *>(T.w) + ((size_t)tile * T.cpr + (size_t)u * 2) * BGL_TILE + lane;
-    uint4 c0 = cp[0], c1 = cp[BGL_TILE];
-    uint32_t s2 = reinterpret_cast<const uint32_t *>(T.s0)[((size_t)tile * T.nunits + u) * BGL_TILE + lane];
-    float sa = __half2float(__ushort_as_half((unsigned short)(s2 & 0xffffu)));
-    float sb = __half2float(__ushort_as_half((unsigned short)(s2 >> 16)));
+    float sa = __half2float(__ushort_as_half((unsigned short)(r.s & 0xffffu)));
+    float sb = __half2float(__ushort_as_half((unsigned short)(r.s >> 16)));
     int lo[8], hi[8];
-    uint32_t raw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    uint32_t raw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w};
 #pragma unroll
     for (int q = 0; q < 8; q++) { lo[q] = nib_lo(raw[q]); hi[q] = nib_hi(raw[q]); }
-    const int K = T.K, ng = K >> 6;
+    const int ng = K >> 6;
 #pragma unroll
     for (int m = 0; m < MB; m++) {
-        int am = C.am[m];
+        const int am = C.am[m];
         ucint xg = uni(A.xw) + ((size_t)am * ng + u) * BGL_XD_DW;
         int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
@@ -121,29 +145,20 @@ __device__ __forceinline__ void unit_q4g32h(const BglDevTensor &T, int tile, int
     }
 }
 
-// ---------------------------------------------------------------------------------- G256SF (W4A8)
-template <int MB>
-__device__ __forceinline__ void unit_g256sf(const BglDevTensor &T, int tile, int lane, int u, const GemvAct &A,
+template <int MB, int NB>
+__device__ __forceinline__ void comp_g256sf(const Raw<BGL_Q4G256SF, NB> &r, int K, int u, const GemvAct &A,
                                             const Cols<MB> &C, float (&acc)[MB]) {
-    const uint4 *cp = reinterpret_cast<const uint4 *>(T.w) + ((size_t)tile * T.cpr + (size_t)u * 8) * BGL_TILE + lane;
-    uint4 ch[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) ch[k] = cp[k * BGL_TILE];
-    size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + lane;
-    float ws = reinterpret_cast<const float *>(T.s0)[so];
-    uint32_t sub4 = T.s1[so];
     int lo[32], hi[32];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        lo[4 * k] = nib_lo(ch[k].x); hi[4 * k] = nib_hi(ch[k].x);
-        lo[4 * k + 1] = nib_lo(ch[k].y); hi[4 * k + 1] = nib_hi(ch[k].y);
-        lo[4 * k + 2] = nib_lo(ch[k].z); hi[4 * k + 2] = nib_hi(ch[k].z);
-        lo[4 * k + 3] = nib_lo(ch[k].w); hi[4 * k + 3] = nib_hi(ch[k].w);
+        lo[4 * k] = nib_lo(r.c[k].x); hi[4 * k] = nib_hi(r.c[k].x);
+        lo[4 * k + 1] = nib_lo(r.c[k].y); hi[4 * k + 1] = nib_hi(r.c[k].y);
+        lo[4 * k + 2] = nib_lo(r.c[k].z); hi[4 * k + 2] = nib_hi(r.c[k].z);
+        lo[4 * k + 3] = nib_lo(r.c[k].w); hi[4 * k + 3] = nib_hi(r.c[k].w);
     }
-    const int K = T.K;
 #pragma unroll
     for (int m = 0; m < MB; m++) {
-        int am = C.am[m];
+        const int am = C.am[m];
         ucint xq = uni(A.xw) + (size_t)am * (K >> 2) + (size_t)u * 64;
         ucint xs = uni(A.xsum) + (size_t)am * (K >> 6) + (size_t)u * 4;
         int comb = 0;
@@ -156,96 +171,83 @@ __device__ __forceinline__ void unit_g256sf(const BglDevTensor &T, int tile, int
                 isum = dot4(hi[8 * sg + q], xq[16 * sg + 2 * q + 1], isum);
             }
             isum -= 8 * xs[sg];
-            comb += isum * (int)((sub4 >> (8 * sg)) & 255u);
+            comb += isum * (int)((r.sub >> (8 * sg)) & 255u);
         }
-        float t = __fmul_rn(__fmul_rn(__fmul_rn((float)comb, ws), C63), uni(A.xs)[(size_t)am * (K >> 8) + u]);
+        float t = __fmul_rn(__fmul_rn(__fmul_rn((float)comb, r.s), C63), uni(A.xs)[(size_t)am * (K >> 8) + u]);
         acc[m] = __fadd_rn(acc[m], t);
     }
 }
 
-// ---------------------------------------------------------------------------------- Q8G64
-template <int ACT, int MB>
-__device__ __forceinline__ void unit_q8g64(const BglDevTensor &T, int tile, int lane, int u, const GemvAct &A,
+template <int ACT, int MB, int NB>
+__device__ __forceinline__ void comp_q8g64(const Raw<BGL_Q8G64, NB> &r, int K, int u, const GemvAct &A,
                                            const Cols<MB> &C, float (&acc)[MB]) {
-    const uint4 *cp = reinterpret_cast<const uint4 *>(T.w) + ((size_t)tile * T.cpr + (size_t)u * 4) * BGL_TILE + lane;
     int w[16];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        uint4 c = cp[k * BGL_TILE];
-        w[4 * k] = (int)c.x; w[4 * k + 1] = (int)c.y; w[4 * k + 2] = (int)c.z; w[4 * k + 3] = (int)c.w;
+        w[4 * k] = (int)r.c[k].x; w[4 * k + 1] = (int)r.c[k].y; w[4 * k + 2] = (int)r.c[k].z; w[4 * k + 3] = (int)r.c[k].w;
     }
-    float s = reinterpret_cast<const float *>(T.s0)[((size_t)tile * T.nunits + u) * BGL_TILE + lane];
-    const int K = T.K, ng = K >> 6;
+    const int ng = K >> 6;
 #pragma unroll
     for (int m = 0; m < MB; m++) {
-        int am = C.am[m];
-        if (ACT == BGL_ACT_F32) {
+        const int am = C.am[m];
+        if constexpr (ACT == BGL_ACT_F32) {
             ucint xg = uni(A.xw) + ((size_t)am * ng + u) * BGL_XD_DW;
             int t0 = 0, t1 = 0, t2 = 0;
 #pragma unroll
             for (int q = 0; q < 16; q++) {
                 t0 = dot4(w[q], xg[q], t0); t1 = dot4(w[q], xg[16 + q], t1); t2 = dot4(w[q], xg[32 + q], t2);
             }
-            float V = fold_digits(t0, t1, t2);
-            acc[m] += s * (V * uni(A.xs)[(size_t)am * ng + u]);
+            acc[m] += r.s * (fold_digits(t0, t1, t2) * uni(A.xs)[(size_t)am * ng + u]);
         } else {
             ucint xq = uni(A.xw) + (size_t)am * (K >> 2) + (size_t)u * 16;
             int isum = 0;
 #pragma unroll
             for (int q = 0; q < 16; q++) isum = dot4(w[q], xq[q], isum);
-            float t = __fmul_rn(__fmul_rn((float)isum, s), uni(A.xs)[(size_t)am * ng + u]);
-            acc[m] = __fadd_rn(acc[m], t);
+            acc[m] = __fadd_rn(acc[m], __fmul_rn(__fmul_rn((float)isum, r.s), uni(A.xs)[(size_t)am * ng + u]));
         }
     }
 }
 
-// ---------------------------------------------------------------------------------- QNG64 (fp32 act)
-template <int NB, int MB>
-__device__ __forceinline__ void unit_qng64(const BglDevTensor &T, int tile, int lane, int u, const GemvAct &A,
+template <int MB, int NB>
+__device__ __forceinline__ void comp_qng64(const Raw<BGL_QNG64, NB> &r, int K, int u, const GemvAct &A,
                                            const Cols<MB> &C, float (&acc)[MB]) {
     constexpr int H8 = (NB >> 3) & 1, H4 = (NB >> 2) & 1, H2 = (NB >> 1) & 1, H1 = NB & 1;
     constexpr int K4 = 8 * H8, K2 = K4 + 4 * H4, K1 = K2 + 2 * H2;
     constexpr int SH4 = 8 * H8, SH2 = SH4 + 4 * H4, SH1 = SH2 + 2 * H2;
     constexpr int CORR = 128 * H8 - (1 << (NB - 1));
-    const uint4 *cp = reinterpret_cast<const uint4 *>(T.w) + ((size_t)tile * T.cpr + (size_t)u * NB) * BGL_TILE + lane;
-    uint4 ch[NB];
-#pragma unroll
-    for (int k = 0; k < NB; k++) ch[k] = cp[k * BGL_TILE];
-    float2 s2 = reinterpret_cast<const float2 *>(T.s0)[((size_t)tile * T.nunits + u) * BGL_TILE + lane];
-    const int K = T.K, ng = K >> 6;
+    const int ng = K >> 6;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const int g = 2 * u + h;
         if (g >= ng) break;
-        const float s = h ? s2.y : s2.x;
-        // unpack this half's fields into byte lanes (element order = x dword order)
+        const float s = h ? r.s.y : r.s.x;
         int f8[16], f4[16], f2[16], f1[16];
-        if (H8) {
+        if constexpr (H8) {
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                uint4 c = ch[4 * h + k];
+                uint4 c = r.c[4 * h + k];
                 f8[4 * k] = (int)c.x; f8[4 * k + 1] = (int)c.y; f8[4 * k + 2] = (int)c.z; f8[4 * k + 3] = (int)c.w;
             }
         }
-        if (H4) {
+        if constexpr (H4) {
 #pragma unroll
             for (int k = 0; k < 2; k++) {
-                uint4 c = ch[K4 + 2 * h + k];
+                uint4 c = r.c[K4 + 2 * h + k];
                 uint32_t r4[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
                 for (int j = 0; j < 4; j++) { f4[8 * k + 2 * j] = nib_lo(r4[j]); f4[8 * k + 2 * j + 1] = nib_hi(r4[j]); }
             }
         }
-        if (H2) {
-            uint4 c = ch[K2 + h];
+        if constexpr (H2) {
+            uint4 c = r.c[K2 + h];
             uint32_t r2[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int t = 0; t < 4; t++) f2[4 * j + t] = (int)((r2[j] >> (2 * t)) & 0x03030303u);
         }
-        if (H1) {
-            uint4 c = ch[K1];
+        if constexpr (H1) {
+            uint4 c = r.c[K1];
             uint32_t r1[2] = {h ? c.z : c.x, h ? c.w : c.y};
 #pragma unroll
             for (int j = 0; j < 2; j++)
@@ -254,32 +256,32 @@ __device__ __forceinline__ void unit_qng64(const BglDevTensor &T, int tile, int 
         }
 #pragma unroll
         for (int m = 0; m < MB; m++) {
-            int am = C.am[m];
+            const int am = C.am[m];
             ucint xg = uni(A.xw) + ((size_t)am * ng + g) * BGL_XD_DW;
             int td[3];
 #pragma unroll
             for (int d = 0; d < 3; d++) {
                 ucint xd = xg + 16 * d;
                 int tot = 0;
-                if (H8) {
+                if constexpr (H8) {
                     int a = 0;
 #pragma unroll
                     for (int q = 0; q < 16; q++) a = dot4(f8[q], xd[q], a);
                     tot += a;
                 }
-                if (H4) {
+                if constexpr (H4) {
                     int a = 0;
 #pragma unroll
                     for (int q = 0; q < 16; q++) a = dot4(f4[q], xd[q], a);
                     tot += a * (1 << SH4);
                 }
-                if (H2) {
+                if constexpr (H2) {
                     int a = 0;
 #pragma unroll
                     for (int q = 0; q < 16; q++) a = dot4(f2[q], xd[q], a);
                     tot += a * (1 << SH2);
                 }
-                if (H1) {
+                if constexpr (H1) {
                     int a = 0;
 #pragma unroll
                     for (int q = 0; q < 16; q++) a = dot4(f1[q], xd[q], a);
@@ -289,90 +291,245 @@ __device__ __forceinline__ void unit_qng64(const BglDevTensor &T, int tile, int 
             }
             int4 d0 = ld_dsum(A, am, K, 2 * g), d1 = ld_dsum(A, am, K, 2 * g + 1);
             td[0] += CORR * (d0.x + d1.x); td[1] += CORR * (d0.y + d1.y); td[2] += CORR * (d0.z + d1.z);
-            float V = fold_digits(td[0], td[1], td[2]);
-            acc[m] += s * (V * uni(A.xs)[(size_t)am * ng + g]);
+            acc[m] += s * (fold_digits(td[0], td[1], td[2]) * uni(A.xs)[(size_t)am * ng + g]);
         }
     }
 }
 
-// ---------------------------------------------------------------------------------- kernel
 template <int FMT, int ACT, int NB, int MB>
-__device__ __forceinline__ void unit_dispatch(const BglDevTensor &T, int tile, int lane, int u, const GemvAct &A,
+__device__ __forceinline__ void comp_dispatch(const Raw<FMT, NB> &r, int K, int u, const GemvAct &A,
                                               const Cols<MB> &C, float (&acc)[MB]) {
-    if constexpr (FMT == BGL_Q4G64) unit_q4g64<ACT, MB>(T, tile, lane, u, A, C, acc);
-    else if constexpr (FMT == BGL_Q4G32H) unit_q4g32h<MB>(T, tile, lane, u, A, C, acc);
-    else if constexpr (FMT == BGL_Q4G256SF) unit_g256sf<MB>(T, tile, lane, u, A, C, acc);
-    else if constexpr (FMT == BGL_Q8G64) unit_q8g64<ACT, MB>(T, tile, lane, u, A, C, acc);
-    else unit_qng64<NB, MB>(T, tile, lane, u, A, C, acc);
+    if constexpr (FMT == BGL_Q4G64) comp_q4g64<ACT, MB, NB>(r, K, u, A, C, acc);
+    else if constexpr (FMT == BGL_Q4G32H) comp_q4g32h<MB, NB>(r, K, u, A, C, acc);
+    else if constexpr (FMT == BGL_Q4G256SF) comp_g256sf<MB, NB>(r, K, u, A, C, acc);
+    else if constexpr (FMT == BGL_Q8G64) comp_q8g64<ACT, MB, NB>(r, K, u, A, C, acc);
+    else comp_qng64<MB, NB>(r, K, u, A, C, acc);
 }
 
-template <int FMT, int ACT, int NB, int MB>
-__global__ __launch_bounds__(BGL_WAVES * BGL_TILE) void k_gemv(GemvLaunch L) {
-    __shared__ float red[BGL_WAVES][MB][BGL_TILE];
-    const int b = blockIdx.x;
+__device__ __forceinline__ int pick_task(const GemvLaunch &L, int b) {
     int ti = 0;
 #pragma unroll
     for (int i = 1; i < BGL_MAX_TASKS; i++) if (i < L.ntasks && b >= L.t[i].blk0) ti = i;
+    return ti;
+}
+
+// ================================================================================== path A kernel
+template <int FMT, int ACT, int NB, int MB>
+__global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv(GemvLaunch L) {
+    __shared__ float red[MAXW][MB][BGL_TILE];
+    const int b = blockIdx.x, ti = pick_task(L, b);
     GemvTask task = L.t[0];
 #pragma unroll
     for (int i = 1; i < BGL_MAX_TASKS; i++) if (i == ti) task = L.t[i];
     const BglDevTensor &T = task.T;
-    const int lb = b - task.blk0, tile = lb / task.ks, s = lb % task.ks;
-    const int ubeg = s * task.gpb;
-    const int uend = min(ubeg + task.gpb, T.nunits);
+    const int tile = b - task.blk0;
+    const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const Cols<MB> C = col_rows<MB>(L.a, L.m0, L.mcols);
+    const int K = T.K, U = T.nunits;
 
     float acc[MB];
 #pragma unroll
     for (int m = 0; m < MB; m++) acc[m] = 0.0f;
-    for (int u = ubeg + wave; u < uend; u += BGL_WAVES) unit_dispatch<FMT, ACT, NB, MB>(T, tile, lane, u, L.a, C, acc);
+    constexpr bool PREFETCH = chunks_per_unit<FMT>(NB) <= 8;
+    int u = wave;
+    Raw<FMT, NB> r0, r1;
+    if (u < U) load_raw<FMT, NB>(r0, T, tile, lane, u);
+    while (u < U) {
+        const int un = u + nw;
+        if constexpr (PREFETCH) {
+            if (un < U) load_raw<FMT, NB>(r1, T, tile, lane, un);
+            comp_dispatch<FMT, ACT, NB, MB>(r0, K, u, L.a, C, acc);
+            r0 = r1;
+        } else {
+            comp_dispatch<FMT, ACT, NB, MB>(r0, K, u, L.a, C, acc);
+            if (un < U) load_raw<FMT, NB>(r0, T, tile, lane, un);
+        }
+        u = un;
+    }
 
 #pragma unroll
     for (int m = 0; m < MB; m++) red[wave][m][lane] = acc[m];
     __syncthreads();
     if (wave != 0) return;
-    float p[MB];
+    const int row = tile * BGL_TILE + lane;
+    if (row >= T.N) return;
+    const float bb = task.bias ? task.bias[row] : 0.0f;
 #pragma unroll
     for (int m = 0; m < MB; m++) {
         float v = red[0][m][lane];
-#pragma unroll
-        for (int w = 1; w < BGL_WAVES; w++) v += red[w][m][lane];
-        p[m] = v;
-    }
-    const int row = tile * BGL_TILE + lane;
-    if (task.ks > 1) {
-        float *tb = L.tbuf + task.tb_off + ((size_t)tile * task.ks + s) * MB * BGL_TILE;
-#pragma unroll
-        for (int m = 0; m < MB; m++) tb[m * BGL_TILE + lane] = p[m];
-        __threadfence();
-        unsigned old = 0;
-        if (lane == 0) old = atomicAdd(&L.ctr[task.ctr_off + tile], 1u);
-        old = __shfl(old, 0, 64);
-        if (old != (unsigned)(task.ks - 1)) return;
-        __threadfence();
-        const float *tb0 = L.tbuf + task.tb_off + (size_t)tile * task.ks * MB * BGL_TILE;
-#pragma unroll
-        for (int m = 0; m < MB; m++) {
-            float v = __hip_atomic_load(tb0 + m * BGL_TILE + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            for (int s2 = 1; s2 < task.ks; s2++)
-                v += __hip_atomic_load(tb0 + ((size_t)s2 * MB + m) * BGL_TILE + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            p[m] = v;
-        }
-        if (lane == 0) __hip_atomic_store(&L.ctr[task.ctr_off + tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (row < T.N) {
-        const float bb = task.bias ? task.bias[row] : 0.0f;
-#pragma unroll
-        for (int m = 0; m < MB; m++)
-            if (m < L.mcols) task.y[(size_t)(L.m0 + m) * task.ystride + row] = bb + p[m];
+        for (int w = 1; w < nw; w++) v += red[w][m][lane];
+        if (m < L.mcols) task.y[(size_t)(L.m0 + m) * task.ystride + row] = bb + v;
     }
 }
 
-// ---------------------------------------------------------------------------------- launcher
+// ================================================================================== path B kernel (W4A8, fused quantization)
+// A workgroup owns TR rows (a 1/(64/TR) slice of a 64-row tile) and the whole K range.  Lane l of a
+// wave handles row l % TR and unit kq = l / TR of each group of KQ = 64/TR consecutive units, so a
+// wave-wide load is KQ runs of TR*16 >= 128 bytes.  Activation bytes come from LDS (each lane reads
+// its own unit's slice; units are padded by 16 bytes so neighbouring units fall in different banks).
+// Dynamic LDS: [xq: U x (unit bytes + 16)][ascale: K/gq][xqsum: K/64][t: U x TR floats].
+
+template <int FMT> struct QUnit {
+    static constexpr int GQ = FMT == BGL_Q4G256SF ? 256 : 64;        // activation quantization group
+    static constexpr int ELEMS = FMT == BGL_Q4G256SF ? 256 : 64;     // elements per work unit
+    static constexpr int STRIDE = ELEMS + 16;                       // padded LDS bytes per unit
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_raw_row(Raw<FMT, 0> &r, const BglDevTensor &T, int tile, int rr, int u) {
+    constexpr int CPU = chunks_per_unit<FMT>(0);
+    const uint4 *cp = reinterpret_cast<const uint4 *>(T.w) + ((size_t)tile * T.cpr + (size_t)u * CPU) * BGL_TILE + rr;
+#pragma unroll
+    for (int k = 0; k < CPU; k++) r.c[k] = cp[k * BGL_TILE];
+    const size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + rr;
+    r.s = reinterpret_cast<const float *>(T.s0)[so];
+    if constexpr (FMT == BGL_Q4G256SF) r.sub = T.s1[so];
+}
+
+template <int FMT>
+__device__ __forceinline__ float unit_term(const Raw<FMT, 0> &r, const int8_t *xq, const float *asc, const int *xsum, int u) {
+    const int4 *x4 = reinterpret_cast<const int4 *>(xq + (size_t)u * QUnit<FMT>::STRIDE);
+    if constexpr (FMT == BGL_Q4G256SF) {
+        int comb = 0;
+#pragma unroll
+        for (int sg = 0; sg < 4; sg++) {
+            int isum = 0;
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const uint4 c = r.c[2 * sg + k];
+                const int4 xa = x4[sg * 4 + 2 * k], xb = x4[sg * 4 + 2 * k + 1];
+                isum = dot4(nib_lo(c.x), xa.x, isum); isum = dot4(nib_hi(c.x), xa.y, isum);
+                isum = dot4(nib_lo(c.y), xa.z, isum); isum = dot4(nib_hi(c.y), xa.w, isum);
+                isum = dot4(nib_lo(c.z), xb.x, isum); isum = dot4(nib_hi(c.z), xb.y, isum);
+                isum = dot4(nib_lo(c.w), xb.z, isum); isum = dot4(nib_hi(c.w), xb.w, isum);
+            }
+            isum -= 8 * xsum[u * 4 + sg];
+            comb += isum * (int)((r.sub >> (8 * sg)) & 255u);
+        }
+        return __fmul_rn(__fmul_rn(__fmul_rn((float)comb, r.s), C63), asc[u]);
+    } else if constexpr (FMT == BGL_Q4G64) {
+        int isum = 0;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint4 c = r.c[k];
+            const int4 xa = x4[2 * k], xb = x4[2 * k + 1];
+            isum = dot4(nib_lo(c.x), xa.x, isum); isum = dot4(nib_hi(c.x), xa.y, isum);
+            isum = dot4(nib_lo(c.y), xa.z, isum); isum = dot4(nib_hi(c.y), xa.w, isum);
+            isum = dot4(nib_lo(c.z), xb.x, isum); isum = dot4(nib_hi(c.z), xb.y, isum);
+            isum = dot4(nib_lo(c.w), xb.z, isum); isum = dot4(nib_hi(c.w), xb.w, isum);
+        }
+        isum -= 8 * xsum[u];
+        return __fmul_rn(__fmul_rn((float)isum, r.s), asc[u]);
+    } else {
+        int isum = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint4 c = r.c[k];
+            const int4 xa = x4[k];
+            isum = dot4((int)c.x, xa.x, isum); isum = dot4((int)c.y, xa.y, isum);
+            isum = dot4((int)c.z, xa.z, isum); isum = dot4((int)c.w, xa.w, isum);
+        }
+        return __fmul_rn(__fmul_rn((float)isum, r.s), asc[u]);
+    }
+}
+
+template <int FMT, int TR>
+__global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int KQ = BGL_TILE / TR, SUBS = BGL_TILE / TR;
+    using QU = QUnit<FMT>;
+    const int b = blockIdx.x, ti = pick_task(L, b);
+    GemvTask task = L.t[0];
+#pragma unroll
+    for (int i = 1; i < BGL_MAX_TASKS; i++) if (i == ti) task = L.t[i];
+    const BglDevTensor &T = task.T;
+    const int lb = b - task.blk0, tile = lb / SUBS, r0 = (lb % SUBS) * TR;
+    const int nw = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int K = T.K, U = T.nunits;
+    int8_t *xq = reinterpret_cast<int8_t *>(lds);
+    float *asc = reinterpret_cast<float *>(lds + (size_t)U * QU::STRIDE);
+    int *xsum = reinterpret_cast<int *>(asc + K / QU::GQ);
+    float *tl = reinterpret_cast<float *>(xsum + K / 64);
+
+    // ---- first weight loads go out before the activation work (they do not depend on it)
+    const int r = lane % TR, kq = lane / TR, rr = r0 + r;
+    int ub = wave * KQ;
+    Raw<FMT, 0> c0, c1;
+    if (ub + kq < U) load_raw_row<FMT>(c0, T, tile, rr, ub + kq);
+
+    // ---- quantize x (q4gemv.h:177-213 / q4gemv_g256.h:72-99), one wave per group; each wave
+    // first loads every group it owns (up to 4 per pass) so the loads overlap
+    const float *x = L.x + (size_t)L.m0 * K;
+    constexpr int PER = QU::GQ / 64;
+    const int NGQ = K / QU::GQ;
+    for (int g0 = wave; g0 < NGQ; g0 += 4 * nw) {
+        float v[4][PER];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int g = g0 + i * nw;
+#pragma unroll
+            for (int j = 0; j < PER; j++) v[i][j] = g < NGQ ? x[g * QU::GQ + 64 * j + lane] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int g = g0 + i * nw;
+            if (g >= NGQ) break;
+            float mx = 1e-8f;
+#pragma unroll
+            for (int j = 0; j < PER; j++) mx = fmaxf(mx, fabsf(v[i][j]));
+            mx = wave_max_f32(mx);
+            const float sc = __fdiv_rn(mx, 127.0f), inv = __fdiv_rn(1.0f, sc);
+            if (lane == 0) asc[g] = sc;
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const float p = __fmul_rn(v[i][j], inv);
+                const float t = __fadd_rn(p, p >= 0.0f ? 0.5f : -0.5f);
+                int q = (int)t;                                // |t| <= 128: no int32 overflow
+                q = q > 127 ? 127 : (q < -128 ? -128 : q);
+                const int e = g * QU::GQ + 64 * j + lane;      // element index
+                xq[(e / QU::ELEMS) * QU::STRIDE + e % QU::ELEMS] = (int8_t)q;
+                const int s = wave_sum_i32(q);
+                if (lane == 0) xsum[g * PER + j] = s;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- per-unit fold terms t[u][row], exactly the reference's per-group expression
+    while (ub < U) {
+        const int un = ub + nw * KQ;
+        if (un + kq < U) load_raw_row<FMT>(c1, T, tile, rr, un + kq);
+        const int u = ub + kq;
+        if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
+        c0 = c1;
+        ub = un;
+    }
+    __syncthreads();
+    if (threadIdx.x >= TR) return;
+    const int row = tile * BGL_TILE + r0 + threadIdx.x;
+    if (row >= T.N) return;
+    // sequential fold in group order; the LDS reads are batched 8 at a time
+    float acc = 0.0f;
+    const float *tr = tl + threadIdx.x;
+    int g = 0;
+    for (; g + 8 <= U; g += 8) {
+        float t8[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) t8[i] = tr[(g + i) * TR];
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc = __fadd_rn(acc, t8[i]);
+    }
+    for (; g < U; g++) acc = __fadd_rn(acc, tr[g * TR]);
+    const float bb = task.bias ? task.bias[row] : 0.0f;
+    task.y[(size_t)L.m0 * task.ystride + row] = __fadd_rn(bb, acc);
+}
+
+// ================================================================================== launchers
 template <int FMT, int ACT, int NB>
-static int launch_mb(int MB, const GemvLaunch &L, int nblocks, hipStream_t st) {
-    dim3 g(nblocks), b(BGL_WAVES * BGL_TILE);
+static int launch_mb(int MB, const GemvLaunch &L, int nblocks, int nw, hipStream_t st) {
+    dim3 g(nblocks), b(nw * BGL_TILE);
     switch (MB) {
     case 1: hipLaunchKernelGGL((k_gemv<FMT, ACT, NB, 1>), g, b, 0, st, L); break;
     case 4: hipLaunchKernelGGL((k_gemv<FMT, ACT, NB, 4>), g, b, 0, st, L); break;
@@ -383,38 +540,70 @@ static int launch_mb(int MB, const GemvLaunch &L, int nblocks, hipStream_t st) {
 }
 
 template <int NB>
-static int launch_qng(int MB, const GemvLaunch &L, int nblocks, hipStream_t st) {
-    return launch_mb<BGL_QNG64, BGL_ACT_F32, NB>(MB, L, nblocks, st);
+static int launch_qng(int MB, const GemvLaunch &L, int nblocks, int nw, hipStream_t st) {
+    return launch_mb<BGL_QNG64, BGL_ACT_F32, NB>(MB, L, nblocks, nw, st);
 }
 
-int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, hipStream_t st) {
+int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, int nw, hipStream_t st) {
     const int fmt = L.t[0].T.fmt;
     if (fmt == BGL_Q4G64)
-        return act == BGL_ACT_F32 ? launch_mb<BGL_Q4G64, BGL_ACT_F32, 0>(MB, L, nblocks, st)
-                                  : launch_mb<BGL_Q4G64, BGL_ACT_W4A8, 0>(MB, L, nblocks, st);
+        return act == BGL_ACT_F32 ? launch_mb<BGL_Q4G64, BGL_ACT_F32, 0>(MB, L, nblocks, nw, st)
+                                  : launch_mb<BGL_Q4G64, BGL_ACT_W4A8, 0>(MB, L, nblocks, nw, st);
     if (fmt == BGL_Q8G64)
-        return act == BGL_ACT_F32 ? launch_mb<BGL_Q8G64, BGL_ACT_F32, 0>(MB, L, nblocks, st)
-                                  : launch_mb<BGL_Q8G64, BGL_ACT_W4A8, 0>(MB, L, nblocks, st);
-    if (fmt == BGL_Q4G32H) return act == BGL_ACT_F32 ? launch_mb<BGL_Q4G32H, BGL_ACT_F32, 0>(MB, L, nblocks, st) : -2;
-    if (fmt == BGL_Q4G256SF) return act == BGL_ACT_W4A8 ? launch_mb<BGL_Q4G256SF, BGL_ACT_W4A8, 0>(MB, L, nblocks, st) : -2;
+        return act == BGL_ACT_F32 ? launch_mb<BGL_Q8G64, BGL_ACT_F32, 0>(MB, L, nblocks, nw, st)
+                                  : launch_mb<BGL_Q8G64, BGL_ACT_W4A8, 0>(MB, L, nblocks, nw, st);
+    if (fmt == BGL_Q4G32H) return act == BGL_ACT_F32 ? launch_mb<BGL_Q4G32H, BGL_ACT_F32, 0>(MB, L, nblocks, nw, st) : -2;
+    if (fmt == BGL_Q4G256SF) return act == BGL_ACT_W4A8 ? launch_mb<BGL_Q4G256SF, BGL_ACT_W4A8, 0>(MB, L, nblocks, nw, st) : -2;
     if (fmt == BGL_QNG64 && act == BGL_ACT_F32) {
         switch (L.t[0].T.bits) {
-        case 2: return launch_qng<2>(MB, L, nblocks, st);
-        case 3: return launch_qng<3>(MB, L, nblocks, st);
-        case 4: return launch_qng<4>(MB, L, nblocks, st);
-        case 5: return launch_qng<5>(MB, L, nblocks, st);
-        case 6: return launch_qng<6>(MB, L, nblocks, st);
-        case 7: return launch_qng<7>(MB, L, nblocks, st);
-        case 8: return launch_qng<8>(MB, L, nblocks, st);
-        case 9: return launch_qng<9>(MB, L, nblocks, st);
-        case 10: return launch_qng<10>(MB, L, nblocks, st);
-        case 11: return launch_qng<11>(MB, L, nblocks, st);
-        case 12: return launch_qng<12>(MB, L, nblocks, st);
-        case 13: return launch_qng<13>(MB, L, nblocks, st);
-        case 14: return launch_qng<14>(MB, L, nblocks, st);
-        case 15: return launch_qng<15>(MB, L, nblocks, st);
+        case 2: return launch_qng<2>(MB, L, nblocks, nw, st);
+        case 3: return launch_qng<3>(MB, L, nblocks, nw, st);
+        case 4: return launch_qng<4>(MB, L, nblocks, nw, st);
+        case 5: return launch_qng<5>(MB, L, nblocks, nw, st);
+        case 6: return launch_qng<6>(MB, L, nblocks, nw, st);
+        case 7: return launch_qng<7>(MB, L, nblocks, nw, st);
+        case 8: return launch_qng<8>(MB, L, nblocks, nw, st);
+        case 9: return launch_qng<9>(MB, L, nblocks, nw, st);
+        case 10: return launch_qng<10>(MB, L, nblocks, nw, st);
+        case 11: return launch_qng<11>(MB, L, nblocks, nw, st);
+        case 12: return launch_qng<12>(MB, L, nblocks, nw, st);
+        case 13: return launch_qng<13>(MB, L, nblocks, nw, st);
+        case 14: return launch_qng<14>(MB, L, nblocks, nw, st);
+        case 15: return launch_qng<15>(MB, L, nblocks, nw, st);
         default: return -2;
         }
     }
     return -2;
+}
+
+size_t bgl_gemv_q_lds(int fmt, int K, int TR) {
+    const int GQ = fmt == BGL_Q4G256SF ? 256 : 64;
+    const int ELEMS = fmt == BGL_Q4G256SF ? 256 : 64;
+    const int U = K / ELEMS;
+    return (size_t)U * (ELEMS + 16) + 4 * (K / GQ) + 4 * (K / 64) + 4 * (size_t)U * TR;
+}
+
+template <int FMT>
+static int launch_q_tr(int TR, const GemvLaunch &L, int nblocks, int nw, size_t lds, hipStream_t st) {
+    dim3 g(nblocks), b(nw * BGL_TILE);
+    switch (TR) {
+    case 64: hipLaunchKernelGGL((k_gemv_q<FMT, 64>), g, b, lds, st, L); return 0;
+    case 32: hipLaunchKernelGGL((k_gemv_q<FMT, 32>), g, b, lds, st, L); return 0;
+    case 16: hipLaunchKernelGGL((k_gemv_q<FMT, 16>), g, b, lds, st, L); return 0;
+    case 8: hipLaunchKernelGGL((k_gemv_q<FMT, 8>), g, b, lds, st, L); return 0;
+    default: return -1;
+    }
+}
+
+// nblocks counts 64-row tiles; each is split into 64/TR workgroups.
+int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, hipStream_t st) {
+    const int fmt = L.t[0].T.fmt;
+    const size_t lds = bgl_gemv_q_lds(fmt, L.t[0].T.K, TR);
+    const int nblocks = ntiles * (BGL_TILE / TR);
+    switch (fmt) {
+    case BGL_Q4G256SF: return launch_q_tr<BGL_Q4G256SF>(TR, L, nblocks, nw, lds, st);
+    case BGL_Q4G64: return launch_q_tr<BGL_Q4G64>(TR, L, nblocks, nw, lds, st);
+    case BGL_Q8G64: return launch_q_tr<BGL_Q8G64>(TR, L, nblocks, nw, lds, st);
+    default: return -2;
+    }
 }

@@ -25,19 +25,27 @@ struct bgl_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     bool own_stream = false;
-    int target_blocks = 1024;
+    int max_waves = 16;                   // wavefronts per GEMV workgroup cap (BGL_MAX_WAVES)
+    bool no_fused = false;                // BGL_NO_FUSED_Q=1: W4A8 M=1 through the separate prep kernel
+    int min_blocks = 256;                 // fused W4A8: split tiles until at least this many workgroups
+    int force_tr = 0;                     // BGL_FORCE_TR: fixed rows per workgroup (tuning)
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
-    DevBuf tbuf, ctr;                     // split-K partials and arrival counters (counters zeroed)
     DevBuf hx, hy, hb;                    // staging for the host-pointer entry points
     DevBuf moe_a, moe_b, moe_c, moe_d, moe_meta;
+    bool prof = false;                    // bracket launches with events (bgl_prof_enable)
+    std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> prof_ev;
+    std::vector<hipEvent_t> ev_pool;
     std::mutex mu;
     std::unordered_map<const void *, bgl_tensor *> host_cache;
 };
 
 int bgl_fail(int code, const char *fmt, ...);
+// Profiling brackets: prof_begin returns a token (or -1 when profiling is off).
+int prof_begin(bgl_ctx *c, int phase);
+void prof_end(bgl_ctx *c, int token);
 int dbuf_reserve(bgl_ctx *c, DevBuf &b, size_t bytes, bool zero);
 int check_wt(int kind, int bits, int out, int in);
 int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, GemvAct &A);
-void plan_task(bgl_ctx *c, const BglDevTensor &T, int total_tiles, int &ks, int &gpb);
+int pick_waves(bgl_ctx *c, int nunits);
 int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &A, int M,
              const float *const *bias, float *const *y, const int *ystride);

@@ -17,15 +17,14 @@ struct BglDevTensor {
 
 #define BGL_MAX_TASKS 4
 
-// One GEMV "task" = one tensor of a (possibly fused) launch.  Blocks [blk0, blk0 + ntiles*ks) of
-// the grid belong to it; block b covers tile (b-blk0)/ks and unit range [s*gpb, (s+1)*gpb).
+// One GEMV "task" = one tensor of a (possibly fused) launch.  Blocks [blk0, blk0 + ntiles) of the
+// grid belong to it; block b computes tile b-blk0 over the whole K range.
 struct GemvTask {
     BglDevTensor T;
     float *y;                 // [M][N] (row stride ystride)
     const float *bias;        // [N] or null
     int ystride;
-    int ks, gpb, blk0;
-    int tb_off, ctr_off;      // partial-sum buffer / counter offsets (in floats / counters)
+    int blk0;
 };
 
 // Activation operands (shared by every task of a launch; all tasks have the same K).
@@ -40,10 +39,9 @@ struct GemvAct {
 struct GemvLaunch {
     GemvTask t[BGL_MAX_TASKS];
     int ntasks;
-    GemvAct a;
+    GemvAct a;                // prepared activation operands (k_gemv)
+    const float *x;           // raw fp32 activations [M][K] (k_gemv_q quantizes them itself)
     int m0, mcols;            // columns [m0, m0+mcols) of the activation (mcols <= MB)
-    float *tbuf;
-    unsigned *ctr;
 };
 
 // ---- kernels (bgl_prep.hip) ----
@@ -63,4 +61,6 @@ __global__ void k_repack_qng_scales(const float *src, int N, int ng, float2 *dst
 __global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *out);
 
 // ---- host-side launchers (bgl_gemv.hip) ----
-int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, hipStream_t st);
+int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, int nw, hipStream_t st);
+int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, hipStream_t st);
+size_t bgl_gemv_q_lds(int fmt, int K, int TR);

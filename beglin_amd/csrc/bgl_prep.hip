@@ -1,27 +1,12 @@
 // bgl_prep.hip -- activation preparation, device packers, and repack into the tiled layout.
 //
-// Every fp32 operation that must reproduce the reference bit for bit is written with the
-// explicit-rounding intrinsics (__fmul_rn / __fdiv_rn / __fadd_rn / __fsub_rn), so no multiply-add
-// is ever contracted and each step rounds exactly as the reference's C expression does.
+// Every fp32 operation that must reproduce the reference bit for bit is a separate IEEE operation:
+// the library is compiled with -ffp-contract=off (no multiply-add is fused), divisions are
+// correctly rounded, and rintf is round-half-even -- each step rounds exactly as the reference's C
+// expression does.
 #include "bgl_device.h"
 #include "bgl_kernels.h"
 
-// ------------------------------------------------------------------ wave reductions
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ int half_sum_i(int v) {      // sum over each 32-lane half
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 // ------------------------------------------------------------------ W4A8 activation quantizer
 // q4gemv.h:177-213 / q4gemv_g256.h:72-99: mx = max(1e-8, max|x|); sc = mx/127; inv = 1/sc;
@@ -39,7 +24,7 @@ __global__ __launch_bounds__(256) void k_act_w4a8(const float *__restrict__ x, i
     float v[4];
     float mx = 1e-8f;
     for (int j = 0; j < per; j++) { v[j] = xp[lane + 64 * j]; mx = fmaxf(mx, fabsf(v[j])); }
-    mx = wave_max(mx);
+    mx = wave_max_f32(mx);
     float sc = __fdiv_rn(mx, 127.0f), inv = __fdiv_rn(1.0f, sc);
     if (lane == 0) ascale[(size_t)m * ng + g] = sc;
     for (int j = 0; j < per; j++) {
@@ -51,7 +36,7 @@ __global__ __launch_bounds__(256) void k_act_w4a8(const float *__restrict__ x, i
         else q = (int)t;                                   // truncation toward zero
         q = q > 127 ? 127 : (q < -128 ? -128 : q);
         xq[(size_t)m * K + (size_t)g * gsize + lane + 64 * j] = (int8_t)q;
-        int s = wave_sum_i(q);
+        int s = wave_sum_i32(q);
         if (lane == 0) xqsum64[(size_t)m * (K >> 6) + (size_t)g * per + j] = s;
     }
 }
@@ -68,7 +53,7 @@ __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, in
     if (wid >= M * ng) return;
     int m = wid / ng, g = wid % ng;
     float v = x[(size_t)m * K + (size_t)g * 64 + lane];
-    float mx = wave_max(fabsf(v));
+    float mx = wave_max_f32(fabsf(v));
     int e = 0;
     if (mx > 0.0f) frexpf(mx, &e);
     int X = (mx > 0.0f) ? (int)rintf(ldexpf(v, 21 - e)) : 0;
@@ -79,10 +64,11 @@ __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, in
     int8_t *dst = xd + ((size_t)m * ng + g) * 192;
     dst[lane] = (int8_t)d0; dst[64 + lane] = (int8_t)d1; dst[128 + lane] = (int8_t)d2;
     if (lane == 0) xs[(size_t)m * ng + g] = (mx > 0.0f) ? ldexpf(1.0f, e - 21) : 0.0f;
-    int s0 = half_sum_i(d0), s1 = half_sum_i(d1), s2 = half_sum_i(d2);
+    int2 s0 = half_sums_i32(d0), s1 = half_sums_i32(d1), s2 = half_sums_i32(d2);
     if ((lane & 31) == 0) {
-        int *ds = dsum + ((size_t)m * (K >> 5) + (size_t)g * 2 + (lane >> 5)) * 4;
-        ds[0] = s0; ds[1] = s1; ds[2] = s2; ds[3] = 0;
+        const int h = lane >> 5;
+        int *ds = dsum + ((size_t)m * (K >> 5) + (size_t)g * 2 + h) * 4;
+        ds[0] = h ? s0.y : s0.x; ds[1] = h ? s1.y : s1.x; ds[2] = h ? s2.y : s2.x; ds[3] = 0;
     }
 }
 

@@ -1,0 +1,332 @@
+"""bench.py -- quantized GEMV / MoE-gather throughput on one MI355X.
+
+Default workload: a Qwen2.5-1.5B decode layer, all seven projections as
+q4g256sf W4A8 GEMVs (q 1536x1536, k/v 256x1536, o 1536x1536, gate/up 8960x1536, down 1536x8960),
+28 layers of distinct weights (696 MB, > 2x the 256 MB MALL), M=1.  One "step" = one pass over the
+28 layers, issued the way the engine issues it: fused q/k/v, o, fused gate+up, down
+(QWEN_FUSED_DISPATCH, qwen_infer.c:1276-1306); each call = activation quantization + GEMV.  The
+step is captured once into a HIP graph and replayed.  Weights are seeded N(0, 0.02), quantized on
+the device by the build's g256sf packer; activations seeded N(0, 1).
+
+Prints ONE JSON line.  `value` = algorithmic bytes per step / step time (GB/s), with
+algorithmic bytes = packed + scale + sub-code bytes + 4*M*K (x) + 4*M*N (y) per call.
+`roofline.achieved` = the same bytes over the summed duration of the GEMV kernel launches alone,
+measured with HIP events on the context's stream.  `cpu_baseline` = the reference's threaded CPU
+path (portable-C restatement, q4pool row-block split) timed on this host on a bounded sample.
+
+Other workloads for the per-config numbers: --workload cfg1 | cfg3 (see --help)."""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "quantized GEMV / MoE-gather achieved HBM GB/s (% of peak) + µs per call at M=1"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def qwen_layer_shapes():
+    """(name, [(out, in), ...]) per call, in issue order."""
+    return [("qkv", [(1536, 1536), (256, 1536), (256, 1536)]), ("o", [(1536, 1536)]),
+            ("gate_up", [(8960, 1536), (8960, 1536)]), ("down", [(1536, 8960)])]
+
+
+def alg_bytes(kind, out, inn, bits, M):
+    w = {1: out * inn / 2 + 4 * out * inn / 64, 2: out * inn + 4 * out * inn / 64,
+         3: out * inn / 2 + 4 * out * inn / 256 + out * inn / 64, 4: out * inn * bits / 8 + 4 * out * inn / 64,
+         5: out * inn / 2 + 2 * out * inn / 32}[kind]
+    return w + 4 * M * inn + 4 * M * out
+
+
+def host_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except Exception:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+# ------------------------------------------------------------------------------------- GPU side
+class Workload:
+    """A list of calls; each call = (tensors, x, ys, act, bytes)."""
+
+    def __init__(self, ctx, torch):
+        self.ctx, self.torch = ctx, torch
+        self.calls = []
+        self.tensors = []
+
+    def add(self, group, x, act, nbytes, tag):
+        ys = [self.torch.empty((x.shape[0], t.info()["out"]), device="cuda") for t in group]
+        self.calls.append((group, x, ys, act, nbytes, tag))
+        self.tensors += group
+
+    def run(self, tags=None):
+        for group, x, ys, act, _, tag in self.calls:
+            if tags is None or tag in tags:
+                if len(group) == 1:
+                    self.ctx.matmul(group[0], x, ys[0], act=act)
+                else:
+                    self.ctx.matmul_group(group, x, ys, act=act)
+
+    def nbytes(self, tags=None):
+        return sum(c[4] for c in self.calls if tags is None or c[5] in tags)
+
+    def ncalls(self, tags=None):
+        return sum(1 for c in self.calls if tags is None or c[5] in tags)
+
+    def free(self):
+        for t in self.tensors:
+            t.free()
+
+
+def gen_weight(torch, gen, out, inn):
+    return torch.randn((out, inn), generator=gen, device="cuda", dtype=torch.float32).mul_(0.02)
+
+
+def build_cfg2(ctx, torch, M, layers, seed):
+    import beglin_amd
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    wl = Workload(ctx, torch)
+    xs = {k: torch.randn((M, k), generator=gen, device="cuda") for k in (1536, 8960)}
+    for _ in range(layers):
+        for tag, shapes in qwen_layer_shapes():
+            group = []
+            nb = 0
+            for out, inn in shapes:
+                w = gen_weight(torch, gen, out, inn)
+                group.append(ctx.quantize(beglin_amd.K_Q4G256SF, w))
+                del w
+                nb += alg_bytes(3, out, inn, 4, M) - 4 * M * inn
+            nb += 4 * M * shapes[0][1]
+            wl.add(group, xs[shapes[0][1]], beglin_amd.ACT_W4A8, nb, tag)
+    return wl
+
+
+def build_rotated(ctx, torch, kind, bits, out, inn, M, seed, act):
+    """Enough distinct copies of one tensor that the rotation exceeds 2x the MALL."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    per = alg_bytes(kind, out, inn, bits, M)
+    copies = max(4, int(2 * MALL_BYTES / per) + 1)
+    wl = Workload(ctx, torch)
+    x = torch.randn((M, inn), generator=gen, device="cuda")
+    for _ in range(copies):
+        w = gen_weight(torch, gen, out, inn)
+        wl.add([ctx.quantize(kind, w, bits=bits, qng64_encoder=(bits != 4))], x, act, per, "gemv")
+        del w
+    return wl
+
+
+def time_graph(torch, stream, fn, steps, warmup):
+    with torch.cuda.stream(stream):
+        fn()                                   # eager once: reserves every scratch buffer
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / steps, wall, g
+
+
+def kernel_roofline(ctx, torch, stream, wl, reps):
+    """Sum of GEMV-kernel durations (HIP events around each launch on the context's stream)."""
+    with torch.cuda.stream(stream):
+        wl.run()
+        torch.cuda.synchronize()
+        ctx.prof_read()
+        ctx.prof_enable(True)
+        for _ in range(reps):
+            wl.run()
+        pr = ctx.prof_read()
+        ctx.prof_enable(False)
+    ms, n = pr["gemv"]
+    ms_prep, n_prep = pr["prep"]
+    return ms / reps, n // reps, ms_prep / reps, n_prep // reps
+
+
+# ------------------------------------------------------------------------------------- CPU baseline
+def cpu_baseline_cfg2(M, budget_s, layers=2, seed=7):
+    """The reference's threaded CPU path (gemv_q4g256sf_sdot_mt, q4gemv_g256.h:339-364 semantics,
+    q4pool row-block split) on `layers` layers of the same shapes."""
+    import ctypes as C
+
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_ffi import Oracle
+    orc = Oracle()
+    rng = np.random.default_rng(seed)
+    T = host_threads()
+    pool = orc.lib.or_pool_create(T, 8960)
+    mats = []
+    nbytes = 0
+    for _ in range(layers):
+        for _, shapes in qwen_layer_shapes():
+            for out, inn in shapes:
+                w = (rng.standard_normal((out, inn), dtype=np.float32) * np.float32(0.02))
+                pk, ws, sub = orc.quantize_g256sf(w)
+                mats.append((pk, ws, sub, out, inn, np.zeros(out, np.float32)))
+                nbytes += alg_bytes(3, out, inn, 4, 1)
+    xs = {k: rng.standard_normal(k, dtype=np.float32) for k in (1536, 8960)}
+    P = lambda a: C.c_void_p(a.ctypes.data)
+
+    def one_pass():
+        for pk, ws, sub, out, inn, y in mats:
+            orc.lib.or_pool_gemv_g256sf_sdot(pool, P(pk), P(ws), P(sub), P(xs[inn]), None, P(y), out, inn)
+
+    one_pass()
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        one_pass()
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s or reps >= 2000:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    orc.lib.or_pool_destroy(pool)
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": T, "kind": "port",
+            "us_per_layer": round(dt / layers * 1e6, 1),
+            "sample": f"{layers} Qwen2.5-1.5B layers of q4g256sf (7 projections each, {nbytes / 1e6:.1f} MB), "
+                      f"M=1 W4A8, {reps} passes over {dt * reps:.1f} s, {T} threads"}
+
+
+def cpu_baseline_rotated(kind, bits, out, inn, budget_s, seed=7):
+    import ctypes as C
+
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_ffi import Oracle
+    orc = Oracle()
+    rng = np.random.default_rng(seed)
+    T = host_threads()
+    pool = orc.lib.or_pool_create(T, inn)
+    w = (rng.standard_normal((out, inn), dtype=np.float32) * np.float32(0.02))
+    if kind == 5:
+        pk, sc = orc.quantize_q4g32h(w)
+    else:
+        pk, sc = orc.quantize_qng64(w, bits)
+    x = rng.standard_normal(inn, dtype=np.float32)
+    y = np.zeros(out, np.float32)
+    P = lambda a: C.c_void_p(a.ctypes.data)
+    nb = alg_bytes(kind, out, inn, bits, 1)
+    orc.lib.or_pool_gemv_f32(pool, kind, bits, P(pk), P(sc), P(x), None, P(y), out, inn)
+    t0 = time.perf_counter()
+    reps = 0
+    while time.perf_counter() - t0 < budget_s and reps < 1000:
+        orc.lib.or_pool_gemv_f32(pool, kind, bits, P(pk), P(sc), P(x), None, P(y), out, inn)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    orc.lib.or_pool_destroy(pool)
+    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": T, "kind": "port",
+            "us_per_call": round(dt * 1e6, 1),
+            "sample": f"one {out}x{inn} tensor (kind {kind}, n={bits}), {reps} calls over {dt * reps:.1f} s, {T} threads"}
+
+
+# ------------------------------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3"])
+    ap.add_argument("--M", type=int, default=1, help="activation rows (cfg2: 1, 4 or 8)")
+    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--bits", type=int, default=15, help="cfg3: qNg64 width n")
+    ap.add_argument("--shape", default="gate", choices=["gate", "down"], help="cfg3: MLP gate (K=4096) or down (K=14336)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print(f"bench.py: this build measures one GPU; --gpus {max(args.gpus, world)} is not supported "
+              "(the path would shard by output rows with one all-gather of y -- not built).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import beglin_amd
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    stream = torch.cuda.Stream()
+    ctx = beglin_amd.Context(0, stream=stream.cuda_stream)
+    M = args.M
+    if args.workload == "cfg2":
+        with torch.cuda.stream(stream):
+            wl = build_cfg2(ctx, torch, M, args.layers, args.seed)
+        torch.cuda.synchronize()
+        workload = f"cfg2: Qwen2.5-1.5B decode layer x{args.layers}, q4g256sf W4A8 GEMV, 7 projections (fused qkv, o, fused gate+up, down), M={M}"
+        dtype = "int8"
+        cfg = {"workload": workload, "layers": args.layers, "M": M, "format": "q4g256sf", "activations": "W4A8 (int8, group 256)",
+               "calls_per_step": wl.ncalls(), "weight_bytes_per_step": int(wl.nbytes()), "seed": args.seed}
+    elif args.workload == "cfg1":
+        with torch.cuda.stream(stream):
+            wl = build_rotated(ctx, torch, 5, 4, 8960, 1536, M, args.seed, beglin_amd.ACT_F32)
+        workload = f"cfg1: int4 g32 fp16-scale GEMV K=1536 N=8960, fp32 activations, M={M}, {wl.ncalls()} rotated copies"
+        dtype = "int8"
+        cfg = {"workload": workload, "M": M, "format": "q4g32h", "copies": wl.ncalls(), "seed": args.seed}
+    else:
+        out, inn = (14336, 4096) if args.shape == "gate" else (4096, 14336)
+        with torch.cuda.stream(stream):
+            wl = build_rotated(ctx, torch, 4, args.bits, out, inn, M, args.seed, beglin_amd.ACT_F32)
+        workload = f"cfg3: qNg64 n={args.bits} GEMV {out}x{inn} (Llama-3.1-8B MLP {args.shape}), fp32 activations, M={M}, {wl.ncalls()} rotated copies"
+        dtype = "int8"
+        cfg = {"workload": workload, "M": M, "format": f"qNg64 n={args.bits}", "copies": wl.ncalls(), "seed": args.seed}
+    torch.cuda.synchronize()
+
+    step_ms, wall, graph = time_graph(torch, stream, wl.run, args.steps, args.warmup)
+    nbytes = wl.nbytes()
+    value = nbytes / (step_ms * 1e-3) / 1e9
+
+    # per-call latency of each call type (graph over all its instances)
+    per_call = {}
+    tags = sorted({c[5] for c in wl.calls})
+    for tag in tags:
+        ms, _, _ = time_graph(torch, stream, lambda: wl.run([tag]), max(5, args.steps // 5), 3)
+        n = wl.ncalls([tag])
+        per_call[tag] = {"us": round(ms * 1e3 / n, 2), "GB/s": round(wl.nbytes([tag]) / (ms * 1e-3) / 1e9, 1)}
+
+    k_ms, k_n, prep_ms, prep_n = kernel_roofline(ctx, torch, stream, wl, reps=3)
+    achieved = nbytes / (k_ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_gemv (bgl_gemv.hip)", "launches_per_step": k_n,
+            "kernel_us_per_launch": round(k_ms * 1e3 / max(k_n, 1), 2),
+            "prep_us_per_launch": round(prep_ms * 1e3 / max(prep_n, 1), 2)}
+
+    cpu = None
+    if not args.no_cpu:
+        if args.workload == "cfg2":
+            cpu = cpu_baseline_cfg2(M, args.cpu_seconds)
+        elif args.workload == "cfg1":
+            cpu = cpu_baseline_rotated(5, 4, 8960, 1536, args.cpu_seconds)
+        else:
+            out, inn = (14336, 4096) if args.shape == "gate" else (4096, 14336)
+            cpu = cpu_baseline_rotated(4, args.bits, out, inn, args.cpu_seconds)
+
+    line = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",
+            "config": cfg, "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4), "us_per_call": per_call,
+            "wall_s_timed": round(wall, 3), "roofline": roof, "cpu_baseline": cpu}
+    print(json.dumps(line), flush=True)
+    del graph
+    wl.free()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -53,6 +53,13 @@ void bgl_ctx_destroy(bgl_ctx *ctx);                         /* q4pool_destroy (q
 int  bgl_synchronize(bgl_ctx *ctx);                         /* mlx_gpu_synchronize (mlx_moe.h:29) */
 void *bgl_ctx_stream(bgl_ctx *ctx);                          /* the hipStream_t work is queued on */
 
+/* ---------------- profiling (the QWEN_PROF phase buckets, qwen_infer.c:1231, :1851-1895) ----------------
+ * While enabled, every kernel the context launches is bracketed by HIP events on its stream.
+ * bgl_prof_read synchronises and reports, per phase (0 = activation prep, 1 = GEMV/gather, 2 = other),
+ * the summed kernel time in ms and the launch count, then clears the records. */
+int  bgl_prof_enable(bgl_ctx *ctx, int on);
+int  bgl_prof_read(bgl_ctx *ctx, double *ms_by_phase, int *launches_by_phase, int nphase);
+
 /* ---------------- weight binding: upload + repack into the tiled device layout ----------------
  * mlx_gpu_bind_af (mlx_moe.h:48-50) / kai_repack_one_lazy (qwen_infer.c:473-487).  Host buffers
  * are read once; the device copy is owned by the returned tensor. */

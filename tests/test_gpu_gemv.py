@@ -139,6 +139,9 @@ def test_gemv_parity(ctx, torch_dev, oracle, kind, bits, act, inn, M):
     print(f"  max-rel {e:.3e}")
     assert np.all(np.isfinite(got))
     assert e <= TOL, e
+    if act == 1 and M == 1:
+        # one-column W4A8 runs the fused kernel, which folds groups in the reference's order
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "fused W4A8 fold not bit-exact"
     t.free()
 
 
@@ -250,3 +253,70 @@ def test_full_size_configs(ctx, torch_dev, oracle, name, kind, bits, act, out, i
     print(f"  max-rel {e:.3e}")
     assert e <= TOL
     t.free()
+
+
+def test_w4a8_fused_and_separate_paths_agree(torch_dev, oracle, monkeypatch):
+    """M=1 W4A8 through the fused-quantization kernel vs through the separate prep kernel."""
+    import beglin_amd
+    torch = torch_dev
+    say("fused vs separate W4A8")
+    out, inn = 320, 2048
+    pk, ws, sub = oracle.quantize_g256sf(weights(1000, out, inn))
+    x = torch.from_numpy(seeded_normal(1001, (1, inn))).cuda()
+    ys = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("BGL_NO_FUSED_Q", flag)
+        c = beglin_amd.Context(0)
+        t = c.bind(3, pk, ws, out, inn, sub=sub)
+        y = torch.empty((1, out), device="cuda")
+        c.matmul(t, x, y, act=1)
+        torch.cuda.synchronize()
+        ys.append(y.cpu().numpy())
+        t.free(); c.close()
+    assert relerr(ys[1], ys[0]) <= 1e-6
+
+
+def test_graph_replays_match_eager(ctx, torch_dev, oracle):
+    """Capture a GEMV sequence into a HIP graph, replay it several times with eager work and
+    synchronisations in between; every replay must equal the eager result bit for bit."""
+    torch = torch_dev
+    say("graph replay")
+    out, inn = 700, 4096
+    tq = ctx.bind(4, *ref_quant(oracle, 4, weights(1100, out, inn), 7)[:2], out, inn, bits=7)
+    pg, ws, sub = oracle.quantize_g256sf(weights(1101, out, inn))
+    tg = ctx.bind(3, pg, ws, out, inn, sub=sub)
+    x = torch.from_numpy(seeded_normal(1102, (4, inn))).cuda()
+    y1 = torch.empty((4, out), device="cuda"); y2 = torch.empty((1, out), device="cuda")
+
+    def step():
+        ctx.matmul(tq, x, y1, act=0)
+        ctx.matmul(tg, x[:1], y2, act=1)
+
+    step(); torch.cuda.synchronize()
+    e1, e2 = y1.clone(), y2.clone()
+    cs = torch.cuda.Stream()
+    import beglin_amd
+    c2 = beglin_amd.Context(0, stream=cs.cuda_stream)
+    tq2 = c2.bind(4, *ref_quant(oracle, 4, weights(1100, out, inn), 7)[:2], out, inn, bits=7)
+    tg2 = c2.bind(3, pg, ws, out, inn, sub=sub)
+
+    def step2():
+        c2.matmul(tq2, x, y1, act=0)
+        c2.matmul(tg2, x[:1], y2, act=1)
+
+    with torch.cuda.stream(cs):
+        step2()
+    torch.cuda.synchronize()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=cs):
+        step2()
+    for rep in range(4):
+        y1.fill_(float("nan")); y2.fill_(float("nan"))
+        with torch.cuda.stream(cs):
+            g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y1, e1) and torch.equal(y2, e2), f"replay {rep} differs"
+        step(); torch.cuda.synchronize()                       # eager work between replays
+    for t in (tq, tg, tq2, tg2):
+        t.free()
+    c2.close()
