@@ -147,6 +147,14 @@ class Context:
         B = (C.c_void_p * n)(*[(b.data_ptr() if b is not None else None) for b in (biases or [None] * n)])
         _check(lib().bgl_matmul_group_dev(self.h, n, W, act, _p(x_dev), B, Y, M), "bgl_matmul_group_dev")
 
+    def prep_only(self, x_dev, act, t):
+        """Prepare activation operands for tensor t's kind (kept in the context)."""
+        M = 1 if x_dev.dim() == 1 else x_dev.shape[0]
+        _check(lib().bgl_prep_act_dev(self.h, act, t.info()["kind"], _p(x_dev), M, x_dev.shape[-1]), "bgl_prep_act_dev")
+
+    def matmul_prepped(self, t, y_dev, act=ACT_F32, bias_dev=None, M=1):
+        _check(lib().bgl_matmul_prepped_dev(self.h, t.h, act, _p(bias_dev), _p(y_dev), M), "bgl_matmul_prepped_dev")
+
     def quant_act_i8(self, x_dev, gsize, xq_dev, ascale_dev):
         M = 1 if x_dev.dim() == 1 else x_dev.shape[0]
         _check(lib().bgl_quant_act_i8_dev(self.h, _p(x_dev), M, x_dev.shape[-1], gsize, _p(xq_dev), _p(ascale_dev)),

@@ -121,16 +121,23 @@ extern "C" int bgl_prof_read(bgl_ctx *c, double *ms, int *cnt, int nphase) {
     if (!c) return bgl_fail(BGL_E_ARG, "bgl_prof_read: NULL context");
     HIPCHK(hipStreamSynchronize(c->stream));
     for (int i = 0; i < nphase; i++) { if (ms) ms[i] = 0.0; if (cnt) cnt[i] = 0; }
+    int bad = 0;
     for (auto &r : c->prof_ev) {
         float t = 0.0f;
-        if (hipEventElapsedTime(&t, r.second.first, r.second.second) == hipSuccess && r.first < nphase) {
-            if (ms) ms[r.first] += t;
-            if (cnt) cnt[r.first] += 1;
+        if (hipEventElapsedTime(&t, r.second.first, r.second.second) == hipSuccess) {
+            if (r.first < nphase) {
+                if (ms) ms[r.first] += t;
+                if (cnt) cnt[r.first] += 1;
+            }
+        } else {
+            bad++;
         }
         c->ev_pool.push_back(r.second.first);
         c->ev_pool.push_back(r.second.second);
     }
     c->prof_ev.clear();
+    (void)hipGetLastError();             // an unreadable event pair must not poison the next call
+    if (bad) return bgl_fail(BGL_E_HIP, "bgl_prof_read: %d event pairs had no timing", bad);
     return 0;
 }
 
@@ -142,7 +149,7 @@ extern "C" void bgl_ctx_destroy(bgl_ctx *c) {
     for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
     for (auto &kv : c->host_cache) bgl_tensor_free(kv.second);
     c->host_cache.clear();
-    DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->hx, &c->hy, &c->hb,
+    DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->part, &c->hx, &c->hy, &c->hb,
                       &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_meta};
     for (DevBuf *b : bufs) dbuf_free(*b);
     if (c->own_stream) (void)hipStreamDestroy(c->stream);
@@ -370,6 +377,8 @@ extern "C" int bgl_dequant_dev(bgl_ctx *c, const bgl_tensor *t, int row0, int nr
 }
 
 // ------------------------------------------------------------------ activation prep
+static int act_group(int kind) { return kind == BGL_Q4G256SF ? 256 : 64; }
+
 int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, GemvAct &A) {
     memset(&A, 0, sizeof A);
     if (act == BGL_ACT_F32) {
@@ -391,6 +400,7 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
         prof_end(c, tok);
     }
     HIPCHK(hipGetLastError());
+    c->prep_act = act; c->prep_gq = gq; c->prep_M = M; c->prep_K = K;
     A.xw = (const int *)c->act_w.p;
     A.xs = (const float *)c->act_s.p;
     A.xsum = (const int *)c->act_sum.p;
@@ -426,6 +436,9 @@ static void fill_tasks(GemvLaunch &L, int n, const BglDevTensor *Ts, const float
         t.bias = bias ? bias[i] : nullptr;
         t.ystride = ystride ? ystride[i] : Ts[i].N;
         t.blk0 = blocks;
+        t.ks = 1;
+        t.gpb = Ts[i].nunits;
+        t.part = nullptr;
         blocks += Ts[i].ntiles;
     }
 }
@@ -437,7 +450,24 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
     int blocks = 0;
     fill_tasks(L, n, Ts, bias, y, ystride, blocks);
     L.a = A;
-    const int nw = pick_waves(c, Ts[0].nunits);
+    L.mtot = M;
+    // Few tiles and a long K: split K over workgroups (>= 8 units per slice) so the launch keeps
+    // enough wavefronts in flight; a second small kernel sums the slices in order.
+    int ks = 1;
+    if (n == 1 && blocks < c->min_blocks && Ts[0].nunits >= 16) {
+        ks = (c->min_blocks + blocks - 1) / blocks;
+        if (ks > Ts[0].nunits / 8) ks = Ts[0].nunits / 8;
+        if (ks < 1) ks = 1;
+    }
+    if (ks > 1) {
+        GemvTask &t = L.t[0];
+        t.gpb = (Ts[0].nunits + ks - 1) / ks;
+        t.ks = (Ts[0].nunits + t.gpb - 1) / t.gpb;
+        if (dbuf_reserve(c, c->part, (size_t)t.ks * M * Ts[0].N * 4, false)) return BGL_E_NOMEM;
+        t.part = (float *)c->part.p;
+        blocks *= t.ks;
+    }
+    const int nw = pick_waves(c, L.t[0].gpb);
     for (int m0 = 0; m0 < M;) {
         int r = M - m0, MB, mc;
         if (r >= 5) { MB = 8; mc = r < 8 ? r : 8; }
@@ -452,6 +482,14 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
         if (rc) return bgl_fail(BGL_E_ARG, "gemv launch: bad column block");
         HIPCHK(hipGetLastError());
         m0 += mc;
+    }
+    if (L.t[0].ks > 1) {
+        const GemvTask &t = L.t[0];
+        int tok = prof_begin(c, 1);
+        hipLaunchKernelGGL(k_splitk_reduce, dim3(nblk((long)M * t.T.N)), dim3(256), 0, c->stream, (const float *)t.part, t.ks, M,
+                           t.T.N, t.bias, t.y, t.ystride);
+        prof_end(c, tok);
+        HIPCHK(hipGetLastError());
     }
     return 0;
 }
@@ -492,7 +530,6 @@ static bool fused_q_ok(bgl_ctx *c, int kind, int K, int M) {
     return bgl_gemv_q_lds(kind, K, 64) <= 64 * 1024;
 }
 
-static int act_group(int kind) { return kind == BGL_Q4G256SF ? 256 : 64; }
 
 extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *w, int act, const float *x_dev,
                                     const float *const *bias_dev, float *const *y_dev, int M) {
@@ -516,6 +553,32 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
     int rc = prep_act(c, act, act_group(kind), x_dev, M, Ts[0].K, A);
     if (rc) return rc;
     return run_gemv(c, n, Ts, act, A, M, bias_dev, y_dev, nullptr);
+}
+
+extern "C" int bgl_prep_act_dev(bgl_ctx *c, int act, int kind, const float *x_dev, int M, int in) {
+    if (!c || !x_dev || M < 1) return bgl_fail(BGL_E_ARG, "bgl_prep_act_dev: bad argument");
+    if (act != BGL_ACT_F32 && act != BGL_ACT_W4A8) return bgl_fail(BGL_E_ARG, "unknown activation mode %d", act);
+    const int gq = act_group(kind);
+    if (in % 64 || in % gq) return bgl_fail(BGL_E_ARG, "bgl_prep_act_dev: in=%d not a multiple of the group", in);
+    HIPCHK(hipSetDevice(c->device));
+    GemvAct A;
+    return prep_act(c, act, gq, x_dev, M, in, A);
+}
+
+extern "C" int bgl_matmul_prepped_dev(bgl_ctx *c, const bgl_tensor *w, int act, const float *bias_dev, float *y_dev, int M) {
+    if (!c || !w || !y_dev || !w->experts.empty()) return bgl_fail(BGL_E_ARG, "bgl_matmul_prepped_dev: bad argument");
+    const BglDevTensor &T = w->T;
+    if (c->prep_act != act || c->prep_K != T.K || c->prep_gq != act_group(T.fmt) || M > c->prep_M)
+        return bgl_fail(BGL_E_ARG, "bgl_matmul_prepped_dev: no prepared activation matches (act %d, in %d, M %d)", act, T.K, M);
+    if (T.fmt == BGL_Q4G256SF && act != BGL_ACT_W4A8)
+        return bgl_fail(BGL_E_UNSUPPORTED, "K_Q4G256SF requires W4A8 activations -- no fp32-activation path exists for g256sf");
+    HIPCHK(hipSetDevice(c->device));
+    GemvAct A;
+    memset(&A, 0, sizeof A);
+    A.xw = (const int *)c->act_w.p; A.xs = (const float *)c->act_s.p; A.xsum = (const int *)c->act_sum.p; A.gq = c->prep_gq;
+    const float *b[1] = {bias_dev};
+    float *y[1] = {y_dev};
+    return run_gemv(c, 1, &T, act, A, M, b, y, nullptr);
 }
 
 extern "C" int bgl_matmul_dev(bgl_ctx *c, const bgl_tensor *w, int act, const float *x_dev, const float *bias_dev,

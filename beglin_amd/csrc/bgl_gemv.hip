@@ -322,17 +322,18 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv(GemvLaunch L) {
 #pragma unroll
     for (int i = 1; i < BGL_MAX_TASKS; i++) if (i == ti) task = L.t[i];
     const BglDevTensor &T = task.T;
-    const int tile = b - task.blk0;
+    const int lb = b - task.blk0, tile = lb / task.ks, split = lb % task.ks;
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const Cols<MB> C = col_rows<MB>(L.a, L.m0, L.mcols);
-    const int K = T.K, U = T.nunits;
+    const int K = T.K;
+    const int ubeg = split * task.gpb, U = min(ubeg + task.gpb, T.nunits);
 
     float acc[MB];
 #pragma unroll
     for (int m = 0; m < MB; m++) acc[m] = 0.0f;
     constexpr bool PREFETCH = chunks_per_unit<FMT>(NB) <= 8;
-    int u = wave;
+    int u = ubeg + wave;
     Raw<FMT, NB> r0, r1;
     if (u < U) load_raw<FMT, NB>(r0, T, tile, lane, u);
     while (u < U) {
@@ -354,6 +355,15 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv(GemvLaunch L) {
     if (wave != 0) return;
     const int row = tile * BGL_TILE + lane;
     if (row >= T.N) return;
+    if (task.ks > 1) {                     // partial of this K slice; k_splitk_reduce adds the slices
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            float v = red[0][m][lane];
+            for (int w = 1; w < nw; w++) v += red[w][m][lane];
+            if (m < L.mcols) task.part[((size_t)split * L.mtot + L.m0 + m) * T.N + row] = v;
+        }
+        return;
+    }
     const float bb = task.bias ? task.bias[row] : 0.0f;
 #pragma unroll
     for (int m = 0; m < MB; m++) {
@@ -361,6 +371,17 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv(GemvLaunch L) {
         for (int w = 1; w < nw; w++) v += red[w][m][lane];
         if (m < L.mcols) task.y[(size_t)(L.m0 + m) * task.ystride + row] = bb + v;
     }
+}
+
+// Sums the K-slice partials in slice order: y[m][r] = bias[r] + sum_s part[s][m][r].
+__global__ void k_splitk_reduce(const float *__restrict__ part, int ks, int M, int N, const float *__restrict__ bias,
+                                float *__restrict__ y, int ystride) {
+    const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (long)M * N) return;
+    const int m = (int)(t / N), r = (int)(t % N);
+    float v = part[t];
+    for (int s = 1; s < ks; s++) v += part[(size_t)s * M * N + t];
+    y[(size_t)m * ystride + r] = (bias ? bias[r] : 0.0f) + v;
 }
 
 // ================================================================================== path B kernel (W4A8, fused quantization)

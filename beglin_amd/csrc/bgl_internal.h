@@ -30,6 +30,8 @@ struct bgl_ctx {
     int min_blocks = 256;                 // fused W4A8: split tiles until at least this many workgroups
     int force_tr = 0;                     // BGL_FORCE_TR: fixed rows per workgroup (tuning)
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
+    int prep_act = -1, prep_gq = 0, prep_M = 0, prep_K = 0;   // what act_* currently hold
+    DevBuf part;                          // K-split partial sums [ks][M][N]
     DevBuf hx, hy, hb;                    // staging for the host-pointer entry points
     DevBuf moe_a, moe_b, moe_c, moe_d, moe_meta;
     bool prof = false;                    // bracket launches with events (bgl_prof_enable)

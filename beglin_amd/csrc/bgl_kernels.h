@@ -25,6 +25,8 @@ struct GemvTask {
     const float *bias;        // [N] or null
     int ystride;
     int blk0;
+    int ks, gpb;              // K split over ks workgroups of gpb units each (ks == 1: no split)
+    float *part;              // ks > 1: partials [ks][M][N], summed by k_splitk_reduce
 };
 
 // Activation operands (shared by every task of a launch; all tasks have the same K).
@@ -42,6 +44,7 @@ struct GemvLaunch {
     GemvAct a;                // prepared activation operands (k_gemv)
     const float *x;           // raw fp32 activations [M][K] (k_gemv_q quantizes them itself)
     int m0, mcols;            // columns [m0, m0+mcols) of the activation (mcols <= MB)
+    int mtot;                 // total columns of the call (partial buffer stride)
 };
 
 // ---- kernels (bgl_prep.hip) ----
@@ -59,6 +62,7 @@ __global__ void k_repack_u32(const uint32_t *src, int N, int U, uint32_t *dst);
 __global__ void k_repack_u64(const uint64_t *src, int N, int U, uint64_t *dst);
 __global__ void k_repack_qng_scales(const float *src, int N, int ng, float2 *dst);
 __global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *out);
+__global__ void k_splitk_reduce(const float *part, int ks, int M, int N, const float *bias, float *y, int ystride);
 
 // ---- host-side launchers (bgl_gemv.hip) ----
 int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, int nw, hipStream_t st);

@@ -92,6 +92,12 @@ int  bgl_matmul_dev(bgl_ctx *ctx, const bgl_tensor *w, int act, const float *x_d
  * qwen_infer.c:1276-1306) in ONE launch.  All must have the same `in` and kind; n <= 4. */
 int  bgl_matmul_group_dev(bgl_ctx *ctx, int n, const bgl_tensor *const *w, int act, const float *x_dev,
                           const float *const *bias_dev, float *const *y_dev, int M);
+/* Prepare activation operands once and reuse them for several GEMVs with the same input (the
+ * caller-side quantization of matmul_sdot, qwen_infer.c:1870-1889, feeding gemm_qXg64_sdot_mt's
+ * xq/ascale arguments, q4gemv.h:779-791).  `kind` selects the activation grouping (g256sf: 256).
+ * The prepared operands live in the context until the next prep or GEMV call that prepares. */
+int  bgl_prep_act_dev(bgl_ctx *ctx, int act, int kind, const float *x_dev, int M, int in);
+int  bgl_matmul_prepped_dev(bgl_ctx *ctx, const bgl_tensor *w, int act, const float *bias_dev, float *y_dev, int M);
 /* W4A8 activation quantizer on device (q4_quant_act_i8, q4gemv.h:177-213; _g256,
  * q4gemv_g256.h:72-99): xq [M][in] int8, ascale [M][in/gsize]. */
 int  bgl_quant_act_i8_dev(bgl_ctx *ctx, const float *x_dev, int M, int in, int gsize, int8_t *xq_dev, float *ascale_dev);

@@ -111,6 +111,8 @@ GEMV_CASES = [
     (1, 0, 0, 1536), (1, 0, 1, 1536), (2, 0, 0, 1024), (2, 0, 1, 1024), (3, 0, 1, 1536), (5, 0, 0, 1536),
     (4, 2, 0, 1024), (4, 3, 0, 1024), (4, 4, 0, 1024), (4, 5, 0, 1408), (4, 7, 0, 1024), (4, 8, 0, 1024),
     (4, 12, 0, 1024), (4, 15, 0, 1024), (4, 9, 0, 192),
+    # few row tiles and a long K: the K dimension is split over workgroups (deterministic tail sum)
+    (1, 0, 0, 4096), (1, 0, 1, 4096), (4, 15, 0, 8192), (5, 0, 0, 8192),
 ]
 
 
@@ -320,3 +322,26 @@ def test_graph_replays_match_eager(ctx, torch_dev, oracle):
     for t in (tq, tg, tq2, tg2):
         t.free()
     c2.close()
+
+
+def test_prepped_activation_reuse(ctx, torch_dev, oracle):
+    """Prepare once, run two GEMVs (gemm_qXg64_sdot_mt's caller-quantized activations)."""
+    torch = torch_dev
+    say("prepped reuse")
+    inn = 2048
+    x = seeded_normal(1200, (3, inn))
+    xd = torch.from_numpy(x).cuda()
+    for act, kind in ((0, 1), (1, 1), (0, 2)):
+        ts, refs = [], []
+        for i, out in enumerate((96, 160)):
+            pk, sc, sub = ref_quant(oracle, kind, weights(1201 + i, out, inn), 0)
+            ts.append(ctx.bind(kind, pk, sc, out, inn))
+            refs.append(oracle.gemm_f32(kind, pk, sc, x) if act == 0 else oracle.matmul_sdot(kind, pk, sc, x))
+        ctx.prep_only(xd, act, ts[0])
+        for t, ref in zip(ts, refs):
+            y = torch.empty((3, t.info()["out"]), device="cuda")
+            ctx.matmul_prepped(t, y, act=act, M=3)
+            torch.cuda.synchronize()
+            assert relerr(y.cpu().numpy(), ref) <= TOL
+        for t in ts:
+            t.free()
