@@ -168,9 +168,21 @@ class Context:
         for e, (kind, bits, pk, sc) in enumerate(descs):
             out = pk.shape[0]
             inn = sc.shape[1] * (32 if kind == K_Q4G32H else 64)
-            arr[e] = capi.bgl_wt(kind, bits, out, inn, pk.ctypes.data, sc.ctypes.data, None)
+            b = bits if kind == K_QNG64 else (8 if kind == K_Q8G64 else 4)
+            arr[e] = capi.bgl_wt(kind, b, out, inn, pk.ctypes.data, sc.ctypes.data, None)
         h = C.c_void_p()
         _check(lib().bgl_bind_experts(self.h, E, arr, C.byref(h)), "bgl_bind_experts")
+        return Tensor(h)
+
+    def experts_from_tensors(self, tensors):
+        """Stack bound single tensors (e.g. from quantize()) into one expert tensor.  The new
+        tensor owns them: their handles are cleared here and freed with the stack."""
+        E = len(tensors)
+        arr = (C.c_void_p * E)(*[t.h.value for t in tensors])
+        h = C.c_void_p()
+        _check(lib().bgl_experts_from_tensors(self.h, E, arr, C.byref(h)), "bgl_experts_from_tensors")
+        for t in tensors:
+            t.h = None
         return Tensor(h)
 
     def gather_matvec(self, experts, x_dev, idx_dev, y_dev):

@@ -150,7 +150,7 @@ extern "C" void bgl_ctx_destroy(bgl_ctx *c) {
     for (auto &kv : c->host_cache) bgl_tensor_free(kv.second);
     c->host_cache.clear();
     DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->part, &c->hx, &c->hy, &c->hb,
-                      &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_meta};
+                      &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_e, &c->moe_f, &c->moe_g, &c->moe_meta};
     for (DevBuf *b : bufs) dbuf_free(*b);
     if (c->own_stream) (void)hipStreamDestroy(c->stream);
     delete c;

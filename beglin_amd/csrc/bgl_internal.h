@@ -33,7 +33,7 @@ struct bgl_ctx {
     int prep_act = -1, prep_gq = 0, prep_M = 0, prep_K = 0;   // what act_* currently hold
     DevBuf part;                          // K-split partial sums [ks][M][N]
     DevBuf hx, hy, hb;                    // staging for the host-pointer entry points
-    DevBuf moe_a, moe_b, moe_c, moe_d, moe_meta;
+    DevBuf moe_a, moe_b, moe_c, moe_d, moe_e, moe_f, moe_g, moe_meta;   // MoE digits x2, fp32 h/down, bucket scratch
     bool prof = false;                    // bracket launches with events (bgl_prof_enable)
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> prof_ev;
     std::vector<hipEvent_t> ev_pool;

@@ -1,22 +1,421 @@
 // bgl_moe.hip -- expert-stacked tensors and the expert-sorted MoE gather.
-#include "../../include/beglin_qgemv.h"
+//
+// One routed FFN call (moe_ffn_batched, qwen_infer.c:5238-5350, routing supplied by the caller):
+//   k_moe_bucket   sort the T*K (token, k) pairs by expert, stable in pair order (the reference's
+//                  bucket fill order) -> segment offsets, permutation, inverse permutation
+//   k_act_x24      exact activation digits of the T token rows, shared by every expert
+//   k_moe_gemv     gate+up of every touched expert with SwiGLU fused, h[s] = silu(g) * u; one
+//                  workgroup per (expert, 64-row tile) so each expert's weights stream once for
+//                  all of its tokens; experts may differ in format (runtime switch per workgroup)
+//   k_moe_gemv     shared-expert gate+up over all T tokens (one by-value pseudo-expert)
+//   k_act_x24      digits of the routed h rows -> k_moe_gemv down projection
+//   k_act_x24      digits of the shared h rows -> k_moe_gemv shared down projection
+//   k_moe_combine  out[t] = sum over t's experts in ascending expert order of w * down, + shared
+// No host->device copies happen inside a call, so the sequence can be captured in a HIP graph.
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+#include "bgl_gemv_impl.h"
 #include "bgl_internal.h"
 
-extern "C" int bgl_bind_experts(bgl_ctx *c, int E, const bgl_wt *experts, bgl_tensor **out) {
-    (void)c; (void)E; (void)experts; (void)out;
-    return bgl_fail(BGL_E_UNSUPPORTED, "bgl_bind_experts: not built yet");
+#define HIPCHK(expr)                                                                             \
+    do {                                                                                         \
+        hipError_t e_ = (expr);                                                                  \
+        if (e_ != hipSuccess) return bgl_fail(BGL_E_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+#define MOE_MB 4            // token columns per weight pass of one tile
+#define MOE_MAXW 8          // waves per workgroup: 512 threads leave 256 VGPRs for the widest formats
+#define MOE_MAX_K 16        // top-K limit of the combine kernel
+
+static inline unsigned nblk(long n, int bs = 256) { return (unsigned)((n + bs - 1) / bs); }
+
+// ====================================================================================== bucketing
+// One workgroup.  off[E+1]: segment starts in sorted order; perm[s]: pair at sorted position s;
+// pos[p]: sorted position of pair p (-1 for an expert id outside [0, E), which is skipped);
+// tok[s] = perm[s] / K, the token row that feeds sorted position s.
+__global__ __launch_bounds__(1024) void k_moe_bucket(const int32_t *__restrict__ idx, int P, int K, int E,
+                                                     int *__restrict__ off, int *__restrict__ perm,
+                                                     int *__restrict__ pos, int *__restrict__ tok) {
+    extern __shared__ int sm[];
+    int *start = sm;               // [E + 1]
+    int *ids = sm + E + 1;         // [P]
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) start[e] = 0;
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        int e = idx[p];
+        if (e < 0 || e >= E) e = -1;
+        ids[p] = e;
+        if (e >= 0) atomicAdd(&start[e], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int e = 0; e < E; e++) { const int n = start[e]; start[e] = run; run += n; }
+        start[E] = run;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) off[e] = start[e];
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        const int e = ids[p];
+        if (e < 0) { pos[p] = -1; continue; }
+        int rank = 0;
+        for (int q = 0; q < p; q++) rank += ids[q] == e;
+        const int s = start[e] + rank;
+        perm[s] = p;
+        pos[p] = s;
+        tok[s] = p / K;
+    }
 }
+
+// ====================================================================================== gather GEMV
+struct MoeTask {
+    const BglDevTensor *ta;      // expert table [E] (gate, or the only projection); null: use da
+    const BglDevTensor *tb;      // up table [E] in SwiGLU mode
+    BglDevTensor da, db;         // by-value single tensor(s) when ta is null (shared experts)
+    int E, tpe;                  // grid = E * tpe workgroups (tpe: 64-row tiles per expert)
+    const int *off;              // [E+1] sorted segment starts; null: one segment [0, ncols)
+    int ncols;
+    const int *cols;             // activation row of sorted position s (null: s)
+    const int *ymap;             // output row of sorted position s (null: s)
+    GemvAct a;                   // exact-digit activations (k_act_x24 layout)
+    float *y;
+    int ystride;
+    int swiglu;                  // y = silu(A x) * (B x)
+};
+
+template <int FMT, int NB, int MB>
+__device__ __forceinline__ void moe_chunk(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
+                                          int tile, int base, int mc, float (*red)[2][MOE_MB][BGL_TILE]) {
+    const int nw = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    Cols<MB> C;
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        const int mm = m < mc ? m : mc - 1;              // padded columns repeat the last one
+        C.am[m] = Mt.cols ? uni(Mt.cols)[base + mm] : base + mm;
+    }
+    float acc[MB], accb[MB];
+#pragma unroll
+    for (int m = 0; m < MB; m++) { acc[m] = 0.0f; accb[m] = 0.0f; }
+    const int K = Ta.K, U = Ta.nunits;
+    for (int u = wave; u < U; u += nw) {
+        Raw<FMT, NB> r;
+        load_raw<FMT, NB>(r, Ta, tile, lane, u);
+        comp_dispatch<FMT, BGL_ACT_F32, NB, MB>(r, K, u, Mt.a, C, acc);
+        if (glu) {
+            load_raw<FMT, NB>(r, Tb, tile, lane, u);
+            comp_dispatch<FMT, BGL_ACT_F32, NB, MB>(r, K, u, Mt.a, C, accb);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MB; m++) { red[wave][0][m][lane] = acc[m]; red[wave][1][m][lane] = accb[m]; }
+    __syncthreads();
+    const int row = tile * BGL_TILE + lane;
+    if (wave == 0 && row < Ta.N) {
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            if (m < mc) {
+                float va = red[0][0][m][lane], vb = red[0][1][m][lane];
+                for (int w = 1; w < nw; w++) { va += red[w][0][m][lane]; vb += red[w][1][m][lane]; }
+                float out = va;
+                if (glu) out = (va / (1.0f + expf(-va))) * vb;   // moe_swiglu_inplace, qwen_infer.c:3475-3481
+                const int yr = Mt.ymap ? Mt.ymap[base + m] : base + m;
+                Mt.y[(size_t)yr * Mt.ystride + row] = out;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+template <int FMT, int NB>
+__device__ __forceinline__ void moe_tile(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
+                                         int tile, int seg0, int ncols, float (*red)[2][MOE_MB][BGL_TILE]) {
+    int c0 = 0;
+    for (; ncols - c0 >= 2; c0 += MOE_MB) {
+        const int rem = ncols - c0;
+        moe_chunk<FMT, NB, MOE_MB>(Mt, Ta, Tb, glu, tile, seg0 + c0, rem < MOE_MB ? rem : MOE_MB, red);
+    }
+    if (c0 < ncols) moe_chunk<FMT, NB, 1>(Mt, Ta, Tb, glu, tile, seg0 + c0, 1, red);
+}
+
+// Expert record through the constant address space: scalar loads, so every address derived from
+// it stays wave-uniform (a plain global load would be treated as divergent).
+__device__ __forceinline__ BglDevTensor ld_tensor(const BglDevTensor *p) {
+    static_assert(sizeof(BglDevTensor) % 4 == 0, "BglDevTensor is loaded as dwords");
+    int w[sizeof(BglDevTensor) / 4];
+    ucint q = uni(reinterpret_cast<const int *>(p));
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(BglDevTensor) / 4); i++) w[i] = q[i];
+    BglDevTensor t;
+    __builtin_memcpy(&t, w, sizeof t);
+    return t;
+}
+
+__global__ __launch_bounds__(MOE_MAXW * BGL_TILE) void k_moe_gemv(MoeTask Mt) {
+    __shared__ float red[MOE_MAXW][2][MOE_MB][BGL_TILE];
+    const int e = blockIdx.x / Mt.tpe, tile = blockIdx.x % Mt.tpe;
+    int seg0 = 0, ncols = Mt.ncols;
+    if (Mt.off) { seg0 = uni(Mt.off)[e]; ncols = uni(Mt.off)[e + 1] - seg0; }
+    if (ncols <= 0) return;                                   // expert not routed to by any pair
+    const BglDevTensor Ta = Mt.ta ? ld_tensor(Mt.ta + e) : Mt.da;
+    if (tile >= Ta.ntiles) return;
+    const bool glu = Mt.swiglu != 0;
+    const BglDevTensor Tb = glu ? (Mt.tb ? ld_tensor(Mt.tb + e) : Mt.db) : Ta;
+    switch (Ta.fmt) {
+    case BGL_Q4G32H: moe_tile<BGL_Q4G32H, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+    case BGL_Q4G64: moe_tile<BGL_Q4G64, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+    case BGL_Q8G64: moe_tile<BGL_Q8G64, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+    case BGL_QNG64:
+        switch (Ta.bits) {
+        case 2: moe_tile<BGL_QNG64, 2>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 3: moe_tile<BGL_QNG64, 3>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 4: moe_tile<BGL_QNG64, 4>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 5: moe_tile<BGL_QNG64, 5>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 6: moe_tile<BGL_QNG64, 6>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 7: moe_tile<BGL_QNG64, 7>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 8: moe_tile<BGL_QNG64, 8>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 9: moe_tile<BGL_QNG64, 9>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 10: moe_tile<BGL_QNG64, 10>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 11: moe_tile<BGL_QNG64, 11>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 12: moe_tile<BGL_QNG64, 12>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 13: moe_tile<BGL_QNG64, 13>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 14: moe_tile<BGL_QNG64, 14>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        case 15: moe_tile<BGL_QNG64, 15>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+        default: break;
+        }
+        break;
+    default: break;
+    }
+}
+
+// ====================================================================================== combine
+// out[t][c] = (((0 + w_a d_a) + w_b d_b) + ...) over t's experts in ascending expert id, then
+// + shared[t][c]: the order in which moe_ffn_batched's bucket loop adds into mlp_out_batch.
+__global__ __launch_bounds__(256) void k_moe_combine(const float *__restrict__ D, const int *__restrict__ pos,
+                                                     const int32_t *__restrict__ idx, const float *__restrict__ w,
+                                                     int T, int K, int H, const float *__restrict__ shared,
+                                                     float *__restrict__ out) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)T * H) return;
+    const int t = (int)(i / H), c = (int)(i % H);
+    const int32_t *it = idx + (size_t)t * K;
+    int order[MOE_MAX_K];
+    for (int k = 0; k < K; k++) order[k] = k;
+    for (int a = 1; a < K; a++)                               // insertion sort: expert id, then k
+        for (int b = a; b > 0 && it[order[b]] < it[order[b - 1]]; b--) {
+            const int tmp = order[b]; order[b] = order[b - 1]; order[b - 1] = tmp;
+        }
+    float acc = 0.0f;
+    for (int a = 0; a < K; a++) {
+        const int p = t * K + order[a];
+        const int s = pos[p];
+        if (s >= 0) acc += w[p] * D[(size_t)s * H + c];
+    }
+    if (shared) acc += shared[i];
+    out[i] = acc;
+}
+
+// ====================================================================================== host side
 extern "C" int bgl_experts_from_tensors(bgl_ctx *c, int E, bgl_tensor *const *experts, bgl_tensor **out) {
-    (void)c; (void)E; (void)experts; (void)out;
-    return bgl_fail(BGL_E_UNSUPPORTED, "bgl_experts_from_tensors: not built yet");
+    if (!c || E < 1 || !experts || !out) return bgl_fail(BGL_E_ARG, "bgl_experts_from_tensors: bad argument");
+    std::vector<BglDevTensor> tab(E);
+    for (int e = 0; e < E; e++) {
+        if (!experts[e] || !experts[e]->experts.empty())
+            return bgl_fail(BGL_E_ARG, "bgl_experts_from_tensors: expert %d is not a single bound tensor", e);
+        if (experts[e]->T.N != experts[0]->T.N || experts[e]->T.K != experts[0]->T.K)
+            return bgl_fail(BGL_E_ARG, "bgl_experts_from_tensors: expert %d shape differs from expert 0", e);
+        if (experts[e]->T.fmt == BGL_Q4G256SF)
+            return bgl_fail(BGL_E_UNSUPPORTED, "bgl_experts_from_tensors: g256sf experts take W4A8 activations only");
+        tab[e] = experts[e]->T;
+    }
+    HIPCHK(hipSetDevice(c->device));
+    void *d = nullptr;
+    HIPCHK(hipMalloc(&d, sizeof(BglDevTensor) * E));
+    hipError_t err = hipMemcpy(d, tab.data(), sizeof(BglDevTensor) * E, hipMemcpyHostToDevice);
+    if (err != hipSuccess) {
+        (void)hipFree(d);
+        return bgl_fail(BGL_E_HIP, "bgl_experts_from_tensors: table copy: %s", hipGetErrorString(err));
+    }
+    bgl_tensor *t = new bgl_tensor();
+    t->T = tab[0];
+    t->dev_table = d;
+    t->owned.push_back(d);
+    t->experts.assign(experts, experts + E);
+    *out = t;
+    return 0;
 }
-extern "C" int bgl_gather_matvec_dev(bgl_ctx *c, const bgl_tensor *experts, const float *x_dev, const int32_t *idx, int N, float *y) {
-    (void)c; (void)experts; (void)x_dev; (void)idx; (void)N; (void)y;
-    return bgl_fail(BGL_E_UNSUPPORTED, "bgl_gather_matvec_dev: not built yet");
+
+extern "C" int bgl_bind_experts(bgl_ctx *c, int E, const bgl_wt *experts, bgl_tensor **out) {
+    if (!c || E < 1 || !experts || !out) return bgl_fail(BGL_E_ARG, "bgl_bind_experts: bad argument");
+    std::vector<bgl_tensor *> ts(E, nullptr);
+    int rc = 0;
+    for (int e = 0; e < E && !rc; e++) {
+        if (experts[e].out != experts[0].out || experts[e].in != experts[0].in)
+            rc = bgl_fail(BGL_E_ARG, "bgl_bind_experts: expert %d shape differs from expert 0", e);
+        else
+            rc = bgl_bind(c, &experts[e], &ts[e]);
+    }
+    if (!rc) rc = bgl_experts_from_tensors(c, E, ts.data(), out);
+    if (rc)
+        for (bgl_tensor *t : ts) bgl_tensor_free(t);
+    return rc;
 }
-extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *g, const bgl_tensor *u, const bgl_tensor *d, const bgl_tensor *sg,
-                               const bgl_tensor *su, const bgl_tensor *sd, const float *x, const int32_t *idx, const float *w,
-                               int T, int K, float *out) {
-    (void)c; (void)g; (void)u; (void)d; (void)sg; (void)su; (void)sd; (void)x; (void)idx; (void)w; (void)T; (void)K; (void)out;
-    return bgl_fail(BGL_E_UNSUPPORTED, "bgl_moe_ffn_dev: not built yet");
+
+struct MoeScratch {
+    int *off, *perm, *pos, *tok;
+};
+
+static int moe_bucket(bgl_ctx *c, const int32_t *idx_dev, int P, int K, int E, MoeScratch &S) {
+    const size_t lds = ((size_t)E + 1 + P) * 4;
+    if (lds > 64 * 1024)
+        return bgl_fail(BGL_E_ARG, "MoE bucketing: %d pairs over %d experts exceed one workgroup's LDS", P, E);
+    if (dbuf_reserve(c, c->moe_meta, ((size_t)E + 1 + 3 * (size_t)P) * 4, false)) return BGL_E_NOMEM;
+    int *b = (int *)c->moe_meta.p;
+    S.off = b; S.perm = b + E + 1; S.pos = S.perm + P; S.tok = S.pos + P;
+    int tok = prof_begin(c, 2);
+    hipLaunchKernelGGL(k_moe_bucket, dim3(1), dim3(1024), lds, c->stream, idx_dev, P, K, E, S.off, S.perm, S.pos, S.tok);
+    prof_end(c, tok);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+// Exact activation digits of M rows of length K into digit slot 0 or 1.
+static int moe_prep(bgl_ctx *c, int slot, const float *x_dev, int M, int K, GemvAct &A) {
+    DevBuf &w = slot ? c->moe_d : c->moe_a;
+    DevBuf &s = slot ? c->moe_e : c->moe_b;
+    DevBuf &d = slot ? c->moe_f : c->moe_c;
+    const int ng = K / 64;
+    if (dbuf_reserve(c, w, (size_t)M * ng * 192, false) || dbuf_reserve(c, s, (size_t)M * ng * 4, false) ||
+        dbuf_reserve(c, d, (size_t)M * (K / 32) * 16, false))
+        return BGL_E_NOMEM;
+    int tok = prof_begin(c, 0);
+    hipLaunchKernelGGL(k_act_x24, dim3(nblk((long)M * ng * 64)), dim3(256), 0, c->stream, x_dev, M, K, (int8_t *)w.p,
+                       (float *)s.p, (int *)d.p);
+    prof_end(c, tok);
+    HIPCHK(hipGetLastError());
+    memset(&A, 0, sizeof A);
+    A.xw = (const int *)w.p; A.xs = (const float *)s.p; A.xsum = (const int *)d.p; A.gq = 64;
+    return 0;
+}
+
+static int moe_launch(bgl_ctx *c, const MoeTask &Mt, int units) {
+    int nw = units < c->max_waves ? units : c->max_waves;
+    if (nw > MOE_MAXW) nw = MOE_MAXW;
+    if (nw < 1) nw = 1;
+    int tok = prof_begin(c, 1);
+    hipLaunchKernelGGL(k_moe_gemv, dim3(Mt.E * Mt.tpe), dim3(nw * BGL_TILE), 0, c->stream, Mt);
+    prof_end(c, tok);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+static int expert_check(const bgl_tensor *t, const char *what) {
+    if (!t || t->experts.empty() || !t->dev_table)
+        return bgl_fail(BGL_E_ARG, "%s must be an expert tensor (bgl_bind_experts / bgl_experts_from_tensors)", what);
+    if (t->T.K % 64) return bgl_fail(BGL_E_ARG, "%s: in=%d is not a multiple of 64", what, t->T.K);
+    return 0;
+}
+
+static void max_units(const bgl_tensor *t, int &tiles, int &units) {
+    tiles = 0; units = 0;
+    for (const bgl_tensor *e : t->experts) {
+        if (e->T.ntiles > tiles) tiles = e->T.ntiles;
+        if (e->T.nunits > units) units = e->T.nunits;
+    }
+}
+
+extern "C" int bgl_gather_matvec_dev(bgl_ctx *c, const bgl_tensor *experts, const float *x_dev,
+                                     const int32_t *idx_dev, int N, float *y_dev) {
+    if (!c || !x_dev || !idx_dev || !y_dev || N < 1) return bgl_fail(BGL_E_ARG, "bgl_gather_matvec_dev: bad argument");
+    int rc = expert_check(experts, "bgl_gather_matvec_dev: experts");
+    if (rc) return rc;
+    HIPCHK(hipSetDevice(c->device));
+    const int E = (int)experts->experts.size();
+    MoeScratch S;
+    if ((rc = moe_bucket(c, idx_dev, N, 1, E, S))) return rc;
+    MoeTask Mt;
+    memset(&Mt, 0, sizeof Mt);
+    if ((rc = moe_prep(c, 0, x_dev, N, experts->T.K, Mt.a))) return rc;
+    int units;
+    max_units(experts, Mt.tpe, units);
+    Mt.ta = (const BglDevTensor *)experts->dev_table; Mt.E = E; Mt.off = S.off;
+    Mt.cols = S.perm; Mt.ymap = S.perm; Mt.y = y_dev; Mt.ystride = experts->T.N;
+    return moe_launch(c, Mt, units);
+}
+
+extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down,
+                               const bgl_tensor *sg, const bgl_tensor *su, const bgl_tensor *sd, const float *x_dev,
+                               const int32_t *idx_dev, const float *w_dev, int T, int K, float *out_dev) {
+    if (!c || !x_dev || !idx_dev || !w_dev || !out_dev || T < 1 || K < 1 || K > MOE_MAX_K)
+        return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: bad argument (T=%d, K=%d; 1 <= K <= %d)", T, K, MOE_MAX_K);
+    int rc;
+    if ((rc = expert_check(gate, "bgl_moe_ffn_dev: gate")) || (rc = expert_check(up, "bgl_moe_ffn_dev: up")) ||
+        (rc = expert_check(down, "bgl_moe_ffn_dev: down")))
+        return rc;
+    const int E = (int)gate->experts.size();
+    if ((int)up->experts.size() != E || (int)down->experts.size() != E)
+        return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: gate/up/down expert counts differ");
+    const int H = gate->T.K, I = gate->T.N;
+    if (up->T.K != H || up->T.N != I || down->T.K != I || down->T.N != H)
+        return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: gate/up [%d x %d] and down [%d x %d] disagree", I, H, down->T.N, down->T.K);
+    for (int e = 0; e < E; e++)
+        if (gate->experts[e]->T.fmt != up->experts[e]->T.fmt || gate->experts[e]->T.bits != up->experts[e]->T.bits)
+            return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: expert %d gate and up differ in format", e);
+    const int nsh = (sg != nullptr) + (su != nullptr) + (sd != nullptr);
+    if (nsh != 0 && nsh != 3) return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: give all three shared tensors or none");
+    int Ish = 0;
+    if (nsh) {
+        if (!sg->experts.empty() || !su->experts.empty() || !sd->experts.empty())
+            return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: shared experts are single tensors");
+        Ish = sg->T.N;
+        if (sg->T.K != H || su->T.K != H || su->T.N != Ish || sd->T.K != Ish || sd->T.N != H)
+            return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: shared shapes disagree with hidden=%d", H);
+        if (sg->T.fmt != su->T.fmt || sg->T.bits != su->T.bits)
+            return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: shared gate and up differ in format");
+        if (sg->T.fmt == BGL_Q4G256SF || sd->T.fmt == BGL_Q4G256SF || Ish % 64)
+            return bgl_fail(BGL_E_UNSUPPORTED, "bgl_moe_ffn_dev: shared experts need fp32-activation formats, in %% 64 == 0");
+    }
+    HIPCHK(hipSetDevice(c->device));
+    const int P = T * K;
+    MoeScratch S;
+    if ((rc = moe_bucket(c, idx_dev, P, K, E, S))) return rc;
+    // fp32 work rows: h [P][I], shared h [T][Ish], routed down [P][H], shared down [T][H]
+    const size_t nh = (size_t)P * I, nsh_h = (size_t)T * Ish, nd = (size_t)P * H, nsd = (size_t)T * H;
+    if (dbuf_reserve(c, c->moe_g, (nh + nsh_h + nd + nsd) * 4, false)) return BGL_E_NOMEM;
+    float *h = (float *)c->moe_g.p, *shh = h + nh, *dd = shh + nsh_h, *sdd = dd + nd;
+
+    MoeTask Mr, Ms;
+    memset(&Mr, 0, sizeof Mr);
+    if ((rc = moe_prep(c, 0, x_dev, T, H, Mr.a))) return rc;
+    int units;
+    max_units(gate, Mr.tpe, units);
+    Mr.ta = (const BglDevTensor *)gate->dev_table; Mr.tb = (const BglDevTensor *)up->dev_table;
+    Mr.E = E; Mr.off = S.off; Mr.cols = S.tok; Mr.y = h; Mr.ystride = I; Mr.swiglu = 1;
+    if ((rc = moe_launch(c, Mr, units))) return rc;
+    if (nsh) {
+        memset(&Ms, 0, sizeof Ms);
+        Ms.a = Mr.a; Ms.da = sg->T; Ms.db = su->T; Ms.E = 1; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
+        Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
+        if ((rc = moe_launch(c, Ms, sg->T.nunits))) return rc;
+    }
+    memset(&Mr, 0, sizeof Mr);
+    if ((rc = moe_prep(c, 1, h, P, I, Mr.a))) return rc;
+    max_units(down, Mr.tpe, units);
+    Mr.ta = (const BglDevTensor *)down->dev_table; Mr.E = E; Mr.off = S.off; Mr.y = dd; Mr.ystride = H;
+    if ((rc = moe_launch(c, Mr, units))) return rc;
+    if (nsh) {
+        memset(&Ms, 0, sizeof Ms);
+        if ((rc = moe_prep(c, 0, shh, T, Ish, Ms.a))) return rc;
+        Ms.da = sd->T; Ms.E = 1; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
+        if ((rc = moe_launch(c, Ms, sd->T.nunits))) return rc;
+    }
+    int tok = prof_begin(c, 2);
+    hipLaunchKernelGGL(k_moe_combine, dim3(nblk((long)T * H)), dim3(256), 0, c->stream, dd, S.pos, idx_dev, w_dev, T, K, H,
+                       nsh ? sdd : nullptr, out_dev);
+    prof_end(c, tok);
+    HIPCHK(hipGetLastError());
+    return 0;
 }

@@ -223,3 +223,47 @@ class OrExpert(C.Structure):
 
 def expert_struct(kind, bits, packed, scales):
     return OrExpert(kind, bits, packed.ctypes.data, scales.ctypes.data)
+
+
+def expert_array(descs):
+    """descs: list of (kind, bits, packed, scales) -> (OrExpert array, keep-alive list)."""
+    arr = (OrExpert * len(descs))()
+    keep = []
+    for e, (kind, bits, pk, sc) in enumerate(descs):
+        pk = np.ascontiguousarray(pk); sc = np.ascontiguousarray(sc)
+        keep += [pk, sc]
+        arr[e] = OrExpert(kind, bits, pk.ctypes.data, sc.ctypes.data)
+    return arr, keep
+
+
+def moe_matvec(oracle, desc, out, inn, x):
+    """or_moe_matvec (qwen_infer.c:3223-3225) for one expert descriptor and one activation row."""
+    arr, keep = expert_array([desc])
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(out, np.float32)
+    oracle.lib.or_moe_matvec(arr, out, inn, _ptr(x), _ptr(y))
+    return y
+
+
+def moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w, naive=False):
+    """or_moe_ffn_bucketed / or_moe_ffn_naive with routing given.  gate/up/down: per-expert
+    descriptor lists; shared: (sg, su, sd) descriptors or None."""
+    E = len(gate)
+    ga, k1 = expert_array(gate)
+    ua, k2 = expert_array(up)
+    da, k3 = expert_array(down)
+    if shared is not None:
+        sa, k4 = expert_array(list(shared))
+        sg, su, sd = C.byref(sa, 0), C.byref(sa, C.sizeof(OrExpert)), C.byref(sa, 2 * C.sizeof(OrExpert))
+        Ish = shared[0][2].shape[0]
+    else:
+        sg = su = sd = None
+        Ish = 0
+    x = np.ascontiguousarray(x, np.float32)
+    idx = np.ascontiguousarray(idx, np.int32)
+    w = np.ascontiguousarray(w, np.float32)
+    T, K = idx.shape
+    out = np.zeros((T, H), np.float32)
+    fn = oracle.lib.or_moe_ffn_naive if naive else oracle.lib.or_moe_ffn_bucketed
+    fn(ga, ua, da, E, sg, su, sd, H, I, Ish, T, K, _ptr(x), _ptr(idx), _ptr(w), _ptr(out))
+    return out

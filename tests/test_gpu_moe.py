@@ -1,0 +1,302 @@
+"""GPU parity of the expert-sorted MoE gather against the CPU oracle, through the C-ABI.
+
+* bgl_gather_matvec_dev: explicit (x, expert) pairs (ffn_gather / mlx_gpu_qng64_gather_probe,
+  mlx_moe.h:89-91) against or_moe_matvec per pair, every expert format, mixed formats, the
+  GATE9 fixture (qwen_infer.c:10811-10875), ids outside [0, E) skipped.
+* bgl_moe_ffn_dev: the routed SwiGLU FFN with shared experts (moe_ffn_batched,
+  qwen_infer.c:5238-5350) against or_moe_ffn_bucketed, routing from or_moe_route, at small sizes
+  and at DeepSeek-V2-Lite's shape; graph replay; error paths.
+Bar: max|y - ref| / max|ref| <= 1e-5 (fp32 arithmetic, summation order differs)."""
+import sys
+
+import numpy as np
+import pytest
+
+from golden.fixtures import gate9, seeded_normal
+from oracle_ffi import moe_ffn, moe_matvec
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "gpu tests need a GPU"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ctx(torch_dev):
+    import beglin_amd
+    c = beglin_amd.Context(0)
+    yield c
+    c.sync()
+    c.close()
+
+
+def relerr(y, r):
+    y = np.asarray(y, np.float64); r = np.asarray(r, np.float64)
+    return float(np.max(np.abs(y - r)) / max(np.max(np.abs(r)), 1e-30))
+
+
+def weights(seed, out, inn, sigma=0.02):
+    w = seeded_normal(seed, (out, inn), sigma)
+    w[np.random.default_rng(seed + 1).random(w.shape) < 0.01] *= 8
+    return w
+
+
+def desc(oracle, kind, bits, w):
+    """Reference-layout expert descriptor (kind, bits, packed, scales) from the oracle packers."""
+    if kind == 1:
+        p, s = oracle.quantize_q4g64(w)
+    elif kind == 2:
+        p, s = oracle.quantize_q8g64(w)
+    elif kind == 4:
+        p, s = oracle.quantize_qng64(w, bits)
+    else:
+        p, s = oracle.quantize_q4g32h(w)
+    return (kind, bits, p, s)
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+FORMATS = [(5, 0), (1, 0), (2, 0), (4, 2), (4, 3), (4, 5), (4, 7), (4, 8), (4, 9), (4, 12), (4, 15)]
+
+
+@pytest.mark.parametrize("kind,bits", FORMATS)
+def test_gather_matvec_parity(ctx, torch_dev, oracle, kind, bits):
+    torch = torch_dev
+    E, out, inn, N = 6, 160, 512, 13
+    say("gather", kind, bits, E, out, inn, N)
+    ds = [desc(oracle, kind, bits, weights(1000 + 10 * e + bits, out, inn)) for e in range(E)]
+    idx = np.random.default_rng(7).integers(0, E, N).astype(np.int32)
+    idx[idx == 4] = 5                                   # one expert with no pair
+    x = seeded_normal(8, (N, inn))
+    ex = ctx.bind_experts(ds)
+    y = torch.full((N, out), 7.0, dtype=torch.float32, device="cuda")
+    ctx.gather_matvec(ex, dev(torch, x), dev(torch, idx), y)
+    ctx.sync()
+    ref = np.stack([moe_matvec(oracle, ds[idx[z]], out, inn, x[z]) for z in range(N)])
+    assert relerr(y.cpu().numpy(), ref) <= TOL
+    ex.free()
+
+
+def test_gather_mixed_formats(ctx, torch_dev, oracle):
+    torch = torch_dev
+    fm = [(5, 0), (2, 0), (4, 7), (4, 15), (1, 0), (4, 2), (5, 0), (4, 10)]
+    E, out, inn, N = len(fm), 200, 768, 41
+    say("gather mixed", E, out, inn, N)
+    ds = [desc(oracle, k, b, weights(2000 + e, out, inn)) for e, (k, b) in enumerate(fm)]
+    idx = np.random.default_rng(9).integers(0, E, N).astype(np.int32)
+    x = seeded_normal(10, (N, inn))
+    ex = ctx.bind_experts(ds)
+    y = torch.zeros((N, out), dtype=torch.float32, device="cuda")
+    ctx.gather_matvec(ex, dev(torch, x), dev(torch, idx), y)
+    ctx.sync()
+    ref = np.stack([moe_matvec(oracle, ds[idx[z]], out, inn, x[z]) for z in range(N)])
+    assert relerr(y.cpu().numpy(), ref) <= TOL
+    info = ex.info()
+    assert info["out"] == out and info["inn"] == inn and info["kind"] == 0
+    ex.free()
+
+
+def test_gate9_gather(ctx, torch_dev, oracle):
+    """GATE9 (qwen_infer.c:10811-10875): E=4, out=8, in=128, n=7, pairs {0,3,1,2,0,3}."""
+    torch = torch_dev
+    g = gate9()
+    say("gate9")
+    ds = [(4, 7) + oracle.quantize_qng64_gguf(g["w"][e], 7) for e in range(g["E"])]
+    ex = ctx.bind_experts(ds)
+    y = torch.zeros((len(g["idx"]), g["out"]), dtype=torch.float32, device="cuda")
+    ctx.gather_matvec(ex, dev(torch, g["x"]), dev(torch, g["idx"]), y)
+    ctx.sync()
+    ref = np.stack([moe_matvec(oracle, ds[e], g["out"], g["inn"], g["x"][z]) for z, e in enumerate(g["idx"])])
+    assert relerr(y.cpu().numpy(), ref) <= TOL
+    ex.free()
+
+
+def test_gather_invalid_ids_skipped(ctx, torch_dev, oracle):
+    torch = torch_dev
+    E, out, inn = 3, 64, 256
+    say("gather invalid ids")
+    ds = [desc(oracle, 5, 0, weights(3000 + e, out, inn)) for e in range(E)]
+    idx = np.array([0, -1, 2, 3, 1, 2], np.int32)
+    x = seeded_normal(11, (len(idx), inn))
+    ex = ctx.bind_experts(ds)
+    y = torch.full((len(idx), out), 3.5, dtype=torch.float32, device="cuda")
+    ctx.gather_matvec(ex, dev(torch, x), dev(torch, idx), y)
+    ctx.sync()
+    yh = y.cpu().numpy()
+    assert np.all(yh[1] == 3.5) and np.all(yh[3] == 3.5)
+    for z in (0, 2, 4, 5):
+        assert relerr(yh[z], moe_matvec(oracle, ds[idx[z]], out, inn, x[z])) <= TOL
+    ex.free()
+
+
+def moe_setup(oracle, seed, E, H, I, Ish, fmts, down_fmts=None, sh_fmt=(5, 0)):
+    gate = [desc(oracle, *fmts[e % len(fmts)], weights(seed + 3 * e, I, H)) for e in range(E)]
+    up = [desc(oracle, *fmts[e % len(fmts)], weights(seed + 3 * e + 1, I, H)) for e in range(E)]
+    dfm = down_fmts or fmts
+    down = [desc(oracle, *dfm[e % len(dfm)], weights(seed + 3 * e + 2, H, I)) for e in range(E)]
+    shared = None
+    if Ish:
+        shared = (desc(oracle, *sh_fmt, weights(seed + 900, Ish, H)), desc(oracle, *sh_fmt, weights(seed + 901, Ish, H)),
+                  desc(oracle, *sh_fmt, weights(seed + 902, H, Ish)))
+    return gate, up, down, shared
+
+
+def run_moe(ctx, torch, gate, up, down, shared, x, idx, w):
+    g, u, d = ctx.bind_experts(gate), ctx.bind_experts(up), ctx.bind_experts(down)
+    sh = None
+    if shared:
+        sh = tuple(ctx.bind(k, p, s, p.shape[0], s.shape[1] * (32 if k == 5 else 64), bits=b) for (k, b, p, s) in shared)
+    out = torch.zeros((x.shape[0], x.shape[1]), dtype=torch.float32, device="cuda")
+    ctx.moe_ffn(g, u, d, sh, dev(torch, x), dev(torch, idx), dev(torch, w), out)
+    ctx.sync()
+    res = out.cpu().numpy()
+    for t in (g, u, d) + (sh or ()):
+        t.free()
+    return res
+
+
+@pytest.mark.parametrize("T,Ish,renorm", [(1, 384, False), (5, 0, True), (33, 384, True), (64, 128, False)])
+def test_moe_ffn_parity(ctx, torch_dev, oracle, T, Ish, renorm):
+    torch = torch_dev
+    E, H, I, K = 16, 256, 192, 4
+    say("moe_ffn", T, Ish, renorm)
+    gate, up, down, shared = moe_setup(oracle, 4000 + T, E, H, I, Ish, [(5, 0)])
+    x = seeded_normal(50 + T, (T, H))
+    idx, w = oracle.route(seeded_normal(60 + T, (T, E)), K, renorm)
+    got = run_moe(ctx, torch, gate, up, down, shared, x, idx, w)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    assert relerr(got, ref) <= TOL
+
+
+def test_moe_ffn_mixed_precision(ctx, torch_dev, oracle):
+    """Per-expert precision as the mixed-precision registration allows (q4g32h, int8, qNg64)."""
+    torch = torch_dev
+    E, H, I, K, T, Ish = 12, 320, 256, 3, 9, 256
+    say("moe_ffn mixed", E, H, I, K, T)
+    fm = [(5, 0), (2, 0), (4, 7), (4, 9), (4, 11), (4, 15)]
+    gate, up, down, shared = moe_setup(oracle, 5000, E, H, I, Ish, fm, down_fmts=fm[::-1], sh_fmt=(2, 0))
+    x = seeded_normal(70, (T, H))
+    idx, w = oracle.route(seeded_normal(71, (T, E)), K, True)
+    got = run_moe(ctx, torch, gate, up, down, shared, x, idx, w)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    assert relerr(got, ref) <= TOL
+    naive = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w, naive=True)
+    assert relerr(got, naive) <= TOL
+
+
+def test_moe_ffn_deepseek_v2_lite_shape(ctx, torch_dev, oracle):
+    """DeepSeek-V2-Lite routed layer: E=64, hidden 2048, expert inter 1408, top-6, 2 shared
+    experts (inter 2816); experts quantized on the device, mixed per-expert precision."""
+    torch = torch_dev
+    E, H, I, K, T, Ish = 64, 2048, 1408, 6, 8, 2816
+    say("moe_ffn dsv2-lite", E, H, I, K, T)
+    fm = [(5, 0), (2, 0), (4, 7), (4, 9), (4, 12), (4, 15)]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(123)
+    descs = {"gate": [], "up": [], "down": []}
+    tens = {"gate": [], "up": [], "down": []}
+    for e in range(E):
+        k, b = fm[e % len(fm)]
+        for name, (o, i) in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I))):
+            wd = torch.randn((o, i), generator=gen, device="cuda") * 0.02
+            t, (p, s, _) = ctx.quantize(k, wd, bits=b, want_ref=True)
+            descs[name].append((k, b, p, s))
+            tens[name].append(t)
+            del wd
+    sh_d, sh_t = [], []
+    for (o, i) in ((Ish, H), (Ish, H), (H, Ish)):
+        wd = torch.randn((o, i), generator=gen, device="cuda") * 0.02
+        t, (p, s, _) = ctx.quantize(5, wd, want_ref=True)
+        sh_d.append((5, 0, p, s)); sh_t.append(t)
+    g = ctx.experts_from_tensors(tens["gate"])
+    u = ctx.experts_from_tensors(tens["up"])
+    d = ctx.experts_from_tensors(tens["down"])
+    x = seeded_normal(80, (T, H))
+    idx, w = oracle.route(seeded_normal(81, (T, E)), K, False)
+    out = torch.zeros((T, H), dtype=torch.float32, device="cuda")
+    ctx.moe_ffn(g, u, d, tuple(sh_t), dev(torch, x), dev(torch, idx), dev(torch, w), out)
+    ctx.sync()
+    ref = moe_ffn(oracle, descs["gate"], descs["up"], descs["down"], tuple(sh_d), H, I, x, idx, w)
+    assert relerr(out.cpu().numpy(), ref) <= TOL
+    for t in [g, u, d] + sh_t:
+        t.free()
+
+
+def test_moe_graph_replays_match_eager(ctx, torch_dev, oracle):
+    import beglin_amd
+    torch = torch_dev
+    E, H, I, K, T, Ish = 8, 256, 128, 2, 6, 128
+    say("moe graph")
+    gate, up, down, shared = moe_setup(oracle, 6000, E, H, I, Ish, [(5, 0), (4, 9)])
+    x = dev(torch, seeded_normal(90, (T, H)))
+    idx_h, w_h = oracle.route(seeded_normal(91, (T, E)), K, True)
+    idx, w = dev(torch, idx_h), dev(torch, w_h)
+    s = torch.cuda.Stream()
+    gc = beglin_amd.Context(0, stream=s.cuda_stream)
+    g, u, d = gc.bind_experts(gate), gc.bind_experts(up), gc.bind_experts(down)
+    sh = tuple(gc.bind(k, p, sc, p.shape[0], sc.shape[1] * (32 if k == 5 else 64), bits=b) for (k, b, p, sc) in shared)
+    out = torch.zeros((T, H), dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(s):
+        gc.moe_ffn(g, u, d, sh, x, idx, w, out)          # eager call sizes every scratch buffer
+    gc.sync()
+    eager = out.cpu().numpy().copy()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        gc.moe_ffn(g, u, d, sh, x, idx, w, out)
+    for r in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager), f"replay {r}"
+        with torch.cuda.stream(s):
+            gc.moe_ffn(g, u, d, sh, x, idx, w, out)       # eager work between replays
+        gc.sync()
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x.cpu().numpy(), idx_h, w_h)
+    assert relerr(eager, ref) <= TOL
+    for t in (g, u, d) + sh:
+        t.free()
+    gc.close()
+
+
+def test_moe_error_paths(ctx, torch_dev, oracle):
+    import beglin_amd
+    torch = torch_dev
+    E, H, I = 4, 128, 64
+    gate, up, down, shared = moe_setup(oracle, 7000, E, H, I, 64, [(5, 0)])
+    g, u, d = ctx.bind_experts(gate), ctx.bind_experts(up), ctx.bind_experts(down)
+    x = torch.zeros((2, H), device="cuda")
+    out = torch.zeros((2, H), device="cuda")
+    idx17 = torch.zeros((2, 17), dtype=torch.int32, device="cuda")
+    w17 = torch.zeros((2, 17), device="cuda")
+    with pytest.raises(beglin_amd.BglError):
+        ctx.moe_ffn(g, u, d, None, x, idx17, w17, out)                 # top-K above 16
+    idx = torch.zeros((2, 2), dtype=torch.int32, device="cuda")
+    w = torch.zeros((2, 2), device="cuda")
+    with pytest.raises(beglin_amd.BglError):
+        ctx.moe_ffn(g, d, d, None, x, idx, w, out)                     # up shaped like down
+    single = ctx.bind(*gate[0][:1], gate[0][2], gate[0][3], I, H)
+    with pytest.raises(beglin_amd.BglError):
+        ctx.moe_ffn(single, u, d, None, x, idx, w, out)               # not an expert stack
+    with pytest.raises(beglin_amd.BglError):
+        ctx.moe_ffn(g, u, d, (single, None, None), x, idx, w, out)    # partial shared set
+    wg = weights(7100, 64, 256)
+    p, sc, sub = oracle.quantize_g256sf(wg)
+    t256 = ctx.bind(3, p, sc, 64, 256, sub=sub)
+    with pytest.raises(beglin_amd.BglError):
+        ctx.experts_from_tensors([t256])                              # W4A8-only format
+    ctx.sync()
+    for t in (g, u, d, single, t256):
+        t.free()

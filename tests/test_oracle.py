@@ -406,3 +406,51 @@ def test_moe_row_equals_decoded_double_dot(oracle):
         y = np.array([oracle.lib.or_moe_row(C.byref(ex), 256, C.c_long(r), _ptr(x)) for r in range(16)])
         d = oracle.decode(kind, p, s, 16, 256, bits=bits).astype(np.float64)
         assert np.allclose(y, d @ x.astype(np.float64), rtol=0, atol=1e-12)
+
+
+def test_moe_ffn_equals_decoded_pipeline(oracle):
+    """The FFN oracle (through the tests' moe_ffn helper) against a dense float64 pipeline over
+    weights decoded by or_decode: pins the plumbing (token rows, expert ids, routing weights,
+    shared expert added once per token) independently of or_moe_row's per-format decode."""
+    from oracle_ffi import moe_ffn
+    E, H, I, Ish, K, T = 6, 128, 64, 128, 2, 5
+    fm = [(5, 0), (2, 0), (4, 9)]
+
+    def mk(e, out, inn, s):
+        k, b = fm[e % 3]
+        w = seeded_normal(s, (out, inn), 0.02)
+        if k == 5:
+            p, sc = oracle.quantize_q4g32h(w)
+        elif k == 2:
+            p, sc = oracle.quantize_q8g64(w)
+        else:
+            p, sc = oracle.quantize_qng64_dense(w, b)
+        return (k, b if k == 4 else (8 if k == 2 else 4), p, sc)
+
+    gate = [mk(e, I, H, 300 + 3 * e) for e in range(E)]
+    up = [mk(e, I, H, 301 + 3 * e) for e in range(E)]
+    down = [mk(e, H, I, 302 + 3 * e) for e in range(E)]
+    shared = (mk(1, Ish, H, 400), mk(1, Ish, H, 401), mk(1, H, Ish, 402))
+    x = seeded_normal(403, (T, H))
+    idx, w = oracle.route(seeded_normal(404, (T, E)), K, True)
+    got = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+
+    def dec(d, out, inn):
+        return oracle.decode(d[0], d[2], d[3], out, inn, bits=d[1]).astype(np.float64)
+
+    def mlp(g, u, dn, inter, xt):
+        a = dec(g, inter, H) @ xt
+        b = dec(u, inter, H) @ xt
+        return dec(dn, H, inter) @ (a / (1.0 + np.exp(-a)) * b)
+
+    want = np.zeros((T, H))
+    for t in range(T):
+        xt = x[t].astype(np.float64)
+        for k in range(K):
+            e = idx[t, k]
+            want[t] += float(w[t, k]) * mlp(gate[e], up[e], down[e], I, xt)
+        want[t] += mlp(*shared, Ish, xt)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+    # dropping the shared expert or one routed pair moves the result far outside that bar
+    no_sh = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
+    assert np.max(np.abs(no_sh - want)) > 1e-3 * np.max(np.abs(want))
