@@ -7,7 +7,8 @@ stream.  Every call goes through the HIP library; if it is not built, importing 
 import ctypes as C
 
 from . import capi
-from .capi import ACT_F32, ACT_W4A8, K_Q4G32H, K_Q4G64, K_Q4G256SF, K_Q8G64, K_QNG64  # noqa: F401
+from .capi import (ACT_F32, ACT_W4A8, K_F16, K_F32, K_Q4G32H, K_Q4G64, K_Q4G64A, K_Q4G256SF,  # noqa: F401
+                   K_Q8G64, K_QNG64)
 
 _lib = None
 
@@ -96,9 +97,11 @@ class Context:
 
     # ---- binding ----
     def bind(self, kind, packed, scales, out, inn, bits=0, sub=None):
-        """Bind host (numpy) buffers in the reference layout."""
+        """Bind host (numpy) buffers in the reference layout (sub: g256sf sub-codes or Q4G64A biases;
+        scales None for the dense kinds)."""
         w = capi.bgl_wt(kind, bits if kind == K_QNG64 else (8 if kind == K_Q8G64 else 4), out, inn,
-                        packed.ctypes.data, scales.ctypes.data, sub.ctypes.data if sub is not None else None)
+                        packed.ctypes.data, scales.ctypes.data if scales is not None else None,
+                        sub.ctypes.data if sub is not None else None)
         h = C.c_void_p()
         _check(lib().bgl_bind(self.h, C.byref(w), C.byref(h)), "bgl_bind")
         return Tensor(h)
@@ -162,14 +165,21 @@ class Context:
 
     # ---- MoE ----
     def bind_experts(self, descs):
-        """descs: list of (kind, bits, packed, scales) numpy tuples, one per expert."""
+        """descs: list of (kind, bits, packed, scales[, bias]) numpy tuples, one per expert; packed is
+        2-D [out][row bytes or elements]; scales None for the dense kinds."""
         E = len(descs)
         arr = (capi.bgl_wt * E)()
-        for e, (kind, bits, pk, sc) in enumerate(descs):
+        for e, d in enumerate(descs):
+            kind, bits, pk, sc = d[:4]
+            bi = d[4] if len(d) > 4 else None
             out = pk.shape[0]
-            inn = sc.shape[1] * (32 if kind == K_Q4G32H else 64)
+            if kind in (K_F16, K_F32):
+                inn = pk.shape[1]
+            else:
+                inn = sc.shape[1] * (32 if kind == K_Q4G32H else 64)
             b = bits if kind == K_QNG64 else (8 if kind == K_Q8G64 else 4)
-            arr[e] = capi.bgl_wt(kind, b, out, inn, pk.ctypes.data, sc.ctypes.data, None)
+            arr[e] = capi.bgl_wt(kind, b, out, inn, pk.ctypes.data, sc.ctypes.data if sc is not None else None,
+                                 bi.ctypes.data if bi is not None else None)
         h = C.c_void_p()
         _check(lib().bgl_bind_experts(self.h, E, arr, C.byref(h)), "bgl_bind_experts")
         return Tensor(h)
@@ -195,3 +205,61 @@ class Context:
         _check(lib().bgl_moe_ffn_dev(self.h, gate.h, up.h, down.h, sg.h if sg else None, su.h if su else None,
                                      sd.h if sd else None, _p(x_dev), _p(idx_dev), _p(w_dev), T, K, _p(out_dev)),
                "bgl_moe_ffn_dev")
+
+
+# ---- the name-keyed registry (mlx_moe.h boundary): thin wrappers, 1 = ok / 0 = failure ----
+class Registry:
+    """bgl_gpu_* entry points with numpy host buffers."""
+
+    @staticmethod
+    def L():
+        return lib()
+
+    def available(self):
+        return lib().bgl_gpu_available()
+
+    def bind_af(self, blob, name, E, out, inn, ng, packed_off, scale_off, bias_off, bits):
+        return lib().bgl_gpu_bind_af(blob.ctypes.data, blob.nbytes, name.encode(), E, out, inn, ng, packed_off,
+                                     scale_off, bias_off, bits)
+
+    def binding_kind(self, name):
+        b = C.c_int()
+        k = lib().bgl_gpu_binding_kind(name.encode(), C.byref(b))
+        return k, b.value
+
+    def snapshot(self, name):
+        sid = C.c_uint64()
+        ok = lib().bgl_gpu_snapshot_binding(name.encode(), C.byref(sid))
+        return ok, sid.value
+
+    def dequant_probe(self, name, e, row, col0, ncols):
+        import numpy as np
+        out = np.zeros(ncols, np.float32)
+        ok = lib().bgl_gpu_dequant_probe(name.encode(), e, row, col0, ncols, out.ctypes.data)
+        return ok, out
+
+    def matvec_probe(self, name, e, x, out):
+        import numpy as np
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(out, np.float32)
+        ok = lib().bgl_gpu_matvec_probe(name.encode(), e, x.ctypes.data, y.ctypes.data)
+        return ok, y
+
+    def ffn_gather(self, name, x, idx, out):
+        import numpy as np
+        x = np.ascontiguousarray(x, np.float32)
+        idx = np.ascontiguousarray(idx, np.int32)
+        y = np.zeros((x.shape[0], out), np.float32)
+        ok = lib().bgl_gpu_ffn_gather(name.encode(), x.ctypes.data, x.shape[0], idx.ctypes.data, y.ctypes.data)
+        return ok, y
+
+    def moe_ffn(self, gate, up, down, shared, x, idx, w):
+        import numpy as np
+        x = np.ascontiguousarray(x, np.float32)
+        idx = np.ascontiguousarray(idx, np.int32)
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.zeros_like(x)
+        sg, su, sd = [s.encode() if s else None for s in (shared or (None, None, None))]
+        ok = lib().bgl_gpu_moe_ffn(gate.encode(), up.encode(), down.encode(), sg, su, sd, x.ctypes.data, x.shape[0],
+                                   idx.ctypes.data, w.ctypes.data, idx.shape[1], out.ctypes.data)
+        return ok, out

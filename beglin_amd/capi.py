@@ -10,10 +10,12 @@ LIB_PATH = os.path.join(HERE, "libbeglin_hip.so")
 
 # mirrors of the header's enums
 K_Q4G64, K_Q8G64, K_Q4G256SF, K_QNG64, K_Q4G32H = 1, 2, 3, 4, 5
+K_Q4G64A, K_F16, K_F32 = 6, 7, 8
 ACT_F32, ACT_W4A8 = 0, 1
 
 _P = C.c_void_p
 _I = C.c_int
+_L = C.c_long
 
 
 class bgl_wt(C.Structure):
@@ -42,7 +44,10 @@ SIGNATURES = [
     ("bgl_matmul_prepped_dev", _I, [_P, _P, _I, _P, _P, _I]),
     ("bgl_quant_act_i8_dev", _I, [_P, _P, _I, _I, _I, _P, _P]),
     ("bgl_gemv_q4g64_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+    ("bgl_gemv_q4g64_mt_fused", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
     ("bgl_gemv_q4g64_sdot_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
+    ("bgl_gemm_qXg64_sdot_mt", _I, [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
+    ("bgl_gemm_q4g256sf_sdot_mt", _I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
     ("bgl_gemv_q8g64_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
     ("bgl_gemv_q8g64_sdot_mt", _I, [_P, _P, _P, _P, _P, _P, _I, _I]),
     ("bgl_gemm_qXg64_mt", _I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _I]),
@@ -56,6 +61,29 @@ SIGNATURES = [
     ("bgl_experts_from_tensors", _I, [_P, _I, C.POINTER(_P), C.POINTER(_P)]),
     ("bgl_gather_matvec_dev", _I, [_P, _P, _P, _P, _I, _P]),
     ("bgl_moe_ffn_dev", _I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
+    # name-keyed registry (mlx_moe.h boundary)
+    ("bgl_gpu_available", _I, []),
+    ("bgl_gpu_synchronize", _I, []),
+    ("bgl_gpu_reset_runtime_epoch", _I, []),
+    ("bgl_gpu_bind_af", _I, [_P, _L, C.c_char_p, _L, _L, _L, _L, _L, _L, _L, _I]),
+    ("bgl_gpu_binding_kind", _I, [C.c_char_p, C.POINTER(_I)]),
+    ("bgl_gpu_snapshot_binding", _I, [C.c_char_p, C.POINTER(C.c_uint64)]),
+    ("bgl_gpu_restore_binding_snapshot", _I, [C.c_uint64]),
+    ("bgl_gpu_drop_binding_snapshot", _I, [C.c_uint64]),
+    ("bgl_gpu_binding_snapshot_count", _I, []),
+    ("bgl_gpu_zerocopy_count", _I, [C.POINTER(_I), C.POINTER(_I), C.POINTER(C.c_size_t)]),
+    ("bgl_gpu_dequant_probe", _I, [C.c_char_p, _L, _L, _L, _I, _P]),
+    ("bgl_gpu_qng64_gather_probe", _I, [_P, _L, _L, _L, _L, _I, _P, _P, _I, _P, _P]),
+    ("bgl_gpu_bind_qng64_dense_probe", _I, [_P, _P, C.c_char_p, _L, _L, _I]),
+    ("bgl_gpu_matvec_probe", _I, [C.c_char_p, _L, _P, _P]),
+    ("bgl_gpu_report_memory", None, [C.POINTER(C.c_size_t)] * 3),
+    ("bgl_gpu_set_batch", _I, [_I]),
+    ("bgl_gpu_set_sort_threshold", _I, [_I]),
+    ("bgl_gpu_test_ffn_uniform", _I, [C.c_char_p] * 3),
+    ("bgl_gpu_ffn_gather", _I, [C.c_char_p, _P, _I, _P, _P]),
+    ("bgl_gpu_moe_ffn", _I, [C.c_char_p] * 6 + [_P, _I, _P, _P, _I, _P]),
+    ("bgl_gpu_context", _P, []),
+    ("bgl_gpu_lookup", _P, [C.c_char_p]),
 ]
 
 

@@ -61,6 +61,18 @@ static void dbuf_free(DevBuf &b) {
     b.p = nullptr; b.bytes = 0;
 }
 
+size_t ctx_scratch(bgl_ctx *c, bool release) {
+    DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->part, &c->hx, &c->hy, &c->hb,
+                      &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_e, &c->moe_f, &c->moe_g, &c->moe_meta};
+    size_t total = 0;
+    for (DevBuf *b : bufs) {
+        total += b->bytes;
+        if (release) dbuf_free(*b);
+    }
+    if (release) { c->prep_act = -1; c->prep_M = 0; c->prep_K = 0; }
+    return total;
+}
+
 extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     if (!out) return bgl_fail(BGL_E_ARG, "bgl_ctx_create: out is NULL");
     int n = 0;
@@ -149,9 +161,7 @@ extern "C" void bgl_ctx_destroy(bgl_ctx *c) {
     for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
     for (auto &kv : c->host_cache) bgl_tensor_free(kv.second);
     c->host_cache.clear();
-    DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->part, &c->hx, &c->hy, &c->hb,
-                      &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_e, &c->moe_f, &c->moe_g, &c->moe_meta};
-    for (DevBuf *b : bufs) dbuf_free(*b);
+    ctx_scratch(c, true);
     if (c->own_stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -167,7 +177,7 @@ extern "C" void *bgl_ctx_stream(bgl_ctx *c) { return c ? (void *)c->stream : nul
 // ------------------------------------------------------------------ tensors
 static int units_of(int kind, int in) {
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q8G64: return in / 64;
+    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q8G64: case BGL_Q4G64A: case BGL_F16: case BGL_F32: return in / 64;
     case BGL_Q4G256SF: return in / 256;
     case BGL_QNG64: return (in / 64 + 1) / 2;
     default: return 0;
@@ -181,8 +191,8 @@ int check_wt(int kind, int bits, int out, int in) {
         if (in % 64) return bgl_fail(BGL_E_ARG, "in=%d %% 64 != 0", in);
         if (kind == BGL_QNG64 && (bits < 2 || bits > 15)) return bgl_fail(BGL_E_ARG, "qNg64 n=%d outside 2..15", bits);
         return 0;
-    case BGL_Q4G32H:
-        if (in % 64) return bgl_fail(BGL_E_ARG, "Q4G32H in=%d %% 64 != 0", in);
+    case BGL_Q4G32H: case BGL_Q4G64A: case BGL_F16: case BGL_F32:
+        if (in % 64) return bgl_fail(BGL_E_ARG, "kind %d: in=%d %% 64 != 0", kind, in);
         return 0;
     case BGL_Q4G256SF:
         if (in % 256) return bgl_fail(BGL_E_ARG, "g256sf in=%d %% 256 != 0", in);
@@ -193,15 +203,17 @@ int check_wt(int kind, int bits, int out, int in) {
 
 static size_t ref_packed_bytes(int kind, int bits, int out, int in) {
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q4G256SF: case BGL_Q4G32H: return (size_t)out * in / 2;
+    case BGL_Q4G64: case BGL_Q4G256SF: case BGL_Q4G32H: case BGL_Q4G64A: return (size_t)out * in / 2;
     case BGL_Q8G64: return (size_t)out * in;
+    case BGL_F16: return (size_t)out * in * 2;
+    case BGL_F32: return (size_t)out * in * 4;
     case BGL_QNG64: return (size_t)out * (in / 64) * bits * 8;
     default: return 0;
     }
 }
 static size_t ref_scale_bytes(int kind, int out, int in) {
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q8G64: case BGL_QNG64: return (size_t)out * (in / 64) * 4;
+    case BGL_Q4G64: case BGL_Q8G64: case BGL_QNG64: case BGL_Q4G64A: return (size_t)out * (in / 64) * 4;
     case BGL_Q4G256SF: return (size_t)out * (in / 256) * 4;
     case BGL_Q4G32H: return (size_t)out * (in / 32) * 2;
     default: return 0;
@@ -215,18 +227,22 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
                        const uint8_t *dsub, bgl_tensor **res) {
     bgl_tensor *t = new bgl_tensor();
     BglDevTensor &T = t->T;
-    T.fmt = kind; T.bits = kind == BGL_QNG64 ? bits : (kind == BGL_Q8G64 ? 8 : 4);
+    T.fmt = kind;
+    T.bits = kind == BGL_QNG64 ? bits : kind == BGL_Q8G64 ? 8 : kind == BGL_F16 ? 16 : kind == BGL_F32 ? 32 : 4;
     T.N = out; T.K = in; T.ntiles = (out + BGL_TILE - 1) / BGL_TILE;
     T.nunits = units_of(kind, in);
-    T.cpu = kind == BGL_Q4G256SF ? 8 : kind == BGL_Q8G64 ? 4 : kind == BGL_QNG64 ? bits : 2;
+    T.cpu = kind == BGL_Q4G256SF ? 8 : kind == BGL_Q8G64 ? 4 : kind == BGL_QNG64 ? bits : kind == BGL_F16 ? 8
+          : kind == BGL_F32 ? 16 : 2;
     T.cpr = T.nunits * T.cpu;
     long rows = (long)T.ntiles * BGL_TILE;
     size_t wbytes = (size_t)rows * T.cpr * 16;
-    size_t s0bytes = (size_t)rows * T.nunits * (kind == BGL_QNG64 ? 8 : 4);
+    const bool dense = kind == BGL_F16 || kind == BGL_F32;
+    size_t s0bytes = dense ? 0 : (size_t)rows * T.nunits * (kind == BGL_QNG64 ? 8 : 4);
+    const bool has_s1 = kind == BGL_Q4G256SF || kind == BGL_Q4G64A;
     void *w = nullptr, *s0 = nullptr, *s1 = nullptr;
     hipError_t e = hipMalloc(&w, wbytes);
-    if (e == hipSuccess) e = hipMalloc(&s0, s0bytes);
-    if (e == hipSuccess && kind == BGL_Q4G256SF) e = hipMalloc(&s1, (size_t)rows * T.nunits * 4);
+    if (e == hipSuccess && s0bytes) e = hipMalloc(&s0, s0bytes);
+    if (e == hipSuccess && has_s1) e = hipMalloc(&s1, (size_t)rows * T.nunits * 4);
     if (e != hipSuccess) {
         if (w) (void)hipFree(w);
         if (s0) (void)hipFree(s0);
@@ -238,11 +254,12 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     t->device_bytes = wbytes + s0bytes + (s1 ? (size_t)rows * T.nunits * 4 : 0);
     long nch = rows * T.cpr;
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q4G256SF:
+    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q4G256SF: case BGL_Q4G64A:
         hipLaunchKernelGGL(k_repack_nib, dim3(nblk(nch)), dim3(256), 0, c->stream, (const uint8_t *)dpk, out, in, (uint8_t *)w);
         break;
-    case BGL_Q8G64:
-        hipLaunchKernelGGL(k_repack_q8, dim3(nblk(nch)), dim3(256), 0, c->stream, (const int8_t *)dpk, out, in, (uint8_t *)w);
+    case BGL_Q8G64: case BGL_F16: case BGL_F32:      // plain 16-byte chunk interleave of the row bytes
+        hipLaunchKernelGGL(k_repack_q8, dim3(nblk(nch)), dim3(256), 0, c->stream, (const int8_t *)dpk, out,
+                           in * (kind == BGL_F16 ? 2 : kind == BGL_F32 ? 4 : 1), (uint8_t *)w);
         break;
     case BGL_QNG64:
         hipLaunchKernelGGL(k_repack_qng, dim3(nblk(rows * T.nunits, 64)), dim3(64), 0, c->stream, (const uint8_t *)dpk, out, in, bits, (uint8_t *)w);
@@ -250,10 +267,10 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     }
     long nu = rows * T.nunits;
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q8G64: case BGL_Q4G32H: case BGL_Q4G256SF:
+    case BGL_Q4G64: case BGL_Q8G64: case BGL_Q4G32H: case BGL_Q4G256SF: case BGL_Q4G64A:
         // Q4G32H: two fp16 per unit read as one u32; the others one fp32 per unit.
         hipLaunchKernelGGL(k_repack_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsc, out, T.nunits, (uint32_t *)s0);
-        if (kind == BGL_Q4G256SF)
+        if (has_s1)   // g256sf: 4 sub-codes per unit; Q4G64A: the fp32 bias per unit
             hipLaunchKernelGGL(k_repack_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsub, out, T.nunits, (uint32_t *)s1);
         break;
     case BGL_QNG64:
@@ -267,19 +284,23 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
 }
 
 extern "C" int bgl_bind(bgl_ctx *c, const bgl_wt *w, bgl_tensor **out) {
-    if (!c || !w || !out || !w->packed || !w->scales) return bgl_fail(BGL_E_ARG, "bgl_bind: NULL argument");
+    if (!c || !w || !out || !w->packed) return bgl_fail(BGL_E_ARG, "bgl_bind: NULL argument");
     int rc = check_wt(w->kind, w->bits, w->out, w->in);
     if (rc) return rc;
+    const bool dense = w->kind == BGL_F16 || w->kind == BGL_F32;
+    if (!dense && !w->scales) return bgl_fail(BGL_E_ARG, "bgl_bind: kind %d needs scales", w->kind);
     if (w->kind == BGL_Q4G256SF && !w->sub) return bgl_fail(BGL_E_ARG, "bgl_bind: g256sf needs sub-codes");
+    if (w->kind == BGL_Q4G64A && !w->sub) return bgl_fail(BGL_E_ARG, "bgl_bind: int4 affine needs biases (sub)");
     HIPCHK(hipSetDevice(c->device));
     size_t pb = ref_packed_bytes(w->kind, w->bits, w->out, w->in), sb = ref_scale_bytes(w->kind, w->out, w->in);
-    size_t subb = w->kind == BGL_Q4G256SF ? (size_t)w->out * (w->in / 64) : 0;
+    size_t subb = w->kind == BGL_Q4G256SF ? (size_t)w->out * (w->in / 64)
+                : w->kind == BGL_Q4G64A ? (size_t)w->out * (w->in / 64) * 4 : 0;
     void *dpk = nullptr, *dsc = nullptr, *dsub = nullptr;
     HIPCHK(hipMalloc(&dpk, pb));
-    HIPCHK(hipMalloc(&dsc, sb));
+    if (sb) HIPCHK(hipMalloc(&dsc, sb));
     if (subb) HIPCHK(hipMalloc(&dsub, subb));
     HIPCHK(hipMemcpyAsync(dpk, w->packed, pb, hipMemcpyHostToDevice, c->stream));
-    HIPCHK(hipMemcpyAsync(dsc, w->scales, sb, hipMemcpyHostToDevice, c->stream));
+    if (sb) HIPCHK(hipMemcpyAsync(dsc, w->scales, sb, hipMemcpyHostToDevice, c->stream));
     if (subb) HIPCHK(hipMemcpyAsync(dsub, w->sub, subb, hipMemcpyHostToDevice, c->stream));
     rc = repack_into(c, w->kind, w->bits, w->out, w->in, dpk, dsc, (const uint8_t *)dsub, out);
     hipError_t e = hipStreamSynchronize(c->stream);
@@ -295,6 +316,8 @@ extern "C" int bgl_quantize_dev(bgl_ctx *c, int kind, int bits, int qng64_encode
     if (!c || !w_dev || !t) return bgl_fail(BGL_E_ARG, "bgl_quantize_dev: NULL argument");
     int rc = check_wt(kind, bits, out, in);
     if (rc) return rc;
+    if (kind == BGL_Q4G64A || kind == BGL_F16 || kind == BGL_F32)
+        return bgl_fail(BGL_E_UNSUPPORTED, "bgl_quantize_dev: kind %d has no packer here (bind its bytes with bgl_bind)", kind);
     if (kind == BGL_QNG64 && qng64_encoder && bits == 4)
         return bgl_fail(BGL_E_ARG, "qng64_quantize_f32 rejects n=4 (qng64_dense.c:9)");
     HIPCHK(hipSetDevice(c->device));
@@ -543,6 +566,8 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
             return bgl_fail(BGL_E_ARG, "bgl_matmul_group_dev: fused tensors must share kind, bits and in");
     }
     const int kind = Ts[0].fmt;
+    if (kind == BGL_Q4G64A || kind == BGL_F16 || kind == BGL_F32)
+        return bgl_fail(BGL_E_UNSUPPORTED, "kind %d runs in the MoE gather only (bgl_gather_matvec_dev / bgl_moe_ffn_dev)", kind);
     if (kind == BGL_Q4G256SF && act != BGL_ACT_W4A8)
         return bgl_fail(BGL_E_UNSUPPORTED, "K_Q4G256SF requires W4A8 activations -- no fp32-activation path exists for g256sf");
     if ((kind == BGL_Q4G32H || kind == BGL_QNG64) && act != BGL_ACT_F32)
@@ -568,6 +593,8 @@ extern "C" int bgl_prep_act_dev(bgl_ctx *c, int act, int kind, const float *x_de
 extern "C" int bgl_matmul_prepped_dev(bgl_ctx *c, const bgl_tensor *w, int act, const float *bias_dev, float *y_dev, int M) {
     if (!c || !w || !y_dev || !w->experts.empty()) return bgl_fail(BGL_E_ARG, "bgl_matmul_prepped_dev: bad argument");
     const BglDevTensor &T = w->T;
+    if (T.fmt == BGL_Q4G64A || T.fmt == BGL_F16 || T.fmt == BGL_F32)
+        return bgl_fail(BGL_E_UNSUPPORTED, "kind %d runs in the MoE gather only", T.fmt);
     if (c->prep_act != act || c->prep_K != T.K || c->prep_gq != act_group(T.fmt) || M > c->prep_M)
         return bgl_fail(BGL_E_ARG, "bgl_matmul_prepped_dev: no prepared activation matches (act %d, in %d, M %d)", act, T.K, M);
     if (T.fmt == BGL_Q4G256SF && act != BGL_ACT_W4A8)
@@ -589,8 +616,8 @@ extern "C" int bgl_matmul_dev(bgl_ctx *c, const bgl_tensor *w, int act, const fl
 }
 
 // ------------------------------------------------------------------ host-pointer drop-ins
-static int host_call(bgl_ctx *c, const bgl_wt &wt, int act, const float *x, const float *bias, float *y, int M) {
-    if (!c || !x || !y || M < 1) return bgl_fail(BGL_E_ARG, "NULL argument");
+// The device copy of a host weight, bound on first use and cached by its packed pointer.
+static int host_tensor(bgl_ctx *c, const bgl_wt &wt, bgl_tensor **res) {
     int rc = check_wt(wt.kind, wt.bits, wt.out, wt.in);
     if (rc) return rc;
     HIPCHK(hipSetDevice(c->device));
@@ -610,6 +637,15 @@ static int host_call(bgl_ctx *c, const bgl_wt &wt, int act, const float *x, cons
         std::lock_guard<std::mutex> lk(c->mu);
         c->host_cache[wt.packed] = t;
     }
+    *res = t;
+    return 0;
+}
+
+static int host_call(bgl_ctx *c, const bgl_wt &wt, int act, const float *x, const float *bias, float *y, int M) {
+    if (!c || !x || !y || M < 1) return bgl_fail(BGL_E_ARG, "NULL argument");
+    bgl_tensor *t = nullptr;
+    int rc = host_tensor(c, wt, &t);
+    if (rc) return rc;
     size_t xb = (size_t)M * wt.in * 4, yb = (size_t)M * wt.out * 4;
     if (dbuf_reserve(c, c->hx, xb, false) || dbuf_reserve(c, c->hy, yb, false) || dbuf_reserve(c, c->hb, (size_t)wt.out * 4, false))
         return BGL_E_NOMEM;
@@ -628,9 +664,57 @@ static bgl_wt mkwt(int kind, int bits, int out, int in, const void *packed, cons
     return w;
 }
 
+// Caller-quantized int8 columns (host xq / ascale) -> the W4A8 operands in the context, then the GEMV.
+static int host_call_i8(bgl_ctx *c, const bgl_wt &wt, const int8_t *xq, const float *ascale, const float *bias,
+                        float *y, int M) {
+    if (!c || !xq || !ascale || !y || M < 1 || M > 64) return bgl_fail(BGL_E_ARG, "bad argument (M=%d, 1..64)", M);
+    const int gq = wt.kind == BGL_Q4G256SF ? 256 : 64, K = wt.in;
+    if (K % gq) return bgl_fail(BGL_E_ARG, "in=%d %% %d != 0", K, gq);
+    bgl_tensor *t = nullptr;
+    int rc = host_tensor(c, wt, &t);
+    if (rc) return rc;
+    const size_t qb = (size_t)M * K, ab = (size_t)M * (K / gq) * 4, qpad = (qb + 255) & ~(size_t)255;
+    const size_t yb = (size_t)M * wt.out * 4;
+    if (dbuf_reserve(c, c->hx, qpad + ab, false) || dbuf_reserve(c, c->hy, yb, false) ||
+        dbuf_reserve(c, c->hb, (size_t)wt.out * 4, false) || dbuf_reserve(c, c->act_w, qb, false) ||
+        dbuf_reserve(c, c->act_s, ab, false) || dbuf_reserve(c, c->act_sum, (size_t)M * (K / 64) * 4, false))
+        return BGL_E_NOMEM;
+    HIPCHK(hipMemcpyAsync(c->hx.p, xq, qb, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(hipMemcpyAsync((char *)c->hx.p + qpad, ascale, ab, hipMemcpyHostToDevice, c->stream));
+    if (bias) HIPCHK(hipMemcpyAsync(c->hb.p, bias, (size_t)wt.out * 4, hipMemcpyHostToDevice, c->stream));
+    const int split = wt.kind == BGL_Q8G64 ? 0 : 1;     // q4 / g256sf callers pass q4_split_act order
+    int tok = prof_begin(c, 0);
+    hipLaunchKernelGGL(k_act_import_i8, dim3(nblk((long)M * (K / 64) * 64)), dim3(256), 0, c->stream,
+                       (const int8_t *)c->hx.p, (const float *)((char *)c->hx.p + qpad), M, K, gq, split,
+                       (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
+    prof_end(c, tok);
+    HIPCHK(hipGetLastError());
+    c->prep_act = BGL_ACT_W4A8; c->prep_gq = gq; c->prep_M = M; c->prep_K = K;
+    rc = bgl_matmul_prepped_dev(c, t, BGL_ACT_W4A8, bias ? (const float *)c->hb.p : nullptr, (float *)c->hy.p, M);
+    if (rc) return rc;
+    HIPCHK(hipMemcpyAsync(y, c->hy.p, yb, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(hipStreamSynchronize(c->stream));
+    return 0;
+}
+
 extern "C" int bgl_gemv_q4g64_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x, const float *bias,
                                  float *y, int out, int in) {
     return host_call(p, mkwt(BGL_Q4G64, 4, out, in, packed, scales, nullptr), BGL_ACT_F32, x, bias, y, 1);
+}
+extern "C" int bgl_gemv_q4g64_mt_fused(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
+                                       const float *bias, float *y, int out, int in) {
+    return host_call(p, mkwt(BGL_Q4G64, 4, out, in, packed, scales, nullptr), BGL_ACT_F32, x, bias, y, 1);
+}
+extern "C" int bgl_gemm_qXg64_sdot_mt(bgl_ctx *p, int bits, const uint8_t *packed, const float *scales, const int8_t *xq,
+                                      const float *ascale, const float *bias, float *y, int out, int in, int M) {
+    if (bits != 4 && bits != 8) return bgl_fail(BGL_E_ARG, "gemm_qXg64_sdot_mt: bits=%d (4 or 8)", bits);
+    return host_call_i8(p, mkwt(bits == 8 ? BGL_Q8G64 : BGL_Q4G64, bits, out, in, packed, scales, nullptr), xq, ascale,
+                        bias, y, M);
+}
+extern "C" int bgl_gemm_q4g256sf_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *wsuper, const uint8_t *subcode,
+                                         const int8_t *xq, const float *ascale, const float *bias, float *y, int out,
+                                         int in, int M) {
+    return host_call_i8(p, mkwt(BGL_Q4G256SF, 4, out, in, packed, wsuper, subcode), xq, ascale, bias, y, M);
 }
 extern "C" int bgl_gemv_q4g64_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x, const float *bias,
                                       float *y, int out, int in) {

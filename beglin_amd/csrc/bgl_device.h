@@ -25,6 +25,9 @@
 #define BGL_Q4G256SF BGL_K_Q4G256SF
 #define BGL_QNG64 BGL_K_QNG64
 #define BGL_Q4G32H BGL_K_Q4G32H
+#define BGL_Q4G64A BGL_K_Q4G64A
+#define BGL_F16 BGL_K_F16
+#define BGL_F32 BGL_K_F32
 
 // fp32 activations are represented exactly enough for the 1e-5 bar as X = rint(x * 2^(21-e)) per
 // 64-group (e = exponent of the group's max |x|, so |X| <= 2^21), split into three balanced

@@ -40,9 +40,12 @@ template <int NB> struct Raw<BGL_Q4G32H, NB> { uint4 c[2]; uint32_t s; };
 template <int NB> struct Raw<BGL_Q4G256SF, NB> { uint4 c[8]; float s; uint32_t sub; };
 template <int NB> struct Raw<BGL_Q8G64, NB> { uint4 c[4]; float s; };
 template <int NB> struct Raw<BGL_QNG64, NB> { uint4 c[NB]; float2 s; };
+template <int NB> struct Raw<BGL_Q4G64A, NB> { uint4 c[2]; float s; float b; };
+template <int NB> struct Raw<BGL_F16, NB> { uint4 c[8]; };
+template <int NB> struct Raw<BGL_F32, NB> { uint4 c[16]; };
 
 template <int FMT> constexpr int chunks_per_unit(int nb) {
-    return FMT == BGL_Q4G256SF ? 8 : FMT == BGL_Q8G64 ? 4 : FMT == BGL_QNG64 ? nb : 2;
+    return FMT == BGL_Q4G256SF ? 8 : FMT == BGL_Q8G64 ? 4 : FMT == BGL_QNG64 ? nb : FMT == BGL_F16 ? 8 : FMT == BGL_F32 ? 16 : 2;
 }
 
 // Weight planes live in global memory; the explicit address space keeps these global (not flat)
@@ -62,13 +65,18 @@ __device__ __forceinline__ void load_raw(Raw<FMT, NB> &r, const BglDevTensor &T,
         const bgl_u32x4 v = cp[k * BGL_TILE];
         r.c[k] = make_uint4(v.x, v.y, v.z, v.w);
     }
+    if constexpr (FMT != BGL_F16 && FMT != BGL_F32) {                 // dense rows carry no scales
     const size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + lane;
-    if constexpr (FMT == BGL_QNG64) {
+    if constexpr (FMT == BGL_Q4G64A) {
+        r.s = ((const BGL_GLOBAL float *)T.s0)[so];
+        r.b = ((const BGL_GLOBAL float *)T.s1)[so];
+    } else if constexpr (FMT == BGL_QNG64) {
         const bgl_f32x2 v = ((const BGL_GLOBAL bgl_f32x2 *)T.s0)[so];
         r.s = make_float2(v.x, v.y);
     } else if constexpr (FMT == BGL_Q4G32H) r.s = ((const BGL_GLOBAL uint32_t *)T.s0)[so];
     else r.s = ((const BGL_GLOBAL float *)T.s0)[so];
     if constexpr (FMT == BGL_Q4G256SF) r.sub = ((const BGL_GLOBAL uint32_t *)T.s1)[so];
+    }
 }
 
 // ================================================================================== path A compute
@@ -294,6 +302,67 @@ __device__ __forceinline__ void comp_qng64(const Raw<BGL_QNG64, NB> &r, int K, i
     }
 }
 
+// int4 affine (AF int4, value = nib*s + b): sum = s * sum(nib*x) + b * sum(x), both sums exact
+// integers over the activation digits, so only the fold rounds.
+template <int MB, int NB>
+__device__ __forceinline__ void comp_q4g64a(const Raw<BGL_Q4G64A, NB> &r, int K, int u, const GemvAct &A,
+                                            const Cols<MB> &C, float (&acc)[MB]) {
+    int lo[8], hi[8];
+    uint32_t raw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w};
+#pragma unroll
+    for (int q = 0; q < 8; q++) { lo[q] = nib_lo(raw[q]); hi[q] = nib_hi(raw[q]); }
+    const int ng = K >> 6;
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        const int am = C.am[m];
+        ucint xg = uni(A.xw) + ((size_t)am * ng + u) * BGL_XD_DW;
+        int t0 = 0, t1 = 0, t2 = 0;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            t0 = dot4(lo[q], xg[2 * q], t0);      t0 = dot4(hi[q], xg[2 * q + 1], t0);
+            t1 = dot4(lo[q], xg[16 + 2 * q], t1); t1 = dot4(hi[q], xg[16 + 2 * q + 1], t1);
+            t2 = dot4(lo[q], xg[32 + 2 * q], t2); t2 = dot4(hi[q], xg[32 + 2 * q + 1], t2);
+        }
+        int4 d0 = ld_dsum(A, am, K, 2 * u), d1 = ld_dsum(A, am, K, 2 * u + 1);
+        const float xs = uni(A.xs)[(size_t)am * ng + u];
+        const float sx = fold_digits(d0.x + d1.x, d0.y + d1.y, d0.z + d1.z) * xs;
+        acc[m] += r.s * (fold_digits(t0, t1, t2) * xs) + r.b * sx;
+    }
+}
+
+// Dense fp16 / fp32 rows against the raw fp32 activation (scalar-loaded), fp32 FMA in column
+// order; each 16-byte chunk is converted where it is used so few weights are live at once.
+template <int FMT, int MB, int NB>
+__device__ __forceinline__ void comp_dense(const Raw<FMT, NB> &r, int K, int u, const GemvAct &A, const Cols<MB> &C,
+                                           float (&acc)[MB]) {
+    constexpr int NCH = FMT == BGL_F16 ? 8 : 16, EPC = 64 / NCH;    // chunks per unit, elements per chunk
+    float a[MB];
+#pragma unroll
+    for (int m = 0; m < MB; m++) a[m] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NCH; k++) {
+        const uint32_t v[4] = {r.c[k].x, r.c[k].y, r.c[k].z, r.c[k].w};
+        float w[EPC];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if constexpr (FMT == BGL_F16) {
+                w[2 * j] = __half2float(__ushort_as_half((unsigned short)(v[j] & 0xffffu)));
+                w[2 * j + 1] = __half2float(__ushort_as_half((unsigned short)(v[j] >> 16)));
+            } else {
+                w[j] = __uint_as_float(v[j]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            ucfloat xr = uni(A.xf) + (size_t)C.am[m] * K + (size_t)u * 64 + k * EPC;
+#pragma unroll
+            for (int i = 0; i < EPC; i++) a[m] = __fmaf_rn(w[i], xr[i], a[m]);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MB; m++) acc[m] += a[m];
+}
+
 template <int FMT, int ACT, int NB, int MB>
 __device__ __forceinline__ void comp_dispatch(const Raw<FMT, NB> &r, int K, int u, const GemvAct &A,
                                               const Cols<MB> &C, float (&acc)[MB]) {
@@ -301,6 +370,8 @@ __device__ __forceinline__ void comp_dispatch(const Raw<FMT, NB> &r, int K, int 
     else if constexpr (FMT == BGL_Q4G32H) comp_q4g32h<MB, NB>(r, K, u, A, C, acc);
     else if constexpr (FMT == BGL_Q4G256SF) comp_g256sf<MB, NB>(r, K, u, A, C, acc);
     else if constexpr (FMT == BGL_Q8G64) comp_q8g64<ACT, MB, NB>(r, K, u, A, C, acc);
+    else if constexpr (FMT == BGL_Q4G64A) comp_q4g64a<MB, NB>(r, K, u, A, C, acc);
+    else if constexpr (FMT == BGL_F16 || FMT == BGL_F32) comp_dense<FMT, MB, NB>(r, K, u, A, C, acc);
     else comp_qng64<MB, NB>(r, K, u, A, C, acc);
 }
 

@@ -46,6 +46,8 @@ int bgl_fail(int code, const char *fmt, ...);
 int prof_begin(bgl_ctx *c, int phase);
 void prof_end(bgl_ctx *c, int token);
 int dbuf_reserve(bgl_ctx *c, DevBuf &b, size_t bytes, bool zero);
+// Bytes of per-call scratch the context holds; with release, frees it (the caller synchronizes).
+size_t ctx_scratch(bgl_ctx *c, bool release);
 int check_wt(int kind, int bits, int out, int in);
 int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, GemvAct &A);
 int pick_waves(bgl_ctx *c, int nunits);

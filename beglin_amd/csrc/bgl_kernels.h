@@ -35,6 +35,7 @@ struct GemvAct {
     const float *xs;          // W4A8: ascale [M][K/gq];          F32: 2^(e-21) [M][K/64]
     const int *xsum;          // W4A8: sum xq per 64 [M][K/64];   F32: digit sums [M][K/32][4]
     const int *colmap;        // optional: column m of this launch reads activation row colmap[m]
+    const float *xf;          // F32: the raw rows [M][K] (dense fp16 / fp32 weights read these)
     int gq;                   // W4A8 activation group (64 or 256)
 };
 
@@ -50,6 +51,8 @@ struct GemvLaunch {
 // ---- kernels (bgl_prep.hip) ----
 __global__ void k_act_w4a8(const float *x, int M, int K, int gsize, int8_t *xq, float *ascale, int *xqsum64);
 __global__ void k_act_x24(const float *x, int M, int K, int8_t *xd, float *xs, int *dsum);
+__global__ void k_act_import_i8(const int8_t *xq, const float *ascale, int M, int K, int gq, int split, int8_t *xw,
+                                float *xs, int *xsum64);
 __global__ void k_quant_q4g64(const float *w, int N, int K, uint8_t *packed, float *scales);
 __global__ void k_quant_q8g64(const float *w, int N, int K, int8_t *codes, float *scales);
 __global__ void k_quant_qng64(const float *w, int N, int K, int n, int dense_floor, uint8_t *planes, float *scales);

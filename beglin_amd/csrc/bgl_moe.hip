@@ -154,6 +154,9 @@ __device__ __forceinline__ BglDevTensor ld_tensor(const BglDevTensor *p) {
     return t;
 }
 
+// WIDE: also the dense fp16 / fp32 cases, whose 64-register units would raise every format's
+// register count (and lower occupancy) if they shared one instantiation.
+template <bool WIDE>
 __global__ __launch_bounds__(MOE_MAXW * BGL_TILE) void k_moe_gemv(MoeTask Mt) {
     __shared__ float red[MOE_MAXW][2][MOE_MB][BGL_TILE];
     const int e = blockIdx.x / Mt.tpe, tile = blockIdx.x % Mt.tpe;
@@ -168,6 +171,9 @@ __global__ __launch_bounds__(MOE_MAXW * BGL_TILE) void k_moe_gemv(MoeTask Mt) {
     case BGL_Q4G32H: moe_tile<BGL_Q4G32H, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
     case BGL_Q4G64: moe_tile<BGL_Q4G64, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
     case BGL_Q8G64: moe_tile<BGL_Q8G64, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+    case BGL_Q4G64A: moe_tile<BGL_Q4G64A, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+    case BGL_F16: if constexpr (WIDE) moe_tile<BGL_F16, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
+    case BGL_F32: if constexpr (WIDE) moe_tile<BGL_F32, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
     case BGL_QNG64:
         switch (Ta.bits) {
         case 2: moe_tile<BGL_QNG64, 2>(Mt, Ta, Tb, glu, tile, seg0, ncols, red); break;
@@ -297,16 +303,27 @@ static int moe_prep(bgl_ctx *c, int slot, const float *x_dev, int M, int K, Gemv
     prof_end(c, tok);
     HIPCHK(hipGetLastError());
     memset(&A, 0, sizeof A);
-    A.xw = (const int *)w.p; A.xs = (const float *)s.p; A.xsum = (const int *)d.p; A.gq = 64;
+    A.xw = (const int *)w.p; A.xs = (const float *)s.p; A.xsum = (const int *)d.p; A.xf = x_dev; A.gq = 64;
     return 0;
 }
 
-static int moe_launch(bgl_ctx *c, const MoeTask &Mt, int units) {
+static bool dense_fmt(int fmt) { return fmt == BGL_F16 || fmt == BGL_F32; }
+
+// Whether a launch meets dense experts: the stack's experts, or the by-value tensors.
+static bool task_wide(const bgl_tensor *stack, const MoeTask &Mt) {
+    if (stack)
+        for (const bgl_tensor *e : stack->experts)
+            if (dense_fmt(e->T.fmt)) return true;
+    return !Mt.ta && (dense_fmt(Mt.da.fmt) || (Mt.swiglu && dense_fmt(Mt.db.fmt)));
+}
+
+static int moe_launch(bgl_ctx *c, const MoeTask &Mt, int units, bool wide) {
     int nw = units < c->max_waves ? units : c->max_waves;
     if (nw > MOE_MAXW) nw = MOE_MAXW;
     if (nw < 1) nw = 1;
     int tok = prof_begin(c, 1);
-    hipLaunchKernelGGL(k_moe_gemv, dim3(Mt.E * Mt.tpe), dim3(nw * BGL_TILE), 0, c->stream, Mt);
+    if (wide) hipLaunchKernelGGL(k_moe_gemv<true>, dim3(Mt.E * Mt.tpe), dim3(nw * BGL_TILE), 0, c->stream, Mt);
+    else hipLaunchKernelGGL(k_moe_gemv<false>, dim3(Mt.E * Mt.tpe), dim3(nw * BGL_TILE), 0, c->stream, Mt);
     prof_end(c, tok);
     HIPCHK(hipGetLastError());
     return 0;
@@ -343,7 +360,7 @@ extern "C" int bgl_gather_matvec_dev(bgl_ctx *c, const bgl_tensor *experts, cons
     max_units(experts, Mt.tpe, units);
     Mt.ta = (const BglDevTensor *)experts->dev_table; Mt.E = E; Mt.off = S.off;
     Mt.cols = S.perm; Mt.ymap = S.perm; Mt.y = y_dev; Mt.ystride = experts->T.N;
-    return moe_launch(c, Mt, units);
+    return moe_launch(c, Mt, units, task_wide(experts, Mt));
 }
 
 extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down,
@@ -394,23 +411,23 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
     max_units(gate, Mr.tpe, units);
     Mr.ta = (const BglDevTensor *)gate->dev_table; Mr.tb = (const BglDevTensor *)up->dev_table;
     Mr.E = E; Mr.off = S.off; Mr.cols = S.tok; Mr.y = h; Mr.ystride = I; Mr.swiglu = 1;
-    if ((rc = moe_launch(c, Mr, units))) return rc;
+    if ((rc = moe_launch(c, Mr, units, task_wide(gate, Mr)))) return rc;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         Ms.a = Mr.a; Ms.da = sg->T; Ms.db = su->T; Ms.E = 1; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
         Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
-        if ((rc = moe_launch(c, Ms, sg->T.nunits))) return rc;
+        if ((rc = moe_launch(c, Ms, sg->T.nunits, task_wide(nullptr, Ms)))) return rc;
     }
     memset(&Mr, 0, sizeof Mr);
     if ((rc = moe_prep(c, 1, h, P, I, Mr.a))) return rc;
     max_units(down, Mr.tpe, units);
     Mr.ta = (const BglDevTensor *)down->dev_table; Mr.E = E; Mr.off = S.off; Mr.y = dd; Mr.ystride = H;
-    if ((rc = moe_launch(c, Mr, units))) return rc;
+    if ((rc = moe_launch(c, Mr, units, task_wide(down, Mr)))) return rc;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         if ((rc = moe_prep(c, 0, shh, T, Ish, Ms.a))) return rc;
         Ms.da = sd->T; Ms.E = 1; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
-        if ((rc = moe_launch(c, Ms, sd->T.nunits))) return rc;
+        if ((rc = moe_launch(c, Ms, sd->T.nunits, task_wide(nullptr, Ms)))) return rc;
     }
     int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_moe_combine, dim3(nblk((long)T * H)), dim3(256), 0, c->stream, dd, S.pos, idx_dev, w_dev, T, K, H,

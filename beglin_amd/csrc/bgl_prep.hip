@@ -72,6 +72,31 @@ __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, in
     }
 }
 
+// ------------------------------------------------------------------ caller-quantized int8 columns
+// q4_quant_act_i8 output handed over by the caller (gemm_qXg64_sdot_mt / gemm_q4g256sf_sdot_mt,
+// q4gemv.h:779, q4gemv_g256.h:368) -> the W4A8 operand layout: natural-order codes, the scales
+// per gq-group and the per-64 code sums.  One wave per (column, 64-group), lane = element.
+// split=1: the source is in q4_split_act order (per 32 bytes: the 16 even then the 16 odd
+// elements, q4gemv.h:306-312).
+__global__ __launch_bounds__(256) void k_act_import_i8(const int8_t *__restrict__ xq, const float *__restrict__ ascale,
+                                                       int M, int K, int gq, int split, int8_t *__restrict__ xw,
+                                                       float *__restrict__ xs, int *__restrict__ xsum64) {
+    const int wid = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    const int ng = K >> 6;
+    if (wid >= M * ng) return;
+    const int m = wid / ng, g = wid % ng;
+    const int i = lane & 31, half = lane >> 5;
+    const int src = split ? half * 32 + ((i & 1) ? 16 : 0) + (i >> 1) : lane;
+    const int v = xq[(size_t)m * K + (size_t)g * 64 + src];
+    xw[(size_t)m * K + (size_t)g * 64 + lane] = (int8_t)v;
+    const int sum = wave_sum_i32(v);
+    const int per = gq >> 6;
+    if (lane == 0) {
+        xsum64[(size_t)m * ng + g] = sum;
+        if (g % per == 0) xs[(size_t)m * (K / gq) + g / per] = ascale[(size_t)m * (K / gq) + g / per];
+    }
+}
+
 // ------------------------------------------------------------------ device packers (reference byte layouts)
 // One thread per (row, group).  Arithmetic identical to the reference packers.
 
@@ -386,11 +411,21 @@ __global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *__restrict
     int r = row0 + (int)(t / T.K), c = (int)(t % T.K);
     int tile = r / BGL_TILE, lane = r % BGL_TILE;
     float v = 0.0f;
-    if (T.fmt == BGL_Q4G64 || T.fmt == BGL_Q4G32H || T.fmt == BGL_Q4G256SF) {
+    if (T.fmt == BGL_F16 || T.fmt == BGL_F32) {
+        const int esz = T.fmt == BGL_F16 ? 2 : 4, per = 16 / esz;
+        const uint8_t *p = T.w + (((size_t)tile * T.cpr + c / per) * BGL_TILE + lane) * 16 + (c % per) * esz;
+        if (T.fmt == BGL_F16) v = __half2float(__ushort_as_half(*reinterpret_cast<const unsigned short *>(p)));
+        else v = *reinterpret_cast<const float *>(p);
+    } else if (T.fmt == BGL_Q4G64 || T.fmt == BGL_Q4G32H || T.fmt == BGL_Q4G256SF || T.fmt == BGL_Q4G64A) {
         int chunk = c / 32, e = c % 32, j = e / 8, q = e % 8;
         const uint8_t *p = T.w + (((size_t)tile * T.cpr + chunk) * BGL_TILE + lane) * 16 + 4 * j;
         int nib = q < 4 ? (p[q] & 15) : (p[q - 4] >> 4);
-        if (T.fmt == BGL_Q4G64) {
+        if (T.fmt == BGL_Q4G64A) {
+            // moe_decode_af's affine arm (qwen_infer.c:2649-2652): (float)nib * s + b
+            size_t o = ((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane;
+            v = __fadd_rn(__fmul_rn((float)nib, reinterpret_cast<const float *>(T.s0)[o]),
+                          reinterpret_cast<const float *>(T.s1)[o]);
+        } else if (T.fmt == BGL_Q4G64) {
             float s = reinterpret_cast<const float *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
             v = (float)(nib - 8) * s;
         } else if (T.fmt == BGL_Q4G32H) {

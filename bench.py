@@ -15,7 +15,11 @@ algorithmic bytes = packed + scale + sub-code bytes + 4*M*K (x) + 4*M*N (y) per 
 stream), i.e. without the inter-launch gaps that `value` includes.  `cpu_baseline` = the reference's threaded CPU
 path (portable-C restatement, q4pool row-block split) timed on this host on a bounded sample.
 
-Other workloads for the per-config numbers: --workload cfg1 | cfg3 (see --help)."""
+Other workloads for the per-config numbers: --workload cfg1 | cfg3 | cfg4 (see --help).
+cfg4 = DeepSeek-V2-Lite routed MoE FFN (E=64 + 2 shared experts, hidden 2048, expert inter 1408,
+top-6 over softmax(N(0,1) router logits)), T=--M tokens, per-expert precision drawn from the seed
+over {q4g32h, q8g64, qNg64 n=7..15}; one step = --layers distinct MoE layers; algorithmic bytes =
+the packed + scale bytes of every expert the step's routing touches (+ shared experts, x, out)."""
 import argparse
 import json
 import os
@@ -121,6 +125,71 @@ def build_rotated(ctx, torch, kind, bits, out, inn, M, seed, act):
     return wl
 
 
+# DeepSeek-V2-Lite routed MoE layer
+DSV2 = dict(E=64, H=2048, I=1408, K=6, Ish=2 * 1408)
+CFG4_FORMATS = [(5, 0), (2, 0)] + [(4, n) for n in range(7, 16)]
+
+
+def wbytes(kind, out, inn, bits):
+    return alg_bytes(kind, out, inn, bits, 0)
+
+
+class MoeWorkload:
+    """`layers` routed MoE layers; each = (gate, up, down, shared, idx, w, bytes touched)."""
+
+    def __init__(self, ctx, torch, T, layers, seed):
+        import beglin_amd
+        self.ctx, self.torch, self.T = ctx, torch, T
+        E, H, I, K, Ish = (DSV2[k] for k in ("E", "H", "I", "K", "Ish"))
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        rng = __import__("numpy").random.default_rng(seed)
+        self.x = torch.randn((T, H), generator=gen, device="cuda")
+        self.layers = []
+        self.formats = []
+        for _ in range(layers):
+            fm = [CFG4_FORMATS[i] for i in rng.integers(0, len(CFG4_FORMATS), E)]
+            shf = CFG4_FORMATS[int(rng.integers(0, len(CFG4_FORMATS)))]
+            stacks = []
+            for (o, i) in ((I, H), (I, H), (H, I)):
+                ts = []
+                for (k, b) in fm:
+                    w = gen_weight(torch, gen, o, i)
+                    ts.append(ctx.quantize(k, w, bits=b))
+                    del w
+                stacks.append(ctx.experts_from_tensors(ts))
+            sh = []
+            for (o, i) in ((Ish, H), (Ish, H), (H, Ish)):
+                w = gen_weight(torch, gen, o, i)
+                sh.append(ctx.quantize(shf[0], w, bits=shf[1]))
+                del w
+            logits = torch.randn((T, E), generator=gen, device="cuda")
+            prob = torch.softmax(logits, dim=-1)                 # moe_softmax_full
+            w, idx = torch.topk(prob, K, dim=-1)                 # moe_top_k_select (no renorm)
+            idx = idx.to(torch.int32).contiguous()
+            touched = sorted(set(idx.cpu().flatten().tolist()))
+            nb = sum(2 * wbytes(fm[e][0], I, H, fm[e][1]) + wbytes(fm[e][0], H, I, fm[e][1]) for e in touched)
+            nb += 2 * wbytes(shf[0], Ish, H, shf[1]) + wbytes(shf[0], H, Ish, shf[1])
+            nb += 2 * 4 * T * H                                      # x in, out
+            out = torch.empty((T, H), device="cuda")
+            self.layers.append((stacks, tuple(sh), idx, w.contiguous(), out, nb, len(touched)))
+            self.formats.append((fm, shf))
+
+    def run(self, tags=None):
+        for stacks, sh, idx, w, out, _, _ in self.layers:
+            self.ctx.moe_ffn(stacks[0], stacks[1], stacks[2], sh, self.x, idx, w, out)
+
+    def nbytes(self, tags=None):
+        return sum(l[5] for l in self.layers)
+
+    def ncalls(self, tags=None):
+        return len(self.layers)
+
+    def free(self):
+        for stacks, sh, *_ in self.layers:
+            for t in list(stacks) + list(sh):
+                t.free()
+
+
 def time_graph(torch, stream, fn, steps, warmup):
     with torch.cuda.stream(stream):
         fn()                                   # eager once: reserves every scratch buffer
@@ -152,7 +221,84 @@ def time_prep(ctx, torch, stream, wl, steps):
     return ms
 
 
+def moe_roofline(ctx, torch, stream, wl, reps):
+    """k_moe_gemv's own time: eager steps with an event pair around every launch (bgl_prof_*),
+    summed per phase on the context's stream; achieved = step bytes / gather-GEMV time."""
+    ctx.prof_enable(True)
+    ctx.prof_read()
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            wl.run()
+    ctx.sync()
+    ph = ctx.prof_read()
+    ctx.prof_enable(False)
+    g_ms, g_n = ph["gemv"][0] / reps, ph["gemv"][1] // reps
+    p_ms, p_n = ph["prep"][0] / reps, ph["prep"][1] // reps
+    o_ms, o_n = ph["other"][0] / reps, ph["other"][1] // reps
+    achieved = wl.nbytes() / (g_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_moe_gemv (bgl_moe.hip)",
+            "launches_per_step": g_n, "kernel_us_per_launch": round(g_ms * 1e3 / max(g_n, 1), 3),
+            "bytes_per_launch": round(wl.nbytes() / max(g_n, 1)),
+            "prep_us_per_step": round(p_ms * 1e3, 2), "prep_launches": p_n,
+            "bucket_combine_us_per_step": round(o_ms * 1e3, 2), "bucket_combine_launches": o_n,
+            "timing": f"eager, event pair per launch, {reps} steps"}
+
+
 # ------------------------------------------------------------------------------------- CPU baseline
+def cpu_baseline_cfg4(wl, budget_s, seed):
+    """moe_ffn_batched's portable C restatement (or_moe_ffn_bucketed, one thread) on layer 0's
+    formats and routing, for its first min(T, 2) tokens; only the experts those tokens touch are
+    quantized (the others are never read)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_ffi import Oracle, moe_ffn
+    orc = Oracle()
+    rng = np.random.default_rng(seed + 1)
+    E, H, I, K, Ish = (DSV2[k] for k in ("E", "H", "I", "K", "Ish"))
+    fm, shf = wl.formats[0]
+    idx = wl.layers[0][2].cpu().numpy()
+    w = wl.layers[0][3].cpu().numpy()
+    T = min(wl.T, 2)
+    idx, w = np.ascontiguousarray(idx[:T]), np.ascontiguousarray(w[:T])
+    touched = sorted(set(idx.flatten().tolist()))
+
+    def q(k, b, o, i):
+        m = (rng.standard_normal((o, i), dtype=np.float32) * np.float32(0.02))
+        if k == 5:
+            p, sc = orc.quantize_q4g32h(m)
+        elif k == 2:
+            p, sc = orc.quantize_q8g64(m)
+        else:
+            p, sc = orc.quantize_qng64(m, b)
+        return (k, b if k == 4 else (8 if k == 2 else 4), p, sc)
+
+    dummy = (5, 4, np.zeros((1, 1), np.uint8), np.zeros((1, 1), np.uint16))
+    gate, up, down = [dummy] * E, [dummy] * E, [dummy] * E
+    gate, up, down = list(gate), list(up), list(down)
+    nb = 0
+    for e in touched:
+        k, b = fm[e]
+        gate[e], up[e], down[e] = q(k, b, I, H), q(k, b, I, H), q(k, b, H, I)
+        nb += 2 * wbytes(k, I, H, b) + wbytes(k, H, I, b)
+    shared = (q(shf[0], shf[1], Ish, H), q(shf[0], shf[1], Ish, H), q(shf[0], shf[1], H, Ish))
+    nb += 2 * wbytes(shf[0], Ish, H, shf[1]) + wbytes(shf[0], H, Ish, shf[1]) + 2 * 4 * T * H
+    x = rng.standard_normal((T, H), dtype=np.float32)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        moe_ffn(orc, gate, up, down, shared, H, I, x, idx, w)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s or reps >= 1000:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "us_per_layer": round(dt * 1e6, 1),
+            "sample": f"layer 0, first {T} token(s), {len(touched)} experts touched + shared ({nb / 1e6:.1f} MB), "
+                      f"or_moe_ffn_bucketed single-threaded, {reps} calls over {dt * reps:.1f} s"}
+
+
+
 def cpu_baseline_cfg2(M, budget_s, layers=2, seed=7):
     """The reference's threaded CPU path (gemv_q4g256sf_sdot_mt, q4gemv_g256.h:339-364 semantics,
     q4pool row-block split) on `layers` layers of the same shapes."""
@@ -235,9 +381,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3"])
-    ap.add_argument("--M", type=int, default=1, help="activation rows (cfg2: 1, 4 or 8)")
-    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4"])
+    ap.add_argument("--M", type=int, default=1, help="activation rows (cfg2: 1, 4 or 8); cfg4: tokens T (1, 8, 64)")
+    ap.add_argument("--layers", type=int, default=None, help="cfg2: 28 layers; cfg4: 8 MoE layers")
     ap.add_argument("--bits", type=int, default=15, help="cfg3: qNg64 width n")
     ap.add_argument("--shape", default="gate", choices=["gate", "down"], help="cfg3: MLP gate (K=4096) or down (K=14336)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -258,6 +404,8 @@ def main():
     stream = torch.cuda.Stream()
     ctx = beglin_amd.Context(0, stream=stream.cuda_stream)
     M = args.M
+    if args.layers is None:
+        args.layers = 8 if args.workload == "cfg4" else 28
     if args.workload == "cfg2":
         with torch.cuda.stream(stream):
             wl = build_cfg2(ctx, torch, M, args.layers, args.seed)
@@ -272,6 +420,16 @@ def main():
         workload = f"cfg1: int4 g32 fp16-scale GEMV K=1536 N=8960, fp32 activations, M={M}, {wl.ncalls()} rotated copies"
         dtype = "int8"
         cfg = {"workload": workload, "M": M, "format": "q4g32h", "copies": wl.ncalls(), "seed": args.seed}
+    elif args.workload == "cfg4":
+        with torch.cuda.stream(stream):
+            wl = MoeWorkload(ctx, torch, M, args.layers, args.seed)
+        touched = [l[6] for l in wl.layers]
+        workload = (f"cfg4: DeepSeek-V2-Lite routed MoE FFN x{args.layers} layers, E=64+2 shared, hidden 2048, "
+                    f"inter 1408, top-6, T={M}, per-expert precision from the seed")
+        dtype = "int8"
+        cfg = {"workload": workload, "T": M, "layers": args.layers, "experts_touched_per_layer": touched,
+               "formats": "q4g32h | q8g64 | qNg64 n=7..15 per expert (fp32 activations)", "seed": args.seed,
+               "bytes_per_step": int(wl.nbytes())}
     else:
         out, inn = (14336, 4096) if args.shape == "gate" else (4096, 14336)
         with torch.cuda.stream(stream):
@@ -286,6 +444,13 @@ def main():
     value = nbytes / (step_ms * 1e-3) / 1e9
 
     # per-call latency of each call type (graph over all its instances)
+    if args.workload == "cfg4":
+        per_call = {"moe_layer": {"us": round(step_ms * 1e3 / args.layers, 2), "GB/s": round(value, 1)}}
+        roof = moe_roofline(ctx, torch, stream, wl, max(3, args.steps // 10))
+        cpu = None if args.no_cpu else cpu_baseline_cfg4(wl, args.cpu_seconds, args.seed)
+        finish(args, wl, ctx, graph, value, step_ms, wall, dtype, cfg, per_call, roof, cpu)
+        return
+
     per_call = {}
     tags = sorted({c[5] for c in wl.calls})
     for tag in tags:
@@ -320,6 +485,10 @@ def main():
             out, inn = (14336, 4096) if args.shape == "gate" else (4096, 14336)
             cpu = cpu_baseline_rotated(4, args.bits, out, inn, args.cpu_seconds)
 
+    finish(args, wl, ctx, graph, value, step_ms, wall, dtype, cfg, per_call, roof, cpu)
+
+
+def finish(args, wl, ctx, graph, value, step_ms, wall, dtype, cfg, per_call, roof, cpu):
     line = {"metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": dtype, "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",

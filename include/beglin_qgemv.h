@@ -9,6 +9,9 @@
  *     that same FATAL, so behaviour at the engine boundary is unchanged.
  *   - weights: "kind" ids 1..4 are the engine's WT kinds (qwen_infer.c:207): 1 K_Q4G64, 2 K_Q8G64,
  *     3 K_Q4G256SF, 4 K_QNG64; 5 is BGL_K_Q4G32H (int4 group-32, fp16 scale, q4gemv nibble pairing).
+ *     6..8 are the AF expert kinds the MoE boundary binds (mlx_gpu_bind_af bits=4/16/32,
+ *     mlx_moe.cpp:146-367): 6 BGL_K_Q4G64A int4 affine (nib*s + b, group 64), 7 BGL_K_F16 and
+ *     8 BGL_K_F32 dense rows.  Kinds 6..8 run in the MoE gather only (fp32 activations).
  *   - *_dev entry points take DEVICE pointers and are asynchronous on the context's stream;
  *     host-pointer entry points (the drop-ins with the reference's exact argument lists) copy
  *     x in and y out and return after y is on the host.
@@ -24,7 +27,8 @@
 extern "C" {
 #endif
 
-enum { BGL_K_Q4G64 = 1, BGL_K_Q8G64 = 2, BGL_K_Q4G256SF = 3, BGL_K_QNG64 = 4, BGL_K_Q4G32H = 5 };
+enum { BGL_K_Q4G64 = 1, BGL_K_Q8G64 = 2, BGL_K_Q4G256SF = 3, BGL_K_QNG64 = 4, BGL_K_Q4G32H = 5,
+       BGL_K_Q4G64A = 6, BGL_K_F16 = 7, BGL_K_F32 = 8 };
 enum { BGL_ACT_F32 = 0, BGL_ACT_W4A8 = 1 };
 enum { BGL_OK = 0, BGL_E_ARG = -1, BGL_E_UNSUPPORTED = -2, BGL_E_HIP = -3, BGL_E_NODEV = -4, BGL_E_NOMEM = -5 };
 
@@ -32,11 +36,13 @@ typedef struct bgl_ctx bgl_ctx;
 typedef struct bgl_tensor bgl_tensor;
 
 /* Weight descriptor: the fields of the engine's WT (qwen_infer.c:208-222).
- *   packed: K_Q4G64/K_Q4G256SF/Q4G32H nibbles [out][in/2] (low nibble = even column);
- *           K_Q8G64 int8 codes [out][in]; K_QNG64 bit planes [out][in/64][n][8].
- *   scales: fp32 [out][in/64] (K_Q4G64, K_Q8G64, K_QNG64); fp32 wsuper [out][in/256] (K_Q4G256SF);
- *           fp16 bits [out][in/32] (Q4G32H).
- *   sub:    K_Q4G256SF only: sub-codes u8 [out][in/64].
+ *   packed: K_Q4G64/K_Q4G256SF/Q4G32H/Q4G64A nibbles [out][in/2] (low nibble = even column; the
+ *           AF int4 u32 words [out][in/8] are the same bytes, mlx_moe.cpp:238-257);
+ *           K_Q8G64 int8 codes [out][in]; K_QNG64 bit planes [out][in/64][n][8];
+ *           F16 / F32: dense fp16 / fp32 rows [out][in].
+ *   scales: fp32 [out][in/64] (K_Q4G64, K_Q8G64, K_QNG64, Q4G64A); fp32 wsuper [out][in/256]
+ *           (K_Q4G256SF); fp16 bits [out][in/32] (Q4G32H); unused (may be NULL) for F16 / F32.
+ *   sub:    K_Q4G256SF: sub-codes u8 [out][in/64]; Q4G64A: fp32 biases [out][in/64] (read as bytes).
  *   bits:   K_QNG64 only: n in 2..15. */
 typedef struct {
     int kind, bits, out, in;
@@ -108,6 +114,8 @@ int  bgl_quant_act_i8_dev(bgl_ctx *ctx, const float *x_dev, int M, int in, int g
  * Synchronous: y is valid on return. */
 int bgl_gemv_q4g64_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
                       const float *bias, float *y, int out, int in);                     /* q4gemv.h:672 */
+int bgl_gemv_q4g64_mt_fused(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
+                            const float *bias, float *y, int out, int in);               /* q4gemv.h:686 (same values as :672) */
 int bgl_gemv_q4g64_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
                            const float *bias, float *y, int out, int in);                /* q4gemv.h:701 */
 int bgl_gemv_q8g64_mt(bgl_ctx *p, const uint8_t *packed, const float *scales, const float *x,
@@ -116,6 +124,15 @@ int bgl_gemv_q8g64_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *scale
                            const float *bias, float *y, int out, int in);                /* q4gemv.h:726 */
 int bgl_gemm_qXg64_mt(bgl_ctx *p, int bits, const uint8_t *packed, const float *scales, const float *x,
                       const float *bias, float *y, int out, int in, int M);              /* q4gemv.h:761 */
+/* Caller-quantized int8 columns (matmul_sdot's serve path, qwen_infer.c:1870-1898): xq [M][in] as
+ * q4_quant_act_i8 produced it -- for bits=4 in q4_split_act's split order ([even16][odd16] per 32
+ * bytes, q4gemv.h:298-312), for bits=8 in natural order -- and ascale [M][in/64]. */
+int bgl_gemm_qXg64_sdot_mt(bgl_ctx *p, int bits, const uint8_t *packed, const float *scales, const int8_t *xq,
+                           const float *ascale, const float *bias, float *y, int out, int in, int M);   /* q4gemv.h:779 */
+/* g256sf with caller-quantized columns: xq split order, ascale [M][in/256] (q4gemv_g256.h:366-383). */
+int bgl_gemm_q4g256sf_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *wsuper, const uint8_t *subcode,
+                              const int8_t *xq, const float *ascale, const float *bias, float *y, int out, int in,
+                              int M);                                                    /* q4gemv_g256.h:368 */
 int bgl_gemv_q4g256sf_sdot_mt(bgl_ctx *p, const uint8_t *packed, const float *wsuper, const uint8_t *subcode,
                               const float *x, const float *bias, float *y, int out, int in);   /* q4gemv_g256.h:339 */
 int bgl_gemm_q4g256sf_mt(bgl_ctx *p, const uint8_t *packed, const float *wsuper, const uint8_t *subcode,
@@ -148,6 +165,64 @@ int bgl_moe_ffn_dev(bgl_ctx *ctx, const bgl_tensor *gate, const bgl_tensor *up, 
                     const bgl_tensor *shared_gate, const bgl_tensor *shared_up, const bgl_tensor *shared_down,
                     const float *x_dev, const int32_t *topk_idx_dev, const float *topk_w_dev, int T, int K,
                     float *out_dev);
+
+/* ---------------- name-keyed MoE registry: the mlx_moe.h GPU boundary ----------------
+ * One process-wide registry on device 0 (own stream, like MLX's default stream).  Each function
+ * has the argument list and the return convention of the mlx_gpu_* function it replaces:
+ * 1 = ok, 0 = failure (bgl_last_error() says why), unless stated otherwise.  Weights are COPIED
+ * into the device layout at bind (the reference wraps the blob zero-copy); the blob may be
+ * released after bgl_gpu_bind_af returns. */
+int bgl_gpu_available(void);                                           /* mlx_moe.h:24 */
+int bgl_gpu_synchronize(void);                                         /* mlx_moe.h:29 */
+/* Synchronizes and releases per-call scratch; bindings stay (mlx_moe.h:36, mlx_moe.cpp:3167-3200). */
+int bgl_gpu_reset_runtime_epoch(void);
+/* E experts [out][in], groups of 64 (ng = in/64), read from blob at the byte offsets.  bits:
+ * 4 int4 affine (scale_off, bias_off), 8 q8g64 (no bias), 2/3/5/6/7/9..15 qNg64 planes,
+ * 16 / 32 dense fp16 / fp32 (no scales); n=8 planes and other widths are refused (mlx_moe.cpp:
+ * 146-367).  Rebinding a name replaces it. */
+int bgl_gpu_bind_af(const uint8_t *blob, long blob_bytes, const char *name, long E, long out, long in, long ng,
+                    long packed_off, long scale_off, long bias_off, int bits);           /* mlx_moe.h:48-50 */
+/* 0 missing, 1 quantized (bits 2..6, 8), 2 dense (16/32), 3 qNg64 planes n=7, 9..15 (mlx_moe.h:57). */
+int bgl_gpu_binding_kind(const char *name, int *bits_out);
+int bgl_gpu_snapshot_binding(const char *name, uint64_t *snapshot_id);  /* mlx_moe.h:63 */
+int bgl_gpu_restore_binding_snapshot(uint64_t snapshot_id);           /* mlx_moe.h:64 */
+int bgl_gpu_drop_binding_snapshot(uint64_t snapshot_id);              /* mlx_moe.h:65 */
+int bgl_gpu_binding_snapshot_count(void);                             /* mlx_moe.h:66: returns the count */
+/* Every binding is an explicit copy: zero_copy = 0, copied = bytes_copied's tensor count; returns
+ * the number of binds performed (mlx_moe.h:72). */
+int bgl_gpu_zerocopy_count(int *zero_copy, int *copied, size_t *bytes_copied);
+/* Decoded weights of expert e, row `row`, columns [col0, col0+ncols) read back from the device
+ * layout (mlx_moe.h:78-79). */
+int bgl_gpu_dequant_probe(const char *name, long e, long row, long col0, int ncols, float *out);
+/* Explicit-pair gather with raw host buffers (mlx_moe.h:89-91): planes [E][out][ng*n*8],
+ * scales [E][out][ng], x [N][in], expert_idx [N], out_buf [N][out]. */
+int bgl_gpu_qng64_gather_probe(const uint8_t *planes, long E, long out, long in, long ng, int n, const float *scales,
+                               const float *x, int N, const int32_t *expert_idx, float *out_buf);
+/* Bind one caller-owned qNg64 tensor (n in {2,3,5,6}) as a single-expert binding (mlx_moe.h:97-98). */
+int bgl_gpu_bind_qng64_dense_probe(const uint8_t *packed, const float *scales, const char *name, long out, long in, int n);
+/* y[out] = W_e x for one expert of a bound tensor, host x / y (mlx_moe.h:121). */
+int bgl_gpu_matvec_probe(const char *name, long e, const float *x, float *y);
+/* Device bytes held by bindings (active), the high-water mark (peak) and per-call scratch (cache). */
+void bgl_gpu_report_memory(size_t *active, size_t *peak, size_t *cache);    /* mlx_moe.h:125 */
+int bgl_gpu_set_batch(int B);                                          /* mlx_moe.h:255: 1 <= B <= 64 */
+/* Recorded for the caller; the gather always sorts pairs by expert, which gives the same values
+ * as the unsorted form (mlx_moe.h:264). */
+int bgl_gpu_set_sort_threshold(int threshold);
+/* 1 uniform, 0 mixed dense / quantized / qNg64-plane roles, -1 a name is not bound (mlx_moe.h:334). */
+int bgl_gpu_test_ffn_uniform(const char *gate_name, const char *up_name, const char *down_name);
+/* The gather itself by name, host buffers: y[z] = W_{idx[z]} x[z] for z < N (ffn_gather's explicit-pair
+ * canonical form, mlx_moe.cpp:1577-1589, :1901-1916). */
+int bgl_gpu_ffn_gather(const char *name, const float *x, int N, const int32_t *expert_idx, float *y);
+/* Routed SwiGLU FFN over bound gate/up/down names (+ optional shared-expert names, NULL for none)
+ * with top-K routing given, host buffers (routed-FFN composition mlx_moe.cpp:2155-2232 /
+ * moe_ffn_batched qwen_infer.c:5238-5350). */
+int bgl_gpu_moe_ffn(const char *gate, const char *up, const char *down, const char *shared_gate,
+                    const char *shared_up, const char *shared_down, const float *x, int T, const int32_t *topk_idx,
+                    const float *topk_w, int K, float *out);
+/* The registry's context, for device-pointer calls on registered tensors. */
+bgl_ctx *bgl_gpu_context(void);
+/* The registry's current device tensor for `name` (NULL if missing). */
+const bgl_tensor *bgl_gpu_lookup(const char *name);
 
 #ifdef __cplusplus
 }

@@ -543,6 +543,32 @@ void or_matmul_sdot(int kind, const void *packed, const float *scales, const uin
 double or_moe_row(const or_expert *w, int in, long row, const float *x) {
     int ng = in / G64;
     double acc = 0.0;
+    if (w->kind == 8) {                        /* bits==32 arm, qwen_infer.c:2674-2682 */
+        const float *pr = (const float *)w->packed + (size_t)row * in;
+        for (int c = 0; c < in; c++) acc += (double)pr[c] * x[c];
+        return acc;
+    }
+    if (w->kind == 7) {                        /* bits==16 arm, qwen_infer.c:2683-2691 */
+        const uint16_t *pr = (const uint16_t *)w->packed + (size_t)row * in;
+        for (int c = 0; c < in; c++) acc += (double)or_f16_to_f32(pr[c]) * x[c];
+        return acc;
+    }
+    if (w->kind == 6) {                        /* int4 affine arm, qwen_infer.c:2780-2798 (no LUT) */
+        const uint8_t *pr = (const uint8_t *)w->packed + (size_t)row * (in / 2);
+        const float *sc = (const float *)w->scales + (size_t)row * ng;
+        const float *bi = (const float *)w->bias + (size_t)row * ng;
+        for (int g = 0; g < ng; g++) {
+            float scale = sc[g], bias = bi[g];
+            for (int ci = 0; ci < G64; ci++) {
+                int c = g * G64 + ci;
+                uint8_t b = pr[c / 2];
+                int nib = (c % 2 == 0) ? (b & 0xF) : ((b >> 4) & 0xF);
+                float wv = (float)nib * scale + bias;
+                acc += (double)wv * x[c];
+            }
+        }
+        return acc;
+    }
     if (w->kind == 2) {
         const int8_t *pr = (const int8_t *)w->packed + (size_t)row * in;
         const float *sc = (const float *)w->scales + (size_t)row * ng;
@@ -580,6 +606,31 @@ double or_moe_row(const or_expert *w, int in, long row, const float *x) {
         acc += (double)wv * x[c];
     }
     return acc;
+}
+
+/* moe_decode_af (qwen_infer.c:2554-2655): one decoded weight, every kind or_moe_row knows.
+ * The int4 arms address the packed row as bytes (the AF u32 words hold the same bytes). */
+float or_moe_decode(const or_expert *w, int in, long row, long col) {
+    int ng = in / G64;
+    long g = col / G64;
+    if (w->kind == 8) return ((const float *)w->packed)[(size_t)row * in + col];
+    if (w->kind == 7) return or_f16_to_f32(((const uint16_t *)w->packed)[(size_t)row * in + col]);
+    if (w->kind == 2)
+        return (float)((const int8_t *)w->packed)[(size_t)row * in + col] * ((const float *)w->scales)[(size_t)row * ng + g];
+    if (w->kind == 4) {
+        int n = w->bits;
+        const uint8_t *grp = (const uint8_t *)w->packed + ((size_t)row * ng + g) * n * 8;
+        int p = (int)(col % G64), u = 0;
+        for (int j = 0; j < n; j++)
+            if ((grp[j * 8 + (p >> 3)] >> (p & 7)) & 1) u |= 1 << j;
+        return (float)(u - (1 << (n - 1))) * ((const float *)w->scales)[(size_t)row * ng + g];
+    }
+    uint8_t b = ((const uint8_t *)w->packed)[(size_t)row * (in / 2) + col / 2];
+    int nib = (col % 2 == 0) ? (b & 0xF) : ((b >> 4) & 0xF);
+    if (w->kind == 5) return (float)(nib - 8) * or_f16_to_f32(((const uint16_t *)w->scales)[(size_t)row * (in / 32) + col / 32]);
+    float scale = ((const float *)w->scales)[(size_t)row * ng + g];
+    if (w->kind == 6) return (float)nib * scale + ((const float *)w->bias)[(size_t)row * ng + g];
+    return ((float)nib - 8.0f) * scale;
 }
 
 /* qwen_infer.c:3223-3225 (moe_matvec_af): y[r] = (float)row_dot. */

@@ -64,13 +64,15 @@ void or_matmul_sdot(int kind, const void *packed, const float *scales, const uin
 
 /* ---------------- MoE ---------------- */
 typedef struct {
-    int kind;            /* 1 q4g64, 2 q8g64, 4 qNg64, 5 q4g32h */
+    int kind;            /* 1 q4g64 (sym), 2 q8g64, 4 qNg64, 5 q4g32h, 6 int4 affine, 7 fp16, 8 fp32 */
     int bits;            /* qNg64 n */
     const void *packed;
-    const void *scales;  /* fp32, or fp16 bits for q4g32h */
+    const void *scales;  /* fp32, or fp16 bits for q4g32h; unused for 7 / 8 */
+    const void *bias;    /* kind 6: fp32 biases [out][in/64] */
 } or_expert;
 
 double or_moe_row(const or_expert *w, int in, long row, const float *x);
+float or_moe_decode(const or_expert *w, int in, long row, long col);
 void or_moe_matvec(const or_expert *w, int out, int in, const float *x, float *y);
 void or_moe_softmax_full(float *x, int n);
 void or_moe_top_k_select(const float *scores, int n, int k, int *out_idx);

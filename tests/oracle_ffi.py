@@ -30,6 +30,7 @@ def load_oracle():
     lib.or_f16_to_f32.argtypes = [C.c_uint16]
     lib.or_quantize_qng64_dense.restype = C.c_int
     lib.or_moe_row.restype = C.c_double
+    lib.or_moe_decode.restype = C.c_float
     lib.or_qng64_decode_code.restype = C.c_float
     lib.or_qng64_decode_code.argtypes = [_P, C.c_int, C.c_int]
     lib.or_pool_create.restype = _P
@@ -218,22 +219,35 @@ class Oracle:
 
 
 class OrExpert(C.Structure):
-    _fields_ = [("kind", C.c_int), ("bits", C.c_int), ("packed", C.c_void_p), ("scales", C.c_void_p)]
+    _fields_ = [("kind", C.c_int), ("bits", C.c_int), ("packed", C.c_void_p), ("scales", C.c_void_p),
+                ("bias", C.c_void_p)]
 
 
-def expert_struct(kind, bits, packed, scales):
-    return OrExpert(kind, bits, packed.ctypes.data, scales.ctypes.data)
+def expert_struct(kind, bits, packed, scales, bias=None):
+    return OrExpert(kind, bits, packed.ctypes.data, scales.ctypes.data if scales is not None else None,
+                    bias.ctypes.data if bias is not None else None)
 
 
 def expert_array(descs):
-    """descs: list of (kind, bits, packed, scales) -> (OrExpert array, keep-alive list)."""
+    """descs: list of (kind, bits, packed, scales[, bias]) -> (OrExpert array, keep-alive list).
+    scales may be None (dense kinds 7 / 8); bias only for kind 6 (int4 affine)."""
     arr = (OrExpert * len(descs))()
     keep = []
-    for e, (kind, bits, pk, sc) in enumerate(descs):
-        pk = np.ascontiguousarray(pk); sc = np.ascontiguousarray(sc)
-        keep += [pk, sc]
-        arr[e] = OrExpert(kind, bits, pk.ctypes.data, sc.ctypes.data)
+    for e, d in enumerate(descs):
+        kind, bits, pk, sc = d[:4]
+        bi = d[4] if len(d) > 4 else None
+        pk = np.ascontiguousarray(pk)
+        sc = np.ascontiguousarray(sc) if sc is not None else None
+        bi = np.ascontiguousarray(bi) if bi is not None else None
+        keep += [pk, sc, bi]
+        arr[e] = expert_struct(kind, bits, pk, sc, bi)
     return arr, keep
+
+
+def moe_decode(oracle, desc, out, inn, row, cols):
+    """or_moe_decode (moe_decode_af) for columns `cols` of one row."""
+    arr, keep = expert_array([desc])
+    return np.array([oracle.lib.or_moe_decode(arr, inn, C.c_long(row), C.c_long(c)) for c in cols], np.float32)
 
 
 def moe_matvec(oracle, desc, out, inn, x):

@@ -52,7 +52,20 @@ def weights(seed, out, inn, sigma=0.02):
 
 
 def desc(oracle, kind, bits, w):
-    """Reference-layout expert descriptor (kind, bits, packed, scales) from the oracle packers."""
+    """Reference-layout expert descriptor (kind, bits, packed, scales[, bias]) from the oracle
+    packers; int4 affine (6) gets seeded random nibbles / scales / biases (any bytes are valid AF
+    int4), dense fp16 (7) / fp32 (8) carry the weights themselves."""
+    if kind == 6:
+        rng = np.random.default_rng(int(abs(w[0, 0]) * 1e9) % (2 ** 31))
+        out, inn = w.shape
+        pk = rng.integers(0, 256, (out, inn // 2), dtype=np.uint8)
+        sc = (rng.random((out, inn // 64), dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+        bi = (rng.standard_normal((out, inn // 64), dtype=np.float32) * np.float32(0.04)).astype(np.float32)
+        return (6, 4, pk, sc, bi)
+    if kind == 7:
+        return (7, 16, w.astype(np.float16).view(np.uint16), None)
+    if kind == 8:
+        return (8, 32, np.ascontiguousarray(w), None)
     if kind == 1:
         p, s = oracle.quantize_q4g64(w)
     elif kind == 2:
@@ -68,7 +81,8 @@ def dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-FORMATS = [(5, 0), (1, 0), (2, 0), (4, 2), (4, 3), (4, 5), (4, 7), (4, 8), (4, 9), (4, 12), (4, 15)]
+FORMATS = [(5, 0), (1, 0), (2, 0), (4, 2), (4, 3), (4, 5), (4, 7), (4, 8), (4, 9), (4, 12), (4, 15), (6, 4), (7, 16),
+           (8, 32)]
 
 
 @pytest.mark.parametrize("kind,bits", FORMATS)
@@ -91,7 +105,7 @@ def test_gather_matvec_parity(ctx, torch_dev, oracle, kind, bits):
 
 def test_gather_mixed_formats(ctx, torch_dev, oracle):
     torch = torch_dev
-    fm = [(5, 0), (2, 0), (4, 7), (4, 15), (1, 0), (4, 2), (5, 0), (4, 10)]
+    fm = [(5, 0), (2, 0), (4, 7), (4, 15), (1, 0), (4, 2), (5, 0), (4, 10), (6, 4), (7, 16), (8, 32)]
     E, out, inn, N = len(fm), 200, 768, 41
     say("gather mixed", E, out, inn, N)
     ds = [desc(oracle, k, b, weights(2000 + e, out, inn)) for e, (k, b) in enumerate(fm)]
@@ -153,11 +167,17 @@ def moe_setup(oracle, seed, E, H, I, Ish, fmts, down_fmts=None, sh_fmt=(5, 0)):
     return gate, up, down, shared
 
 
+def bind_one(ctx, d):
+    k, b, p, sc = d[:4]
+    inn = p.shape[1] if k in (7, 8) else sc.shape[1] * (32 if k == 5 else 64)
+    return ctx.bind(k, p, sc, p.shape[0], inn, bits=b, sub=d[4] if len(d) > 4 else None)
+
+
 def run_moe(ctx, torch, gate, up, down, shared, x, idx, w):
     g, u, d = ctx.bind_experts(gate), ctx.bind_experts(up), ctx.bind_experts(down)
     sh = None
     if shared:
-        sh = tuple(ctx.bind(k, p, s, p.shape[0], s.shape[1] * (32 if k == 5 else 64), bits=b) for (k, b, p, s) in shared)
+        sh = tuple(bind_one(ctx, d) for d in shared)
     out = torch.zeros((x.shape[0], x.shape[1]), dtype=torch.float32, device="cuda")
     ctx.moe_ffn(g, u, d, sh, dev(torch, x), dev(torch, idx), dev(torch, w), out)
     ctx.sync()
@@ -181,11 +201,12 @@ def test_moe_ffn_parity(ctx, torch_dev, oracle, T, Ish, renorm):
 
 
 def test_moe_ffn_mixed_precision(ctx, torch_dev, oracle):
-    """Per-expert precision as the mixed-precision registration allows (q4g32h, int8, qNg64)."""
+    """Per-expert precision as the mixed-precision registration allows (q4g32h, int8, qNg64, AF
+    int4 affine, dense fp16 / fp32)."""
     torch = torch_dev
     E, H, I, K, T, Ish = 12, 320, 256, 3, 9, 256
     say("moe_ffn mixed", E, H, I, K, T)
-    fm = [(5, 0), (2, 0), (4, 7), (4, 9), (4, 11), (4, 15)]
+    fm = [(5, 0), (2, 0), (4, 7), (4, 9), (6, 4), (4, 15), (7, 16), (8, 32), (4, 11)]
     gate, up, down, shared = moe_setup(oracle, 5000, E, H, I, Ish, fm, down_fmts=fm[::-1], sh_fmt=(2, 0))
     x = seeded_normal(70, (T, H))
     idx, w = oracle.route(seeded_normal(71, (T, E)), K, True)
@@ -246,7 +267,7 @@ def test_moe_graph_replays_match_eager(ctx, torch_dev, oracle):
     s = torch.cuda.Stream()
     gc = beglin_amd.Context(0, stream=s.cuda_stream)
     g, u, d = gc.bind_experts(gate), gc.bind_experts(up), gc.bind_experts(down)
-    sh = tuple(gc.bind(k, p, sc, p.shape[0], sc.shape[1] * (32 if k == 5 else 64), bits=b) for (k, b, p, sc) in shared)
+    sh = tuple(bind_one(gc, d) for d in shared)
     out = torch.zeros((T, H), dtype=torch.float32, device="cuda")
     with torch.cuda.stream(s):
         gc.moe_ffn(g, u, d, sh, x, idx, w, out)          # eager call sizes every scratch buffer

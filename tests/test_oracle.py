@@ -454,3 +454,54 @@ def test_moe_ffn_equals_decoded_pipeline(oracle):
     # dropping the shared expert or one routed pair moves the result far outside that bar
     no_sh = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
     assert np.max(np.abs(no_sh - want)) > 1e-3 * np.max(np.abs(want))
+
+
+def _af_descs(oracle, out=24, inn=256, seed=11):
+    """One descriptor per MoE row kind: (kind, bits, packed, scales[, bias])."""
+    rng = np.random.default_rng(seed)
+    w = seeded_normal(seed, (out, inn), 0.02)
+    ng = inn // 64
+    p1, s1 = oracle.quantize_q4g64(w)
+    p2, s2 = oracle.quantize_q8g64(w)
+    p4, s4 = oracle.quantize_qng64_dense(w, 9)
+    p5, s5 = oracle.quantize_q4g32h(w)
+    nib = rng.integers(0, 256, (out, inn // 2), dtype=np.uint8)
+    sa = (rng.random((out, ng), dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    ba = (rng.standard_normal((out, ng), dtype=np.float32) * np.float32(0.03)).astype(np.float32)
+    f16 = w.astype(np.float16).view(np.uint16)
+    return {1: (1, 4, p1, s1), 2: (2, 8, p2, s2), 4: (4, 9, p4, s4), 5: (5, 4, p5, s5),
+            6: (6, 4, nib, sa, ba), 7: (7, 16, f16, None), 8: (8, 32, w, None)}
+
+
+def test_moe_decode_and_row_agree_for_every_kind(oracle):
+    """or_moe_row (the per-kind row loops of moe_matvec_af_row) equals the double dot over
+    or_moe_decode (moe_decode_af) -- two separate restatements of each kind's decode."""
+    from oracle_ffi import expert_array, moe_decode
+    out, inn = 24, 256
+    x = seeded_normal(12, (inn,))
+    for kind, d in _af_descs(oracle, out, inn).items():
+        arr, keep = expert_array([d])
+        for r in (0, 7, out - 1):
+            dec = moe_decode(oracle, d, out, inn, r, range(inn)).astype(np.float64)
+            row = oracle.lib.or_moe_row(arr, inn, C.c_long(r), _ptr(x))
+            assert abs(row - dec @ x.astype(np.float64)) <= 1e-12 * max(1.0, abs(row)), kind
+
+
+def test_moe_decode_dense_and_affine_fixed_points(oracle):
+    """fp16 decode == numpy's float16 widening; fp32 decode returns the stored float; int4 affine
+    with bias = -8*scale reproduces the symmetric int4 decode to within one rounding."""
+    from oracle_ffi import moe_decode
+    out, inn = 24, 256
+    d = _af_descs(oracle, out, inn)
+    f16 = d[7][2]
+    for r in (0, 5):
+        got = moe_decode(oracle, d[7], out, inn, r, range(inn))
+        assert np.array_equal(got, f16[r].view(np.float16).astype(np.float32))
+        assert np.array_equal(moe_decode(oracle, d[8], out, inn, r, range(inn)), d[8][2][r])
+    p1, s1 = d[1][2], d[1][3]
+    aff = (6, 4, p1, s1, (np.float32(-8.0) * s1).astype(np.float32))
+    for r in (0, 3, 11):
+        sym = moe_decode(oracle, d[1], out, inn, r, range(inn))
+        af = moe_decode(oracle, aff, out, inn, r, range(inn))
+        tol = np.repeat(s1[r], 64) * np.float32(2 ** -20)
+        assert np.all(np.abs(af - sym) <= tol)
