@@ -190,10 +190,27 @@ class MoeWorkload:
                 t.free()
 
 
+EAGER = False        # --eager: launch the step's kernels directly (counter-collection runs)
+
+
 def time_graph(torch, stream, fn, steps, warmup):
     with torch.cuda.stream(stream):
         fn()                                   # eager once: reserves every scratch buffer
     torch.cuda.synchronize()
+    if EAGER:
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record(stream)
+            for _ in range(steps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+        return e0.elapsed_time(e1) / steps, wall, None
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         fn()
@@ -375,6 +392,18 @@ def cpu_baseline_rotated(kind, bits, out, inn, budget_s, seed=7):
             "sample": f"one {out}x{inn} tensor (kind {kind}, n={bits}), {reps} calls over {dt * reps:.1f} s, {T} threads"}
 
 
+def copy_calib(mib):
+    import torch
+    n = (mib << 20) // 4
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calib_bytes_read": n * 4, "copy_calib_bytes_written": n * 4, "launches": 5}), flush=True)
+
+
 # ------------------------------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -389,7 +418,17 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--eager", action="store_true", help="no HIP graph: launch every kernel directly (for "
+                    "rocprofv3 --pmc passes); timings then include host launch gaps")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB 5 times (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes) and exit")
     args = ap.parse_args()
+    if args.copy_calib:
+        copy_calib(args.copy_calib)
+        return
+    global EAGER
+    EAGER = args.eager
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -474,6 +513,17 @@ def main():
             "launches_per_step": launches, "kernel_us_per_launch": round(k_ms * 1e3 / launches, 3),
             "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3),
             "bytes_per_launch": round(nbytes / launches)}
+
+    # HBM traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this
+    # same workload, scaled by a known-size copy (profiles/traffic.json)
+    if args.workload == "cfg2" and M == 1 and args.layers == 28:
+        try:
+            tr = json.load(open(os.path.join(ROOT, "profiles", "traffic.json")))["cfg2_M1"]
+            roof["traffic"] = tr["traffic_bytes_per_launch"]
+            roof["traffic_over_algorithmic"] = round(tr["traffic_bytes_per_launch"] / (nbytes / launches), 3)
+            roof["traffic_source"] = tr["summary"]
+        except (OSError, KeyError, ValueError):
+            pass
 
     cpu = None
     if not args.no_cpu:

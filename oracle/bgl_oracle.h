@@ -8,6 +8,22 @@
  * Every function cites the reference file:line it restates (paths relative to the
  * reference repository root).  Build: oracle/Makefile, compiled with -ffp-contract=off
  * so every fp32 expression rounds exactly as written (the literal C semantics).
+ *
+ * Parity status (what pins each function; tests/test_oracle.py):
+ *   - or_quantize_q4g64_ef / _q8g64 / _qng64_gguf / _qng64_dense / _q4_0, or_decode_*,
+ *     or_qng64_decode_code, or_qng64_matvec_f32: byte-exact against the reference's own C
+ *     (oracle/_ref, built from the reference sources), the tiny_st control constants and the
+ *     qng64_dense_test KAT.
+ *   - or_f32_to_f16 / or_f16_to_f32: exhaustive over all 2^16 halves / IEEE RNE cases.
+ *   - or_gemm_f32, or_moe_row, or_moe_decode, or_moe_matvec: equal to the double product over
+ *     independently decoded weights; the reference's vDSP_dotpr summation order (closed
+ *     Accelerate library) is parity unpinned beyond the 1e-5 tolerance.
+ *   - or_quant_act_i8, or_gemm_*_sdot, or_matmul_sdot: reference rounding cases + the identity
+ *     against the de-quantized product + batched == per-column.
+ *   - or_quantize_g256sf: parity unpinned (the reference ships no g256sf emitter); held to its
+ *     invariants (sub codes in [1,63], effective scale >= group max / 7, decode error bound).
+ *   - or_moe_route / _softmax_full / _top_k_select / _topk_renorm: brute force; or_moe_ffn_*:
+ *     bucketed == naive and a dense float64 pipeline over decoded weights.
  */
 #ifndef BGL_ORACLE_H
 #define BGL_ORACLE_H
