@@ -97,6 +97,8 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     if (c->force_tr != 0 && c->force_tr != 8 && c->force_tr != 16 && c->force_tr != 32 && c->force_tr != 64) c->force_tr = 0;
     const char *nf = getenv("BGL_NO_FUSED_Q");
     c->no_fused = nf && atoi(nf) != 0;
+    const char *nm = getenv("BGL_NO_MFMA");
+    c->no_mfma = nm && atoi(nm) != 0;
     *out = c;
     return 0;
 }
@@ -574,6 +576,11 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
         return bgl_fail(BGL_E_UNSUPPORTED, "kind %d has fp32-activation kernels only", kind);
     HIPCHK(hipSetDevice(c->device));
     if (act == BGL_ACT_W4A8 && fused_q_ok(c, kind, Ts[0].K, M)) return run_gemv_q(c, n, Ts, x_dev, bias_dev, y_dev);
+    if (act == BGL_ACT_F32 && M >= BGL_MFMA_MIN_M && !c->no_mfma) {
+        bool ok = true;
+        for (int i = 0; i < n; i++) ok = ok && bgl_mfma_ok(Ts[i].fmt, Ts[i].bits);
+        if (ok) return run_gemm_mfma(c, n, Ts, x_dev, M, bias_dev, y_dev, nullptr);
+    }
     GemvAct A;
     int rc = prep_act(c, act, act_group(kind), x_dev, M, Ts[0].K, A);
     if (rc) return rc;

@@ -27,6 +27,7 @@ struct bgl_ctx {
     bool own_stream = false;
     int max_waves = 16;                   // wavefronts per GEMV workgroup cap (BGL_MAX_WAVES)
     bool no_fused = false;                // BGL_NO_FUSED_Q=1: W4A8 M=1 through the separate prep kernel
+    bool no_mfma = false;                 // BGL_NO_MFMA=1: fp32-activation M >= 16 through the dot4 kernels
     int min_blocks = 256;                 // fused W4A8: split tiles until at least this many workgroups
     int force_tr = 0;                     // BGL_FORCE_TR: fixed rows per workgroup (tuning)
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
@@ -53,3 +54,8 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
 int pick_waves(bgl_ctx *c, int nunits);
 int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &A, int M,
              const float *const *bias, float *const *y, const int *ystride);
+// Batched fp32-activation GEMM on the matrix cores (bgl_mfma.hip): formats it takes, and the call.
+#define BGL_MFMA_MIN_M 16
+bool bgl_mfma_ok(int fmt, int bits);
+int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
+                  float *const *y, const int *ystride);

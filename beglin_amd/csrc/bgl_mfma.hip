@@ -1,0 +1,416 @@
+// bgl_mfma.hip -- batched GEMM for M >= 16 activation rows on the gfx950 fp16 matrix cores
+// (the M-column case of gemm_qXg64_mt / qng64_matmul_f32, q4gemv.h:761-769, qng64_dense.c:70-79).
+//
+// Numerics.  Weight codes are exact in fp16 (int4 and int8 codes, qNg64 codes for n <= 10), so
+// the decode is exact.  Each activation column is scaled by a power of two so its largest
+// magnitude lies in [2^13, 2^14), then split as hi = fp16(x'), lo = fp16(x' - hi): hi + lo holds
+// x' to about 2^-22 of the column maximum.  v_mfma_f32_16x16x32_f16 multiplies exactly and
+// accumulates in fp32; each quantization group's partial sum is folded with its fp32 scale (one
+// FMA per output per group) and the column factor 2^-(14-e) is applied at the end.
+//
+// Layout.  A (weights, 16 rows x 32 k per instruction): lane l holds row l%16 and the 8 elements
+// 8*(l/16)..+7 of the 32-element K-step -- with the device's 16-byte chunk layout that is one
+// dword (int4) or two (int8) per lane and row block, and a wave's load covers 256 contiguous
+// bytes.  The int4 nibble order (byte i: element i low, element 4+i high) decodes into halves in
+// the order {0,2,1,3,4,6,5,7}; the activation fragments are stored in that same order, since the
+// MFMA only needs A and B to agree element for element.  B (activations, 32 k x 16 columns):
+// lane l holds column l%16, elements 8*(l/16)..+7.  D: lane l holds column l%16, rows
+// 4*(l/16)..+3 of the 16-row block.
+//
+// Work split.  A workgroup = 4 waves = 4 consecutive 64-row weight tiles (256 rows) over one
+// K range; the 4 waves share the activation fragments of that range, staged through LDS in
+// blocks of MF_KC K-steps (double buffered).  Each wave computes its tile's 4 row blocks x CT
+// column tiles.  Shapes with few tiles split K over blockIdx.y into fp32 partials that
+// k_splitk_reduce adds in split order (deterministic; no atomics).
+#include <string.h>
+
+#include "bgl_gemv_impl.h"
+#include "bgl_internal.h"
+
+#define HIPCHK(expr)                                                                             \
+    do {                                                                                         \
+        hipError_t e_ = (expr);                                                                  \
+        if (e_ != hipSuccess) return bgl_fail(BGL_E_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+typedef _Float16 mf_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mf_h2 __attribute__((ext_vector_type(2)));
+typedef float mf_f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int mf_u4 __attribute__((ext_vector_type(4)));
+
+#define MF_WAVES 4           // waves per workgroup = 64-row weight tiles per workgroup
+#define MF_KC 4              // K-steps (32 elements each) per staged activation block
+#define MF_MAXCT 4           // column tiles (16 columns each) per launch: up to 64 columns
+#define MF_MAXN 10           // qNg64 widths whose codes are exact in fp16 via the 1024+u trick
+
+static inline unsigned nblk(long n, int bs = 256) { return (unsigned)((n + bs - 1) / bs); }
+
+struct MfmaLaunch {
+    BglDevTensor T;
+    const uint4 *xf;         // activation fragments [K/32][CT][2][64] x 16 B
+    const float *colinv;     // [16*CT] column factors 2^(e-14)
+    const float *bias;       // [N] or null
+    float *y;                // y[m][n] at y + m*ystride + n
+    int ystride;
+    float *part;             // K-split partials [S][M][N] (S > 1)
+    int M;                   // valid columns (<= 16*CT)
+    int kps;                 // K-steps per split
+};
+
+// ==================================================================================== activations
+// One workgroup per column m < 16*CT (columns >= M are zero).  x: [M][K] rows of this launch.
+__global__ __launch_bounds__(256) void k_act_frag(const float *__restrict__ x, int M, int K, int CT,
+                                                  uint4 *__restrict__ xf, float *__restrict__ colinv) {
+    __shared__ float wmax[4];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const float *xr = x + (size_t)m * K;
+    float mx = 0.0f;
+    if (m < M)
+        for (int k = t; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+    mx = wave_max_f32(mx);
+    if ((t & 63) == 0) wmax[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int e = 0;
+    if (mx > 0.0f) frexpf(mx, &e);                       // mx in [2^(e-1), 2^e)
+    const float sc = mx > 0.0f ? ldexpf(1.0f, 14 - e) : 1.0f;
+    if (t == 0) colinv[m] = mx > 0.0f ? ldexpf(1.0f, e - 14) : 1.0f;
+    const int ct = m >> 4, ml = m & 15;
+    for (int g = t; g < K / 8; g += 256) {               // one 8-element slot per iteration
+        const int k0 = 8 * g, s = k0 >> 5, q = (k0 & 31) >> 3;
+        const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+        _Float16 hi[8], lo[8];
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const float v = m < M ? xr[k0 + perm[p]] * sc : 0.0f;   // power-of-two scaling: exact
+            const _Float16 h = (_Float16)v;
+            hi[p] = h;
+            lo[p] = (_Float16)(v - (float)h);
+        }
+        uint4 H, L;
+        memcpy(&H, hi, 16);
+        memcpy(&L, lo, 16);
+        const size_t base = ((size_t)s * CT + ct) * 2 * 64 + ml + 16 * q;
+        xf[base] = H;
+        xf[base + 64] = L;
+    }
+}
+
+// ==================================================================================== weights
+// Raw A-fragment words of one K-step for one lane (row 16*rb + lane%16, slot q = lane/16).
+template <int FMT, int NB> struct ARaw { uint32_t w[1]; };
+template <int NB> struct ARaw<BGL_Q8G64, NB> { uint32_t w[2]; };
+template <int NB> struct ARaw<BGL_QNG64, NB> {
+    static constexpr int H8 = (NB >> 3) & 1, H4 = (NB >> 2) & 1, H2 = (NB >> 1) & 1, H1 = NB & 1;
+    uint32_t w[2 * H8 + H4 + H2 + H1 > 0 ? 2 * H8 + H4 + H2 + H1 : 1];
+};
+
+template <int FMT> constexpr int ksteps_per_unit() { return FMT == BGL_QNG64 ? 4 : 2; }
+
+template <int FMT, int NB>
+__device__ __forceinline__ void ld_a(ARaw<FMT, NB> &a, const BglDevTensor &T, int tile, int rb, int s, int lane) {
+    const int row = 16 * rb + (lane & 15), q = lane >> 4;
+    constexpr int SPU = ksteps_per_unit<FMT>();
+    const int u = s / SPU, j = s % SPU;
+    const BGL_GLOBAL uint8_t *base = (const BGL_GLOBAL uint8_t *)T.w;
+    auto chunk = [&](int c) { return base + (((size_t)tile * T.cpr + (size_t)u * T.cpu + c) * BGL_TILE + row) * 16; };
+    if constexpr (FMT == BGL_Q8G64) {
+        const BGL_GLOBAL uint32_t *p = (const BGL_GLOBAL uint32_t *)(chunk(2 * j + (q >> 1)) + 8 * (q & 1));
+        a.w[0] = p[0]; a.w[1] = p[1];
+    } else if constexpr (FMT == BGL_QNG64) {
+        constexpr int H8 = ARaw<FMT, NB>::H8, H4 = ARaw<FMT, NB>::H4, H2 = ARaw<FMT, NB>::H2, H1 = ARaw<FMT, NB>::H1;
+        constexpr int K4 = 8 * H8, K2 = K4 + 4 * H4, K1 = K2 + 2 * H2;
+        int i = 0;
+        if constexpr (H8) {
+            const BGL_GLOBAL uint32_t *p = (const BGL_GLOBAL uint32_t *)(chunk(2 * j + (q >> 1)) + 8 * (q & 1));
+            a.w[i++] = p[0]; a.w[i++] = p[1];
+        }
+        if constexpr (H4) a.w[i++] = *(const BGL_GLOBAL uint32_t *)(chunk(K4 + j) + 4 * q);
+        if constexpr (H2) a.w[i++] = *(const BGL_GLOBAL uint32_t *)(chunk(K2 + (j >> 1)) + 4 * (2 * (j & 1) + (q >> 1)));
+        if constexpr (H1) a.w[i++] = *(const BGL_GLOBAL uint32_t *)(chunk(K1) + 4 * j);
+    } else {                                             // int4: chunk j of the unit, dword q
+        a.w[0] = *(const BGL_GLOBAL uint32_t *)(chunk(j) + 4 * q);
+    }
+}
+
+__device__ __forceinline__ uint32_t sub_h2(uint32_t p, _Float16 c) {
+    mf_h2 v = __builtin_bit_cast(mf_h2, p);
+    const mf_h2 cc = {c, c};
+    v = v + cc;                                          // exact: both operands and the result are fp16 integers
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Codes of the lane's 8 elements as halves in the order {0,2,1,3,4,6,5,7}.
+template <int FMT, int NB>
+__device__ __forceinline__ mf_h8 dec_a(const ARaw<FMT, NB> &a, int q) {
+    constexpr uint32_t MAG = 0x64006400u;                // fp16 1024.0 in both halves
+    uint32_t p02, p13, p46, p57;
+    _Float16 off;
+    if constexpr (FMT == BGL_Q8G64) {
+        const uint32_t x0 = a.w[0] ^ 0x80808080u, x1 = a.w[1] ^ 0x80808080u;   // u = code + 128
+        p02 = (x0 & 0x00FF00FFu) | MAG; p13 = ((x0 >> 8) & 0x00FF00FFu) | MAG;
+        p46 = (x1 & 0x00FF00FFu) | MAG; p57 = ((x1 >> 8) & 0x00FF00FFu) | MAG;
+        off = (_Float16)-1152.0f;
+    } else if constexpr (FMT == BGL_QNG64) {
+        constexpr int H8 = ARaw<FMT, NB>::H8, H4 = ARaw<FMT, NB>::H4, H2 = ARaw<FMT, NB>::H2, H1 = ARaw<FMT, NB>::H1;
+        constexpr int SH4 = 8 * H8, SH2 = SH4 + 4 * H4, SH1 = SH2 + 2 * H2;
+        uint32_t u02 = 0, u13 = 0, u46 = 0, u57 = 0;
+        int i = 0;
+        if constexpr (H8) {
+            const uint32_t x0 = a.w[i] ^ 0x80808080u, x1 = a.w[i + 1] ^ 0x80808080u;
+            u02 = x0 & 0x00FF00FFu; u13 = (x0 >> 8) & 0x00FF00FFu;
+            u46 = x1 & 0x00FF00FFu; u57 = (x1 >> 8) & 0x00FF00FFu;
+            i += 2;
+        }
+        if constexpr (H4) {
+            const uint32_t w = a.w[i++];
+            u02 |= (w & 0x000F000Fu) << SH4; u13 |= ((w >> 8) & 0x000F000Fu) << SH4;
+            u46 |= ((w >> 4) & 0x000F000Fu) << SH4; u57 |= ((w >> 12) & 0x000F000Fu) << SH4;
+        }
+        if constexpr (H2) {
+            const uint32_t w = a.w[i++] >> (4 * (q & 1));   // crumbs 2(q%2) (elements 0..3) and +1 (4..7)
+            u02 |= (w & 0x00030003u) << SH2; u13 |= ((w >> 8) & 0x00030003u) << SH2;
+            u46 |= ((w >> 2) & 0x00030003u) << SH2; u57 |= ((w >> 10) & 0x00030003u) << SH2;
+        }
+        if constexpr (H1) {
+            const uint32_t w = a.w[i++] >> (2 * q);          // bits 2q (elements 0..3) and 2q+1 (4..7)
+            u02 |= (w & 0x00010001u) << SH1; u13 |= ((w >> 8) & 0x00010001u) << SH1;
+            u46 |= ((w >> 1) & 0x00010001u) << SH1; u57 |= ((w >> 9) & 0x00010001u) << SH1;
+        }
+        p02 = u02 | MAG; p13 = u13 | MAG; p46 = u46 | MAG; p57 = u57 | MAG;
+        off = (_Float16)(-(1024.0f + (float)(1 << (NB - 1))));
+    } else {
+        const uint32_t w = a.w[0];
+        p02 = (w & 0x000F000Fu) | MAG; p13 = ((w >> 8) & 0x000F000Fu) | MAG;
+        p46 = ((w >> 4) & 0x000F000Fu) | MAG; p57 = ((w >> 12) & 0x000F000Fu) | MAG;
+        off = (_Float16)-1032.0f;
+    }
+    mf_u4 r = {sub_h2(p02, off), sub_h2(p13, off), sub_h2(p46, off), sub_h2(p57, off)};
+    return __builtin_bit_cast(mf_h8, r);
+}
+
+// Scales of rows 16*rb + 4*(lane/16) + v (v = 0..3) for group g of unit u: the D rows of the lane.
+template <int FMT>
+__device__ __forceinline__ mf_f4 ld_scales(const BglDevTensor &T, int tile, int rb, int u, int lane, int g) {
+    const size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + 16 * rb + 4 * (lane >> 4);
+    mf_f4 s;
+    if constexpr (FMT == BGL_QNG64) {                    // float2 per row: group g of the pair
+        const BGL_GLOBAL float *p = (const BGL_GLOBAL float *)T.s0 + 2 * so + g;
+        s[0] = p[0]; s[1] = p[2]; s[2] = p[4]; s[3] = p[6];
+    } else if constexpr (FMT == BGL_Q4G32H) {            // u32 per row: two fp16, half g (32 elements)
+        const BGL_GLOBAL uint32_t *p = (const BGL_GLOBAL uint32_t *)T.s0 + so;
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            s[v] = __half2float(__ushort_as_half((unsigned short)(g ? (p[v] >> 16) : (p[v] & 0xffffu))));
+    } else {
+        const BGL_GLOBAL float *p = (const BGL_GLOBAL float *)T.s0 + so;
+        s[0] = p[0]; s[1] = p[1]; s[2] = p[2]; s[3] = p[3];
+    }
+    return s;
+}
+
+// ==================================================================================== GEMM kernel
+template <int FMT, int NB, int CT>
+__global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
+    __shared__ uint4 stage[2][MF_KC * CT * 2 * 64];
+    const BglDevTensor &T = L.T;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4;
+    const int tile = blockIdx.x * MF_WAVES + wave;
+    const bool active = tile < T.ntiles;
+    const int KS = T.K >> 5;
+    const int s0 = blockIdx.y * L.kps, s1 = min(s0 + L.kps, KS);
+    const int nblocks = (s1 - s0 + MF_KC - 1) / MF_KC;
+    constexpr int SPU = ksteps_per_unit<FMT>();
+    constexpr int SPG = FMT == BGL_Q4G32H ? 1 : 2;       // K-steps per scale group
+    constexpr int PER_T = MF_KC * CT * 2 * 64 / (MF_WAVES * 64);   // uint4 per thread per block
+
+    mf_f4 acc[4][CT], cg[4][CT];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) { acc[r][c] = mf_f4{0, 0, 0, 0}; cg[r][c] = mf_f4{0, 0, 0, 0}; }
+
+    // activation block b -> registers (K-steps past s1 read as zeros)
+    uint4 breg[PER_T];
+    auto load_b = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < PER_T; i++) {
+            const int e = threadIdx.x + i * MF_WAVES * 64;             // index within the block
+            const int j = e / (CT * 2 * 64);
+            const int s = s0 + b * MF_KC + j;
+            breg[i] = s < s1 ? L.xf[(size_t)(s0 + b * MF_KC) * CT * 2 * 64 + e] : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store_b = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < PER_T; i++) stage[buf][threadIdx.x + i * MF_WAVES * 64] = breg[i];
+    };
+
+    load_b(0);
+    store_b(0);
+    __syncthreads();
+    for (int b = 0; b < nblocks; b++) {
+        if (b + 1 < nblocks) load_b(b + 1);
+        if (active) {
+#pragma unroll
+            for (int j = 0; j < MF_KC; j++) {
+                const int s = s0 + b * MF_KC + j;
+                if (s >= s1) break;
+                mf_h8 A[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++) {
+                    ARaw<FMT, NB> a;
+                    ld_a<FMT, NB>(a, T, tile, rb, s, lane);
+                    A[rb] = dec_a<FMT, NB>(a, q);
+                }
+#pragma unroll
+                for (int c = 0; c < CT; c++) {
+                    const uint4 bh = stage[b & 1][((j * CT + c) * 2 + 0) * 64 + lane];
+                    const uint4 bl = stage[b & 1][((j * CT + c) * 2 + 1) * 64 + lane];
+                    const mf_h8 Bh = __builtin_bit_cast(mf_h8, bh), Bl = __builtin_bit_cast(mf_h8, bl);
+#pragma unroll
+                    for (int rb = 0; rb < 4; rb++) {
+                        cg[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb], Bh, cg[rb][c], 0, 0, 0);
+                        cg[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb], Bl, cg[rb][c], 0, 0, 0);
+                    }
+                }
+                if ((s + 1) % SPG == 0) {                 // group complete: fold with its scales
+                    const int u = s / SPU;
+                    const int g = FMT == BGL_Q4G32H ? (s & 1) : (FMT == BGL_QNG64 ? ((s % SPU) >> 1) : 0);
+#pragma unroll
+                    for (int rb = 0; rb < 4; rb++) {
+                        const mf_f4 sc = ld_scales<FMT>(T, tile, rb, u, lane, g);
+#pragma unroll
+                        for (int c = 0; c < CT; c++) {
+#pragma unroll
+                            for (int v = 0; v < 4; v++) acc[rb][c][v] = __fmaf_rn(cg[rb][c][v], sc[v], acc[rb][c][v]);
+                            cg[rb][c] = mf_f4{0, 0, 0, 0};
+                        }
+                    }
+                }
+            }
+        }
+        if (b + 1 < nblocks) store_b((b + 1) & 1);
+        __syncthreads();
+    }
+    if (!active) return;
+
+    const int nsplit = gridDim.y;
+#pragma unroll
+    for (int rb = 0; rb < 4; rb++) {
+        const int n0 = tile * BGL_TILE + 16 * rb + 4 * q;
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            const int m = 16 * c + (lane & 15);
+            if (m >= L.M) continue;
+            const float ci = L.colinv[m];
+            float *dst = nsplit > 1 ? L.part + ((size_t)blockIdx.y * L.M + m) * T.N : L.y + (size_t)m * L.ystride;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int n = n0 + v;
+                if (n < T.N) {
+                    float o = acc[rb][c][v] * ci;
+                    if (nsplit == 1 && L.bias) o += L.bias[n];
+                    dst[n] = o;
+                }
+            }
+        }
+    }
+}
+
+// ==================================================================================== host side
+bool bgl_mfma_ok(int fmt, int bits) {
+    if (fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64) return true;
+    return fmt == BGL_QNG64 && bits >= 2 && bits <= MF_MAXN;
+}
+
+template <int FMT, int NB>
+static int launch_fmt(const MfmaLaunch &L, int CT, dim3 grid, hipStream_t st) {
+    switch (CT) {
+    case 1: hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, 1>), grid, dim3(MF_WAVES * 64), 0, st, L); return 0;
+    case 2: hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, 2>), grid, dim3(MF_WAVES * 64), 0, st, L); return 0;
+    case 3: hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, 3>), grid, dim3(MF_WAVES * 64), 0, st, L); return 0;
+    case 4: hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, 4>), grid, dim3(MF_WAVES * 64), 0, st, L); return 0;
+    default: return -1;
+    }
+}
+
+static int launch_any(const MfmaLaunch &L, int CT, dim3 grid, hipStream_t st) {
+    switch (L.T.fmt) {
+    case BGL_Q4G64: return launch_fmt<BGL_Q4G64, 0>(L, CT, grid, st);
+    case BGL_Q4G32H: return launch_fmt<BGL_Q4G32H, 0>(L, CT, grid, st);
+    case BGL_Q8G64: return launch_fmt<BGL_Q8G64, 0>(L, CT, grid, st);
+    case BGL_QNG64:
+        switch (L.T.bits) {
+        case 2: return launch_fmt<BGL_QNG64, 2>(L, CT, grid, st);
+        case 3: return launch_fmt<BGL_QNG64, 3>(L, CT, grid, st);
+        case 4: return launch_fmt<BGL_QNG64, 4>(L, CT, grid, st);
+        case 5: return launch_fmt<BGL_QNG64, 5>(L, CT, grid, st);
+        case 6: return launch_fmt<BGL_QNG64, 6>(L, CT, grid, st);
+        case 7: return launch_fmt<BGL_QNG64, 7>(L, CT, grid, st);
+        case 8: return launch_fmt<BGL_QNG64, 8>(L, CT, grid, st);
+        case 9: return launch_fmt<BGL_QNG64, 9>(L, CT, grid, st);
+        case 10: return launch_fmt<BGL_QNG64, 10>(L, CT, grid, st);
+        default: return -1;
+        }
+    default: return -1;
+    }
+}
+
+// y[m][n] = bias[n] + sum_k W[n][k] x[m][k] for the n tensors of a group sharing x, M >= 1 columns
+// (the caller routes M >= 16 here).  Columns go in launches of up to 64.
+int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
+                  float *const *y, const int *ystride) {
+    const int K = Ts[0].K;
+    if (K % 64) return bgl_fail(BGL_E_ARG, "MFMA path: in=%d %% 64 != 0", K);
+    for (int i = 0; i < n; i++)
+        if (!bgl_mfma_ok(Ts[i].fmt, Ts[i].bits)) return bgl_fail(BGL_E_UNSUPPORTED, "MFMA path: kind %d", Ts[i].fmt);
+    const int KS = K / 32;
+    for (int m0 = 0; m0 < M; m0 += 16 * MF_MAXCT) {
+        const int Mc = M - m0 < 16 * MF_MAXCT ? M - m0 : 16 * MF_MAXCT;
+        const int CT = (Mc + 15) / 16;
+        const size_t fbytes = (size_t)KS * CT * 2 * 64 * 16;
+        if (dbuf_reserve(c, c->act_w, fbytes, false) || dbuf_reserve(c, c->act_s, (size_t)16 * CT * 4, false)) return BGL_E_NOMEM;
+        int tok = prof_begin(c, 0);
+        hipLaunchKernelGGL(k_act_frag, dim3(16 * CT), dim3(256), 0, c->stream, x_dev + (size_t)m0 * K, Mc, K, CT,
+                           (uint4 *)c->act_w.p, (float *)c->act_s.p);
+        prof_end(c, tok);
+        HIPCHK(hipGetLastError());
+        c->prep_act = -1;                                 // the activation buffers now hold fragments
+        for (int i = 0; i < n; i++) {
+            const BglDevTensor &T = Ts[i];
+            const int wgr = (T.ntiles + MF_WAVES - 1) / MF_WAVES;
+            const int spu = T.fmt == BGL_QNG64 ? 4 : 2;
+            int S = (c->min_blocks + wgr - 1) / wgr;     // split K until the grid has ~min_blocks workgroups
+            int maxS = KS / (2 * MF_KC);                  // at least two staged blocks per split
+            if (maxS > 16) maxS = 16;
+            if (S > maxS) S = maxS;
+            if (S < 1) S = 1;
+            int kps = (KS + S - 1) / S;
+            kps = (kps + spu - 1) / spu * spu;            // splits end on unit boundaries
+            S = (KS + kps - 1) / kps;
+            MfmaLaunch L;
+            memset(&L, 0, sizeof L);
+            L.T = T; L.xf = (const uint4 *)c->act_w.p; L.colinv = (const float *)c->act_s.p;
+            L.bias = bias ? bias[i] : nullptr;
+            const int ys = ystride ? ystride[i] : T.N;
+            L.y = y[i] + (size_t)m0 * ys; L.ystride = ys; L.M = Mc; L.kps = kps;
+            if (S > 1) {
+                if (dbuf_reserve(c, c->part, (size_t)S * Mc * T.N * 4, false)) return BGL_E_NOMEM;
+                L.part = (float *)c->part.p;
+            }
+            tok = prof_begin(c, 1);
+            if (launch_any(L, CT, dim3(wgr, S), c->stream)) return bgl_fail(BGL_E_UNSUPPORTED, "MFMA path: format");
+            prof_end(c, tok);
+            HIPCHK(hipGetLastError());
+            if (S > 1) {
+                tok = prof_begin(c, 2);
+                hipLaunchKernelGGL(k_splitk_reduce, dim3(nblk((long)Mc * T.N)), dim3(256), 0, c->stream,
+                                   (const float *)c->part.p, S, Mc, T.N, L.bias, L.y, ys);
+                prof_end(c, tok);
+                HIPCHK(hipGetLastError());
+            }
+        }
+    }
+    return 0;
+}
