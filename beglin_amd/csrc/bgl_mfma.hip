@@ -38,7 +38,9 @@ typedef _Float16 mf_h2 __attribute__((ext_vector_type(2)));
 typedef float mf_f4 __attribute__((ext_vector_type(4)));
 typedef unsigned int mf_u4 __attribute__((ext_vector_type(4)));
 
-#define MF_WAVES 4           // waves per workgroup = 64-row weight tiles per workgroup
+#define MF_TILES 4           // 64-row weight tiles per workgroup (they share the staged activations)
+#define MF_RBW 2             // 16-row blocks per wave: two waves per tile
+#define MF_WAVES (MF_TILES * 4 / MF_RBW)
 #define MF_KC 4              // K-steps (32 elements each) per staged activation block
 #define MF_MAXCT 4           // column tiles (16 columns each) per launch: up to 64 columns
 #define MF_MAXN 10           // qNg64 widths whose codes are exact in fp16 via the 1024+u trick
@@ -58,15 +60,32 @@ struct MfmaLaunch {
 };
 
 // ==================================================================================== activations
-// One workgroup per column m < 16*CT (columns >= M are zero).  x: [M][K] rows of this launch.
+// Grid (16*CT columns, K/2048 chunks); columns >= M are zero.  x: [M][K] rows of this launch.
+// Every chunk's workgroup reduces its column's max over all of K (the column is L2-resident), so
+// the split needs no second pass.
+#define MF_PREP_CHUNK 2048
 __global__ __launch_bounds__(256) void k_act_frag(const float *__restrict__ x, int M, int K, int CT,
                                                   uint4 *__restrict__ xf, float *__restrict__ colinv) {
     __shared__ float wmax[4];
     const int m = blockIdx.x, t = threadIdx.x;
     const float *xr = x + (size_t)m * K;
     float mx = 0.0f;
-    if (m < M)
-        for (int k = t; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+    if (m < M) {                                         // K % 64 == 0: whole float4s, 4 in flight per thread
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+        const int n4 = K >> 2;
+        int k = t;
+        for (; k + 3 * 256 < n4; k += 4 * 256) {
+            const float4 a = x4[k], b = x4[k + 256], c = x4[k + 512], d = x4[k + 768];
+            mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                 fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+            mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))),
+                                 fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w)))));
+        }
+        for (; k < n4; k += 256) {
+            const float4 a = x4[k];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        }
+    }
     mx = wave_max_f32(mx);
     if ((t & 63) == 0) wmax[t >> 6] = mx;
     __syncthreads();
@@ -74,26 +93,26 @@ __global__ __launch_bounds__(256) void k_act_frag(const float *__restrict__ x, i
     int e = 0;
     if (mx > 0.0f) frexpf(mx, &e);                       // mx in [2^(e-1), 2^e)
     const float sc = mx > 0.0f ? ldexpf(1.0f, 14 - e) : 1.0f;
-    if (t == 0) colinv[m] = mx > 0.0f ? ldexpf(1.0f, e - 14) : 1.0f;
+    if (t == 0 && blockIdx.y == 0) colinv[m] = mx > 0.0f ? ldexpf(1.0f, e - 14) : 1.0f;
     const int ct = m >> 4, ml = m & 15;
-    for (int g = t; g < K / 8; g += 256) {               // one 8-element slot per iteration
-        const int k0 = 8 * g, s = k0 >> 5, q = (k0 & 31) >> 3;
-        const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-        _Float16 hi[8], lo[8];
+    const int g = blockIdx.y * (MF_PREP_CHUNK / 8) + t;  // one 8-element slot per thread
+    if (g >= K / 8) return;
+    const int k0 = 8 * g, s = k0 >> 5, q = (k0 & 31) >> 3;
+    const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    _Float16 hi[8], lo[8];
 #pragma unroll
-        for (int p = 0; p < 8; p++) {
-            const float v = m < M ? xr[k0 + perm[p]] * sc : 0.0f;   // power-of-two scaling: exact
-            const _Float16 h = (_Float16)v;
-            hi[p] = h;
-            lo[p] = (_Float16)(v - (float)h);
-        }
-        uint4 H, L;
-        memcpy(&H, hi, 16);
-        memcpy(&L, lo, 16);
-        const size_t base = ((size_t)s * CT + ct) * 2 * 64 + ml + 16 * q;
-        xf[base] = H;
-        xf[base + 64] = L;
+    for (int p = 0; p < 8; p++) {
+        const float v = m < M ? xr[k0 + perm[p]] * sc : 0.0f;   // power-of-two scaling: exact
+        const _Float16 h = (_Float16)v;
+        hi[p] = h;
+        lo[p] = (_Float16)(v - (float)h);
     }
+    uint4 H, L;
+    memcpy(&H, hi, 16);
+    memcpy(&L, lo, 16);
+    const size_t base = ((size_t)s * CT + ct) * 2 * 64 + ml + 16 * q;
+    xf[base] = H;
+    xf[base + 64] = L;
 }
 
 // ==================================================================================== weights
@@ -189,116 +208,193 @@ __device__ __forceinline__ mf_h8 dec_a(const ARaw<FMT, NB> &a, int q) {
     return __builtin_bit_cast(mf_h8, r);
 }
 
-// Scales of rows 16*rb + 4*(lane/16) + v (v = 0..3) for group g of unit u: the D rows of the lane.
-template <int FMT>
-__device__ __forceinline__ mf_f4 ld_scales(const BglDevTensor &T, int tile, int rb, int u, int lane, int g) {
-    const size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + 16 * rb + 4 * (lane >> 4);
-    mf_f4 s;
-    if constexpr (FMT == BGL_QNG64) {                    // float2 per row: group g of the pair
-        const BGL_GLOBAL float *p = (const BGL_GLOBAL float *)T.s0 + 2 * so + g;
-        s[0] = p[0]; s[1] = p[2]; s[2] = p[4]; s[3] = p[6];
-    } else if constexpr (FMT == BGL_Q4G32H) {            // u32 per row: two fp16, half g (32 elements)
-        const BGL_GLOBAL uint32_t *p = (const BGL_GLOBAL uint32_t *)T.s0 + so;
-#pragma unroll
-        for (int v = 0; v < 4; v++)
-            s[v] = __half2float(__ushort_as_half((unsigned short)(g ? (p[v] >> 16) : (p[v] & 0xffffu))));
-    } else {
-        const BGL_GLOBAL float *p = (const BGL_GLOBAL float *)T.s0 + so;
-        s[0] = p[0]; s[1] = p[1]; s[2] = p[2]; s[3] = p[3];
-    }
-    return s;
+// Raw A words per K-step and row block.  A block is 8 K-steps for int4 with up to 32 columns and 4
+// otherwise: about 8 KiB of weights in flight per wave, two blocks of them in registers.
+template <int FMT, int NB> constexpr int a_words() {
+    return FMT == BGL_Q8G64 ? 2 : FMT == BGL_QNG64 ? 2 * ((NB >> 3) & 1) + ((NB >> 2) & 1) + ((NB >> 1) & 1) + (NB & 1) : 1;
 }
+template <int FMT, int NB, int CT> constexpr int block_ksteps() { return (CT <= 2 && a_words<FMT, NB>() == 1) ? 8 : 4; }
+// bytes of scale data per row and unit in the device layout
+template <int FMT> constexpr int scale_bytes() { return FMT == BGL_QNG64 ? 8 : 4; }
 
 // ==================================================================================== GEMM kernel
 template <int FMT, int NB, int CT>
 __global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
-    __shared__ uint4 stage[2][MF_KC * CT * 2 * 64];
+    constexpr int KC = block_ksteps<FMT, NB, CT>();
+    constexpr int SPU = ksteps_per_unit<FMT>();
+    constexpr int UPB = KC / SPU;                                  // units per block
+    constexpr int SCW = scale_bytes<FMT>();
+    // in LDS every format keeps fp32 scales; Q4G32H's fp16 pair becomes a float2 per row (as qNg64)
+    constexpr int SCL = FMT == BGL_Q4G32H ? 8 : SCW;
+    constexpr int BF = KC * CT * 2 * 64;                           // activation uint4 per block
+    constexpr int SF = MF_TILES * UPB * 64 * SCW / 16;             // scale uint4 per block in global layout
+    constexpr int SFL = MF_TILES * UPB * 64 * SCL / 16;            // ... and in LDS
+    constexpr int NT = MF_WAVES * 64;
+    constexpr int PER_B = BF / NT, PER_S = (SF + NT - 1) / NT;
+    constexpr int SPG = FMT == BGL_Q4G32H ? 1 : 2;                 // K-steps per scale group
+    __shared__ uint4 stage[2][BF + SFL];
+
     const BglDevTensor &T = L.T;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4;
-    const int tile = blockIdx.x * MF_WAVES + wave;
+    const int wt = wave / (4 / MF_RBW), rbase = (wave % (4 / MF_RBW)) * MF_RBW;   // tile in the group, first row block
+    const int tile0 = blockIdx.x * MF_TILES, tile = tile0 + wt;
     const bool active = tile < T.ntiles;
     const int KS = T.K >> 5;
     const int s0 = blockIdx.y * L.kps, s1 = min(s0 + L.kps, KS);
-    const int nblocks = (s1 - s0 + MF_KC - 1) / MF_KC;
-    constexpr int SPU = ksteps_per_unit<FMT>();
-    constexpr int SPG = FMT == BGL_Q4G32H ? 1 : 2;       // K-steps per scale group
-    constexpr int PER_T = MF_KC * CT * 2 * 64 / (MF_WAVES * 64);   // uint4 per thread per block
+    const int nblocks = (s1 - s0 + KC - 1) / KC;
+    const int u0 = s0 / SPU;
 
-    mf_f4 acc[4][CT], cg[4][CT];
+    mf_f4 acc[MF_RBW][CT], cg[MF_RBW][CT];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int r = 0; r < MF_RBW; r++)
 #pragma unroll
         for (int c = 0; c < CT; c++) { acc[r][c] = mf_f4{0, 0, 0, 0}; cg[r][c] = mf_f4{0, 0, 0, 0}; }
 
-    // activation block b -> registers (K-steps past s1 read as zeros)
-    uint4 breg[PER_T];
-    auto load_b = [&](int b) {
+    // ---- staged data of block b (activation fragments + the 4 tiles' scales) ----
+    uint4 breg[PER_B], sreg[PER_S];
+    // Every global load below is unconditional, from an address clamped into the tensor, and the
+    // unwanted values are dropped by a select: conditional loads would keep the compiler from
+    // counting outstanding loads, and it would then wait for all of them before each block.
+    auto load_stage = [&](int b) {
+        const int sb = s0 + b * KC;
 #pragma unroll
-        for (int i = 0; i < PER_T; i++) {
-            const int e = threadIdx.x + i * MF_WAVES * 64;             // index within the block
-            const int j = e / (CT * 2 * 64);
-            const int s = s0 + b * MF_KC + j;
-            breg[i] = s < s1 ? L.xf[(size_t)(s0 + b * MF_KC) * CT * 2 * 64 + e] : make_uint4(0, 0, 0, 0);
+        for (int i = 0; i < PER_B; i++) {
+            const int e = threadIdx.x + i * NT;
+            const int s = sb + e / (CT * 2 * 64);
+            const int sc = s < s1 ? s : s1 - 1;
+            const bgl_u32x4 g = ((const BGL_GLOBAL bgl_u32x4 *)L.xf)[((size_t)sc * CT * 2 * 64) + e % (CT * 2 * 64)];
+            breg[i] = make_uint4(g.x, g.y, g.z, g.w);            // out-of-range steps are zeroed at the store
+        }
+#pragma unroll
+        for (int i = 0; i < PER_S; i++) {
+            const int e = threadIdx.x + i * NT;                    // uint4 index: [wt][ub][row*SCW/16]
+            const int per_tile = UPB * 64 * SCW / 16;
+            const int ec = e < SF ? e : SF - 1;
+            const int st = ec / per_tile, rem = ec % per_tile;
+            const int ub = rem / (64 * SCW / 16);
+            const int t = tile0 + st, u = u0 + b * UPB + ub;
+            const int tc = t < T.ntiles ? t : T.ntiles - 1, uc = u < T.nunits ? u : T.nunits - 1;
+            const bgl_u32x4 g = ((const BGL_GLOBAL bgl_u32x4 *)T.s0)[((size_t)tc * T.nunits + uc) * (64 * SCW / 16) +
+                                                                      rem % (64 * SCW / 16)];
+            sreg[i] = make_uint4(g.x, g.y, g.z, g.w);            // rows past the tensor never reach y
         }
     };
-    auto store_b = [&](int buf) {
+    auto store_stage = [&](int buf, int b) {
 #pragma unroll
-        for (int i = 0; i < PER_T; i++) stage[buf][threadIdx.x + i * MF_WAVES * 64] = breg[i];
+        for (int i = 0; i < PER_B; i++) {
+            const int e = threadIdx.x + i * NT;
+            const bool in = s0 + b * KC + e / (CT * 2 * 64) < s1;
+            stage[buf][e] = in ? breg[i] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < PER_S; i++) {
+            const int e = threadIdx.x + i * NT;
+            if (e < SF) {
+                if constexpr (FMT == BGL_Q4G32H) {                  // 4 rows x (fp16 lo, fp16 hi) -> 4 float2
+                    const uint32_t w[4] = {sreg[i].x, sreg[i].y, sreg[i].z, sreg[i].w};
+                    float f[8];
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        f[2 * v] = __half2float(__ushort_as_half((unsigned short)(w[v] & 0xffffu)));
+                        f[2 * v + 1] = __half2float(__ushort_as_half((unsigned short)(w[v] >> 16)));
+                    }
+                    uint4 a, b;
+                    memcpy(&a, f, 16);
+                    memcpy(&b, f + 4, 16);
+                    stage[buf][BF + 2 * e] = a;
+                    stage[buf][BF + 2 * e + 1] = b;
+                } else {
+                    stage[buf][BF + e] = sreg[i];
+                }
+            }
+        }
     };
 
-    load_b(0);
-    store_b(0);
-    __syncthreads();
-    for (int b = 0; b < nblocks; b++) {
-        if (b + 1 < nblocks) load_b(b + 1);
-        if (active) {
+    // ---- weights of block b for this wave: the register ring ----
+    struct WR { ARaw<FMT, NB> a[KC][MF_RBW]; };
+    const int tile_c = active ? tile : T.ntiles - 1;               // inactive waves read a real tile
+    auto load_w = [&](WR &W, int b) {
 #pragma unroll
-            for (int j = 0; j < MF_KC; j++) {
-                const int s = s0 + b * MF_KC + j;
-                if (s >= s1) break;
-                mf_h8 A[4];
+        for (int j = 0; j < KC; j++) {
+            const int s = s0 + b * KC + j;
+            const int sc = s < s1 ? s : s1 - 1;                     // past the split: reread, unused
 #pragma unroll
-                for (int rb = 0; rb < 4; rb++) {
-                    ARaw<FMT, NB> a;
-                    ld_a<FMT, NB>(a, T, tile, rb, s, lane);
-                    A[rb] = dec_a<FMT, NB>(a, q);
+            for (int r = 0; r < MF_RBW; r++) ld_a<FMT, NB>(W.a[j][r], T, tile_c, rbase + r, sc, lane);
+        }
+    };
+
+    auto compute = [&](const WR &W, int b) {
+        const uint4 *stg = stage[b & 1];
+        const float *scl = reinterpret_cast<const float *>(stg + BF);
+#pragma unroll
+        for (int j = 0; j < KC; j++) {
+            const int s = s0 + b * KC + j;
+            if (s >= s1) break;
+            mf_h8 A[MF_RBW];
+#pragma unroll
+            for (int r = 0; r < MF_RBW; r++) A[r] = dec_a<FMT, NB>(W.a[j][r], q);
+            const bool gstart = j % SPG == 0;                       // first K-step of a scale group
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                const mf_h8 Bh = __builtin_bit_cast(mf_h8, stg[((j * CT + c) * 2 + 0) * 64 + lane]);
+                const mf_h8 Bl = __builtin_bit_cast(mf_h8, stg[((j * CT + c) * 2 + 1) * 64 + lane]);
+#pragma unroll
+                for (int r = 0; r < MF_RBW; r++) {
+                    cg[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], Bh, gstart ? mf_f4{0, 0, 0, 0} : cg[r][c], 0, 0, 0);
+                    cg[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], Bl, cg[r][c], 0, 0, 0);
                 }
+            }
+            if ((j + 1) % SPG == 0) {                                // group complete: fold with its scales
+                const int ub = j / SPU;
+                const int g = FMT == BGL_Q4G32H ? (j & 1) : (FMT == BGL_QNG64 ? ((j % SPU) >> 1) : 0);
 #pragma unroll
-                for (int c = 0; c < CT; c++) {
-                    const uint4 bh = stage[b & 1][((j * CT + c) * 2 + 0) * 64 + lane];
-                    const uint4 bl = stage[b & 1][((j * CT + c) * 2 + 1) * 64 + lane];
-                    const mf_h8 Bh = __builtin_bit_cast(mf_h8, bh), Bl = __builtin_bit_cast(mf_h8, bl);
-#pragma unroll
-                    for (int rb = 0; rb < 4; rb++) {
-                        cg[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb], Bh, cg[rb][c], 0, 0, 0);
-                        cg[rb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb], Bl, cg[rb][c], 0, 0, 0);
+                for (int rb = 0; rb < MF_RBW; rb++) {
+                    const int r0 = 16 * (rbase + rb) + 4 * q;
+                    mf_f4 sc;
+                    if constexpr (FMT == BGL_QNG64 || FMT == BGL_Q4G32H) {   // float2 per row: group g
+                        const float *p = scl + ((wt * UPB + ub) * 64 + r0) * 2 + g;
+                        sc = mf_f4{p[0], p[2], p[4], p[6]};
+                    } else {
+                        const float *p = scl + (wt * UPB + ub) * 64 + r0;
+                        sc = mf_f4{p[0], p[1], p[2], p[3]};
                     }
-                }
-                if ((s + 1) % SPG == 0) {                 // group complete: fold with its scales
-                    const int u = s / SPU;
-                    const int g = FMT == BGL_Q4G32H ? (s & 1) : (FMT == BGL_QNG64 ? ((s % SPU) >> 1) : 0);
 #pragma unroll
-                    for (int rb = 0; rb < 4; rb++) {
-                        const mf_f4 sc = ld_scales<FMT>(T, tile, rb, u, lane, g);
+                    for (int c = 0; c < CT; c++) {
 #pragma unroll
-                        for (int c = 0; c < CT; c++) {
-#pragma unroll
-                            for (int v = 0; v < 4; v++) acc[rb][c][v] = __fmaf_rn(cg[rb][c][v], sc[v], acc[rb][c][v]);
-                            cg[rb][c] = mf_f4{0, 0, 0, 0};
-                        }
+                        for (int v = 0; v < 4; v++) acc[rb][c][v] = __fmaf_rn(cg[rb][c][v], sc[v], acc[rb][c][v]);
                     }
                 }
             }
         }
-        if (b + 1 < nblocks) store_b((b + 1) & 1);
+    };
+
+    WR w0, w1;
+    load_stage(0);
+    load_w(w0, 0);
+    store_stage(0, 0);
+    __syncthreads();
+    // The next block's loads are issued on every iteration (past the end they reread the last
+    // K-step and are never used), so the number of loads in flight is the same on every path and
+    // compute waits only for its own block.
+    for (int b = 0; b < nblocks; b += 2) {
+        load_stage(b + 1);
+        load_w(w1, b + 1);
+        if (active) compute(w0, b);
+        store_stage((b + 1) & 1, b + 1);    // past the end it fills a buffer nobody reads again
+        __syncthreads();
+        if (b + 1 >= nblocks) break;
+        load_stage(b + 2);
+        load_w(w0, b + 2);
+        if (active) compute(w1, b + 1);
+        store_stage(b & 1, b + 2);
         __syncthreads();
     }
     if (!active) return;
 
     const int nsplit = gridDim.y;
 #pragma unroll
-    for (int rb = 0; rb < 4; rb++) {
-        const int n0 = tile * BGL_TILE + 16 * rb + 4 * q;
+    for (int rb = 0; rb < MF_RBW; rb++) {
+        const int n0 = tile * BGL_TILE + 16 * (rbase + rb) + 4 * q;
 #pragma unroll
         for (int c = 0; c < CT; c++) {
             const int m = 16 * c + (lane & 15);
@@ -372,18 +468,22 @@ int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev,
         const size_t fbytes = (size_t)KS * CT * 2 * 64 * 16;
         if (dbuf_reserve(c, c->act_w, fbytes, false) || dbuf_reserve(c, c->act_s, (size_t)16 * CT * 4, false)) return BGL_E_NOMEM;
         int tok = prof_begin(c, 0);
-        hipLaunchKernelGGL(k_act_frag, dim3(16 * CT), dim3(256), 0, c->stream, x_dev + (size_t)m0 * K, Mc, K, CT,
-                           (uint4 *)c->act_w.p, (float *)c->act_s.p);
+        hipLaunchKernelGGL(k_act_frag, dim3(16 * CT, (K + MF_PREP_CHUNK - 1) / MF_PREP_CHUNK), dim3(256), 0, c->stream,
+                           x_dev + (size_t)m0 * K, Mc, K, CT, (uint4 *)c->act_w.p, (float *)c->act_s.p);
         prof_end(c, tok);
         HIPCHK(hipGetLastError());
         c->prep_act = -1;                                 // the activation buffers now hold fragments
         for (int i = 0; i < n; i++) {
             const BglDevTensor &T = Ts[i];
-            const int wgr = (T.ntiles + MF_WAVES - 1) / MF_WAVES;
+            const int wgr = (T.ntiles + MF_TILES - 1) / MF_TILES;
             const int spu = T.fmt == BGL_QNG64 ? 4 : 2;
             int S = (c->min_blocks + wgr - 1) / wgr;     // split K until the grid has ~min_blocks workgroups
             int maxS = KS / (2 * MF_KC);                  // at least two staged blocks per split
             if (maxS > 16) maxS = 16;
+            // the partials (written and read back once each) stay under half the weight bytes
+            const double wbytes = (double)T.N * T.K * (T.fmt == BGL_Q8G64 ? 1.0625 : T.fmt == BGL_QNG64 ? T.bits / 8.0 + 0.0625 : 0.5625);
+            const int capS = (int)(0.5 * wbytes / (8.0 * Mc * T.N));
+            if (maxS > capS) maxS = capS;
             if (S > maxS) S = maxS;
             if (S < 1) S = 1;
             int kps = (KS + S - 1) / S;

@@ -15,7 +15,10 @@ algorithmic bytes = packed + scale + sub-code bytes + 4*M*K (x) + 4*M*N (y) per 
 stream), i.e. without the inter-launch gaps that `value` includes.  `cpu_baseline` = the reference's threaded CPU
 path (portable-C restatement, q4pool row-block split) timed on this host on a bounded sample.
 
-Other workloads for the per-config numbers: --workload cfg1 | cfg3 | cfg4 (see --help).
+Other workloads for the per-config numbers: --workload cfg1 | cfg3 | cfg4 | cfg5 (see --help).
+cfg5 = Llama-3.1-8B projections (q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down
+4096x14336) at M=32 fp32 activation rows on the matrix-core path: attention int8 (q8g64), MLP
+int4 g32 (Q4G32H), a seeded 20% of the tensors qNg64 n=5; one step = --layers layers.
 cfg4 = DeepSeek-V2-Lite routed MoE FFN (E=64 + 2 shared experts, hidden 2048, expert inter 1408,
 top-6 over softmax(N(0,1) router logits)), T=--M tokens, per-expert precision drawn from the seed
 over {q4g32h, q8g64, qNg64 n=7..15}; one step = --layers distinct MoE layers; algorithmic bytes =
@@ -108,6 +111,50 @@ def build_cfg2(ctx, torch, M, layers, seed):
                 nb += alg_bytes(3, out, inn, 4, M) - 4 * M * inn
             nb += 4 * M * shapes[0][1]
             wl.add(group, xs[shapes[0][1]], beglin_amd.ACT_W4A8, nb, tag)
+    return wl
+
+
+def llama8b_layer_shapes():
+    return [("qkv", [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096)]), ("o", [("o", 4096, 4096)]),
+            ("gate_up", [("gate", 14336, 4096), ("up", 14336, 4096)]), ("down", [("down", 4096, 14336)])]
+
+
+def cfg5_kinds(layers, seed):
+    """Per-tensor (kind, bits): attention int8, MLP Q4G32H, a seeded 20% of all tensors qNg64 n=5."""
+    import numpy as np
+    rng = np.random.default_rng(seed + 5)
+    out = []
+    for _ in range(layers):
+        lay = {}
+        for _, shapes in llama8b_layer_shapes():
+            for name, _, _ in shapes:
+                base = (2, 8) if name in ("q", "k", "v", "o") else (5, 4)
+                lay[name] = (4, 5) if rng.random() < 0.2 else base
+        out.append(lay)
+    return out
+
+
+def build_cfg5(ctx, torch, M, layers, seed):
+    """Fused groups only where the tensors share a kind (the engine's fused blobs are one kind)."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    wl = Workload(ctx, torch)
+    xs = {k: torch.randn((M, k), generator=gen, device="cuda") for k in (4096, 14336)}
+    kinds = cfg5_kinds(layers, seed)
+    for li in range(layers):
+        for tag, shapes in llama8b_layer_shapes():
+            groups = {}
+            for name, out, inn in shapes:
+                groups.setdefault(kinds[li][name], []).append((name, out, inn))
+            for (kind, bits), members in groups.items():
+                group, nb = [], 0
+                for name, out, inn in members:
+                    w = gen_weight(torch, gen, out, inn)
+                    group.append(ctx.quantize(kind, w, bits=bits))
+                    del w
+                    nb += alg_bytes(kind, out, inn, bits, M) - 4 * M * inn
+                nb += 4 * M * members[0][2]
+                wl.add(group, xs[members[0][2]], 0, nb, tag)
+    wl.kinds = kinds
     return wl
 
 
@@ -262,7 +309,90 @@ def moe_roofline(ctx, torch, stream, wl, reps):
             "timing": f"eager, event pair per launch, {reps} steps"}
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def mfma_roofline(ctx, torch, stream, wl, M, reps):
+    """k_gemm_mfma's own time: eager steps with an event pair per launch (phase 1 = the GEMM
+    kernel, 0 = activation fragments, 2 = K-split reduce); achieved = step bytes / GEMM time.
+    Matrix-core rate: the kernel issues 2 (hi, lo) x ceil(M/16)*16 x N_tiles*64 x K x 2 flops per
+    call; useful flops are 2*M*N*K."""
+    ctx.prof_enable(True)
+    ctx.prof_read()
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            wl.run()
+    ctx.sync()
+    ph = ctx.prof_read()
+    ctx.prof_enable(False)
+    g_ms, g_n = ph["gemv"][0] / reps, ph["gemv"][1] // reps
+    p_ms, o_ms = ph["prep"][0] / reps, ph["other"][0] / reps
+    achieved = wl.nbytes() / (g_ms * 1e-3) / 1e9
+    useful, issued = 0.0, 0.0
+    mp = (M + 15) // 16 * 16
+    for group, x, ys, act, nb, tag in wl.calls:
+        for t in group:
+            inf = t.info()
+            useful += 2.0 * M * inf["out"] * inf["inn"]
+            issued += 2.0 * 2 * mp * ((inf["out"] + 63) // 64 * 64) * inf["inn"]
+    tflops = issued / (g_ms * 1e-3) / 1e12
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_gemm_mfma (bgl_mfma.hip)",
+            "launches_per_step": g_n, "kernel_us_per_launch": round(g_ms * 1e3 / max(g_n, 1), 3),
+            "bytes_per_launch": round(wl.nbytes() / max(g_n, 1)),
+            "mfma": {"issued_tflops": round(tflops, 1), "useful_tflops": round(useful / (g_ms * 1e-3) / 1e12, 1),
+                     "peak_fp16_tflops": MFMA_F16_PEAK_TFLOPS, "util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)},
+            "prep_us_per_step": round(p_ms * 1e3, 2), "reduce_us_per_step": round(o_ms * 1e3, 2),
+            "timing": f"eager, event pair per launch, {reps} steps"}
+
+
 # ------------------------------------------------------------------------------------- CPU baseline
+def cpu_baseline_cfg5(M, budget_s, seed):
+    """The reference's fp32-activation GEMV restated (or_pool_gemv_f32 per column, q4pool row-block
+    split) on one layer of the same shapes and precision map; timed columns scaled to M."""
+    import ctypes as C
+
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_ffi import Oracle
+    orc = Oracle()
+    rng = np.random.default_rng(seed)
+    T = host_threads()
+    pool = orc.lib.or_pool_create(T, 14336)
+    kinds = cfg5_kinds(1, seed)[0]
+    mats, nb = [], 0
+    for _, shapes in llama8b_layer_shapes():
+        for name, out, inn in shapes:
+            kind, bits = kinds[name]
+            w = (rng.standard_normal((out, inn), dtype=np.float32) * np.float32(0.02))
+            if kind == 2:
+                pk, sc = orc.quantize_q8g64(w)
+            elif kind == 5:
+                pk, sc = orc.quantize_q4g32h(w)
+            else:
+                pk, sc = orc.quantize_qng64(w, bits)
+            mats.append((kind, bits, pk, sc, out, inn, np.zeros(out, np.float32)))
+            nb += alg_bytes(kind, out, inn, bits, M)
+    xs = {k: rng.standard_normal((M, k), dtype=np.float32) for k in (4096, 14336)}
+    P = lambda a: C.c_void_p(a.ctypes.data)
+    t0 = time.perf_counter()
+    cols = 0
+    while True:
+        for kind, bits, pk, sc, out, inn, y in mats:
+            xr = np.ascontiguousarray(xs[inn][cols % M])
+            orc.lib.or_pool_gemv_f32(pool, kind, bits, P(pk), P(sc), P(xr), None, P(y), out, inn)
+        cols += 1
+        if time.perf_counter() - t0 >= budget_s or cols >= M:
+            break
+    el = time.perf_counter() - t0
+    dt = el / cols * M                                    # one layer at M columns
+    orc.lib.or_pool_destroy(pool)
+    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": T, "kind": "port",
+            "us_per_layer": round(dt * 1e6, 1),
+            "sample": f"one Llama-3.1-8B layer (7 tensors, same precision map), {cols} of {M} columns timed "
+                      f"({el:.1f} s) and scaled to {M}, per column through the row-block pool, {T} threads"}
+
+
 def cpu_baseline_cfg4(wl, budget_s, seed):
     """moe_ffn_batched's portable C restatement (or_moe_ffn_bucketed, one thread) on layer 0's
     formats and routing, for its first min(T, 2) tokens; only the experts those tokens touch are
@@ -410,9 +540,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4"])
-    ap.add_argument("--M", type=int, default=1, help="activation rows (cfg2: 1, 4 or 8); cfg4: tokens T (1, 8, 64)")
-    ap.add_argument("--layers", type=int, default=None, help="cfg2: 28 layers; cfg4: 8 MoE layers")
+    ap.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--M", type=int, default=None,
+                    help="activation rows (default 1; cfg2: 1, 4 or 8; cfg5: 32); cfg4: tokens T (1, 8, 64)")
+    ap.add_argument("--layers", type=int, default=None, help="cfg2: 28 layers; cfg4: 8 MoE layers; cfg5: 4 layers")
     ap.add_argument("--bits", type=int, default=15, help="cfg3: qNg64 width n")
     ap.add_argument("--shape", default="gate", choices=["gate", "down"], help="cfg3: MLP gate (K=4096) or down (K=14336)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -442,10 +573,21 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     stream = torch.cuda.Stream()
     ctx = beglin_amd.Context(0, stream=stream.cuda_stream)
-    M = args.M
     if args.layers is None:
-        args.layers = 8 if args.workload == "cfg4" else 28
-    if args.workload == "cfg2":
+        args.layers = {"cfg4": 8, "cfg5": 4}.get(args.workload, 28)
+    if args.M is None:
+        args.M = 32 if args.workload == "cfg5" else 1
+    M = args.M
+    if args.workload == "cfg5":
+        with torch.cuda.stream(stream):
+            wl = build_cfg5(ctx, torch, M, args.layers, args.seed)
+        workload = (f"cfg5: Llama-3.1-8B projections x{args.layers} layers, M={M} fp32 rows, attention int8, "
+                    f"MLP int4 g32, seeded 20% qNg64 n=5, matrix-core path")
+        dtype = "fp16 (exact codes; activations hi+lo fp16)"
+        nq = sum(1 for lay in wl.kinds for v in lay.values() if v == (4, 5))
+        cfg = {"workload": workload, "M": M, "layers": args.layers, "calls_per_step": wl.ncalls(),
+               "qng64_n5_tensors": nq, "tensors": 7 * args.layers, "bytes_per_step": int(wl.nbytes()), "seed": args.seed}
+    elif args.workload == "cfg2":
         with torch.cuda.stream(stream):
             wl = build_cfg2(ctx, torch, M, args.layers, args.seed)
         torch.cuda.synchronize()
@@ -483,6 +625,12 @@ def main():
     value = nbytes / (step_ms * 1e-3) / 1e9
 
     # per-call latency of each call type (graph over all its instances)
+    if args.workload == "cfg5":
+        per_call = {"layer": {"us": round(step_ms * 1e3 / args.layers, 2), "GB/s": round(value, 1)}}
+        roof = mfma_roofline(ctx, torch, stream, wl, M, max(3, args.steps // 10))
+        cpu = None if args.no_cpu else cpu_baseline_cfg5(M, args.cpu_seconds, args.seed)
+        finish(args, wl, ctx, graph, value, step_ms, wall, dtype, cfg, per_call, roof, cpu)
+        return
     if args.workload == "cfg4":
         per_call = {"moe_layer": {"us": round(step_ms * 1e3 / args.layers, 2), "GB/s": round(value, 1)}}
         roof = moe_roofline(ctx, torch, stream, wl, max(3, args.steps // 10))
