@@ -257,7 +257,9 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     long nch = rows * T.cpr;
     switch (kind) {
     case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q4G256SF: case BGL_Q4G64A:
-        hipLaunchKernelGGL(k_repack_nib, dim3(nblk(nch)), dim3(256), 0, c->stream, (const uint8_t *)dpk, out, in, (uint8_t *)w);
+        // g256sf is only read by the int8-activation kernels, which take its codes as signed nibbles
+        hipLaunchKernelGGL(k_repack_nib, dim3(nblk(nch)), dim3(256), 0, c->stream, (const uint8_t *)dpk, out, in,
+                           kind == BGL_Q4G256SF ? 0x88888888u : 0u, (uint8_t *)w);
         break;
     case BGL_Q8G64: case BGL_F16: case BGL_F32:      // plain 16-byte chunk interleave of the row bytes
         hipLaunchKernelGGL(k_repack_q8, dim3(nblk(nch)), dim3(256), 0, c->stream, (const int8_t *)dpk, out,
@@ -519,6 +521,8 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
     return 0;
 }
 
+#define BGL_GEMV_Q_LDS_MAX (64 * 1024)
+
 // W4A8 with one activation column: quantization fused into the GEMV workgroups (one launch).
 static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, const float *const *bias,
                       float *const *y) {
@@ -536,6 +540,7 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
     if (Ts[0].K >= 4096)
         while (TR > 16 && (long)blocks * (BGL_TILE / TR) < c->min_blocks) TR >>= 1;
     if (c->force_tr) TR = c->force_tr;
+    while (TR > 8 && bgl_gemv_q_lds(Ts[0].fmt, Ts[0].K, TR) > BGL_GEMV_Q_LDS_MAX) TR >>= 1;   // the t[u][row] terms shrink with TR
     const int KQ = BGL_TILE / TR, U = Ts[0].nunits;
     int nw = (U + KQ - 1) / KQ;
     if (nw > c->max_waves) nw = c->max_waves;
@@ -552,7 +557,7 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
 static bool fused_q_ok(bgl_ctx *c, int kind, int K, int M) {
     if (M != 1 || c->no_fused) return false;
     if (kind != BGL_Q4G256SF && kind != BGL_Q4G64 && kind != BGL_Q8G64) return false;
-    return bgl_gemv_q_lds(kind, K, 64) <= 64 * 1024;
+    return bgl_gemv_q_lds(kind, K, 8) <= BGL_GEMV_Q_LDS_MAX;
 }
 
 

@@ -26,6 +26,36 @@ __device__ __forceinline__ int pick_task(const GemvLaunch &L, int b) {
     return ti;
 }
 
+// The task of workgroup b, its weight pointers and the activation row.  Every task's blk0 and
+// pointers are read from the kernel arguments in one round of independent scalar loads: the single
+// empty asm statement makes all of them opaque at once, so the compiler can neither split the loads
+// into rounds nor turn the selects into a second load through a selected address (each dependent
+// round trip to the kernel arguments delays the first weight loads).
+struct TaskSel {
+    int ti, blk0;
+    const uint8_t *w;
+    const void *s0;
+    const uint32_t *s1;
+    const float *x;           // activation row m0 of the launch
+    int cpr, nunits, nthreads;
+};
+static_assert(BGL_MAX_TASKS == 4, "select_task names four tasks");
+__device__ __forceinline__ TaskSel select_task(const GemvLaunch &L, int b) {
+    const uint8_t *w0 = L.t[0].T.w, *w1 = L.t[1].T.w, *w2 = L.t[2].T.w, *w3 = L.t[3].T.w;
+    const void *a0 = L.t[0].T.s0, *a1 = L.t[1].T.s0, *a2 = L.t[2].T.s0, *a3 = L.t[3].T.s0;
+    const uint32_t *c0 = L.t[0].T.s1, *c1 = L.t[1].T.s1, *c2 = L.t[2].T.s1, *c3 = L.t[3].T.s1;
+    int b0 = L.t[0].blk0, b1 = L.t[1].blk0, b2 = L.t[2].blk0, b3 = L.t[3].blk0, nt = L.ntasks;
+    const float *x = L.x + (size_t)L.m0 * L.t[0].T.K;
+    int cpr = L.t[0].T.cpr, nu = L.t[0].T.nunits, nth = blockDim.x;
+    asm volatile("" : "+s"(w0), "+s"(w1), "+s"(w2), "+s"(w3), "+s"(a0), "+s"(a1), "+s"(a2), "+s"(a3), "+s"(c0), "+s"(c1),
+                 "+s"(c2), "+s"(c3), "+s"(b0), "+s"(b1), "+s"(b2), "+s"(b3), "+s"(nt), "+s"(x), "+s"(cpr), "+s"(nu), "+s"(nth));
+    TaskSel r{0, b0, w0, a0, c0, x, cpr, nu, nth};
+    if (nt > 1 && b >= b1) r = TaskSel{1, b1, w1, a1, c1, x, cpr, nu, nth};
+    if (nt > 2 && b >= b2) r = TaskSel{2, b2, w2, a2, c2, x, cpr, nu, nth};
+    if (nt > 3 && b >= b3) r = TaskSel{3, b3, w3, a3, c3, x, cpr, nu, nth};
+    return r;
+}
+
 // ================================================================================== path A kernel
 template <int FMT, int ACT, int NB, int MB>
 __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv(GemvLaunch L) {
@@ -102,46 +132,171 @@ __global__ void k_splitk_reduce(const float *__restrict__ part, int ks, int M, i
 // wave handles row l % TR and unit kq = l / TR of each group of KQ = 64/TR consecutive units, so a
 // wave-wide load is KQ runs of TR*16 >= 128 bytes.  Activation bytes come from LDS (each lane reads
 // its own unit's slice; units are padded by 16 bytes so neighbouring units fall in different banks).
-// Dynamic LDS: [xq: U x (unit bytes + 16)][ascale: K/gq][xqsum: K/64][t: U x TR floats].
+//
+// The activations are quantized in passes of 256 consecutive values, lane l holding values 4l..4l+3
+// (one float4 load, one packed dword store): a pass is one g256 group (wave-wide max) or four g64
+// groups (one per 16-lane row, row-wide max and sum).  A wave's first QP passes are loaded before its
+// first weight units and the quantization is branch-free, so it waits only for the x loads (vector
+// memory loads retire in order) and runs while the weight bytes are still arriving.  Lanes past K
+// store into a dummy slot after the real ones.
+// Dynamic LDS: [xq: (U+1) x (unit bytes + 16)][ascale: K/gq + 1][xqsum: K/64 + 1][t: U x TR floats].
 
 template <int FMT> struct QUnit {
     static constexpr int GQ = FMT == BGL_Q4G256SF ? 256 : 64;        // activation quantization group
     static constexpr int ELEMS = FMT == BGL_Q4G256SF ? 256 : 64;     // elements per work unit
     static constexpr int STRIDE = ELEMS + 16;                       // padded LDS bytes per unit
+    static constexpr bool XSUM = FMT == BGL_Q4G64;                  // unsigned nibbles: needs sum(xq) per 64
 };
 
 template <int FMT>
 __device__ __forceinline__ void load_raw_row(Raw<FMT, 0> &r, const BglDevTensor &T, int tile, int rr, int u) {
     constexpr int CPU = chunks_per_unit<FMT>(0);
-    const uint4 *cp = reinterpret_cast<const uint4 *>(T.w) + ((size_t)tile * T.cpr + (size_t)u * CPU) * BGL_TILE + rr;
+    // global address space: flat loads would also count against the LDS wait counter
+    const BGL_GLOBAL bgl_u32x4 *cp = (const BGL_GLOBAL bgl_u32x4 *)(T.w) + ((size_t)tile * T.cpr + (size_t)u * CPU) * BGL_TILE + rr;
 #pragma unroll
-    for (int k = 0; k < CPU; k++) r.c[k] = cp[k * BGL_TILE];
+    for (int k = 0; k < CPU; k++) {
+        const bgl_u32x4 v = cp[k * BGL_TILE];
+        r.c[k] = make_uint4(v.x, v.y, v.z, v.w);
+    }
     const size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + rr;
-    r.s = reinterpret_cast<const float *>(T.s0)[so];
-    if constexpr (FMT == BGL_Q4G256SF) r.sub = T.s1[so];
+    r.s = ((const BGL_GLOBAL float *)T.s0)[so];
+    if constexpr (FMT == BGL_Q4G256SF) r.sub = ((const BGL_GLOBAL uint32_t *)T.s1)[so];
 }
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false); }
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+
+// q4_quant_act_i8's rounding (q4gemv.h:199-206): q = (int)(x*inv + (x*inv >= 0 ? 0.5 : -0.5)),
+// clamped to [-128, 127].  copysign(0.5, p) differs from the comparison only at p = -0, where both
+// truncate to 0.
+__device__ __forceinline__ uint32_t quant_byte(float x, float inv) {
+    const float p = __fmul_rn(x, inv);
+    int q = (int)__fadd_rn(p, __builtin_copysignf(0.5f, p));   // |.| <= 128.5: no int32 overflow
+    q = q > 127 ? 127 : (q < -128 ? -128 : q);
+    return (uint32_t)q & 255u;
+}
+
+// Quantizes QP passes (pass i = values 256*(p0 + i*nw) .. +255; lane l holds values 4l..4l+3 of each
+// in v[i]) into LDS.  The passes are processed in lockstep so their dependency chains interleave.
+// |x| is maximised on its bit pattern (the same order as the float values for non-NaN inputs).
+// GQ=256: one pass is one group; its four row maxima are combined with readlane, and one IEEE
+// division pair serves every pass (lane i computes pass i's scale and reciprocal).  GQ=64: one pass
+// is four groups, one per 16-lane row.  Lanes past K store into the dummy slots.
+template <int FMT, int QP>
+__device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int nw, int K, int NGQ, int U, int lane,
+                                             int8_t *xq, float *asc, int *xsum) {
+    using QU = QUnit<FMT>;
+    uint32_t m[QP];
+#pragma unroll
+    for (int i = 0; i < QP; i++)
+        m[i] = umax(umax(abs_bits(v[i].x), abs_bits(v[i].y)), umax(abs_bits(v[i].z), abs_bits(v[i].w)));
+#pragma unroll
+    for (int i = 0; i < QP; i++) m[i] = umax(m[i], dpp_u<0xB1>(m[i]));
+#pragma unroll
+    for (int i = 0; i < QP; i++) m[i] = umax(m[i], dpp_u<0x4E>(m[i]));
+#pragma unroll
+    for (int i = 0; i < QP; i++) m[i] = umax(m[i], dpp_u<0x141>(m[i]));
+#pragma unroll
+    for (int i = 0; i < QP; i++) m[i] = umax(m[i], dpp_u<0x140>(m[i]));   // row maxima in every lane
+    float inv[QP];
+    if constexpr (QU::GQ == 256) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < QP; i++) {
+            const uint32_t M = umax(umax((uint32_t)__builtin_amdgcn_readlane((int)m[i], 0), (uint32_t)__builtin_amdgcn_readlane((int)m[i], 16)),
+                                    umax((uint32_t)__builtin_amdgcn_readlane((int)m[i], 32), (uint32_t)__builtin_amdgcn_readlane((int)m[i], 48)));
+            mx = (i == 0 || lane == i) ? __uint_as_float(M) : mx;
+        }
+        mx = fmaxf(1e-8f, mx);                         // mx starts at 1e-8 (q4gemv_g256.h:78)
+        const float sc = __fdiv_rn(mx, 127.0f), iv = __fdiv_rn(1.0f, sc);
+#pragma unroll
+        for (int i = 0; i < QP; i++) inv[i] = rlane_f(iv, i);
+        if (lane < QP) {
+            const int p = p0 + lane * nw;
+            asc[256 * p < K ? p : NGQ] = sc;
+        }
+    } else {
+        float sc[QP];
+#pragma unroll
+        for (int i = 0; i < QP; i++) sc[i] = __fdiv_rn(fmaxf(1e-8f, __uint_as_float(m[i])), 127.0f);   // mx starts at 1e-8 (q4gemv.h:182)
+#pragma unroll
+        for (int i = 0; i < QP; i++) inv[i] = __fdiv_rn(1.0f, sc[i]);
+        if ((lane & 15) == 0) {
+#pragma unroll
+            for (int i = 0; i < QP; i++) {
+                const int e = 256 * (p0 + i * nw) + 4 * lane;
+                asc[e < K ? e / 64 : NGQ] = sc[i];
+            }
+        }
+    }
+    uint32_t word[QP];
+#pragma unroll
+    for (int i = 0; i < QP; i++)
+        word[i] = quant_byte(v[i].x, inv[i]) | (quant_byte(v[i].y, inv[i]) << 8) | (quant_byte(v[i].z, inv[i]) << 16) |
+                  (quant_byte(v[i].w, inv[i]) << 24);
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        const int e = 256 * (p0 + i * nw) + 4 * lane;
+        const bool ok = e < K;                         // K % 64 == 0: whole 16-lane rows are in or out
+        *reinterpret_cast<uint32_t *>(xq + (ok ? e / QU::ELEMS : U) * QU::STRIDE + e % QU::ELEMS) = word[i];
+    }
+    if constexpr (QU::XSUM) {
+        int sm[QP];
+#pragma unroll
+        for (int i = 0; i < QP; i++) {
+            const uint32_t w = word[i];
+            sm[i] = (int)(int8_t)(w & 255u) + (int)(int8_t)((w >> 8) & 255u) + (int)(int8_t)((w >> 16) & 255u) + (int)(int8_t)(w >> 24);
+        }
+#pragma unroll
+        for (int i = 0; i < QP; i++) sm[i] = row_sum_i32(sm[i]);
+        if ((lane & 15) == 0) {
+#pragma unroll
+            for (int i = 0; i < QP; i++) {
+                const int e = 256 * (p0 + i * nw) + 4 * lane;
+                xsum[e < K ? e / 64 : K / 64] = sm[i];
+            }
+        }
+    }
+}
+
+template <int QP>
+__device__ __forceinline__ void load_xpass(float4 (&v)[QP], const float *x, int p0, int nw, int K, int lane) {
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        const int e = min(256 * (p0 + i * nw) + 4 * lane, K - 4);      // clamped: always a valid address
+        const bgl_f32x4 t = *((const BGL_GLOBAL bgl_f32x4 *)(x + e));
+        v[i] = make_float4(t.x, t.y, t.z, t.w);
+    }
+}
+
+// g256sf codes are stored as signed nibbles (code ^ 8 = the 4-bit two's complement of code-8), so
+// masking a nibble into the high half of a byte gives 16*(code-8) as an int8 and dot4 sums come out
+// as exactly 16x the reference's integer sums.
+__device__ __forceinline__ int snib_lo16(uint32_t w) { return (int)((w << 4) & 0xF0F0F0F0u); }
+__device__ __forceinline__ int snib_hi16(uint32_t w) { return (int)(w & 0xF0F0F0F0u); }
 
 template <int FMT>
 __device__ __forceinline__ float unit_term(const Raw<FMT, 0> &r, const int8_t *xq, const float *asc, const int *xsum, int u) {
     const int4 *x4 = reinterpret_cast<const int4 *>(xq + (size_t)u * QUnit<FMT>::STRIDE);
     if constexpr (FMT == BGL_Q4G256SF) {
-        int comb = 0;
+        int comb16 = 0;                                // 16 * sum_sg isum_sg * sub_sg, |.| < 2^29
 #pragma unroll
         for (int sg = 0; sg < 4; sg++) {
-            int isum = 0;
+            int isum16 = 0;
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 const uint4 c = r.c[2 * sg + k];
                 const int4 xa = x4[sg * 4 + 2 * k], xb = x4[sg * 4 + 2 * k + 1];
-                isum = dot4(nib_lo(c.x), xa.x, isum); isum = dot4(nib_hi(c.x), xa.y, isum);
-                isum = dot4(nib_lo(c.y), xa.z, isum); isum = dot4(nib_hi(c.y), xa.w, isum);
-                isum = dot4(nib_lo(c.z), xb.x, isum); isum = dot4(nib_hi(c.z), xb.y, isum);
-                isum = dot4(nib_lo(c.w), xb.z, isum); isum = dot4(nib_hi(c.w), xb.w, isum);
+                isum16 = dot4(snib_lo16(c.x), xa.x, isum16); isum16 = dot4(snib_hi16(c.x), xa.y, isum16);
+                isum16 = dot4(snib_lo16(c.y), xa.z, isum16); isum16 = dot4(snib_hi16(c.y), xa.w, isum16);
+                isum16 = dot4(snib_lo16(c.z), xb.x, isum16); isum16 = dot4(snib_hi16(c.z), xb.y, isum16);
+                isum16 = dot4(snib_lo16(c.w), xb.z, isum16); isum16 = dot4(snib_hi16(c.w), xb.w, isum16);
             }
-            isum -= 8 * xsum[u * 4 + sg];
-            comb += isum * (int)((r.sub >> (8 * sg)) & 255u);
+            comb16 += isum16 * (int)((r.sub >> (8 * sg)) & 255u);
         }
-        return __fmul_rn(__fmul_rn(__fmul_rn((float)comb, r.s), C63), asc[u]);
+        return __fmul_rn(__fmul_rn(__fmul_rn((float)(comb16 >> 4), r.s), C63), asc[u]);
     } else if constexpr (FMT == BGL_Q4G64) {
         int isum = 0;
 #pragma unroll
@@ -168,82 +323,62 @@ __device__ __forceinline__ float unit_term(const Raw<FMT, 0> &r, const int8_t *x
     }
 }
 
-template <int FMT, int TR>
+template <int FMT, int TR, int QP>
 __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     extern __shared__ __align__(16) unsigned char lds[];
     constexpr int KQ = BGL_TILE / TR, SUBS = BGL_TILE / TR;
     using QU = QUnit<FMT>;
-    const int b = blockIdx.x, ti = pick_task(L, b);
-    GemvTask task = L.t[0];
-#pragma unroll
-    for (int i = 1; i < BGL_MAX_TASKS; i++) if (i == ti) task = L.t[i];
-    const BglDevTensor &T = task.T;
-    const int lb = b - task.blk0, tile = lb / SUBS, r0 = (lb % SUBS) * TR;
-    const int nw = blockDim.x >> 6;
+    const int b = blockIdx.x;
+    const TaskSel sel = select_task(L, b);
+    BglDevTensor T = L.t[0].T;                          // fmt, K, cpr, nunits are shared by all tasks
+    T.w = sel.w; T.s0 = sel.s0; T.s1 = sel.s1; T.cpr = sel.cpr; T.nunits = sel.nunits;
+    const int lb = b - sel.blk0, tile = lb / SUBS, r0 = (lb % SUBS) * TR;
+    const int nw = sel.nthreads >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int K = T.K, U = T.nunits;
+    const int K = T.K, U = T.nunits, NGQ = K / QU::GQ, NP = (K + 255) / 256;
     int8_t *xq = reinterpret_cast<int8_t *>(lds);
-    float *asc = reinterpret_cast<float *>(lds + (size_t)U * QU::STRIDE);
-    int *xsum = reinterpret_cast<int *>(asc + K / QU::GQ);
-    float *tl = reinterpret_cast<float *>(xsum + K / 64);
+    float *asc = reinterpret_cast<float *>(lds + (size_t)(U + 1) * QU::STRIDE);
+    int *xsum = reinterpret_cast<int *>(asc + NGQ + 1);
+    float *tl = reinterpret_cast<float *>(xsum + K / 64 + 1);
+    const float *x = sel.x;
 
-    // ---- first weight loads go out before the activation work (they do not depend on it)
+    // ---- x loads of the first pass, then the first weight units (unconditional, clamped)
+    float4 v[QP];
+    load_xpass<QP>(v, x, wave, nw, K, lane);
+    __builtin_amdgcn_sched_barrier(0);
     const int r = lane % TR, kq = lane / TR, rr = r0 + r;
     int ub = wave * KQ;
     Raw<FMT, 0> c0, c1;
-    if (ub + kq < U) load_raw_row<FMT>(c0, T, tile, rr, ub + kq);
+    load_raw_row<FMT>(c0, T, tile, rr, min(ub + kq, U - 1));
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- quantize x (q4gemv.h:177-213 / q4gemv_g256.h:72-99), one wave per group; each wave
-    // first loads every group it owns (up to 4 per pass) so the loads overlap
-    const float *x = L.x + (size_t)L.m0 * K;
-    constexpr int PER = QU::GQ / 64;
-    const int NGQ = K / QU::GQ;
-    for (int g0 = wave; g0 < NGQ; g0 += 4 * nw) {
-        float v[4][PER];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int g = g0 + i * nw;
-#pragma unroll
-            for (int j = 0; j < PER; j++) v[i][j] = g < NGQ ? x[g * QU::GQ + 64 * j + lane] : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int g = g0 + i * nw;
-            if (g >= NGQ) break;
-            float mx = 1e-8f;
-#pragma unroll
-            for (int j = 0; j < PER; j++) mx = fmaxf(mx, fabsf(v[i][j]));
-            mx = wave_max_f32(mx);
-            const float sc = __fdiv_rn(mx, 127.0f), inv = __fdiv_rn(1.0f, sc);
-            if (lane == 0) asc[g] = sc;
-#pragma unroll
-            for (int j = 0; j < PER; j++) {
-                const float p = __fmul_rn(v[i][j], inv);
-                const float t = __fadd_rn(p, p >= 0.0f ? 0.5f : -0.5f);
-                int q = (int)t;                                // |t| <= 128: no int32 overflow
-                q = q > 127 ? 127 : (q < -128 ? -128 : q);
-                const int e = g * QU::GQ + 64 * j + lane;      // element index
-                xq[(e / QU::ELEMS) * QU::STRIDE + e % QU::ELEMS] = (int8_t)q;
-                const int s = wave_sum_i32(q);
-                if (lane == 0) xsum[g * PER + j] = s;
-            }
-        }
+    // ---- quantize x (q4gemv.h:177-213 / q4gemv_g256.h:72-99).  The first passes stay outside the
+    // loop: a loop header joining the back edge (whose x loads are the newest) would make the
+    // compiler wait for the weight loads as well.
+    quant_passes<FMT, QP>(v, wave, nw, K, NGQ, U, lane, xq, asc, xsum);
+    for (int p0 = wave + QP * nw; p0 < NP; p0 += QP * nw) {
+        load_xpass<QP>(v, x, p0, nw, K, lane);
+        quant_passes<FMT, QP>(v, p0, nw, K, NGQ, U, lane, xq, asc, xsum);
     }
     __syncthreads();
 
     // ---- per-unit fold terms t[u][row], exactly the reference's per-group expression
-    while (ub < U) {
-        const int un = ub + nw * KQ;
-        if (un + kq < U) load_raw_row<FMT>(c1, T, tile, rr, un + kq);
-        const int u = ub + kq;
+    for (;;) {
+        const int un = ub + nw * KQ, u = ub + kq;
+        if (un >= U) {
+            if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
+            break;
+        }
+        load_raw_row<FMT>(c1, T, tile, rr, min(un + kq, U - 1));
         if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
         c0 = c1;
         ub = un;
     }
     __syncthreads();
     if (threadIdx.x >= TR) return;
+    const GemvTask &task = L.t[sel.ti];
     const int row = tile * BGL_TILE + r0 + threadIdx.x;
-    if (row >= T.N) return;
+    if (row >= task.T.N) return;
     // sequential fold in group order; the LDS reads are batched 8 at a time
     float acc = 0.0f;
     const float *tr = tl + threadIdx.x;
@@ -314,30 +449,43 @@ size_t bgl_gemv_q_lds(int fmt, int K, int TR) {
     const int GQ = fmt == BGL_Q4G256SF ? 256 : 64;
     const int ELEMS = fmt == BGL_Q4G256SF ? 256 : 64;
     const int U = K / ELEMS;
-    return (size_t)U * (ELEMS + 16) + 4 * (K / GQ) + 4 * (K / 64) + 4 * (size_t)U * TR;
+    return (size_t)(U + 1) * (ELEMS + 16) + 4 * (size_t)(K / GQ + 1) + 4 * (size_t)(K / 64 + 1) + 4 * (size_t)U * TR;
 }
 
-template <int FMT>
+template <int FMT, int QP>
 static int launch_q_tr(int TR, const GemvLaunch &L, int nblocks, int nw, size_t lds, hipStream_t st) {
     dim3 g(nblocks), b(nw * BGL_TILE);
     switch (TR) {
-    case 64: hipLaunchKernelGGL((k_gemv_q<FMT, 64>), g, b, lds, st, L); return 0;
-    case 32: hipLaunchKernelGGL((k_gemv_q<FMT, 32>), g, b, lds, st, L); return 0;
-    case 16: hipLaunchKernelGGL((k_gemv_q<FMT, 16>), g, b, lds, st, L); return 0;
-    case 8: hipLaunchKernelGGL((k_gemv_q<FMT, 8>), g, b, lds, st, L); return 0;
+    case 64: hipLaunchKernelGGL((k_gemv_q<FMT, 64, QP>), g, b, lds, st, L); return 0;
+    case 32: hipLaunchKernelGGL((k_gemv_q<FMT, 32, QP>), g, b, lds, st, L); return 0;
+    case 16: hipLaunchKernelGGL((k_gemv_q<FMT, 16, QP>), g, b, lds, st, L); return 0;
+    case 8: hipLaunchKernelGGL((k_gemv_q<FMT, 8, QP>), g, b, lds, st, L); return 0;
     default: return -1;
     }
 }
 
-// nblocks counts 64-row tiles; each is split into 64/TR workgroups.
+template <int FMT>
+static int launch_q_qp(int QP, int TR, const GemvLaunch &L, int nblocks, int nw, size_t lds, hipStream_t st) {
+    switch (QP) {
+    case 1: return launch_q_tr<FMT, 1>(TR, L, nblocks, nw, lds, st);
+    case 2: return launch_q_tr<FMT, 2>(TR, L, nblocks, nw, lds, st);
+    default: return launch_q_tr<FMT, 4>(TR, L, nblocks, nw, lds, st);
+    }
+}
+
+// ntiles counts 64-row tiles; each is split into 64/TR workgroups.  QP (quantization passes per
+// wave loaded up front) covers a wave's whole share of the 256-value passes when that is <= 4.
 int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, hipStream_t st) {
-    const int fmt = L.t[0].T.fmt;
-    const size_t lds = bgl_gemv_q_lds(fmt, L.t[0].T.K, TR);
+    const int fmt = L.t[0].T.fmt, K = L.t[0].T.K;
+    if (K < 64 || K % 64) return -1;
+    const size_t lds = bgl_gemv_q_lds(fmt, K, TR);
     const int nblocks = ntiles * (BGL_TILE / TR);
+    const int pw = ((K + 255) / 256 + nw - 1) / nw;
+    const int QP = pw <= 1 ? 1 : pw <= 2 ? 2 : 4;
     switch (fmt) {
-    case BGL_Q4G256SF: return launch_q_tr<BGL_Q4G256SF>(TR, L, nblocks, nw, lds, st);
-    case BGL_Q4G64: return launch_q_tr<BGL_Q4G64>(TR, L, nblocks, nw, lds, st);
-    case BGL_Q8G64: return launch_q_tr<BGL_Q8G64>(TR, L, nblocks, nw, lds, st);
+    case BGL_Q4G256SF: return launch_q_qp<BGL_Q4G256SF>(QP, TR, L, nblocks, nw, lds, st);
+    case BGL_Q4G64: return launch_q_qp<BGL_Q4G64>(QP, TR, L, nblocks, nw, lds, st);
+    case BGL_Q8G64: return launch_q_qp<BGL_Q8G64>(QP, TR, L, nblocks, nw, lds, st);
     default: return -2;
     }
 }

@@ -54,6 +54,7 @@ template <int FMT> constexpr int chunks_per_unit(int nb) {
 #define BGL_GLOBAL __attribute__((address_space(1)))
 typedef unsigned int bgl_u32x4 __attribute__((ext_vector_type(4)));
 typedef float bgl_f32x2 __attribute__((ext_vector_type(2)));
+typedef float bgl_f32x4 __attribute__((ext_vector_type(4)));
 
 template <int FMT, int NB>
 __device__ __forceinline__ void load_raw(Raw<FMT, NB> &r, const BglDevTensor &T, int tile, int lane, int u) {
@@ -151,35 +152,37 @@ __device__ __forceinline__ void comp_q4g32h(const Raw<BGL_Q4G32H, NB> &r, int K,
     }
 }
 
+// g256sf codes are stored as signed nibbles (code ^ 8): (w << 4) & 0xF0F0F0F0 and w & 0xF0F0F0F0 are
+// 16*(code-8) as int8, so the dot4 sums are exactly 16x the reference's isum (no sum(xq) term).
 template <int MB, int NB>
 __device__ __forceinline__ void comp_g256sf(const Raw<BGL_Q4G256SF, NB> &r, int K, int u, const GemvAct &A,
                                             const Cols<MB> &C, float (&acc)[MB]) {
     int lo[32], hi[32];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        lo[4 * k] = nib_lo(r.c[k].x); hi[4 * k] = nib_hi(r.c[k].x);
-        lo[4 * k + 1] = nib_lo(r.c[k].y); hi[4 * k + 1] = nib_hi(r.c[k].y);
-        lo[4 * k + 2] = nib_lo(r.c[k].z); hi[4 * k + 2] = nib_hi(r.c[k].z);
-        lo[4 * k + 3] = nib_lo(r.c[k].w); hi[4 * k + 3] = nib_hi(r.c[k].w);
+        const uint32_t d[4] = {r.c[k].x, r.c[k].y, r.c[k].z, r.c[k].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            lo[4 * k + j] = (int)((d[j] << 4) & 0xF0F0F0F0u);
+            hi[4 * k + j] = (int)(d[j] & 0xF0F0F0F0u);
+        }
     }
 #pragma unroll
     for (int m = 0; m < MB; m++) {
         const int am = C.am[m];
         ucint xq = uni(A.xw) + (size_t)am * (K >> 2) + (size_t)u * 64;
-        ucint xs = uni(A.xsum) + (size_t)am * (K >> 6) + (size_t)u * 4;
-        int comb = 0;
+        int comb16 = 0;
 #pragma unroll
         for (int sg = 0; sg < 4; sg++) {
-            int isum = 0;
+            int isum16 = 0;
 #pragma unroll
             for (int q = 0; q < 8; q++) {
-                isum = dot4(lo[8 * sg + q], xq[16 * sg + 2 * q], isum);
-                isum = dot4(hi[8 * sg + q], xq[16 * sg + 2 * q + 1], isum);
+                isum16 = dot4(lo[8 * sg + q], xq[16 * sg + 2 * q], isum16);
+                isum16 = dot4(hi[8 * sg + q], xq[16 * sg + 2 * q + 1], isum16);
             }
-            isum -= 8 * xs[sg];
-            comb += isum * (int)((r.sub >> (8 * sg)) & 255u);
+            comb16 += isum16 * (int)((r.sub >> (8 * sg)) & 255u);
         }
-        float t = __fmul_rn(__fmul_rn(__fmul_rn((float)comb, r.s), C63), uni(A.xs)[(size_t)am * (K >> 8) + u]);
+        float t = __fmul_rn(__fmul_rn(__fmul_rn((float)(comb16 >> 4), r.s), C63), uni(A.xs)[(size_t)am * (K >> 8) + u]);
         acc[m] = __fadd_rn(acc[m], t);
     }
 }

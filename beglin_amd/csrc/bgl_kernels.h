@@ -58,7 +58,7 @@ __global__ void k_quant_q8g64(const float *w, int N, int K, int8_t *codes, float
 __global__ void k_quant_qng64(const float *w, int N, int K, int n, int dense_floor, uint8_t *planes, float *scales);
 __global__ void k_quant_q4g32h(const float *w, int N, int K, uint8_t *packed, uint16_t *scales16);
 __global__ void k_quant_g256sf(const float *w, int N, int K, uint8_t *packed, float *wsuper, uint8_t *sub);
-__global__ void k_repack_nib(const uint8_t *src, int N, int K, uint8_t *dst);
+__global__ void k_repack_nib(const uint8_t *src, int N, int K, uint32_t flip, uint8_t *dst);
 __global__ void k_repack_q8(const int8_t *src, int N, int K, uint8_t *dst);
 __global__ void k_repack_qng(const uint8_t *src, int N, int K, int n, uint8_t *dst);
 __global__ void k_repack_u32(const uint32_t *src, int N, int U, uint32_t *dst);

@@ -254,7 +254,7 @@ __global__ void k_quant_g256sf(const float *__restrict__ w, int N, int K, uint8_
 // ------------------------------------------------------------------ repack: reference layout -> tiles
 // int4 nibbles: one thread per (row, 16-byte chunk).  Reference byte b holds element 2b (low) and
 // 2b+1 (high); the device chunk's dword j byte i holds element 8j+i (low) and 8j+4+i (high).
-__global__ void k_repack_nib(const uint8_t *__restrict__ src, int N, int K, uint8_t *__restrict__ dst) {
+__global__ void k_repack_nib(const uint8_t *__restrict__ src, int N, int K, uint32_t flip, uint8_t *__restrict__ dst) {
     int cpr = K / 32;
     long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
     long ntiles = (N + BGL_TILE - 1) / BGL_TILE;
@@ -272,6 +272,7 @@ __global__ void k_repack_nib(const uint8_t *__restrict__ src, int N, int K, uint
                 uint32_t n1 = (e1 & 1) ? (b[e1 >> 1] >> 4) : (b[e1 >> 1] & 15);
                 outw[j] |= (n0 | (n1 << 4)) << (8 * i);
             }
+        for (int j = 0; j < 4; j++) outw[j] ^= flip;     // 0x88888888: signed-nibble layout (g256sf)
     }
     int tile = r / BGL_TILE, lane = r % BGL_TILE;
     uint4 *d = reinterpret_cast<uint4 *>(dst + (((size_t)tile * cpr + c) * BGL_TILE + lane) * 16);
@@ -420,6 +421,7 @@ __global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *__restrict
         int chunk = c / 32, e = c % 32, j = e / 8, q = e % 8;
         const uint8_t *p = T.w + (((size_t)tile * T.cpr + chunk) * BGL_TILE + lane) * 16 + 4 * j;
         int nib = q < 4 ? (p[q] & 15) : (p[q - 4] >> 4);
+        if (T.fmt == BGL_Q4G256SF) nib ^= 8;                 // stored as signed nibbles
         if (T.fmt == BGL_Q4G64A) {
             // moe_decode_af's affine arm (qwen_infer.c:2649-2652): (float)nib * s + b
             size_t o = ((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane;

@@ -113,6 +113,9 @@ GEMV_CASES = [
     (4, 12, 0, 1024), (4, 15, 0, 1024), (4, 9, 0, 192),
     # few row tiles and a long K: the K dimension is split over workgroups (deterministic tail sum)
     (1, 0, 0, 4096), (1, 0, 1, 4096), (4, 15, 0, 8192), (5, 0, 0, 8192),
+    # W4A8 quantization passes of 256 values: partial last pass (K % 256 != 0), four passes per
+    # wave (g256sf K=8960), and more passes than one round of loads covers (K=20480)
+    (1, 0, 1, 320), (2, 0, 1, 1408), (3, 0, 1, 8960), (1, 0, 1, 20480),
 ]
 
 
