@@ -346,33 +346,44 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     float4 v[QP];
     load_xpass<QP>(v, x, wave, nw, K, lane);
     __builtin_amdgcn_sched_barrier(0);
-    const int r = lane % TR, kq = lane / TR, rr = r0 + r;
-    int ub = wave * KQ;
-    Raw<FMT, 0> c0, c1;
-    load_raw_row<FMT>(c0, T, tile, rr, min(ub + kq, U - 1));
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- quantize x (q4gemv.h:177-213 / q4gemv_g256.h:72-99).  The first passes stay outside the
-    // loop: a loop header joining the back edge (whose x loads are the newest) would make the
-    // compiler wait for the weight loads as well.
-    quant_passes<FMT, QP>(v, wave, nw, K, NGQ, U, lane, xq, asc, xsum);
-    for (int p0 = wave + QP * nw; p0 < NP; p0 += QP * nw) {
-        load_xpass<QP>(v, x, p0, nw, K, lane);
-        quant_passes<FMT, QP>(v, p0, nw, K, NGQ, U, lane, xq, asc, xsum);
-    }
-    __syncthreads();
-
-    // ---- per-unit fold terms t[u][row], exactly the reference's per-group expression
-    for (;;) {
-        const int un = ub + nw * KQ, u = ub + kq;
-        if (un >= U) {
-            if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
-            break;
+    // Waves [0, nwl) own weight units; any further waves of the launch only quantize.  The two
+    // roles are separate branches so the weight waves' wait for x is not merged with a path that
+    // issued no weight loads.
+    const int nwl = min(nw, (U + KQ - 1) / KQ);
+    if (wave < nwl) {
+        const int r = lane % TR, kq = lane / TR, rr = r0 + r;
+        int ub = wave * KQ;
+        Raw<FMT, 0> c0, c1;
+        load_raw_row<FMT>(c0, T, tile, rr, min(ub + kq, U - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        // quantize x (q4gemv.h:177-213 / q4gemv_g256.h:72-99).  The first passes stay outside the
+        // loop: a loop header joining the back edge (whose x loads are the newest) would make the
+        // compiler wait for the weight loads as well.
+        quant_passes<FMT, QP>(v, wave, nw, K, NGQ, U, lane, xq, asc, xsum);
+        for (int p0 = wave + QP * nw; p0 < NP; p0 += QP * nw) {
+            load_xpass<QP>(v, x, p0, nw, K, lane);
+            quant_passes<FMT, QP>(v, p0, nw, K, NGQ, U, lane, xq, asc, xsum);
         }
-        load_raw_row<FMT>(c1, T, tile, rr, min(un + kq, U - 1));
-        if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
-        c0 = c1;
-        ub = un;
+        __syncthreads();
+        // per-unit fold terms t[u][row], exactly the reference's per-group expression
+        for (;;) {
+            const int un = ub + nwl * KQ, u = ub + kq;
+            if (un >= U) {
+                if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
+                break;
+            }
+            load_raw_row<FMT>(c1, T, tile, rr, min(un + kq, U - 1));
+            if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
+            c0 = c1;
+            ub = un;
+        }
+    } else {
+        quant_passes<FMT, QP>(v, wave, nw, K, NGQ, U, lane, xq, asc, xsum);
+        for (int p0 = wave + QP * nw; p0 < NP; p0 += QP * nw) {
+            load_xpass<QP>(v, x, p0, nw, K, lane);
+            quant_passes<FMT, QP>(v, p0, nw, K, NGQ, U, lane, xq, asc, xsum);
+        }
+        __syncthreads();
     }
     __syncthreads();
     if (threadIdx.x >= TR) return;
