@@ -535,16 +535,17 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
     L.m0 = 0;
     L.mcols = 1;
     // Rows per workgroup: split 64-row tiles until the launch has >= 512 workgroups (8 rows at the
-    // least), so the weight stream is spread over every CU.  Waves: those that own weight units,
-    // plus quantization-only waves up to ceil(passes / 4) (at least 3), since every workgroup
-    // quantizes the whole activation row.  (Measured on 1536x1536, 2048x1536, 17920x1536 and
-    // 1536x8960 g256sf launches: within 0.1 us of the best shape found for each.)
+    // least), so the weight stream is spread over every CU.  Waves: ceil(passes / 4), at least 3,
+    // since every workgroup quantizes the whole activation row; the waves take the weight units in
+    // turn (the last ones only quantize when there are fewer units than waves).  (Measured on
+    // 1536x1536, 2048x1536, 17920x1536 and 1536x8960 g256sf launches: the best shape found for
+    // each, or within 0.05 us of it.)
     int TR = 64;
     while (TR > 8 && (long)blocks * (BGL_TILE / TR) < 512) TR >>= 1;
     if (c->force_tr) TR = c->force_tr;
     while (TR > 8 && bgl_gemv_q_lds(Ts[0].fmt, Ts[0].K, TR) > BGL_GEMV_Q_LDS_MAX) TR >>= 1;   // the t[u][row] terms shrink with TR
-    const int KQ = BGL_TILE / TR, U = Ts[0].nunits, NP = (Ts[0].K + 255) / 256;
-    int nw = std::max((U + KQ - 1) / KQ, std::min(16, std::max(3, (NP + 3) / 4)));
+    const int KQ = BGL_TILE / TR, NP = (Ts[0].K + 255) / 256;
+    int nw = std::min(16, std::max(3, (NP + 3) / 4));
     if (nw > c->max_waves) nw = c->max_waves;
     // every task block of the launch uses the same TR; remap blk0 to workgroup units
     for (int i = 0; i < n; i++) L.t[i].blk0 *= KQ;

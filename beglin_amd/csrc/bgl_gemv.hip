@@ -148,19 +148,29 @@ template <int FMT> struct QUnit {
     static constexpr bool XSUM = FMT == BGL_Q4G64;                  // unsigned nibbles: needs sum(xq) per 64
 };
 
-template <int FMT>
-__device__ __forceinline__ void load_raw_row(Raw<FMT, 0> &r, const BglDevTensor &T, int tile, int rr, int u) {
-    constexpr int CPU = chunks_per_unit<FMT>(0);
+// A lane's share of one work unit: H lanes (lane l and its partner l ^ TR when H == 2) split the
+// unit's chunks, part h holding chunks [h*CP, (h+1)*CP).  Partners read the same scale words.
+template <int FMT, int H> struct RawPart {
+    static constexpr int CP = chunks_per_unit<FMT>(0) / H;
+    uint4 c[CP];
+    float s;
+    uint32_t sub;             // g256sf: this part's sub-codes, from the low byte up
+};
+
+template <int FMT, int H>
+__device__ __forceinline__ void load_part(RawPart<FMT, H> &r, const BglDevTensor &T, int tile, int rr, int u, int h) {
+    constexpr int CPU = chunks_per_unit<FMT>(0), CP = CPU / H;
     // global address space: flat loads would also count against the LDS wait counter
-    const BGL_GLOBAL bgl_u32x4 *cp = (const BGL_GLOBAL bgl_u32x4 *)(T.w) + ((size_t)tile * T.cpr + (size_t)u * CPU) * BGL_TILE + rr;
+    const BGL_GLOBAL bgl_u32x4 *cp =
+        (const BGL_GLOBAL bgl_u32x4 *)(T.w) + ((size_t)tile * T.cpr + (size_t)u * CPU + h * CP) * BGL_TILE + rr;
 #pragma unroll
-    for (int k = 0; k < CPU; k++) {
+    for (int k = 0; k < CP; k++) {
         const bgl_u32x4 v = cp[k * BGL_TILE];
         r.c[k] = make_uint4(v.x, v.y, v.z, v.w);
     }
     const size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + rr;
     r.s = ((const BGL_GLOBAL float *)T.s0)[so];
-    if constexpr (FMT == BGL_Q4G256SF) r.sub = ((const BGL_GLOBAL uint32_t *)T.s1)[so];
+    if constexpr (FMT == BGL_Q4G256SF) r.sub = ((const BGL_GLOBAL uint32_t *)T.s1)[so] >> (h * 8 * (4 / H));
 }
 
 template <int CTRL>
@@ -277,13 +287,18 @@ __device__ __forceinline__ void load_xpass(float4 (&v)[QP], const float *x, int 
 __device__ __forceinline__ int snib_lo16(uint32_t w) { return (int)((w << 4) & 0xF0F0F0F0u); }
 __device__ __forceinline__ int snib_hi16(uint32_t w) { return (int)(w & 0xF0F0F0F0u); }
 
-template <int FMT>
-__device__ __forceinline__ float unit_term(const Raw<FMT, 0> &r, const int8_t *xq, const float *asc, const int *xsum, int u) {
+// The exact integer part of a unit's dot product over this lane's chunks (partners' parts add up
+// to the reference's integer sum): g256sf 16 * sum_sg isum_sg * sub_sg over its sub-groups, |.| < 2^29;
+// q4g64 sum code*xq (the -8*sum(xq) term is applied once, in unit_float); q8g64 sum code*xq.
+template <int FMT, int H>
+__device__ __forceinline__ int unit_part(const RawPart<FMT, H> &r, const int8_t *xq, int u, int h) {
+    constexpr int CP = RawPart<FMT, H>::CP;
     const int4 *x4 = reinterpret_cast<const int4 *>(xq + (size_t)u * QUnit<FMT>::STRIDE);
     if constexpr (FMT == BGL_Q4G256SF) {
-        int comb16 = 0;                                // 16 * sum_sg isum_sg * sub_sg, |.| < 2^29
+        x4 += h * CP * 2;                              // 32 activation bytes per chunk
+        int comb16 = 0;
 #pragma unroll
-        for (int sg = 0; sg < 4; sg++) {
+        for (int sg = 0; sg < CP / 2; sg++) {
             int isum16 = 0;
 #pragma unroll
             for (int k = 0; k < 2; k++) {
@@ -296,11 +311,12 @@ __device__ __forceinline__ float unit_term(const Raw<FMT, 0> &r, const int8_t *x
             }
             comb16 += isum16 * (int)((r.sub >> (8 * sg)) & 255u);
         }
-        return __fmul_rn(__fmul_rn(__fmul_rn((float)(comb16 >> 4), r.s), C63), asc[u]);
+        return comb16;
     } else if constexpr (FMT == BGL_Q4G64) {
+        x4 += h * CP * 2;
         int isum = 0;
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
+        for (int k = 0; k < CP; k++) {
             const uint4 c = r.c[k];
             const int4 xa = x4[2 * k], xb = x4[2 * k + 1];
             isum = dot4(nib_lo(c.x), xa.x, isum); isum = dot4(nib_hi(c.x), xa.y, isum);
@@ -308,19 +324,28 @@ __device__ __forceinline__ float unit_term(const Raw<FMT, 0> &r, const int8_t *x
             isum = dot4(nib_lo(c.z), xb.x, isum); isum = dot4(nib_hi(c.z), xb.y, isum);
             isum = dot4(nib_lo(c.w), xb.z, isum); isum = dot4(nib_hi(c.w), xb.w, isum);
         }
-        isum -= 8 * xsum[u];
-        return __fmul_rn(__fmul_rn((float)isum, r.s), asc[u]);
+        return isum;
     } else {
+        x4 += h * CP;                                  // 16 activation bytes per chunk
         int isum = 0;
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < CP; k++) {
             const uint4 c = r.c[k];
             const int4 xa = x4[k];
             isum = dot4((int)c.x, xa.x, isum); isum = dot4((int)c.y, xa.y, isum);
             isum = dot4((int)c.z, xa.z, isum); isum = dot4((int)c.w, xa.w, isum);
         }
-        return __fmul_rn(__fmul_rn((float)isum, r.s), asc[u]);
+        return isum;
     }
+}
+
+// The unit's fp32 term, exactly the reference's per-group expression (q4gemv_g256.h:154,
+// q4gemv.h:241): g256sf ((comb * wsuper) * (1/63)) * ascale; q4g64 / q8g64 (isum * wscale) * ascale.
+template <int FMT>
+__device__ __forceinline__ float unit_float(int isum, float s, const float *asc, const int *xsum, int u) {
+    if constexpr (FMT == BGL_Q4G256SF) return __fmul_rn(__fmul_rn(__fmul_rn((float)(isum >> 4), s), C63), asc[u]);
+    else if constexpr (FMT == BGL_Q4G64) return __fmul_rn(__fmul_rn((float)(isum - 8 * xsum[u]), s), asc[u]);
+    else return __fmul_rn(__fmul_rn((float)isum, s), asc[u]);
 }
 
 template <int FMT, int TR, int QP>
@@ -349,12 +374,14 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     // Waves [0, nwl) own weight units; any further waves of the launch only quantize.  The two
     // roles are separate branches so the weight waves' wait for x is not merged with a path that
     // issued no weight loads.
-    const int nwl = min(nw, (U + KQ - 1) / KQ);
+    constexpr int H = TR <= 32 ? 2 : 1;                  // lanes sharing one unit
+    constexpr int UPI = KQ / H;                          // units per wave and iteration
+    const int nwl = min(nw, (U + UPI - 1) / UPI);
     if (wave < nwl) {
-        const int r = lane % TR, kq = lane / TR, rr = r0 + r;
-        int ub = wave * KQ;
-        Raw<FMT, 0> c0, c1;
-        load_raw_row<FMT>(c0, T, tile, rr, min(ub + kq, U - 1));
+        const int r = lane % TR, j = lane / TR, kq = j / H, h = j % H, rr = r0 + r;
+        int ub = wave * UPI;
+        RawPart<FMT, H> c0, c1;
+        load_part<FMT, H>(c0, T, tile, rr, min(ub + kq, U - 1), h);
         __builtin_amdgcn_sched_barrier(0);
         // quantize x (q4gemv.h:177-213 / q4gemv_g256.h:72-99).  The first passes stay outside the
         // loop: a loop header joining the back edge (whose x loads are the newest) would make the
@@ -365,15 +392,20 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
             quant_passes<FMT, QP>(v, p0, nw, K, NGQ, U, lane, xq, asc, xsum);
         }
         __syncthreads();
-        // per-unit fold terms t[u][row], exactly the reference's per-group expression
+        // per-unit fold terms t[u][row]; every lane computes (the partner exchange is wave-wide)
+        auto emit = [&](const RawPart<FMT, H> &c, int u) {
+            int p = unit_part<FMT, H>(c, xq, min(u, U - 1), h);
+            if constexpr (H == 2) p += __shfl_xor(p, TR);
+            if (h == 0 && u < U) tl[u * TR + r] = unit_float<FMT>(p, c.s, asc, xsum, u);
+        };
         for (;;) {
-            const int un = ub + nwl * KQ, u = ub + kq;
-            if (un >= U) {
-                if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
+            const int un = ub + nwl * UPI, u = ub + kq;
+            if (un >= U) {                  // last iteration: no prefetch, so no join before the wait
+                emit(c0, u);
                 break;
             }
-            load_raw_row<FMT>(c1, T, tile, rr, min(un + kq, U - 1));
-            if (u < U) tl[u * TR + r] = unit_term<FMT>(c0, xq, asc, xsum, u);
+            load_part<FMT, H>(c1, T, tile, rr, min(un + kq, U - 1), h);
+            emit(c0, u);
             c0 = c1;
             ub = un;
         }
