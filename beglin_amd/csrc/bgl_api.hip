@@ -240,8 +240,8 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     long rows = (long)T.ntiles * BGL_TILE;
     size_t wbytes = (size_t)rows * T.cpr * 16;
     const bool dense = kind == BGL_F16 || kind == BGL_F32;
-    size_t s0bytes = dense ? 0 : (size_t)rows * T.nunits * (kind == BGL_QNG64 ? 8 : 4);
-    const bool has_s1 = kind == BGL_Q4G256SF || kind == BGL_Q4G64A;
+    size_t s0bytes = dense ? 0 : (size_t)rows * T.nunits * (kind == BGL_QNG64 || kind == BGL_Q4G256SF ? 8 : 4);
+    const bool has_s1 = kind == BGL_Q4G64A;
     void *w = nullptr, *s0 = nullptr, *s1 = nullptr;
     hipError_t e = hipMalloc(&w, wbytes);
     if (e == hipSuccess && s0bytes) e = hipMalloc(&s0, s0bytes);
@@ -272,11 +272,15 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     }
     long nu = rows * T.nunits;
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q8G64: case BGL_Q4G32H: case BGL_Q4G256SF: case BGL_Q4G64A:
+    case BGL_Q4G64: case BGL_Q8G64: case BGL_Q4G32H: case BGL_Q4G64A:
         // Q4G32H: two fp16 per unit read as one u32; the others one fp32 per unit.
         hipLaunchKernelGGL(k_repack_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsc, out, T.nunits, (uint32_t *)s0);
-        if (has_s1)   // g256sf: 4 sub-codes per unit; Q4G64A: the fp32 bias per unit
+        if (has_s1)   // Q4G64A: the fp32 bias per unit
             hipLaunchKernelGGL(k_repack_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsub, out, T.nunits, (uint32_t *)s1);
+        break;
+    case BGL_Q4G256SF:   // wsuper and the unit's 4 sub-codes in one 8-byte word
+        hipLaunchKernelGGL(k_repack_zip_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsc, (const uint32_t *)dsub,
+                           out, T.nunits, (uint2 *)s0);
         break;
     case BGL_QNG64:
         hipLaunchKernelGGL(k_repack_qng_scales, dim3(nblk(nu)), dim3(256), 0, c->stream, (const float *)dsc, out, in / 64, (float2 *)s0);

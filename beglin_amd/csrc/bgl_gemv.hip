@@ -169,8 +169,13 @@ __device__ __forceinline__ void load_part(RawPart<FMT, H> &r, const BglDevTensor
         r.c[k] = make_uint4(v.x, v.y, v.z, v.w);
     }
     const size_t so = ((size_t)tile * T.nunits + u) * BGL_TILE + rr;
-    r.s = ((const BGL_GLOBAL float *)T.s0)[so];
-    if constexpr (FMT == BGL_Q4G256SF) r.sub = ((const BGL_GLOBAL uint32_t *)T.s1)[so] >> (h * 8 * (4 / H));
+    if constexpr (FMT == BGL_Q4G256SF) {
+        const bgl_u32x2 w = ((const BGL_GLOBAL bgl_u32x2 *)T.s0)[so];
+        r.s = __uint_as_float(w.x);
+        r.sub = w.y >> (h * 8 * (4 / H));
+    } else {
+        r.s = ((const BGL_GLOBAL float *)T.s0)[so];
+    }
 }
 
 template <int CTRL>

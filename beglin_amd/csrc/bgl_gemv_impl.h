@@ -54,6 +54,7 @@ template <int FMT> constexpr int chunks_per_unit(int nb) {
 #define BGL_GLOBAL __attribute__((address_space(1)))
 typedef unsigned int bgl_u32x4 __attribute__((ext_vector_type(4)));
 typedef float bgl_f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int bgl_u32x2 __attribute__((ext_vector_type(2)));
 typedef float bgl_f32x4 __attribute__((ext_vector_type(4)));
 
 template <int FMT, int NB>
@@ -75,8 +76,11 @@ __device__ __forceinline__ void load_raw(Raw<FMT, NB> &r, const BglDevTensor &T,
         const bgl_f32x2 v = ((const BGL_GLOBAL bgl_f32x2 *)T.s0)[so];
         r.s = make_float2(v.x, v.y);
     } else if constexpr (FMT == BGL_Q4G32H) r.s = ((const BGL_GLOBAL uint32_t *)T.s0)[so];
-    else r.s = ((const BGL_GLOBAL float *)T.s0)[so];
-    if constexpr (FMT == BGL_Q4G256SF) r.sub = ((const BGL_GLOBAL uint32_t *)T.s1)[so];
+    else if constexpr (FMT == BGL_Q4G256SF) {
+        const bgl_u32x2 w = ((const BGL_GLOBAL bgl_u32x2 *)T.s0)[so];
+        r.s = __uint_as_float(w.x);
+        r.sub = w.y;
+    } else r.s = ((const BGL_GLOBAL float *)T.s0)[so];
     }
 }
 

@@ -5,7 +5,8 @@
 // A bound tensor in the tiled device layout.  Work unit per format (one wave iteration):
 //   Q4G64   64 elements, 2 chunks, s0 = fp32 scale
 //   Q4G32H  64 elements, 2 chunks, s0 = u32 holding the two fp16 group-32 scales (low = first)
-//   G256SF  256 elements, 8 chunks, s0 = fp32 wsuper, s1 = u32 of the 4 sub-codes (byte s = sub s)
+//   G256SF  256 elements, 8 chunks, s0 = u32x2 (x = fp32 wsuper bits, y = the 4 sub-codes, byte s =
+//           sub s), one load per unit; codes stored as signed nibbles (code ^ 8)
 //   Q8G64   64 elements, 4 chunks, s0 = fp32 scale
 //   QNG64   128 elements (a pair of 64-groups), n chunks, s0 = float2 (the two group scales)
 struct BglDevTensor {
@@ -63,6 +64,7 @@ __global__ void k_repack_q8(const int8_t *src, int N, int K, uint8_t *dst);
 __global__ void k_repack_qng(const uint8_t *src, int N, int K, int n, uint8_t *dst);
 __global__ void k_repack_u32(const uint32_t *src, int N, int U, uint32_t *dst);
 __global__ void k_repack_u64(const uint64_t *src, int N, int U, uint64_t *dst);
+__global__ void k_repack_zip_u32(const uint32_t *a, const uint32_t *b, int N, int U, uint2 *dst);
 __global__ void k_repack_qng_scales(const float *src, int N, int ng, float2 *dst);
 __global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *out);
 __global__ void k_splitk_reduce(const float *part, int ks, int M, int N, const float *bias, float *y, int ystride);

@@ -376,6 +376,19 @@ __global__ void k_repack_u32(const uint32_t *__restrict__ src, int N, int U, uin
     dst[((size_t)tile * U + u) * BGL_TILE + lane] = r < N ? src[(size_t)r * U + u] : 0u;
 }
 
+// Two per-(row, unit) u32 arrays [N][U] -> one 8-byte word per unit in the tile layout
+// [tile][u][lane] (x from a, y from b): the g256sf wsuper and its four sub-codes travel together.
+__global__ void k_repack_zip_u32(const uint32_t *__restrict__ a, const uint32_t *__restrict__ b, int N, int U,
+                                 uint2 *__restrict__ dst) {
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    long ntiles = (N + BGL_TILE - 1) / BGL_TILE;
+    if (t >= ntiles * BGL_TILE * U) return;
+    int r = (int)(t / U), u = (int)(t % U);
+    int tile = r / BGL_TILE, lane = r % BGL_TILE;
+    const size_t i = (size_t)r * U + u;
+    dst[((size_t)tile * U + u) * BGL_TILE + lane] = r < N ? make_uint2(a[i], b[i]) : make_uint2(0u, 0u);
+}
+
 // Per-(row, unit) pairs of 16-bit fp16 scales or 8-byte float pairs, and 4 sub-codes -> one word.
 __global__ void k_repack_u64(const uint64_t *__restrict__ src, int N, int U, uint64_t *__restrict__ dst) {
     long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -436,8 +449,9 @@ __global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *__restrict
             v = (float)(nib - 8) * __half2float(__ushort_as_half(h));
         } else {
             size_t o = ((size_t)tile * T.nunits + c / 256) * BGL_TILE + lane;
-            float ws = reinterpret_cast<const float *>(T.s0)[o];
-            uint32_t sub4 = T.s1[o];
+            const uint2 wsub = reinterpret_cast<const uint2 *>(T.s0)[o];
+            float ws = __uint_as_float(wsub.x);
+            uint32_t sub4 = wsub.y;
             float sc = (float)((sub4 >> (8 * ((c / 64) & 3))) & 255);
             v = (float)(nib - 8) * __fmul_rn(ws, __fdiv_rn(sc, 63.0f));
         }
