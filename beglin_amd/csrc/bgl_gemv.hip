@@ -427,18 +427,26 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     const GemvTask &task = L.t[sel.ti];
     const int row = tile * BGL_TILE + r0 + threadIdx.x;
     if (row >= task.T.N) return;
-    // sequential fold in group order; the LDS reads are batched 8 at a time
+    // sequential fold in group order; the LDS reads go out 8 at a time, one batch ahead of the adds
     float acc = 0.0f;
     const float *tr = tl + threadIdx.x;
-    int g = 0;
-    for (; g + 8 <= U; g += 8) {
-        float t8[8];
+    const int U8 = U & ~7;
+    float t8[8], n8[8];
+    if (U8) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) t8[i] = tr[(g + i) * TR];
+        for (int i = 0; i < 8; i++) t8[i] = tr[i * TR];
+    }
+    for (int g = 0; g < U8; g += 8) {
+        if (g + 8 < U8) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) n8[i] = tr[(g + 8 + i) * TR];
+        }
 #pragma unroll
         for (int i = 0; i < 8; i++) acc = __fadd_rn(acc, t8[i]);
+#pragma unroll
+        for (int i = 0; i < 8; i++) t8[i] = n8[i];
     }
-    for (; g < U; g++) acc = __fadd_rn(acc, tr[g * TR]);
+    for (int g = U8; g < U; g++) acc = __fadd_rn(acc, tr[g * TR]);
     const float bb = task.bias ? task.bias[row] : 0.0f;
     task.y[(size_t)L.m0 * task.ystride + row] = __fadd_rn(bb, acc);
 }

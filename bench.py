@@ -657,7 +657,7 @@ def main():
     achieved = nbytes / (k_ms * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemv_q<fmt,TR> (bgl_gemv.hip)" if prep_ms == 0.0 else "k_gemv<fmt,act,n,MB> (bgl_gemv.hip)",
+            "kernel": "k_gemv_q<fmt,TR,QP> (bgl_gemv.hip)" if prep_ms == 0.0 else "k_gemv<fmt,act,n,MB> (bgl_gemv.hip)",
             "launches_per_step": launches, "kernel_us_per_launch": round(k_ms * 1e3 / launches, 3),
             "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3),
             "bytes_per_launch": round(nbytes / launches)}
