@@ -206,6 +206,17 @@ class Context:
                                      sd.h if sd else None, _p(x_dev), _p(idx_dev), _p(w_dev), T, K, _p(out_dev)),
                "bgl_moe_ffn_dev")
 
+    def moe_route(self, router_w, x_dev, K, idx_dev, w_dev, router_b=None, renorm=False):
+        E, inn = router_w.shape
+        _check(lib().bgl_moe_route_dev(self.h, _p(router_w), _p(router_b) if router_b is not None else None, E, inn, _p(x_dev),
+                                       x_dev.shape[0], K, 1 if renorm else 0, _p(idx_dev), _p(w_dev)), "bgl_moe_route_dev")
+
+    def moe_layer(self, router_w, gate, up, down, shared, x_dev, K, out_dev, router_b=None, renorm=False):
+        sg, su, sd = (shared or (None, None, None))
+        _check(lib().bgl_moe_layer_dev(self.h, _p(router_w), _p(router_b) if router_b is not None else None, 1 if renorm else 0,
+                                       gate.h, up.h, down.h, sg.h if sg else None, su.h if su else None, sd.h if sd else None,
+                                       _p(x_dev), x_dev.shape[0], K, _p(out_dev)), "bgl_moe_layer_dev")
+
 
 # ---- the name-keyed registry (mlx_moe.h boundary): thin wrappers, 1 = ok / 0 = failure ----
 class Registry:

@@ -61,6 +61,8 @@ SIGNATURES = [
     ("bgl_experts_from_tensors", _I, [_P, _I, C.POINTER(_P), C.POINTER(_P)]),
     ("bgl_gather_matvec_dev", _I, [_P, _P, _P, _P, _I, _P]),
     ("bgl_moe_ffn_dev", _I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
+    ("bgl_moe_route_dev", _I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _P, _P]),
+    ("bgl_moe_layer_dev", _I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     # name-keyed registry (mlx_moe.h boundary)
     ("bgl_gpu_available", _I, []),
     ("bgl_gpu_synchronize", _I, []),

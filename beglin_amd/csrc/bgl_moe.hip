@@ -436,3 +436,139 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
     HIPCHK(hipGetLastError());
     return 0;
 }
+
+// ================================================================================== router
+// The routing of moe_ffn_batched (qwen_infer.c:5243-5257, :5275), in two kernels: the scores
+// (one wave per token and expert, so the router matrix streams through many CUs), then the
+// softmax / top-K / renorm of each token (one wave per token):
+//   scores[e] = (float)(sum_c (double)W[e][c] * x[c]) (+ b[e])       moe_matvec_f32, :3460-3466
+//   softmax: max, expf(s - max) in float, double sum, (float)(e / sum)  moe_softmax_full, :3467-3472
+//   top-K: repeated strict maximum, ties to the lowest expert id       moe_top_k_select, :3514-3521
+//   optional renorm: the K weights over their double sum               moe_topk_renorm, :3529-3534
+// The router dot products run in double on every lane (fma with exact float products) and are
+// combined across the wave; the softmax sum runs sequentially in expert order as the reference's.
+// exp is evaluated in double and rounded once to float.
+#define ROUTE_MAXE 256
+#define ROUTE_EPW 4          // experts per scores workgroup: one per wave
+
+// scores[t][e] = (float)(sum_c (double)W[e][c] * x[t][c]) (+ b[e]); grid (T, ceil(E/4)), one wave
+// per expert so the router matrix is read by many CUs at once.
+__global__ __launch_bounds__(ROUTE_EPW * 64) void k_moe_router_scores(const float *__restrict__ W, const float *__restrict__ bias,
+                                                                      int E, int H, const float *__restrict__ x,
+                                                                      float *__restrict__ scores) {
+    const int t = blockIdx.x, e = blockIdx.y * ROUTE_EPW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (e >= E) return;
+    const float *we = W + (size_t)e * H, *xt = x + (size_t)t * H;
+    double acc = 0.0;
+    for (int c = 4 * lane; c < H; c += 256) {
+        const float4 wv = *reinterpret_cast<const float4 *>(we + c), xv = *reinterpret_cast<const float4 *>(xt + c);
+        acc = fma((double)wv.x, (double)xv.x, acc);
+        acc = fma((double)wv.y, (double)xv.y, acc);
+        acc = fma((double)wv.z, (double)xv.z, acc);
+        acc = fma((double)wv.w, (double)xv.w, acc);
+    }
+    for (int o = 32; o; o >>= 1) acc += __shfl_xor(acc, o);
+    if (lane == 0) scores[(size_t)t * E + e] = bias ? __fadd_rn((float)acc, bias[e]) : (float)acc;
+}
+
+// softmax, top-K and renorm of one token per wave (grid T, 64 threads).
+__global__ __launch_bounds__(64) void k_moe_route_topk(const float *__restrict__ scores, int E, int K, int renorm,
+                                                       int32_t *__restrict__ idx_out, float *__restrict__ w_out) {
+    __shared__ float sc[ROUTE_MAXE];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    constexpr int PL = ROUTE_MAXE / 64;                      // scores per lane: expert lane + 64j
+    float v[PL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PL; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? scores[(size_t)t * E + e] : 0.0f;
+        if (e < E) mx = fmaxf(mx, v[j]);
+    }
+    for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+#pragma unroll
+    for (int j = 0; j < PL; j++) {
+        const int e = lane + 64 * j;
+        if (e < E) {
+            v[j] = (float)exp((double)__fsub_rn(v[j], mx));
+            sc[e] = v[j];
+        }
+    }
+    __syncthreads();                                         // the workgroup is this one wave
+    double sum = 0.0;
+    if (lane == 0)
+        for (int e = 0; e < E; e++) sum += (double)sc[e];
+    sum = __shfl(sum, 0);
+    unsigned used = 0;                                       // bit j: expert lane + 64j selected
+#pragma unroll
+    for (int j = 0; j < PL; j++) v[j] = (float)((double)v[j] / sum);
+    float sel_w[MOE_MAX_K];
+    int sel_i[MOE_MAX_K];
+    for (int k = 0; k < K; k++) {
+        // this lane's best unselected expert (lowest id first among equal values), then the wave's
+        float bv = -1.0f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < PL; j++) {
+            const int e = lane + 64 * j;
+            if (e < E && !((used >> j) & 1u) && v[j] > bv) { bv = v[j]; bi = e; }
+        }
+        for (int o = 32; o; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if ((bi & 63) == lane) used |= 1u << (bi >> 6);
+        sel_w[k] = bv;
+        sel_i[k] = bi;
+    }
+    if (lane != 0) return;
+    if (renorm) {
+        double s = 0.0;
+        for (int k = 0; k < K; k++) s += (double)sel_w[k];
+        if (s > 0.0)
+            for (int k = 0; k < K; k++) sel_w[k] = (float)((double)sel_w[k] / s);
+    }
+    for (int k = 0; k < K; k++) {
+        idx_out[(size_t)t * K + k] = sel_i[k];
+        w_out[(size_t)t * K + k] = sel_w[k];
+    }
+}
+
+extern "C" int bgl_moe_route_dev(bgl_ctx *c, const float *rw_dev, const float *rb_dev, int E, int in, const float *x_dev,
+                                 int T, int K, int renorm, int32_t *idx_dev, float *w_dev) {
+    if (!c || !rw_dev || !x_dev || !idx_dev || !w_dev || T < 1)
+        return bgl_fail(BGL_E_ARG, "bgl_moe_route_dev: bad argument");
+    if (E < 1 || E > ROUTE_MAXE || K < 1 || K > E || K > MOE_MAX_K)
+        return bgl_fail(BGL_E_ARG, "bgl_moe_route_dev: need 1 <= K <= min(E, %d) and E <= %d (E=%d, K=%d)", MOE_MAX_K, ROUTE_MAXE, E, K);
+    if (in < 4 || in % 4 || ((uintptr_t)rw_dev | (uintptr_t)x_dev) % 16)
+        return bgl_fail(BGL_E_ARG, "bgl_moe_route_dev: in=%d must be a multiple of 4 with 16-byte aligned rows", in);
+    HIPCHK(hipSetDevice(c->device));
+    if (dbuf_reserve(c, c->moe_scores, (size_t)T * E * 4, false)) return BGL_E_NOMEM;
+    float *scores = (float *)c->moe_scores.p;
+    int tok = prof_begin(c, 2);
+    hipLaunchKernelGGL(k_moe_router_scores, dim3(T, (E + ROUTE_EPW - 1) / ROUTE_EPW), dim3(ROUTE_EPW * 64), 0, c->stream, rw_dev,
+                       rb_dev, E, in, x_dev, scores);
+    prof_end(c, tok);
+    HIPCHK(hipGetLastError());
+    tok = prof_begin(c, 2);
+    hipLaunchKernelGGL(k_moe_route_topk, dim3(T), dim3(64), 0, c->stream, (const float *)scores, E, K, renorm ? 1 : 0, idx_dev, w_dev);
+    prof_end(c, tok);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+extern "C" int bgl_moe_layer_dev(bgl_ctx *c, const float *rw_dev, const float *rb_dev, int renorm, const bgl_tensor *gate,
+                                 const bgl_tensor *up, const bgl_tensor *down, const bgl_tensor *sg, const bgl_tensor *su,
+                                 const bgl_tensor *sd, const float *x_dev, int T, int K, float *out_dev) {
+    if (!c || !gate || T < 1 || K < 1) return bgl_fail(BGL_E_ARG, "bgl_moe_layer_dev: bad argument");
+    int rc;
+    if ((rc = expert_check(gate, "bgl_moe_layer_dev: gate"))) return rc;
+    const int E = (int)gate->experts.size(), H = gate->T.K;
+    HIPCHK(hipSetDevice(c->device));
+    if (dbuf_reserve(c, c->moe_route, (size_t)T * K * 8, false)) return BGL_E_NOMEM;
+    int32_t *idx = (int32_t *)c->moe_route.p;
+    float *w = (float *)(idx + (size_t)T * K);
+    if ((rc = bgl_moe_route_dev(c, rw_dev, rb_dev, E, H, x_dev, T, K, renorm, idx, w))) return rc;
+    return bgl_moe_ffn_dev(c, gate, up, down, sg, su, sd, x_dev, idx, w, T, K, out_dev);
+}

@@ -20,9 +20,11 @@ cfg5 = Llama-3.1-8B projections (q/o 4096x4096, k/v 1024x4096, gate/up 14336x409
 4096x14336) at M=32 fp32 activation rows on the matrix-core path: attention int8 (q8g64), MLP
 int4 g32 (Q4G32H), a seeded 20% of the tensors qNg64 n=5; one step = --layers layers.
 cfg4 = DeepSeek-V2-Lite routed MoE FFN (E=64 + 2 shared experts, hidden 2048, expert inter 1408,
-top-6 over softmax(N(0,1) router logits)), T=--M tokens, per-expert precision drawn from the seed
-over {q4g32h, q8g64, qNg64 n=7..15}; one step = --layers distinct MoE layers; algorithmic bytes =
-the packed + scale bytes of every expert the step's routing touches (+ shared experts, x, out)."""
+top-6), the whole layer on the device: fp32 router [64 x 2048] with N(0, 1/2048) entries (N(0,1)
+logits), softmax, top-6, sort, SwiGLU experts, combine, shared experts; T=--M tokens, per-expert
+precision drawn from the seed over {q4g32h, q8g64, qNg64 n=7..15}; one step = --layers distinct
+MoE layers; algorithmic bytes = the packed + scale bytes of every expert the step's routing
+touches (+ shared experts, router weights, x, out)."""
 import argparse
 import json
 import os
@@ -182,7 +184,9 @@ def wbytes(kind, out, inn, bits):
 
 
 class MoeWorkload:
-    """`layers` routed MoE layers; each = (gate, up, down, shared, idx, w, bytes touched)."""
+    """`layers` routed MoE layers, each run whole on the device (bgl_moe_layer_dev: router, sort,
+    gate/up/SwiGLU, down, combine, shared experts); layer = (stacks, shared, idx, w, out, bytes
+    touched, experts touched, router weights)."""
 
     def __init__(self, ctx, torch, T, layers, seed):
         import beglin_amd
@@ -209,21 +213,24 @@ class MoeWorkload:
                 w = gen_weight(torch, gen, o, i)
                 sh.append(ctx.quantize(shf[0], w, bits=shf[1]))
                 del w
-            logits = torch.randn((T, E), generator=gen, device="cuda")
-            prob = torch.softmax(logits, dim=-1)                 # moe_softmax_full
-            w, idx = torch.topk(prob, K, dim=-1)                 # moe_top_k_select (no renorm)
-            idx = idx.to(torch.int32).contiguous()
+            # router [E][H] fp32 with N(0, 1/H) entries: N(0, 1) logits for N(0, 1) tokens
+            rw = torch.randn((E, H), generator=gen, device="cuda") * (1.0 / H ** 0.5)
+            idx = torch.empty((T, K), dtype=torch.int32, device="cuda")
+            w = torch.empty((T, K), device="cuda")
+            ctx.moe_route(rw, self.x, K, idx, w)             # once here, to count the experts the step reads
             touched = sorted(set(idx.cpu().flatten().tolist()))
             nb = sum(2 * wbytes(fm[e][0], I, H, fm[e][1]) + wbytes(fm[e][0], H, I, fm[e][1]) for e in touched)
             nb += 2 * wbytes(shf[0], Ish, H, shf[1]) + wbytes(shf[0], H, Ish, shf[1])
+            nb += 4 * E * H                                          # router weights
             nb += 2 * 4 * T * H                                      # x in, out
             out = torch.empty((T, H), device="cuda")
-            self.layers.append((stacks, tuple(sh), idx, w.contiguous(), out, nb, len(touched)))
+            self.layers.append((stacks, tuple(sh), idx, w, out, nb, len(touched), rw))
             self.formats.append((fm, shf))
 
     def run(self, tags=None):
-        for stacks, sh, idx, w, out, _, _ in self.layers:
-            self.ctx.moe_ffn(stacks[0], stacks[1], stacks[2], sh, self.x, idx, w, out)
+        K = DSV2["K"]
+        for stacks, sh, idx, w, out, _, _, rw in self.layers:
+            self.ctx.moe_layer(rw, stacks[0], stacks[1], stacks[2], sh, self.x, K, out)
 
     def nbytes(self, tags=None):
         return sum(l[5] for l in self.layers)
@@ -305,7 +312,7 @@ def moe_roofline(ctx, torch, stream, wl, reps):
             "launches_per_step": g_n, "kernel_us_per_launch": round(g_ms * 1e3 / max(g_n, 1), 3),
             "bytes_per_launch": round(wl.nbytes() / max(g_n, 1)),
             "prep_us_per_step": round(p_ms * 1e3, 2), "prep_launches": p_n,
-            "bucket_combine_us_per_step": round(o_ms * 1e3, 2), "bucket_combine_launches": o_n,
+            "route_bucket_combine_us_per_step": round(o_ms * 1e3, 2), "route_bucket_combine_launches": o_n,
             "timing": f"eager, event pair per launch, {reps} steps"}
 
 
@@ -394,9 +401,9 @@ def cpu_baseline_cfg5(M, budget_s, seed):
 
 
 def cpu_baseline_cfg4(wl, budget_s, seed):
-    """moe_ffn_batched's portable C restatement (or_moe_ffn_bucketed, one thread) on layer 0's
-    formats and routing, for its first min(T, 2) tokens; only the experts those tokens touch are
-    quantized (the others are never read)."""
+    """moe_ffn_batched's portable C restatement (router scores, routing and or_moe_ffn_bucketed,
+    one thread) on layer 0's router and formats, for min(T, 2) tokens; only the experts those tokens
+    touch are quantized (the others are never read)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_ffi import Oracle, moe_ffn
@@ -404,10 +411,10 @@ def cpu_baseline_cfg4(wl, budget_s, seed):
     rng = np.random.default_rng(seed + 1)
     E, H, I, K, Ish = (DSV2[k] for k in ("E", "H", "I", "K", "Ish"))
     fm, shf = wl.formats[0]
-    idx = wl.layers[0][2].cpu().numpy()
-    w = wl.layers[0][3].cpu().numpy()
+    rw = wl.layers[0][7].cpu().numpy()
     T = min(wl.T, 2)
-    idx, w = np.ascontiguousarray(idx[:T]), np.ascontiguousarray(w[:T])
+    x = rng.standard_normal((T, H), dtype=np.float32)
+    idx, w = orc.route(orc.router_logits(rw, x), K)
     touched = sorted(set(idx.flatten().tolist()))
 
     def q(k, b, o, i):
@@ -429,11 +436,11 @@ def cpu_baseline_cfg4(wl, budget_s, seed):
         gate[e], up[e], down[e] = q(k, b, I, H), q(k, b, I, H), q(k, b, H, I)
         nb += 2 * wbytes(k, I, H, b) + wbytes(k, H, I, b)
     shared = (q(shf[0], shf[1], Ish, H), q(shf[0], shf[1], Ish, H), q(shf[0], shf[1], H, Ish))
-    nb += 2 * wbytes(shf[0], Ish, H, shf[1]) + wbytes(shf[0], H, Ish, shf[1]) + 2 * 4 * T * H
-    x = rng.standard_normal((T, H), dtype=np.float32)
+    nb += 2 * wbytes(shf[0], Ish, H, shf[1]) + wbytes(shf[0], H, Ish, shf[1]) + 4 * E * H + 2 * 4 * T * H
     t0 = time.perf_counter()
     reps = 0
     while True:
+        idx, w = orc.route(orc.router_logits(rw, x), K)
         moe_ffn(orc, gate, up, down, shared, H, I, x, idx, w)
         reps += 1
         if time.perf_counter() - t0 >= budget_s or reps >= 1000:
@@ -441,8 +448,9 @@ def cpu_baseline_cfg4(wl, budget_s, seed):
     dt = (time.perf_counter() - t0) / reps
     return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "us_per_layer": round(dt * 1e6, 1),
-            "sample": f"layer 0, first {T} token(s), {len(touched)} experts touched + shared ({nb / 1e6:.1f} MB), "
-                      f"or_moe_ffn_bucketed single-threaded, {reps} calls over {dt * reps:.1f} s"}
+            "sample": f"layer 0, {T} token(s), router + {len(touched)} experts touched + shared ({nb / 1e6:.1f} MB), "
+                      f"or_moe_router_logits + or_moe_route + or_moe_ffn_bucketed single-threaded, {reps} calls over "
+                      f"{dt * reps:.1f} s"}
 
 
 
@@ -605,8 +613,8 @@ def main():
         with torch.cuda.stream(stream):
             wl = MoeWorkload(ctx, torch, M, args.layers, args.seed)
         touched = [l[6] for l in wl.layers]
-        workload = (f"cfg4: DeepSeek-V2-Lite routed MoE FFN x{args.layers} layers, E=64+2 shared, hidden 2048, "
-                    f"inter 1408, top-6, T={M}, per-expert precision from the seed")
+        workload = (f"cfg4: DeepSeek-V2-Lite routed MoE layer x{args.layers} (router + top-6 + experts + shared on "
+                    f"the device), E=64+2 shared, hidden 2048, inter 1408, T={M}, per-expert precision from the seed")
         dtype = "int8"
         cfg = {"workload": workload, "T": M, "layers": args.layers, "experts_touched_per_layer": touched,
                "formats": "q4g32h | q8g64 | qNg64 n=7..15 per expert (fp32 activations)", "seed": args.seed,

@@ -165,6 +165,21 @@ int bgl_moe_ffn_dev(bgl_ctx *ctx, const bgl_tensor *gate, const bgl_tensor *up, 
                     const bgl_tensor *shared_gate, const bgl_tensor *shared_up, const bgl_tensor *shared_down,
                     const float *x_dev, const int32_t *topk_idx_dev, const float *topk_w_dev, int T, int K,
                     float *out_dev);
+/* Router of the routed FFN (moe_ffn_batched's routing, qwen_infer.c:5243-5257, :5275): per token,
+ * scores = W_r x (+ b) accumulated in double (moe_matvec_f32, :3460-3466), softmax
+ * (moe_softmax_full, :3467-3472), top-K by repeated strict maximum with ties to the lowest expert id
+ * (moe_top_k_select, :3514-3521), and with renorm != 0 the K weights divided by their sum
+ * (moe_topk_renorm, :3529-3534; MOE_NORM_TOPK_PROB).  router_w_dev fp32 [E][in] (16-byte aligned,
+ * in % 4 == 0), router_b_dev [E] or NULL, x_dev [T][in]; writes topk_idx_dev / topk_w_dev [T][K].
+ * E <= 256, K <= min(E, 16). */
+int bgl_moe_route_dev(bgl_ctx *ctx, const float *router_w_dev, const float *router_b_dev, int E, int in,
+                      const float *x_dev, int T, int K, int renorm, int32_t *topk_idx_dev, float *topk_w_dev);
+/* The whole routed FFN step on the device (moe_ffn_batched, qwen_infer.c:5238-5350): bgl_moe_route_dev
+ * then bgl_moe_ffn_dev, with the routing kept in the context's scratch.  E = the experts in gate. */
+int bgl_moe_layer_dev(bgl_ctx *ctx, const float *router_w_dev, const float *router_b_dev, int renorm,
+                      const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down,
+                      const bgl_tensor *shared_gate, const bgl_tensor *shared_up, const bgl_tensor *shared_down,
+                      const float *x_dev, int T, int K, float *out_dev);
 
 /* ---------------- name-keyed MoE registry: the mlx_moe.h GPU boundary ----------------
  * One process-wide registry on device 0 (own stream, like MLX's default stream).  Each function

@@ -675,6 +675,19 @@ void or_moe_swiglu_inplace(float *gate, const float *up, int n) {
     }
 }
 
+/* Router scores of moe_ffn_batched (qwen_infer.c:5243-5250): moe_matvec_f32 (:3460-3466), a
+ * sequential double accumulation per expert row cast to float, then + the router bias in float. */
+void or_moe_router_logits(const float *w, const float *bias, const float *x, int T, int E, int H, float *logits) {
+    for (int t = 0; t < T; t++)
+        for (int e = 0; e < E; e++) {
+            double acc = 0.0;
+            for (int c = 0; c < H; c++) acc += (double)w[(long)e * H + c] * x[(long)t * H + c];
+            float s = (float)acc;
+            if (bias) s += bias[e];
+            logits[(long)t * E + e] = s;
+        }
+}
+
 /* Routing of moe_ffn_batched (qwen_infer.c:5251-5257, 5275): softmax over the router scores,
  * top-k, optional renorm; the per-token weight is the (renormalised) softmax probability. */
 void or_moe_route(const float *logits, int T, int E, int K, int renorm, int *top_idx, float *top_w) {

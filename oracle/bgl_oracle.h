@@ -22,6 +22,7 @@
  *     against the de-quantized product + batched == per-column.
  *   - or_quantize_g256sf: parity unpinned (the reference ships no g256sf emitter); held to its
  *     invariants (sub codes in [1,63], effective scale >= group max / 7, decode error bound).
+ *   - or_moe_router_logits: a pure-Python sequential double loop (the reference order), bit for bit.
  *   - or_moe_route / _softmax_full / _top_k_select / _topk_renorm: brute force; or_moe_ffn_*:
  *     bucketed == naive and a dense float64 pipeline over decoded weights.
  */
@@ -95,6 +96,7 @@ void or_moe_top_k_select(const float *scores, int n, int k, int *out_idx);
 void or_moe_topk_renorm(float *scores, const int *idx, int k);
 void or_moe_swiglu_inplace(float *gate, const float *up, int n);
 void or_moe_route(const float *logits, int T, int E, int K, int renorm, int *top_idx, float *top_w);
+void or_moe_router_logits(const float *w, const float *bias, const float *x, int T, int E, int H, float *logits);
 void or_moe_ffn_bucketed(const or_expert *gate, const or_expert *up, const or_expert *down, int E,
                          const or_expert *sh_gate, const or_expert *sh_up, const or_expert *sh_down,
                          int H, int I, int Ish, int T, int K, const float *x,

@@ -217,6 +217,16 @@ class Oracle:
         self.lib.or_moe_route(_ptr(logits), T, E, K, int(renorm), _ptr(idx), _ptr(w))
         return idx, w
 
+    def router_logits(self, w, x, bias=None):
+        w = np.ascontiguousarray(w, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        E, H = w.shape
+        T = x.shape[0]
+        out = np.zeros((T, E), np.float32)
+        self.lib.or_moe_router_logits(_ptr(w), _ptr(np.ascontiguousarray(bias, np.float32)) if bias is not None else None,
+                                      _ptr(x), T, E, H, _ptr(out))
+        return out
+
 
 class OrExpert(C.Structure):
     _fields_ = [("kind", C.c_int), ("bits", C.c_int), ("packed", C.c_void_p), ("scales", C.c_void_p),

@@ -6,6 +6,9 @@
 * bgl_moe_ffn_dev: the routed SwiGLU FFN with shared experts (moe_ffn_batched,
   qwen_infer.c:5238-5350) against or_moe_ffn_bucketed, routing from or_moe_route, at small sizes
   and at DeepSeek-V2-Lite's shape; graph replay; error paths.
+* bgl_moe_route_dev / bgl_moe_layer_dev: the router (double-accumulated scores, softmax, top-K
+  with ties to the lowest id, renorm) against or_moe_router_logits + or_moe_route, and the whole
+  layer on the device against the oracle pipeline.
 Bar: max|y - ref| / max|ref| <= 1e-5 (fp32 arithmetic, summation order differs)."""
 import sys
 
@@ -290,6 +293,90 @@ def test_moe_graph_replays_match_eager(ctx, torch_dev, oracle):
     for t in (g, u, d) + sh:
         t.free()
     gc.close()
+
+
+ROUTE_CASES = [(1, 64, 6, False, False), (7, 64, 6, True, True), (64, 64, 6, False, True), (5, 8, 2, True, False),
+               (3, 160, 8, False, True), (2, 256, 16, True, True)]
+
+
+@pytest.mark.parametrize("T,E,K,renorm,bias", ROUTE_CASES)
+def test_moe_route_parity(ctx, torch_dev, oracle, T, E, K, renorm, bias):
+    """Device router (bgl_moe_route_dev) against or_moe_router_logits + or_moe_route: the chosen
+    experts equal in selection order, the weights within 1e-6."""
+    torch = torch_dev
+    H = 2048 if E == 64 else 256
+    say("route", T, E, K, renorm, bias)
+    w = seeded_normal(900 + E, (E, H), 0.05)
+    x = seeded_normal(901 + T, (T, H))
+    b = seeded_normal(902, (E,), 0.1) if bias else None
+    ridx, rw = oracle.route(oracle.router_logits(w, x, b), K, renorm)
+    idx = torch.full((T, K), -1, dtype=torch.int32, device="cuda")
+    wd = torch.full((T, K), float("nan"), device="cuda")
+    ctx.moe_route(dev(torch, w), dev(torch, x), K, idx, wd, router_b=dev(torch, b) if bias else None, renorm=renorm)
+    ctx.sync()
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(wd.cpu().numpy(), rw, rtol=1e-6, atol=1e-9)
+    if renorm:
+        np.testing.assert_allclose(wd.cpu().numpy().sum(axis=1), 1.0, rtol=1e-6)
+
+
+def test_moe_route_ties_go_to_lowest_id(ctx, torch_dev, oracle):
+    """Identical router rows give identical probabilities; the repeated strict maximum
+    (moe_top_k_select, qwen_infer.c:3514-3521) takes the lowest expert id first."""
+    torch = torch_dev
+    E, H, K, T = 64, 256, 6, 4
+    say("route ties")
+    x = seeded_normal(911, (T, H))
+    w = seeded_normal(910, (E, H), 0.05)
+    w[3] = x[0] * np.float32(0.02)                  # the top score of token 0
+    w[40] = w[3]; w[17] = w[3]
+    w[50] = w[9]; w[21] = w[9]
+    ridx, rw = oracle.route(oracle.router_logits(w, x), K, False)
+    assert list(ridx[0][:3]) == [3, 17, 40]
+    idx = torch.full((T, K), -1, dtype=torch.int32, device="cuda")
+    wd = torch.zeros((T, K), device="cuda")
+    ctx.moe_route(dev(torch, w), dev(torch, x), K, idx, wd)
+    ctx.sync()
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(wd.cpu().numpy(), rw, rtol=1e-6, atol=1e-9)
+
+
+@pytest.mark.parametrize("T,renorm", [(1, False), (9, True), (64, False)])
+def test_moe_layer_parity(ctx, torch_dev, oracle, T, renorm):
+    """bgl_moe_layer_dev (router + routed FFN + shared experts on the device) against the oracle's
+    router logits, routing and bucketed FFN."""
+    torch = torch_dev
+    E, H, I, K, Ish = 16, 256, 192, 4, 128
+    say("moe_layer", T, renorm)
+    gate, up, down, shared = moe_setup(oracle, 6100, E, H, I, Ish, [(5, 0), (2, 0), (4, 7)])
+    x = seeded_normal(6101 + T, (T, H))
+    rwt = seeded_normal(6102, (E, H), 0.05)
+    b = seeded_normal(6103, (E,), 0.1)
+    idx, w = oracle.route(oracle.router_logits(rwt, x, b), K, renorm)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    g, u, d = ctx.bind_experts(gate), ctx.bind_experts(up), ctx.bind_experts(down)
+    sh = tuple(bind_one(ctx, dd) for dd in shared)
+    out = torch.full((T, H), float("nan"), device="cuda")
+    ctx.moe_layer(dev(torch, rwt), g, u, d, sh, dev(torch, x), K, out, router_b=dev(torch, b), renorm=renorm)
+    ctx.sync()
+    assert relerr(out.cpu().numpy(), ref) <= TOL
+    for t in (g, u, d) + sh:
+        t.free()
+
+
+def test_moe_route_error_paths(ctx, torch_dev):
+    import beglin_amd
+    torch = torch_dev
+    x = torch.zeros((2, 256), device="cuda")
+    idx = torch.zeros((2, 8), dtype=torch.int32, device="cuda")
+    w = torch.zeros((2, 8), device="cuda")
+    with pytest.raises(beglin_amd.BglError):
+        ctx.moe_route(torch.zeros((4, 256), device="cuda"), x, 8, idx, w)        # K > E
+    with pytest.raises(beglin_amd.BglError):
+        ctx.moe_route(torch.zeros((300, 256), device="cuda"), x, 8, idx, w)      # E > 256
+    with pytest.raises(beglin_amd.BglError):
+        ctx.moe_route(torch.zeros((8, 254), device="cuda"), torch.zeros((2, 254), device="cuda"), 2, idx, w)   # in % 4
+    ctx.sync()
 
 
 def test_moe_error_paths(ctx, torch_dev, oracle):

@@ -333,6 +333,33 @@ def test_g256sf_packer_roundtrip(oracle):
 
 
 # ---------------------------------------------------------------- MoE
+def test_router_logits_match_sequential_double(oracle):
+    """or_moe_router_logits (moe_matvec_f32, qwen_infer.c:3460-3466, + bias) against a pure-Python
+    loop in the reference order: Python floats are IEEE doubles and a product of two floats is
+    exact in double, so `acc += w * x` rounds exactly as the C loop does.  Bit for bit."""
+    rng = np.random.default_rng(77)
+    T, E, H = 3, 8, 96
+    w = (rng.standard_normal((E, H)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    x[1, ::7] *= np.float32(1e4)                       # wide dynamic range: the double sum rounds
+    b = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    got = oracle.router_logits(w, x, b)
+    got_nb = oracle.router_logits(w, x)
+    for t in range(T):
+        for e in range(E):
+            acc = 0.0
+            for c in range(H):
+                acc += float(w[e, c]) * float(x[t, c])
+            ref = np.float32(acc)
+            assert got_nb[t, e].view(np.uint32) == ref.view(np.uint32)
+            assert got[t, e].view(np.uint32) == np.float32(ref + b[e]).view(np.uint32)
+    # a float accumulator (the plausible mistake) differs on the wide-range row
+    accf = np.float32(0.0)
+    for c in range(H):
+        accf = np.float32(accf + w[0, c] * x[1, c])
+    assert accf != got_nb[1, 0]
+
+
 def test_route_matches_brute_force(oracle):
     lg = seeded_normal(100, (64, 64))
     idx, wts = oracle.route(lg, 6)
