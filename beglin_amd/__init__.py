@@ -264,6 +264,24 @@ class Registry:
         ok = lib().bgl_gpu_ffn_gather(name.encode(), x.ctypes.data, x.shape[0], idx.ctypes.data, y.ctypes.data)
         return ok, y
 
+    def bind_router(self, name, w, bias=None):
+        import numpy as np
+        w = np.ascontiguousarray(w, np.float32)
+        b = np.ascontiguousarray(bias, np.float32) if bias is not None else None
+        return lib().bgl_gpu_bind_router(name.encode(), w.ctypes.data, b.ctypes.data if b is not None else None,
+                                         w.shape[0], w.shape[1])
+
+    def moe_layer(self, router, gate, up, down, shared, x, K, renorm=False):
+        import numpy as np
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        idx = np.zeros((x.shape[0], K), np.int32)
+        w = np.zeros((x.shape[0], K), np.float32)
+        sg, su, sd = [s.encode() if s else None for s in (shared or (None, None, None))]
+        ok = lib().bgl_gpu_moe_layer(router.encode(), gate.encode(), up.encode(), down.encode(), sg, su, sd, x.ctypes.data,
+                                     x.shape[0], K, 1 if renorm else 0, out.ctypes.data, idx.ctypes.data, w.ctypes.data)
+        return ok, out, idx, w
+
     def moe_ffn(self, gate, up, down, shared, x, idx, w):
         import numpy as np
         x = np.ascontiguousarray(x, np.float32)

@@ -65,6 +65,9 @@ SIGNATURES = [
     ("bgl_moe_layer_dev", _I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
     # name-keyed registry (mlx_moe.h boundary)
     ("bgl_gpu_available", _I, []),
+    ("bgl_gpu_bind_router", _I, [C.c_char_p, _P, _P, _L, _L]),
+    ("bgl_gpu_moe_layer", _I, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, _P, _I, _I,
+                               _I, _P, _P, _P]),
     ("bgl_gpu_synchronize", _I, []),
     ("bgl_gpu_reset_runtime_epoch", _I, []),
     ("bgl_gpu_bind_af", _I, [_P, _L, C.c_char_p, _L, _L, _L, _L, _L, _L, _L, _I]),

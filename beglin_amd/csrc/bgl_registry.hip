@@ -22,10 +22,17 @@ struct Entry {
     int bits = 0;                     // width as bound: 2..15, 16 or 32
 };
 
+// A MoE router: fp32 [E][in] and an optional bias [E], on the device.
+struct Router {
+    std::shared_ptr<void> w, bias;
+    int E = 0, in = 0;
+};
+
 struct Registry {
     std::mutex mu;
     bgl_ctx *ctx = nullptr;
     std::unordered_map<std::string, Entry> names;
+    std::unordered_map<std::string, Router> routers;
     std::unordered_map<uint64_t, std::pair<std::string, Entry>> snaps;
     uint64_t next_snap = 1;
     int bound = 0;                    // binds performed (mlx_gpu_zerocopy_count's return value)
@@ -66,6 +73,7 @@ size_t active_bytes(Registry &R) {
     auto add = [&](const Entry &e) { if (seen.insert(e.t.get()).second) total += tensor_bytes(e.t.get()); };
     for (auto &kv : R.names) add(kv.second);
     for (auto &kv : R.snaps) add(kv.second.second);
+    for (auto &kv : R.routers) total += (size_t)kv.second.E * kv.second.in * 4 + (kv.second.bias ? (size_t)kv.second.E * 4 : 0);
     return total;
 }
 
@@ -446,4 +454,85 @@ extern "C" int bgl_gpu_moe_ffn(const char *gate, const char *up, const char *dow
                         (const int32_t *)dst[1], (const float *)dst[2], T, K, (float *)c->hy.p))
         return 0;
     return fetch(c, out, c->hy.p, (size_t)T * H * 4) == 0 ? 1 : 0;
+}
+
+// ---------------------------------------------------------------- router + whole routed layer
+namespace {
+std::shared_ptr<void> dev_copy(bgl_ctx *c, const void *src, size_t bytes) {
+    void *d = nullptr;
+    if (hipMalloc(&d, bytes) != hipSuccess) return nullptr;
+    if (hipMemcpyAsync(d, src, bytes, hipMemcpyHostToDevice, c->stream) != hipSuccess || hipStreamSynchronize(c->stream) != hipSuccess) {
+        (void)hipFree(d);
+        return nullptr;
+    }
+    return std::shared_ptr<void>(d, [c](void *p) {
+        (void)bgl_synchronize(c);
+        (void)hipFree(p);
+    });
+}
+}  // namespace
+
+extern "C" int bgl_gpu_bind_router(const char *name, const float *w, const float *bias, long E, long in) {
+    Registry &R = reg();
+    std::lock_guard<std::mutex> lk(R.mu);
+    if (!reg_ctx(R) || !name || !w || E < 1 || E > 256 || in < 4 || in % 4) {
+        bgl_fail(BGL_E_ARG, "bgl_gpu_bind_router: bad argument (E=%ld in 1..256, in=%ld a multiple of 4)", E, in);
+        return 0;
+    }
+    Router r;
+    r.E = (int)E;
+    r.in = (int)in;
+    r.w = dev_copy(R.ctx, w, (size_t)E * in * 4);
+    if (bias) r.bias = dev_copy(R.ctx, bias, (size_t)E * 4);
+    if (!r.w || (bias && !r.bias)) {
+        bgl_fail(BGL_E_NOMEM, "bgl_gpu_bind_router: device copy of '%s' failed", name);
+        return 0;
+    }
+    R.routers[name] = r;
+    R.bytes_copied += (size_t)E * in * 4;
+    R.peak = std::max(R.peak, active_bytes(R));
+    return 1;
+}
+
+extern "C" int bgl_gpu_moe_layer(const char *router, const char *gate, const char *up, const char *down,
+                                 const char *shared_gate, const char *shared_up, const char *shared_down, const float *x,
+                                 int T, int K, int renorm, float *out, int32_t *topk_idx, float *topk_w) {
+    Registry &R = reg();
+    std::lock_guard<std::mutex> lk(R.mu);
+    auto rt = router ? R.routers.find(router) : R.routers.end();
+    const Entry *g = find(R, gate), *u = find(R, up), *d = find(R, down);
+    if (!reg_ctx(R) || rt == R.routers.end() || !g || !u || !d || !x || !out || T < 1 || K < 1) return 0;
+    const bgl_tensor *sh[3] = {nullptr, nullptr, nullptr};
+    const char *shn[3] = {shared_gate, shared_up, shared_down};
+    for (int i = 0; i < 3; i++) {
+        if (!shn[i]) continue;
+        const Entry *s = find(R, shn[i]);
+        if (!s || s->t->experts.size() != 1) {
+            bgl_fail(BGL_E_ARG, "bgl_gpu_moe_layer: shared tensor '%s' missing or not a single expert", shn[i]);
+            return 0;
+        }
+        sh[i] = s->t->experts[0];
+    }
+    int H = 0;
+    (void)bgl_tensor_info(g->t.get(), nullptr, nullptr, nullptr, &H, nullptr);
+    const Router &r = rt->second;
+    if (r.in != H || r.E != (int)g->t->experts.size()) {
+        bgl_fail(BGL_E_ARG, "bgl_gpu_moe_layer: router [%d x %d] does not match %zu experts of in=%d", r.E, r.in,
+                 g->t->experts.size(), H);
+        return 0;
+    }
+    bgl_ctx *c = R.ctx;
+    const void *src[1] = {x};
+    const size_t bytes[1] = {(size_t)T * H * 4};
+    void *dst[1];
+    if (stage_in(c, src, bytes, 1, dst)) return 0;
+    if (dbuf_reserve(c, c->hy, (size_t)T * H * 4, false)) return 0;
+    if (bgl_moe_layer_dev(c, (const float *)r.w.get(), (const float *)r.bias.get(), renorm, g->t.get(), u->t.get(), d->t.get(),
+                          sh[0], sh[1], sh[2], (const float *)dst[0], T, K, (float *)c->hy.p))
+        return 0;
+    if (fetch(c, out, c->hy.p, (size_t)T * H * 4)) return 0;
+    const int32_t *ridx = (const int32_t *)c->moe_route.p;
+    if (topk_idx && fetch(c, topk_idx, ridx, (size_t)T * K * 4)) return 0;
+    if (topk_w && fetch(c, topk_w, ridx + (size_t)T * K, (size_t)T * K * 4)) return 0;
+    return 1;
 }

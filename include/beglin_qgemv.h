@@ -231,6 +231,18 @@ int bgl_gpu_ffn_gather(const char *name, const float *x, int N, const int32_t *e
 /* Routed SwiGLU FFN over bound gate/up/down names (+ optional shared-expert names, NULL for none)
  * with top-K routing given, host buffers (routed-FFN composition mlx_moe.cpp:2155-2232 /
  * moe_ffn_batched qwen_infer.c:5238-5350). */
+/* The router of a MoE layer, registered by name: fp32 [E][in] (the engine's router weights,
+ * qwen_infer.c:5244) and an optional bias [E] (:5247-5250), copied to the device.  No mlx_moe.h
+ * counterpart (the MLX path wraps the host router per call, mlx_moe.cpp:2534): it lets
+ * bgl_gpu_moe_layer run moe_ffn_batched whole.  1 = ok, 0 = failure. */
+int bgl_gpu_bind_router(const char *name, const float *w, const float *bias, long E, long in);
+/* moe_ffn_batched (qwen_infer.c:5238-5350) by names, routing included: bgl_moe_layer_dev on the
+ * registry's context with host x [T][in] / out [T][in]; renorm = MOE_NORM_TOPK_PROB.  topk_idx /
+ * topk_w [T][K] (either may be NULL) receive the routing (the engine's routing capture, :5274-5278).
+ * 1 = ok, 0 = failure. */
+int bgl_gpu_moe_layer(const char *router, const char *gate, const char *up, const char *down,
+                      const char *shared_gate, const char *shared_up, const char *shared_down, const float *x, int T,
+                      int K, int renorm, float *out, int32_t *topk_idx, float *topk_w);
 int bgl_gpu_moe_ffn(const char *gate, const char *up, const char *down, const char *shared_gate,
                     const char *shared_up, const char *shared_down, const float *x, int T, const int32_t *topk_idx,
                     const float *topk_w, int K, float *out);

@@ -246,6 +246,38 @@ def test_registry_moe_ffn_by_name(R, oracle):
     assert R.moe_ffn("ffn.gate", "ffn.up", "ffn.none", None, x, idx, w)[0] == 0
 
 
+def test_registry_moe_layer_with_router(R, oracle):
+    """moe_ffn_batched by names with the router registered (bgl_gpu_bind_router): the routing the
+    call returns equals or_moe_router_logits + or_moe_route, the output the oracle's bucketed FFN."""
+    say("registry moe_layer")
+    E, H, I, K, T, Ish = 8, 256, 128, 3, 6, 192
+    rw = seeded_normal(540, (E, H), 0.06)
+    rb = seeded_normal(541, (E,), 0.1)
+    assert R.bind_router("ffn.router", rw, rb) == 1
+    x = seeded_normal(542, (T, H))
+    ridx, rwt = oracle.route(oracle.router_logits(rw, x, rb), K, True)
+    ok, got, idx, w = R.moe_layer("ffn.router", "ffn.gate", "ffn.up", "ffn.down", ("ffn.sg", "ffn.su", "ffn.sd"), x, K,
+                                  renorm=True)
+    assert ok == 1
+    assert np.array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rwt, rtol=1e-6, atol=1e-9)
+    descs = {}
+    for role, bits in {"gate": 4, "up": 4, "down": 9}.items():
+        o, i = (I, H) if role != "down" else (H, I)
+        descs[role] = bind_all(R, oracle, {f"ffn.{role}": bits}, E, o, i, 500 + len(descs))[f"ffn.{role}"]
+    for role, (o, i) in (("sg", (Ish, H)), ("su", (Ish, H)), ("sd", (H, Ish))):
+        descs[role] = bind_all(R, oracle, {f"ffn.{role}": 8}, 1, o, i, 520 + len(descs))[f"ffn.{role}"]
+    ok, got, idx, w = R.moe_layer("ffn.router", "ffn.gate", "ffn.up", "ffn.down", ("ffn.sg", "ffn.su", "ffn.sd"), x, K,
+                                  renorm=True)
+    shared = (descs["sg"][0], descs["su"][0], descs["sd"][0])
+    ref = moe_ffn(oracle, descs["gate"], descs["up"], descs["down"], shared, H, I, x, ridx, rwt)
+    assert ok == 1 and relerr(got, ref) <= TOL
+    assert R.moe_layer("ffn.nope", "ffn.gate", "ffn.up", "ffn.down", None, x, K)[0] == 0          # unknown router
+    assert R.bind_router("ffn.r5", seeded_normal(543, (5, H), 0.05)) == 1
+    assert R.moe_layer("ffn.r5", "ffn.gate", "ffn.up", "ffn.down", None, x, K)[0] == 0            # E mismatch
+    assert R.bind_router("ffn.bad", seeded_normal(544, (4, 6), 0.05)) == 0                        # in % 4
+
+
 def test_memory_report_epoch_and_counters(R, lib, oracle):
     import ctypes as C
     say("registry memory / epoch")
