@@ -106,6 +106,14 @@ class Context:
         _check(lib().bgl_bind(self.h, C.byref(w), C.byref(h)), "bgl_bind")
         return Tensor(h)
 
+    def bind_qng64_mixed(self, planes, offsets, bits, scales, out, inn):
+        """Bind a mixed per-cell qNg64 tensor (numpy planes u8, offsets u32 [cells+1], bits u8 [cells],
+        scales f32 [cells])."""
+        h = C.c_void_p()
+        _check(lib().bgl_bind_qng64_mixed(self.h, planes.ctypes.data, planes.nbytes, offsets.ctypes.data, bits.ctypes.data,
+                                          scales.ctypes.data, out, inn, C.byref(h)), "bgl_bind_qng64_mixed")
+        return Tensor(h)
+
     def quantize(self, kind, w_dev, bits=0, qng64_encoder=1, want_ref=False):
         """Quantize fp32 weights already on the device (torch tensor [out][in]).  With want_ref the
         reference-layout bytes come back as numpy arrays."""
@@ -262,6 +270,18 @@ class Registry:
         idx = np.ascontiguousarray(idx, np.int32)
         y = np.zeros((x.shape[0], out), np.float32)
         ok = lib().bgl_gpu_ffn_gather(name.encode(), x.ctypes.data, x.shape[0], idx.ctypes.data, y.ctypes.data)
+        return ok, y
+
+    def bind_mixed(self, name, planes, offsets, bits, scales, out, inn):
+        return lib().bgl_gpu_bind_qng64_mixed_dense_probe(planes.ctypes.data, planes.nbytes, offsets.ctypes.data,
+                                                          bits.ctypes.data, scales.ctypes.data, name.encode(), out, inn)
+
+    def mixed_probe(self, planes, offsets, bits, scales, out, inn, x):
+        import numpy as np
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros((x.shape[0], out), np.float32)
+        ok = lib().bgl_gpu_qng64_mixed_dense_probe(planes.ctypes.data, planes.nbytes, offsets.ctypes.data, bits.ctypes.data,
+                                                   scales.ctypes.data, out, inn, x.ctypes.data, x.shape[0], y.ctypes.data)
         return ok, y
 
     def bind_router(self, name, w, bias=None):

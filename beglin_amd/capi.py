@@ -66,6 +66,9 @@ SIGNATURES = [
     # name-keyed registry (mlx_moe.h boundary)
     ("bgl_gpu_available", _I, []),
     ("bgl_gpu_bind_router", _I, [C.c_char_p, _P, _P, _L, _L]),
+    ("bgl_bind_qng64_mixed", _I, [_P, _P, _L, _P, _P, _P, _I, _I, C.POINTER(_P)]),
+    ("bgl_gpu_qng64_mixed_dense_probe", _I, [_P, _L, _P, _P, _P, _L, _L, _P, _I, _P]),
+    ("bgl_gpu_bind_qng64_mixed_dense_probe", _I, [_P, _L, _P, _P, _P, C.c_char_p, _L, _L]),
     ("bgl_gpu_moe_layer", _I, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, _P, _I, _I,
                                _I, _P, _P, _P]),
     ("bgl_gpu_synchronize", _I, []),

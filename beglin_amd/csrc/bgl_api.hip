@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
@@ -317,6 +318,61 @@ extern "C" int bgl_bind(bgl_ctx *c, const bgl_wt *w, bgl_tensor **out) {
     if (dsub) (void)hipFree(dsub);
     if (rc) return rc;
     if (e != hipSuccess) return bgl_fail(BGL_E_HIP, "bind sync: %s", hipGetErrorString(e));
+    return 0;
+}
+
+// The checks of the mixed binders (mlx_moe.cpp:1750-1758 / :1790-1798): offsets[0] = 0,
+// offsets[cells] = planes_bytes, each cell exactly n*8 bytes with 2 <= n <= 15, scales finite and > 0.
+static int mixed_check(const uint8_t *planes, long planes_bytes, const uint32_t *offsets, const uint8_t *bits,
+                       const float *scales, long out, long in, int *W) {
+    if (!planes || !offsets || !bits || !scales || planes_bytes <= 0 || out <= 0 || in <= 0 || in % 64)
+        return bgl_fail(BGL_E_ARG, "mixed qNg64: bad argument (in %% 64 == 0, buffers non-NULL)");
+    const long ng = in / 64;
+    const size_t cells = (size_t)out * (size_t)ng;
+    if (offsets[0] != 0 || (long)offsets[cells] != planes_bytes)
+        return bgl_fail(BGL_E_ARG, "mixed qNg64: offsets[0] must be 0 and offsets[%zu] = planes_bytes", cells);
+    int w = 2;
+    for (size_t i = 0; i < cells; ++i) {
+        const int n = (int)bits[i];
+        if (n < 2 || n > 15) return bgl_fail(BGL_E_ARG, "mixed qNg64: cell %zu has n=%d (2..15)", i, n);
+        if (offsets[i + 1] < offsets[i] || (size_t)(offsets[i + 1] - offsets[i]) != (size_t)n * 8u)
+            return bgl_fail(BGL_E_ARG, "mixed qNg64: cell %zu spans %u bytes, not n*8", i, offsets[i + 1] - offsets[i]);
+        if (!std::isfinite(scales[i]) || scales[i] <= 0.0f) return bgl_fail(BGL_E_ARG, "mixed qNg64: cell %zu scale", i);
+        if (n > w) w = n;
+    }
+    *W = w;
+    return 0;
+}
+
+extern "C" int bgl_bind_qng64_mixed(bgl_ctx *c, const uint8_t *planes, long planes_bytes, const uint32_t *offsets,
+                                    const uint8_t *bits, const float *scales, int out, int in, bgl_tensor **res) {
+    if (!c || !res) return bgl_fail(BGL_E_ARG, "bgl_bind_qng64_mixed: NULL argument");
+    int W = 0, rc = mixed_check(planes, planes_bytes, offsets, bits, scales, out, in, &W);
+    if (rc) return rc;
+    HIPCHK(hipSetDevice(c->device));
+    const size_t cells = (size_t)out * (in / 64);
+    void *dpl = nullptr, *doff = nullptr, *dbits = nullptr, *dsc = nullptr, *dense = nullptr;
+    hipError_t e = hipMalloc(&dpl, planes_bytes);
+    if (e == hipSuccess) e = hipMalloc(&doff, (cells + 1) * 4);
+    if (e == hipSuccess) e = hipMalloc(&dbits, cells);
+    if (e == hipSuccess) e = hipMalloc(&dsc, cells * 4);
+    if (e == hipSuccess) e = hipMalloc(&dense, cells * W * 8);
+    if (e == hipSuccess) e = hipMemcpyAsync(dpl, planes, planes_bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(doff, offsets, (cells + 1) * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dbits, bits, cells, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dsc, scales, cells * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_mixed_qng_to_dense, dim3(nblk((long)cells)), dim3(256), 0, c->stream, (const uint8_t *)dpl,
+                           (const uint32_t *)doff, (const uint8_t *)dbits, (long)cells, W, (uint8_t *)dense);
+        e = hipGetLastError();
+    }
+    rc = e == hipSuccess ? repack_into(c, BGL_QNG64, W, out, in, dense, dsc, nullptr, res)
+                         : bgl_fail(BGL_E_HIP, "bgl_bind_qng64_mixed: %s", hipGetErrorString(e));
+    const hipError_t es = hipStreamSynchronize(c->stream);
+    for (void *p : {dpl, doff, dbits, dsc, dense})
+        if (p) (void)hipFree(p);
+    if (rc) return rc;
+    if (es != hipSuccess) return bgl_fail(BGL_E_HIP, "bgl_bind_qng64_mixed sync: %s", hipGetErrorString(es));
     return 0;
 }
 

@@ -65,6 +65,8 @@ __global__ void k_repack_qng(const uint8_t *src, int N, int K, int n, uint8_t *d
 __global__ void k_repack_u32(const uint32_t *src, int N, int U, uint32_t *dst);
 __global__ void k_repack_u64(const uint64_t *src, int N, int U, uint64_t *dst);
 __global__ void k_repack_zip_u32(const uint32_t *a, const uint32_t *b, int N, int U, uint2 *dst);
+__global__ void k_mixed_qng_to_dense(const uint8_t *planes, const uint32_t *offsets, const uint8_t *bits, long cells, int W,
+                                     uint8_t *dst);
 __global__ void k_repack_qng_scales(const float *src, int N, int ng, float2 *dst);
 __global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *out);
 __global__ void k_splitk_reduce(const float *part, int ks, int M, int N, const float *bias, float *y, int ystride);

@@ -399,6 +399,28 @@ __global__ void k_repack_u64(const uint64_t *__restrict__ src, int N, int U, uin
     dst[((size_t)tile * U + u) * BGL_TILE + lane] = r < N ? src[(size_t)r * U + u] : 0ull;
 }
 
+// Mixed per-cell qNg64 (MixedQNg64Tensor, mlx_moe.cpp:87-93) -> the dense width-W plane layout
+// (qng64_dense.c:19-27): one thread per (row, 64-group) cell.  A cell holds n = bits[cell] planes of
+// 8 bytes at planes + offsets[cell] (plane j: bit j of element p at byte p>>3, bit p&7, i.e. bit p of
+// the little-endian u64) and decodes to (u - 2^(n-1)) * scale (mlx_moe.cpp:1708-1722).  Re-biasing
+// u' = u + 2^(W-1) - 2^(n-1) keeps every code (u' - 2^(W-1) = u - 2^(n-1)); the add runs bit-sliced
+// over the 64 elements, one u64 per plane.
+__global__ void k_mixed_qng_to_dense(const uint8_t *__restrict__ planes, const uint32_t *__restrict__ offsets,
+                                     const uint8_t *__restrict__ bits, long cells, int W, uint8_t *__restrict__ dst) {
+    const long cell = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (cell >= cells) return;
+    const int n = bits[cell];
+    const uint64_t *src = reinterpret_cast<const uint64_t *>(planes + offsets[cell]);   // offsets are multiples of 8
+    uint64_t *out = reinterpret_cast<uint64_t *>(dst + (size_t)cell * W * 8);
+    const uint32_t D = (1u << (W - 1)) - (1u << (n - 1));
+    uint64_t carry = 0;
+    for (int j = 0; j < W; j++) {
+        const uint64_t a = j < n ? src[j] : 0ull, d = ((D >> j) & 1u) ? ~0ull : 0ull;
+        out[j] = a ^ d ^ carry;
+        carry = (a & d) | (carry & (a ^ d));
+    }
+}
+
 // qNg64 scales [N][ng] fp32 -> [tile][pair][lane] float2 (odd ng: second scale 0).
 __global__ void k_repack_qng_scales(const float *__restrict__ src, int N, int ng, float2 *__restrict__ dst) {
     int np = (ng + 1) / 2;

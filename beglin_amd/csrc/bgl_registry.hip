@@ -19,7 +19,8 @@ namespace {
 
 struct Entry {
     std::shared_ptr<bgl_tensor> t;    // expert stack (E >= 1)
-    int bits = 0;                     // width as bound: 2..15, 16 or 32
+    int bits = 0;                     // width as bound: 2..15, 16 or 32 (mixed: the widest cell)
+    bool mixed = false;               // mixed per-cell qNg64 (kind 4, no tensor-wide width)
 };
 
 // A MoE router: fp32 [E][in] and an optional bias [E], on the device.
@@ -266,6 +267,7 @@ extern "C" int bgl_gpu_binding_kind(const char *name, int *bits_out) {
     if (bits_out) *bits_out = 0;
     const Entry *e = find(R, name);
     if (!e) return 0;
+    if (e->mixed) return 4;           // mlx_moe.cpp:477-481: the width is cell-local, bits_out = 0
     if (bits_out) *bits_out = e->bits;
     return kind_class(e->bits);
 }
@@ -319,6 +321,7 @@ extern "C" int bgl_gpu_dequant_probe(const char *name, long e, long row, long co
     std::lock_guard<std::mutex> lk(R.mu);
     const Entry *en = find(R, name);
     if (!reg_ctx(R) || !en || !out) return 0;
+    if (en->mixed) return 0;          // the reference's probe has no mixed arm
     const bgl_tensor *st = en->t.get();
     const long E = (long)st->experts.size();
     int O = 0, K = 0;
@@ -535,4 +538,45 @@ extern "C" int bgl_gpu_moe_layer(const char *router, const char *gate, const cha
     if (topk_idx && fetch(c, topk_idx, ridx, (size_t)T * K * 4)) return 0;
     if (topk_w && fetch(c, topk_w, ridx + (size_t)T * K, (size_t)T * K * 4)) return 0;
     return 1;
+}
+
+// ---------------------------------------------------------------- mixed per-cell qNg64 (QT-4 probes)
+extern "C" int bgl_gpu_bind_qng64_mixed_dense_probe(const uint8_t *planes, long planes_bytes, const uint32_t *offsets,
+                                                    const uint8_t *bits, const float *scales, const char *name, long out,
+                                                    long in) {
+    Registry &R = reg();
+    std::lock_guard<std::mutex> lk(R.mu);
+    if (!reg_ctx(R) || !name || out <= 0 || out > INT_MAX || in <= 0 || in > INT_MAX) return 0;
+    bgl_tensor *t = nullptr, *st = nullptr;
+    if (bgl_bind_qng64_mixed(R.ctx, planes, planes_bytes, offsets, bits, scales, (int)out, (int)in, &t)) return 0;
+    if (bgl_experts_from_tensors(R.ctx, 1, &t, &st)) {
+        bgl_tensor_free(t);
+        return 0;
+    }
+    int W = 0;
+    (void)bgl_tensor_info(t, nullptr, &W, nullptr, nullptr, nullptr);
+    put(R, name, st, W);
+    R.names[name].mixed = true;
+    return 1;
+}
+
+extern "C" int bgl_gpu_qng64_mixed_dense_probe(const uint8_t *planes, long planes_bytes, const uint32_t *offsets,
+                                               const uint8_t *bits, const float *scales, long out, long in, const float *x,
+                                               int batch, float *out_buf) {
+    Registry &R = reg();
+    std::lock_guard<std::mutex> lk(R.mu);
+    if (!reg_ctx(R) || !x || !out_buf || batch <= 0 || out <= 0 || out > INT_MAX || in <= 0 || in > INT_MAX) return 0;
+    bgl_ctx *c = R.ctx;
+    bgl_tensor *t = nullptr;
+    if (bgl_bind_qng64_mixed(c, planes, planes_bytes, offsets, bits, scales, (int)out, (int)in, &t)) return 0;
+    const void *src[1] = {x};
+    const size_t bytes[1] = {(size_t)batch * in * 4};
+    void *dst[1];
+    int ok = 0;
+    if (!stage_in(c, src, bytes, 1, dst) && !dbuf_reserve(c, c->hy, (size_t)batch * out * 4, false) &&
+        !bgl_matmul_dev(c, t, BGL_ACT_F32, (const float *)dst[0], nullptr, (float *)c->hy.p, batch))
+        ok = fetch(c, out_buf, c->hy.p, (size_t)batch * out * 4) == 0;
+    (void)bgl_synchronize(c);
+    bgl_tensor_free(t);
+    return ok;
 }

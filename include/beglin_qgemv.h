@@ -70,6 +70,13 @@ int  bgl_prof_read(bgl_ctx *ctx, double *ms_by_phase, int *launches_by_phase, in
  * mlx_gpu_bind_af (mlx_moe.h:48-50) / kai_repack_one_lazy (qwen_infer.c:473-487).  Host buffers
  * are read once; the device copy is owned by the returned tensor. */
 int  bgl_bind(bgl_ctx *ctx, const bgl_wt *w, bgl_tensor **out);
+/* Mixed per-cell qNg64 (MixedQNg64Tensor, mlx_moe.cpp:87-93): one width n = bits[cell] (2..15) per
+ * (row, 64-group) cell, n bit-planes of 8 bytes at planes + offsets[cell] (the qng64_dense.c plane
+ * layout), value (u - 2^(n-1)) * scales[cell].  offsets has out*in/64 + 1 entries; the checks of
+ * mlx_moe.cpp:1750-1758 apply.  The cells are re-biased to the tensor's widest n on the device, so
+ * the result is a K_QNG64 tensor of that width with bit-identical values. */
+int  bgl_bind_qng64_mixed(bgl_ctx *ctx, const uint8_t *planes, long planes_bytes, const uint32_t *offsets,
+                          const uint8_t *bits, const float *scales, int out, int in, bgl_tensor **res);
 /* Quantize fp32 weights already on the device with the reference packer of `kind`, straight into
  * the device layout (load-time transcode: gguf_quantize_q4g64_error_feedback / gguf_quantize_q8g64 /
  * gguf_quantize_qNg64 (gguf_transcode.c:24-162), qng64_quantize_f32 (qng64_dense.c:29-68,
@@ -215,6 +222,13 @@ int bgl_gpu_qng64_gather_probe(const uint8_t *planes, long E, long out, long in,
                                const float *x, int N, const int32_t *expert_idx, float *out_buf);
 /* Bind one caller-owned qNg64 tensor (n in {2,3,5,6}) as a single-expert binding (mlx_moe.h:97-98). */
 int bgl_gpu_bind_qng64_dense_probe(const uint8_t *packed, const float *scales, const char *name, long out, long in, int n);
+/* Mixed per-cell qNg64 probes (mlx_moe.h:104-116): the one-shot GEMV out_buf [batch][out] = W x for
+ * x [batch][in] (registry untouched), and the binder (kind 4, bits 0 in bgl_gpu_binding_kind; served by
+ * bgl_gpu_matvec_probe with e = 0; bgl_gpu_dequant_probe refuses it, as the reference's does). */
+int bgl_gpu_qng64_mixed_dense_probe(const uint8_t *planes, long planes_bytes, const uint32_t *offsets, const uint8_t *bits,
+                                    const float *scales, long out, long in, const float *x, int batch, float *out_buf);
+int bgl_gpu_bind_qng64_mixed_dense_probe(const uint8_t *planes, long planes_bytes, const uint32_t *offsets,
+                                         const uint8_t *bits, const float *scales, const char *name, long out, long in);
 /* y[out] = W_e x for one expert of a bound tensor, host x / y (mlx_moe.h:121). */
 int bgl_gpu_matvec_probe(const char *name, long e, const float *x, float *y);
 /* Device bytes held by bindings (active), the high-water mark (peak) and per-call scratch (cache). */

@@ -675,6 +675,25 @@ void or_moe_swiglu_inplace(float *gate, const float *up, int n) {
     }
 }
 
+/* Mixed per-cell qNg64 (MixedQNg64Tensor, mlx_moe.cpp:87-93) decoded as the QT-4 GEMV kernel does
+ * (mlx_moe.cpp:1708-1722): cell (r, g) has n = bits[cell] planes of 8 bytes at planes + offsets[cell];
+ * element p's bit j is bit (p & 7) of byte j*8 + (p >> 3); value (u - 2^(n-1)) * scales[cell]. */
+void or_decode_qng64_mixed(const uint8_t *planes, const uint32_t *offsets, const uint8_t *bits, const float *scales,
+                           int out, int in, float *w) {
+    const int ng = in / 64;
+    for (int r = 0; r < out; r++)
+        for (int g = 0; g < ng; g++) {
+            const size_t cell = (size_t)r * ng + g;
+            const int n = bits[cell];
+            const uint8_t *pl = planes + offsets[cell];
+            for (int p = 0; p < 64; p++) {
+                int u = 0;
+                for (int j = 0; j < n; j++) u |= ((pl[j * 8 + (p >> 3)] >> (p & 7)) & 1) << j;
+                w[(size_t)r * in + g * 64 + p] = (float)(u - (1 << (n - 1))) * scales[cell];
+            }
+        }
+}
+
 /* Router scores of moe_ffn_batched (qwen_infer.c:5243-5250): moe_matvec_f32 (:3460-3466), a
  * sequential double accumulation per expert row cast to float, then + the router bias in float. */
 void or_moe_router_logits(const float *w, const float *bias, const float *x, int T, int E, int H, float *logits) {

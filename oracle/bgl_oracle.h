@@ -23,6 +23,8 @@
  *   - or_quantize_g256sf: parity unpinned (the reference ships no g256sf emitter); held to its
  *     invariants (sub codes in [1,63], effective scale >= group max / 7, decode error bound).
  *   - or_moe_router_logits: a pure-Python sequential double loop (the reference order), bit for bit.
+ *   - or_decode_qng64_mixed: equal to or_decode_qng64 when every cell has the same n, and to an
+ *     independent Python bit-plane decode for random per-cell widths.
  *   - or_moe_route / _softmax_full / _top_k_select / _topk_renorm: brute force; or_moe_ffn_*:
  *     bucketed == naive and a dense float64 pipeline over decoded weights.
  */
@@ -58,6 +60,8 @@ void or_decode_q4_0(const uint8_t *blocks, int64_t n, float *w);
 void or_decode_q4g32h(const uint8_t *packed, const uint16_t *scales16, int out, int in, float *w);
 void or_decode_g256sf(const uint8_t *packed, const float *wsuper, const uint8_t *sub, int out, int in, float *w);
 float or_qng64_decode_code(const uint8_t *group, int n, int index);
+void or_decode_qng64_mixed(const uint8_t *planes, const uint32_t *offsets, const uint8_t *bits, const float *scales,
+                           int out, int in, float *w);
 
 /* ---------------- fp32-activation GEMV (y = W x + bias), x [M][in], y [M][out] ----------------
  * kind: 1 q4g64, 2 q8g64, 4 qNg64 (bits=n), 5 q4g32h (packed + fp16 scales in `scales`). */

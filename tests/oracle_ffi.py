@@ -217,6 +217,11 @@ class Oracle:
         self.lib.or_moe_route(_ptr(logits), T, E, K, int(renorm), _ptr(idx), _ptr(w))
         return idx, w
 
+    def decode_qng64_mixed(self, planes, offsets, bits, scales, out, inn):
+        w = np.zeros((out, inn), np.float32)
+        self.lib.or_decode_qng64_mixed(_ptr(planes), _ptr(offsets), _ptr(bits), _ptr(scales), out, inn, _ptr(w))
+        return w
+
     def router_logits(self, w, x, bias=None):
         w = np.ascontiguousarray(w, np.float32)
         x = np.ascontiguousarray(x, np.float32)
@@ -291,3 +296,30 @@ def moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w, naive=False):
     fn = oracle.lib.or_moe_ffn_naive if naive else oracle.lib.or_moe_ffn_bucketed
     fn(ga, ua, da, E, sg, su, sd, H, I, Ish, T, K, _ptr(x), _ptr(idx), _ptr(w), _ptr(out))
     return out
+
+
+def mixed_qng64_random(rng, out, inn, widths):
+    """A mixed per-cell qNg64 tensor (MixedQNg64Tensor layout): per (row, 64-group) cell a width
+    drawn from `widths`, random plane bytes, positive scales; offsets[cells] = planes bytes."""
+    ng = inn // 64
+    bits = rng.choice(np.asarray(widths, np.uint8), size=out * ng).astype(np.uint8)
+    offsets = np.zeros(out * ng + 1, np.uint32)
+    offsets[1:] = np.cumsum(bits.astype(np.uint32) * 8)
+    planes = rng.integers(0, 256, int(offsets[-1]), dtype=np.uint8)
+    scales = (rng.random(out * ng, dtype=np.float32) * np.float32(0.01) + np.float32(1e-4)).astype(np.float32)
+    return planes, offsets, bits, scales
+
+
+def mixed_qng64_py_decode(planes, offsets, bits, scales, out, inn):
+    """Independent decode of the mixed layout: numpy bit unpacking, LSB first within each byte, so
+    plane j's bit p is element p's bit j."""
+    ng = inn // 64
+    w = np.zeros((out, inn), np.float32)
+    for cell in range(out * ng):
+        n, base = int(bits[cell]), int(offsets[cell])
+        pl = np.unpackbits(planes[base: base + n * 8].reshape(n, 8), axis=1, bitorder="little").astype(np.int64)
+        u = (pl << np.arange(n, dtype=np.int64)[:, None]).sum(axis=0)
+        code = (u - (1 << (n - 1))).astype(np.float32)
+        r, g = divmod(cell, ng)
+        w[r, g * 64:(g + 1) * 64] = code * scales[cell]
+    return w

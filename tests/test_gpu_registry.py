@@ -278,6 +278,61 @@ def test_registry_moe_layer_with_router(R, oracle):
     assert R.bind_router("ffn.bad", seeded_normal(544, (4, 6), 0.05)) == 0                        # in % 4
 
 
+def test_mixed_qng64_bind_decode_and_probes(R, lib, oracle):
+    """Mixed per-cell qNg64 (mlx_moe.h:104-116): device decode bit-exact against the oracle; the
+    one-shot GEMV probe (batch 1 / 3 / 20, the last on the matrix-core path when every width <= 10)
+    and the bound name through the matvec probe against the decoded product; kind 4 with bits 0;
+    the dequant probe and experts e != 0 refused; snapshot / restore; the binders' checks."""
+    import torch
+    import beglin_amd
+    from oracle_ffi import mixed_qng64_random
+    say("mixed qNg64")
+    rng = np.random.default_rng(77)
+    out, inn = 200, 512
+    for widths in (list(range(2, 16)), [2, 3, 4, 5, 6], [9]):
+        planes, offsets, bits, scales = mixed_qng64_random(rng, out, inn, widths)
+        wref = oracle.decode_qng64_mixed(planes, offsets, bits, scales, out, inn)
+        ctx = beglin_amd.Context(0)
+        t = ctx.bind_qng64_mixed(planes, offsets, bits, scales, out, inn)
+        assert t.info()["kind"] == 4 and t.info()["bits"] == max(widths)
+        dq = torch.empty((out, inn), device="cuda")
+        ctx.dequant(t, 0, out, dq)
+        ctx.sync()
+        assert np.array_equal(dq.cpu().numpy().view(np.uint32), wref.view(np.uint32)), widths
+        t.free(); ctx.close()
+        for batch in (1, 3, 20):
+            x = seeded_normal(600 + batch, (batch, inn))
+            ok, y = R.mixed_probe(planes, offsets, bits, scales, out, inn, x)
+            ref = x.astype(np.float64) @ wref.astype(np.float64).T
+            assert ok == 1 and relerr(y, ref) <= TOL, (widths, batch)
+    assert R.bind_mixed("mx.t", planes, offsets, bits, scales, out, inn) == 1
+    assert R.binding_kind("mx.t") == (4, 0)
+    x = seeded_normal(610, (inn,))
+    ok, y = R.matvec_probe("mx.t", 0, x, out)
+    assert ok == 1 and relerr(y, wref.astype(np.float64) @ x.astype(np.float64)) <= TOL
+    assert R.matvec_probe("mx.t", 1, x, out)[0] == 0
+    assert R.dequant_probe("mx.t", 0, 0, 0, 64)[0] == 0
+    ok, sid = R.snapshot("mx.t")
+    assert ok == 1
+    bind_all(R, oracle, {"mx.t": 8}, 1, out, inn, 620)
+    assert R.binding_kind("mx.t") == (1, 8)
+    assert lib.bgl_gpu_restore_binding_snapshot(sid) == 1 and R.binding_kind("mx.t") == (4, 0)
+    assert np.array_equal(R.matvec_probe("mx.t", 0, x, out)[1], y)
+    assert lib.bgl_gpu_drop_binding_snapshot(sid) == 1
+    # the binders' checks (mlx_moe.cpp:1750-1758): every refusal leaves the binding as it was
+    bad = offsets.copy(); bad[0] = 8
+    assert R.bind_mixed("mx.t", planes, bad, bits, scales, out, inn) == 0
+    bad = offsets.copy(); bad[-1] += 8
+    assert R.bind_mixed("mx.t", planes, bad, bits, scales, out, inn) == 0
+    b16 = bits.copy(); b16[3] = 16
+    assert R.bind_mixed("mx.t", planes, offsets, b16, scales, out, inn) == 0
+    for v in (0.0, -1.0, np.inf, np.nan):
+        s = scales.copy(); s[5] = v
+        assert R.bind_mixed("mx.t", planes, offsets, bits, s, out, inn) == 0
+        assert R.mixed_probe(planes, offsets, bits, s, out, inn, x[None])[0] == 0
+    assert R.binding_kind("mx.t") == (4, 0)
+
+
 def test_memory_report_epoch_and_counters(R, lib, oracle):
     import ctypes as C
     say("registry memory / epoch")

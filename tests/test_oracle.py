@@ -333,6 +333,41 @@ def test_g256sf_packer_roundtrip(oracle):
 
 
 # ---------------------------------------------------------------- MoE
+def test_mixed_qng64_decode_uniform_equals_dense(oracle):
+    """A mixed tensor whose cells all have the same n is the qng64_dense layout (qng64_dense.c:19-27
+    vs mlx_moe.cpp:1708-1722): or_decode_qng64_mixed equals or_decode_qng64 on the same bytes."""
+    from oracle_ffi import mixed_qng64_py_decode
+    out, inn = 9, 256
+    for n in (2, 3, 4, 5, 7, 8, 12, 15):
+        w = seeded_normal(300 + n, (out, inn), 0.02)
+        planes, scales = oracle.quantize_qng64_gguf(w, n)
+        cells = out * inn // 64
+        offsets = (np.arange(cells + 1, dtype=np.uint32) * np.uint32(n * 8)).astype(np.uint32)
+        bits = np.full(cells, n, np.uint8)
+        got = oracle.decode_qng64_mixed(planes.reshape(-1), offsets, bits, scales.reshape(-1), out, inn)
+        ref = oracle.decode(4, planes, scales, out, inn, bits=n)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), n
+        py = mixed_qng64_py_decode(planes.reshape(-1), offsets, bits, scales.reshape(-1), out, inn)
+        assert np.array_equal(py.view(np.uint32), ref.view(np.uint32)), n
+
+
+def test_mixed_qng64_decode_random_widths(oracle):
+    """Per-cell widths 2..15 (4 included, which the dense packer refuses) against the independent
+    Python bit-plane decode, bit for bit; the extreme codes of every width are reached."""
+    from oracle_ffi import mixed_qng64_py_decode, mixed_qng64_random
+    rng = np.random.default_rng(31)
+    out, inn = 7, 320
+    planes, offsets, bits, scales = mixed_qng64_random(rng, out, inn, list(range(2, 16)))
+    planes[:int(offsets[1])] = 0xFF                  # cell 0: all-ones code, 2^(n-1) - 1
+    planes[int(offsets[1]):int(offsets[2])] = 0      # cell 1: all-zero code, -2^(n-1)
+    got = oracle.decode_qng64_mixed(planes, offsets, bits, scales, out, inn)
+    ref = mixed_qng64_py_decode(planes, offsets, bits, scales, out, inn)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    n0, n1 = int(bits[0]), int(bits[1])
+    assert np.all(got[0, :64] == np.float32((1 << (n0 - 1)) - 1) * scales[0])
+    assert np.all(got[0, 64:128] == np.float32(-(1 << (n1 - 1))) * scales[1])
+
+
 def test_router_logits_match_sequential_double(oracle):
     """or_moe_router_logits (moe_matvec_f32, qwen_infer.c:3460-3466, + bias) against a pure-Python
     loop in the reference order: Python floats are IEEE doubles and a product of two floats is
