@@ -226,6 +226,50 @@ class Context:
                                        _p(x_dev), x_dev.shape[0], K, _p(out_dev)), "bgl_moe_layer_dev")
 
 
+class Model:
+    """Weights loaded from the int4 layout manifest + blob (bgl_model_load_int4) or from the
+    repacked-layout cache (bgl_model_load_cache)."""
+
+    def __init__(self, ctx, layout, blob, cache=None):
+        self.ctx, self.layout, self.blob = ctx, layout, blob
+        h = C.c_void_p()
+        if cache is not None:
+            _check(lib().bgl_model_load_cache(ctx.h, cache.encode(), layout.encode(), blob.encode(), C.byref(h)),
+                   "bgl_model_load_cache")
+        else:
+            _check(lib().bgl_model_load_int4(ctx.h, layout.encode(), blob.encode(), C.byref(h)), "bgl_model_load_int4")
+        self.h = h
+
+    def __len__(self):
+        return lib().bgl_model_count(self.h)
+
+    def find(self, name):
+        """(kind, out, in, Tensor or None, address of the f32 data or None); the model owns the tensor."""
+        k, o, i = C.c_int(), C.c_int(), C.c_int()
+        t, f = C.c_void_p(), C.c_void_p()
+        _check(lib().bgl_model_find(self.h, name.encode(), C.byref(k), C.byref(o), C.byref(i), C.byref(t), C.byref(f)),
+               "bgl_model_find")
+        return k.value, o.value, i.value, (Tensor(t) if t.value else None), f.value
+
+    def save_cache(self, path):
+        _check(lib().bgl_model_save_cache(self.h, path.encode(), self.layout.encode(), self.blob.encode()), "bgl_model_save_cache")
+
+    def close(self):
+        if self.h:
+            lib().bgl_model_free(self.h)
+            self.h = None
+
+
+def layout_check(layout, blob):
+    n = C.c_int()
+    rc = lib().bgl_int4_layout_check(layout.encode(), blob.encode(), C.byref(n))
+    return rc, n.value
+
+
+def cache_valid(cache, layout, blob):
+    return lib().bgl_model_cache_valid(cache.encode(), layout.encode(), blob.encode())
+
+
 # ---- the name-keyed registry (mlx_moe.h boundary): thin wrappers, 1 = ok / 0 = failure ----
 class Registry:
     """bgl_gpu_* entry points with numpy host buffers."""

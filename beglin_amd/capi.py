@@ -67,6 +67,14 @@ SIGNATURES = [
     ("bgl_gpu_available", _I, []),
     ("bgl_gpu_bind_router", _I, [C.c_char_p, _P, _P, _L, _L]),
     ("bgl_bind_qng64_mixed", _I, [_P, _P, _L, _P, _P, _P, _I, _I, C.POINTER(_P)]),
+    ("bgl_int4_layout_check", _I, [C.c_char_p, C.c_char_p, C.POINTER(_I)]),
+    ("bgl_model_load_int4", _I, [_P, C.c_char_p, C.c_char_p, C.POINTER(_P)]),
+    ("bgl_model_count", _I, [_P]),
+    ("bgl_model_find", _I, [_P, C.c_char_p, C.POINTER(_I), C.POINTER(_I), C.POINTER(_I), C.POINTER(_P), C.POINTER(_P)]),
+    ("bgl_model_free", _I, [_P]),
+    ("bgl_model_save_cache", _I, [_P, C.c_char_p, C.c_char_p, C.c_char_p]),
+    ("bgl_model_cache_valid", _I, [C.c_char_p, C.c_char_p, C.c_char_p]),
+    ("bgl_model_load_cache", _I, [_P, C.c_char_p, C.c_char_p, C.c_char_p, C.POINTER(_P)]),
     ("bgl_gpu_qng64_mixed_dense_probe", _I, [_P, _L, _P, _P, _P, _L, _L, _P, _I, _P]),
     ("bgl_gpu_bind_qng64_mixed_dense_probe", _I, [_P, _L, _P, _P, _P, C.c_char_p, _L, _L]),
     ("bgl_gpu_moe_layer", _I, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, _P, _I, _I,

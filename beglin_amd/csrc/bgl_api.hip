@@ -226,11 +226,10 @@ static size_t ref_scale_bytes(int kind, int out, int in) {
 
 static inline unsigned nblk(long n, int bs = 256) { return (unsigned)((n + bs - 1) / bs); }
 
-// Repack reference-layout device buffers into a new tensor.
-static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const void *dpk, const void *dsc,
-                       const uint8_t *dsub, bgl_tensor **res) {
-    bgl_tensor *t = new bgl_tensor();
-    BglDevTensor &T = t->T;
+// The tiled device layout of a (kind, bits, out, in) tensor: its record and the byte sizes of its
+// three allocations (chunks, per-unit scales, per-unit second word; 0 when absent).
+void device_layout(int kind, int bits, int out, int in, BglDevTensor &T, size_t bytes[3]) {
+    T = BglDevTensor{};
     T.fmt = kind;
     T.bits = kind == BGL_QNG64 ? bits : kind == BGL_Q8G64 ? 8 : kind == BGL_F16 ? 16 : kind == BGL_F32 ? 32 : 4;
     T.N = out; T.K = in; T.ntiles = (out + BGL_TILE - 1) / BGL_TILE;
@@ -238,11 +237,32 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     T.cpu = kind == BGL_Q4G256SF ? 8 : kind == BGL_Q8G64 ? 4 : kind == BGL_QNG64 ? bits : kind == BGL_F16 ? 8
           : kind == BGL_F32 ? 16 : 2;
     T.cpr = T.nunits * T.cpu;
-    long rows = (long)T.ntiles * BGL_TILE;
-    size_t wbytes = (size_t)rows * T.cpr * 16;
+    const long rows = (long)T.ntiles * BGL_TILE;
     const bool dense = kind == BGL_F16 || kind == BGL_F32;
-    size_t s0bytes = dense ? 0 : (size_t)rows * T.nunits * (kind == BGL_QNG64 || kind == BGL_Q4G256SF ? 8 : 4);
-    const bool has_s1 = kind == BGL_Q4G64A;
+    bytes[0] = (size_t)rows * T.cpr * 16;
+    bytes[1] = dense ? 0 : (size_t)rows * T.nunits * (kind == BGL_QNG64 || kind == BGL_Q4G256SF ? 8 : 4);
+    bytes[2] = kind == BGL_Q4G64A ? (size_t)rows * T.nunits * 4 : 0;
+}
+
+bgl_tensor *tensor_from_parts(const BglDevTensor &T, void *w, void *s0, void *s1, size_t device_bytes) {
+    bgl_tensor *t = new bgl_tensor();
+    t->T = T;
+    t->T.w = (const uint8_t *)w; t->T.s0 = s0; t->T.s1 = (const uint32_t *)s1;
+    t->owned = {w, s0, s1};
+    t->device_bytes = device_bytes;
+    return t;
+}
+
+// Repack reference-layout device buffers into a new tensor.
+static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const void *dpk, const void *dsc,
+                       const uint8_t *dsub, bgl_tensor **res) {
+    bgl_tensor *t = new bgl_tensor();
+    BglDevTensor &T = t->T;
+    size_t lb[3];
+    device_layout(kind, bits, out, in, T, lb);
+    const long rows = (long)T.ntiles * BGL_TILE;
+    const size_t wbytes = lb[0], s0bytes = lb[1];
+    const bool has_s1 = lb[2] != 0;
     void *w = nullptr, *s0 = nullptr, *s1 = nullptr;
     hipError_t e = hipMalloc(&w, wbytes);
     if (e == hipSuccess && s0bytes) e = hipMalloc(&s0, s0bytes);

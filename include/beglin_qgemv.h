@@ -153,6 +153,29 @@ int bgl_gemv_q4g32h_mt(bgl_ctx *p, const uint8_t *packed, const uint16_t *scales
 /* Drop the cached device copy bound to `packed` (rebind after the caller changes the bytes). */
 int bgl_forget(bgl_ctx *p, const void *packed);
 
+/* ---------------- int4-mode loader and the repacked-layout cache ----------------
+ * load_int4 (qwen_infer.c:554-615): the layout manifest, one line "name kind doff out in ng soff
+ * [soff2]" per tensor over the weight blob; kinds q4g64, q8g64, q4g256sf (8th field: sub-code offset)
+ * and f32.  Every check of the reference loader applies (ng and in divisibility, 64-byte alignment of
+ * the int4 offsets, extents inside the blob, unknown kinds, duplicate names, at most 512 tensors);
+ * a failed check loads nothing.  Quantized tensors are bound on the device (the model owns them:
+ * do not free what bgl_model_find returns); f32 tensors stay in the read-only mapped blob.
+ * bgl_int4_layout_check runs the parse and the checks only (no device work). */
+typedef struct bgl_model bgl_model;
+int bgl_int4_layout_check(const char *layout_path, const char *blob_path, int *n_tensors);
+int bgl_model_load_int4(bgl_ctx *ctx, const char *layout_path, const char *blob_path, bgl_model **out);
+int bgl_model_count(const bgl_model *m);
+/* kind: BGL_K_* of a bound tensor (then *t is set) or 0 for f32 (then *f32 points into the blob). */
+int bgl_model_find(const bgl_model *m, const char *name, int *kind, int *out, int *in, bgl_tensor **t, const float **f32);
+int bgl_model_free(bgl_model *m);
+/* The repacked device layout on disk (the .beglin cache pattern, gguf_cache.c): valid only for the
+ * same blob and manifest (size and mtime), device architecture and device-layout version; opened
+ * without following symlinks; a directory pointing outside the file is an error. */
+int bgl_model_save_cache(const bgl_model *m, const char *cache_path, const char *layout_path, const char *blob_path);
+int bgl_model_cache_valid(const char *cache_path, const char *layout_path, const char *blob_path);   /* 1 / 0 */
+int bgl_model_load_cache(bgl_ctx *ctx, const char *cache_path, const char *layout_path, const char *blob_path,
+                         bgl_model **out);
+
 /* ---------------- MoE: expert-sorted gather ----------------
  * An E-stacked expert tensor (MoeAFTensor, qwen_infer.c:2358-2444; per-expert widths like
  * st_register_moe_experts_mixed_as, :16439-16564): E descriptors, each expert with its own kind.

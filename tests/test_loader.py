@@ -1,0 +1,83 @@
+"""The int4-mode layout parse and its checks (load_int4, qwen_infer.c:554-615) through
+bgl_int4_layout_check: no device work, so these run without a GPU.  Each refusal mirrors one FATAL
+of the reference loader; parsing stops quietly at the first line without the seven leading fields,
+as the reference's fscanf loop does."""
+import os
+
+import pytest
+
+from loader_fixture import build
+
+
+@pytest.fixture()
+def model(oracle, tmp_path):
+    return build(oracle, str(tmp_path))
+
+
+def check(layout, blob):
+    import beglin_amd
+    return beglin_amd.layout_check(layout, blob)
+
+
+def rewrite(layout, edit):
+    lines = open(layout).read().splitlines()
+    lines = edit(lines)
+    with open(layout, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+def test_valid_layout(model):
+    layout, blob, refs = model
+    assert check(layout, blob) == (0, len(refs))
+
+
+@pytest.mark.parametrize("case", [
+    "misaligned_q4", "misaligned_g256", "missing_soff2", "g256_in", "g256_ng", "q4_in", "q4_ng", "q8_ng", "extent_q4",
+    "extent_q8", "extent_g256_sub", "extent_f32", "unknown_kind", "duplicate", "negative_dim", "negative_off",
+])
+def test_refusals(model, case):
+    layout, blob, _ = model
+    wb = os.path.getsize(blob)
+
+    def field(i, j, v):
+        def ed(lines):
+            f = lines[i].split()
+            f[j] = str(v)
+            lines[i] = " ".join(f)
+            return lines
+        return ed
+
+    edits = {
+        "misaligned_q4": field(0, 2, 8), "misaligned_g256": field(2, 7, int(open(layout).read().splitlines()[2].split()[7]) + 4),
+        "missing_soff2": lambda L: L[:2] + [" ".join(L[2].split()[:7])],
+        "g256_in": field(2, 4, 1024 + 64), "g256_ng": field(2, 5, 16), "q4_in": field(0, 4, 500), "q4_ng": field(0, 5, 9),
+        "q8_ng": field(1, 5, 3), "extent_q4": field(0, 3, 100000), "extent_q8": field(1, 2, wb - 64),
+        "extent_g256_sub": field(2, 7, wb - 64), "extent_f32": field(3, 3, wb),
+        "unknown_kind": field(1, 1, "q6k"), "duplicate": field(1, 0, "q.proj"), "negative_dim": field(0, 3, -1),
+        "negative_off": field(0, 2, -64),
+    }
+    rewrite(layout, edits[case])
+    rc, _ = check(layout, blob)
+    assert rc < 0, case
+
+
+def test_too_many_tensors(oracle, tmp_path):
+    layout, blob, _ = build(oracle, str(tmp_path), [("n", "f32", 4, 0)])
+    with open(layout, "w") as f:
+        f.write("".join(f"t{i} f32 0 4 0 0 0\n" for i in range(513)))
+    assert check(layout, blob)[0] < 0
+    with open(layout, "w") as f:
+        f.write("".join(f"t{i} f32 0 4 0 0 0\n" for i in range(512)))
+    assert check(layout, blob) == (0, 512)
+
+
+def test_parse_stops_at_a_short_line(model):
+    layout, blob, refs = model
+    rewrite(layout, lambda L: L[:2] + ["garbage line"] + L[2:])
+    assert check(layout, blob) == (0, 2)
+
+
+def test_missing_files(model, tmp_path):
+    layout, blob, _ = model
+    assert check(str(tmp_path / "nope.txt"), blob)[0] < 0
+    assert check(layout, str(tmp_path / "nope.bin"))[0] < 0
