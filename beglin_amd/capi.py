@@ -6,7 +6,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libbeglin_hip.so")
+# BGL_LIB names another build of the same C-ABI (A/B timing of two builds); default: the in-tree one
+LIB_PATH = os.environ.get("BGL_LIB") or os.path.join(HERE, "libbeglin_hip.so")
 
 # mirrors of the header's enums
 K_Q4G64, K_Q8G64, K_Q4G256SF, K_QNG64, K_Q4G32H = 1, 2, 3, 4, 5

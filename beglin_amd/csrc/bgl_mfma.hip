@@ -44,6 +44,9 @@ typedef unsigned int mf_u4 __attribute__((ext_vector_type(4)));
 #define MF_KC 4              // K-steps (32 elements each) per staged activation block
 #define MF_MAXCT 4           // column tiles (16 columns each) per launch: up to 64 columns
 #define MF_MAXN 10           // qNg64 widths whose codes are exact in fp16 via the 1024+u trick
+#ifndef MF_WPE_INT4
+#define MF_WPE_INT4 0      // 1: ask for 4 waves per SIMD on the int4 kernels of up to 32 columns
+#endif
 
 static inline unsigned nblk(long n, int bs = 256) { return (unsigned)((n + bs - 1) / bs); }
 
@@ -208,18 +211,23 @@ __device__ __forceinline__ mf_h8 dec_a(const ARaw<FMT, NB> &a, int q) {
     return __builtin_bit_cast(mf_h8, r);
 }
 
-// Raw A words per K-step and row block.  A block is 8 K-steps for int4 with up to 32 columns and 4
-// otherwise: about 8 KiB of weights in flight per wave, two blocks of them in registers.
+// Raw A words per K-step and row block.  A block is 4 K-steps; two blocks of weights are in
+// registers per wave (the ring), and two workgroups share a CU where the registers allow.
 template <int FMT, int NB> constexpr int a_words() {
     return FMT == BGL_Q8G64 ? 2 : FMT == BGL_QNG64 ? 2 * ((NB >> 3) & 1) + ((NB >> 2) & 1) + ((NB >> 1) & 1) + (NB & 1) : 1;
 }
-template <int FMT, int NB, int CT> constexpr int block_ksteps() { return (CT <= 2 && a_words<FMT, NB>() == 1) ? 8 : 4; }
+template <int FMT, int NB, int CT> constexpr int block_ksteps() { return 4; }
+// Occupancy asked of the compiler: 4 waves per SIMD (two 8-wave workgroups per CU, <= 128 VGPRs)
+// where the kernel fits without spilling -- up to 32 columns of one-word (int4) weights; the
+// others keep their registers.
+template <int FMT, int NB, int CT> constexpr int mfma_waves_per_eu() { return MF_WPE_INT4 && CT <= 2 && a_words<FMT, NB>() == 1 ? 4 : 1; }
 // bytes of scale data per row and unit in the device layout
 template <int FMT> constexpr int scale_bytes() { return FMT == BGL_QNG64 ? 8 : 4; }
 
 // ==================================================================================== GEMM kernel
 template <int FMT, int NB, int CT>
-__global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
+__global__ __launch_bounds__(MF_WAVES * 64) __attribute__((amdgpu_waves_per_eu(mfma_waves_per_eu<FMT, NB, CT>()))) void
+k_gemm_mfma(MfmaLaunch L) {
     constexpr int KC = block_ksteps<FMT, NB, CT>();
     constexpr int SPU = ksteps_per_unit<FMT>();
     constexpr int UPB = KC / SPU;                                  // units per block
@@ -251,11 +259,11 @@ __global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
         for (int c = 0; c < CT; c++) { acc[r][c] = mf_f4{0, 0, 0, 0}; cg[r][c] = mf_f4{0, 0, 0, 0}; }
 
     // ---- staged data of block b (activation fragments + the 4 tiles' scales) ----
-    uint4 breg[PER_B], sreg[PER_S];
+    struct SR { uint4 b[PER_B], s[PER_S]; };
     // Every global load below is unconditional, from an address clamped into the tensor, and the
     // unwanted values are dropped by a select: conditional loads would keep the compiler from
     // counting outstanding loads, and it would then wait for all of them before each block.
-    auto load_stage = [&](int b) {
+    auto load_stage = [&](SR &R, int b) {
         const int sb = s0 + b * KC;
 #pragma unroll
         for (int i = 0; i < PER_B; i++) {
@@ -263,7 +271,7 @@ __global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
             const int s = sb + e / (CT * 2 * 64);
             const int sc = s < s1 ? s : s1 - 1;
             const bgl_u32x4 g = ((const BGL_GLOBAL bgl_u32x4 *)L.xf)[((size_t)sc * CT * 2 * 64) + e % (CT * 2 * 64)];
-            breg[i] = make_uint4(g.x, g.y, g.z, g.w);            // out-of-range steps are zeroed at the store
+            R.b[i] = make_uint4(g.x, g.y, g.z, g.w);             // out-of-range steps are zeroed at the store
         }
 #pragma unroll
         for (int i = 0; i < PER_S; i++) {
@@ -276,22 +284,22 @@ __global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
             const int tc = t < T.ntiles ? t : T.ntiles - 1, uc = u < T.nunits ? u : T.nunits - 1;
             const bgl_u32x4 g = ((const BGL_GLOBAL bgl_u32x4 *)T.s0)[((size_t)tc * T.nunits + uc) * (64 * SCW / 16) +
                                                                       rem % (64 * SCW / 16)];
-            sreg[i] = make_uint4(g.x, g.y, g.z, g.w);            // rows past the tensor never reach y
+            R.s[i] = make_uint4(g.x, g.y, g.z, g.w);             // rows past the tensor never reach y
         }
     };
-    auto store_stage = [&](int buf, int b) {
+    auto store_stage = [&](int buf, const SR &R, int b) {
 #pragma unroll
         for (int i = 0; i < PER_B; i++) {
             const int e = threadIdx.x + i * NT;
             const bool in = s0 + b * KC + e / (CT * 2 * 64) < s1;
-            stage[buf][e] = in ? breg[i] : make_uint4(0, 0, 0, 0);
+            stage[buf][e] = in ? R.b[i] : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < PER_S; i++) {
             const int e = threadIdx.x + i * NT;
             if (e < SF) {
                 if constexpr (FMT == BGL_Q4G32H) {                  // 4 rows x (fp16 lo, fp16 hi) -> 4 float2
-                    const uint32_t w[4] = {sreg[i].x, sreg[i].y, sreg[i].z, sreg[i].w};
+                    const uint32_t w[4] = {R.s[i].x, R.s[i].y, R.s[i].z, R.s[i].w};
                     float f[8];
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
@@ -304,7 +312,7 @@ __global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
                     stage[buf][BF + 2 * e] = a;
                     stage[buf][BF + 2 * e + 1] = b;
                 } else {
-                    stage[buf][BF + e] = sreg[i];
+                    stage[buf][BF + e] = R.s[i];
                 }
             }
         }
@@ -326,10 +334,11 @@ __global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
     auto compute = [&](const WR &W, int b) {
         const uint4 *stg = stage[b & 1];
         const float *scl = reinterpret_cast<const float *>(stg + BF);
+        // K-steps past the split still run: their staged activations are zero and their weights
+        // are rereads of real codes, so they add exact zeros, and the block stays one straight-line
+        // region the scheduler can interleave (a per-step exit made every step its own block).
 #pragma unroll
         for (int j = 0; j < KC; j++) {
-            const int s = s0 + b * KC + j;
-            if (s >= s1) break;
             mf_h8 A[MF_RBW];
 #pragma unroll
             for (int r = 0; r < MF_RBW; r++) A[r] = dec_a<FMT, NB>(W.a[j][r], q);
@@ -368,26 +377,35 @@ __global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
         }
     };
 
-    WR w0, w1;
-    load_stage(0);
+    // Pipeline: block b is computed while block b+2's weights and staged data (activation
+    // fragments and scales) are loading and block b+1's staged data goes to LDS -- both streams
+    // have a full block of compute between issue and use.  Iteration b uses weight registers w[b%3]
+    // and loads w[(b+2)%3]; it stores staged set (b+1)%2 and refills set b%2.  Every load is issued
+    // on every path (past the end they reread the last K-step and are never used), so the number
+    // of loads in flight is the same everywhere and each wait covers only its own block.
+    WR w0, w1, w2;
+    SR r0, r1;
+    load_stage(r0, 0);
     load_w(w0, 0);
-    store_stage(0, 0);
+    load_stage(r1, 1);
+    load_w(w1, 1);
+    store_stage(0, r0, 0);
     __syncthreads();
-    // The next block's loads are issued on every iteration (past the end they reread the last
-    // K-step and are never used), so the number of loads in flight is the same on every path and
-    // compute waits only for its own block.
-    for (int b = 0; b < nblocks; b += 2) {
-        load_stage(b + 1);
-        load_w(w1, b + 1);
-        if (active) compute(w0, b);
-        store_stage((b + 1) & 1, b + 1);    // past the end it fills a buffer nobody reads again
+    auto iter = [&](WR &wc, WR &wl, SR &rs, SR &rl, int b) {
+        load_stage(rl, b + 2);
+        load_w(wl, b + 2);
+        if (active) compute(wc, b);
+        store_stage((b + 1) & 1, rs, b + 1);   // past the end it fills a buffer nobody reads again
         __syncthreads();
-        if (b + 1 >= nblocks) break;
-        load_stage(b + 2);
-        load_w(w0, b + 2);
-        if (active) compute(w1, b + 1);
-        store_stage(b & 1, b + 2);
-        __syncthreads();
+        return b + 1 < nblocks;
+    };
+    for (int b = 0; b < nblocks; b += 6) {
+        if (!iter(w0, w2, r1, r0, b)) break;
+        if (!iter(w1, w0, r0, r1, b + 1)) break;
+        if (!iter(w2, w1, r1, r0, b + 2)) break;
+        if (!iter(w0, w2, r0, r1, b + 3)) break;
+        if (!iter(w1, w0, r1, r0, b + 4)) break;
+        if (!iter(w2, w1, r0, r1, b + 5)) break;
     }
     if (!active) return;
 
