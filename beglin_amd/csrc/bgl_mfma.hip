@@ -17,18 +17,25 @@
 // lane l holds column l%16, elements 8*(l/16)..+7.  D: lane l holds column l%16, rows
 // 4*(l/16)..+3 of the 16-row block.
 //
-// Work split.  A workgroup = 8 waves = 4 consecutive 64-row weight tiles (256 rows) over one K
-// range; two waves share a tile (two 16-row blocks each).  The activation fragments and scales of
-// 4 consecutive K-steps (a block) are staged through LDS, double buffered, and shared by every
-// wave.  Shapes with few tiles split K over workgroups into fp32 partials that k_mfma_reduce adds
-// in split order (deterministic; no atomics).  All tensors of a group (same format and K, one
-// activation) run in one launch and one reduce.
+// Work split.  A workgroup owns 4 consecutive 64-row weight tiles (256 rows) over one K range (a
+// split) and has KW K-slices of 8 waves; in a slice two waves share a tile (two 16-row blocks
+// each).  The split's activation fragments and the 4 tiles' scales are staged in LDS once (up to
+// 144 KB, which bounds the split's length), then each wave streams its own weights with no further
+// barrier: a register ring keeps the next K-steps' loads in flight.  Splits are sized so the grid
+// fills the chip; k_mfma_reduce adds their fp32 partials in split order (deterministic; no
+// atomics).  All tensors of a group (same format and K, one activation) run in one launch and one
+// reduce.  (A reduce inside the GEMM by the last workgroup of each row group -- an agent-scope
+// ticket -- measured slower: the cache write-back and the serial tail cost more than the launch.)
 //
-// Memory access.  Weights, fragments and scales are read with buffer loads: the per-lane part of
-// every address is fixed for the whole kernel and the per-step part is a scalar offset, so the
-// loads cost no vector ALU work.  The fragment buffer is zero-padded to whole blocks and the weight
-// and scale offsets are clamped into the tensor, so no load is conditional (a conditional load
-// makes the compiler wait for every load in flight) and steps past K add exact zeros.
+// Memory access.  Weights are read a whole 16-byte chunk row per lane (buffer_load_dwordx4: each
+// quarter-wave reads 256 contiguous bytes) and the operand layout above -- four lanes per row -- is
+// rebuilt with v_permlane16/32_swap; the per-lane part of every address is fixed for the kernel and
+// the per-step part is a scalar offset, so the loads cost no vector ALU work.  Offsets are clamped
+// into the tensors, so no load is conditional (a conditional load makes the compiler wait for
+// every load in flight), and steps past K meet zero fragments.
+//
+// Schedule.  The fold is software-pipelined: a group's MFMA sums are folded while the next group's
+// MFMAs run, so the vector ALUs and the matrix cores overlap.
 #include <string.h>
 
 #include "bgl_gemv_impl.h"
@@ -49,13 +56,10 @@ typedef unsigned int mf_u2 __attribute__((ext_vector_type(2)));
 #define MF_TILES 4           // 64-row weight tiles per workgroup (they share the staged activations)
 #define MF_RBW 2             // 16-row blocks per wave: two waves per tile
 #define MF_WAVES (MF_TILES * 4 / MF_RBW)
-#define MF_KC 4              // K-steps (32 elements each) per staged block
+#define MF_KSTEP_PAD 16      // split length granularity in K-steps (every ring depth divides it)
 #define MF_MAXCT 4           // column tiles (16 columns each) per launch: up to 64 columns
 #define MF_MAXN 10           // qNg64 widths whose codes are exact in fp16 via the 1024+u trick
-#define MF_MAXS 16           // K splits per tensor
 #define MF_RSRC_W3 0x00020000   // buffer resource word 3 on gfx9: 32-bit data format, raw addressing
-
-static inline unsigned nblk(long n, int bs = 256) { return (unsigned)((n + bs - 1) / bs); }
 
 struct MfmaTask {
     BglDevTensor T;
@@ -65,78 +69,15 @@ struct MfmaTask {
     int ystride;
     int wg0;                 // first workgroup of this task in the launch
     int wgr;                 // workgroups along the rows (groups of 4 tiles)
-    int kps;                 // K-steps per split, a multiple of the block size
+    int kps;                 // K-steps per split, a multiple of MF_KSTEP_PAD
 };
 
 struct MfmaLaunch {
     MfmaTask t[BGL_MAX_TASKS];
     int ntasks;
     int M;                   // valid columns (<= 16*CT)
-    const uint4 *xf;         // activation fragments [KSP][CT][2][64] x 16 B, zero past K
-    const float *colinv;     // [16*CT] column factors 2^(e-14)
-    int xf_steps;            // KSP: K-steps held in xf (K/32 rounded up to whole blocks)
+    const float *x;          // activations x[m][k], M rows of K floats
 };
-
-// ==================================================================================== activations
-// Grid (16*CT columns, KSP*4/256 chunks of 256 8-element slots), 256 threads; columns >= M and
-// slots past K are zero.  x: [M][K] rows of this launch.  Every chunk's workgroup reduces its
-// column's max over all of K (the column is L2-resident), so no second pass is needed; a thread's
-// own 8 values and its share of the column are loaded in one round before any is used.
-#define MF_PREP_SLOTS 256
-#define MF_PREP_BATCH 16
-__global__ __launch_bounds__(256) void k_act_frag(const float *__restrict__ x, int M, int K, int KSP, int CT,
-                                                  uint4 *__restrict__ xf, float *__restrict__ colinv) {
-    __shared__ float wmax[4];
-    const int m = blockIdx.x, t = threadIdx.x;
-    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)(m < M ? m : 0) * K);   // K % 64 == 0
-    const int n4 = K >> 2;
-    const int g = blockIdx.y * MF_PREP_SLOTS + t;                                        // this thread's slot
-    const bool own = m < M && g < (K >> 3);
-    const int gc = own ? g : 0;
-    const float4 a = x4[2 * gc], b = x4[2 * gc + 1];
-    float mx = 0.0f;
-    if (m < M) {                                                                         // uniform per workgroup
-        for (int k0 = 0; k0 < n4; k0 += MF_PREP_BATCH * 256) {
-            float4 v[MF_PREP_BATCH];
-#pragma unroll
-            for (int i = 0; i < MF_PREP_BATCH; i++) {
-                const int k = k0 + t + i * 256;
-                v[i] = x4[k < n4 ? k : n4 - 1];
-            }
-#pragma unroll
-            for (int i = 0; i < MF_PREP_BATCH; i++) {
-                const float mm = fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
-                mx = k0 + t + i * 256 < n4 ? fmaxf(mx, mm) : mx;
-            }
-        }
-    }
-    mx = wave_max_f32(mx);
-    if ((t & 63) == 0) wmax[t >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    int e = 0;
-    if (mx > 0.0f) frexpf(mx, &e);                       // mx in [2^(e-1), 2^e)
-    const float sc = mx > 0.0f ? ldexpf(1.0f, 14 - e) : 1.0f;
-    if (t == 0 && blockIdx.y == 0) colinv[m] = mx > 0.0f ? ldexpf(1.0f, e - 14) : 1.0f;
-    if (g >= KSP * 4) return;
-    const int ct = m >> 4, ml = m & 15;
-    const int s = g >> 2, q = g & 3;
-    const float v8[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};   // element order {0,2,1,3,4,6,5,7}
-    _Float16 hi[8], lo[8];
-#pragma unroll
-    for (int p = 0; p < 8; p++) {
-        const float v = own ? v8[p] * sc : 0.0f;         // power-of-two scaling: exact
-        const _Float16 h = (_Float16)v;
-        hi[p] = h;
-        lo[p] = (_Float16)(v - (float)h);
-    }
-    uint4 H, L;
-    memcpy(&H, hi, 16);
-    memcpy(&L, lo, 16);
-    const size_t base = ((size_t)s * CT + ct) * 2 * 64 + ml + 16 * q;
-    xf[base] = H;
-    xf[base + 64] = L;
-}
 
 // ==================================================================================== weights
 // Raw A-fragment words of one K-step for one lane (row 16*rb + lane%16, slot q = lane/16).
@@ -157,43 +98,123 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t mf_rsrc(const void *p, uint32_
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, MF_RSRC_W3);
 }
 
-// Per-lane byte offsets of a wave's A fragments within a tile's chunk (row block rb0; row block
-// rb0+r adds 256 bytes), fixed for the kernel.  ld_a adds the K-step's scalar offset.
-struct AOff { uint32_t o8, o4, o2, o1; };
+// Code planes of a format: byte codes (q8g64; qNg64 with n >= 8), nibbles (int4; qNg64 bit 2 of
+// n), crumbs and single bits (qNg64).
+template <int FMT, int NB> struct Planes {
+    static constexpr int P8 = FMT == BGL_Q8G64 ? 1 : FMT == BGL_QNG64 ? (NB >> 3) & 1 : 0;
+    static constexpr int P4 = FMT == BGL_Q4G64 || FMT == BGL_Q4G32H ? 1 : FMT == BGL_QNG64 ? (NB >> 2) & 1 : 0;
+    static constexpr int P2 = FMT == BGL_QNG64 ? (NB >> 1) & 1 : 0;
+    static constexpr int P1 = FMT == BGL_QNG64 ? NB & 1 : 0;
+    static constexpr int WORDS = 8 * P8 + 4 * P4 + 4 * P2 + 4 * P1;   // per lane and K-step pair
+};
+
+// Raw words of one K-step pair (s, s+1) for a wave's two 16-row blocks, as loaded.
+//  - byte codes and nibbles are read a whole 16-byte chunk row per lane (one buffer_load_dwordx4
+//    covers 32 rows of two chunks: lanes 32..63 take the second), so each quarter-wave reads 256
+//    contiguous bytes; the MFMA operand layout (4 lanes per row) is rebuilt with lane swaps;
+//  - crumbs and bits (2/n and 1/n of a qNg64 tensor's bytes) are read as the operand's own dword.
+template <int FMT, int NB> struct PRaw {
+    using P = Planes<FMT, NB>;
+    uint32_t w8[P::P8 ? 8 : 1];      // byte codes: K-step j of the pair in words 4j..4j+3
+    uint32_t w4[P::P4 ? 4 : 1];      // nibbles: lanes < 32 K-step s, lanes >= 32 K-step s+1
+    uint32_t w2[P::P2 ? 4 : 1];      // crumb operand word of [j][rb]
+    uint32_t w1[P::P1 ? 4 : 1];      // bit operand word of [j][rb]
+};
+
+// Per-lane byte offsets within a tile's chunk, fixed for the kernel: the chunk-row reads (rows
+// 16*rb0 + lane%32 of chunk lane/32) and the operand-dword reads of row block rb0 (rb0+1 adds
+// 256 bytes).
+struct AOff { uint32_t op, o2, o1; };
 
 __device__ __forceinline__ AOff a_offsets(int rb0, int lane) {
-    const uint32_t row = 16 * rb0 + (lane & 15), q = lane >> 4;
     AOff o;
-    o.o8 = (q >> 1) * 1024 + row * 16 + 8 * (q & 1);     // byte codes: chunk 2j + q/2, bytes 8(q%2)..+7
-    o.o4 = row * 16 + 4 * q;                             // nibble chunk: dword q
+    o.op = (uint32_t)(lane >> 5) * 1024u + (uint32_t)(16 * rb0 + (lane & 31)) * 16u;
+    const uint32_t row = 16 * rb0 + (lane & 15), q = lane >> 4;
     o.o2 = row * 16 + 4 * (q >> 1);                      // crumb chunk: dword 2(j%2) + q/2
     o.o1 = row * 16;                                     // bit chunk: dword j
     return o;
 }
 
-// A words of K-step sc (already clamped into the tensor) for row block r of the wave; tchunk is
-// the first chunk of the wave's tile.
+// Loads K-steps s, s+1 (s even, already clamped into the tensor) of the wave's rows; tchunk is the
+// first chunk of the wave's tile.
 template <int FMT, int NB>
-__device__ __forceinline__ void ld_a(ARaw<FMT, NB> &a, __amdgpu_buffer_rsrc_t rs, const AOff &o, uint32_t tchunk,
-                                     int sc, int r) {
-    const uint32_t rofs = 256u * r;
-    if constexpr (FMT == BGL_Q8G64) {                    // 4 chunks per 64-element unit: K-step s is chunks 2s, 2s+1
-        const mf_u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, o.o8 + rofs, (tchunk + 2u * sc) * 1024u, 0);
-        a.w[0] = v[0]; a.w[1] = v[1];
-    } else if constexpr (FMT == BGL_QNG64) {
-        constexpr int H8 = ARaw<FMT, NB>::H8, H4 = ARaw<FMT, NB>::H4, H2 = ARaw<FMT, NB>::H2, H1 = ARaw<FMT, NB>::H1;
-        constexpr int K4 = 8 * H8, K2 = K4 + 4 * H4, K1 = K2 + 2 * H2;
-        const uint32_t u = (uint32_t)sc >> 2, j = (uint32_t)sc & 3, c0 = tchunk + u * NB;
-        int i = 0;
-        if constexpr (H8) {
-            const mf_u2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, o.o8 + rofs, (c0 + 2 * j) * 1024u, 0);
-            a.w[i++] = v[0]; a.w[i++] = v[1];
+__device__ __forceinline__ void ld_pair(PRaw<FMT, NB> &p, __amdgpu_buffer_rsrc_t rs, const AOff &o, uint32_t tchunk, int s) {
+    using P = Planes<FMT, NB>;
+    if constexpr (FMT == BGL_Q8G64) {                    // K-step s is chunks 2s, 2s+1
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const mf_u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, o.op, (tchunk + 2u * (s + j)) * 1024u, 0);
+            p.w8[4 * j] = v[0]; p.w8[4 * j + 1] = v[1]; p.w8[4 * j + 2] = v[2]; p.w8[4 * j + 3] = v[3];
         }
-        if constexpr (H4) a.w[i++] = __builtin_amdgcn_raw_buffer_load_b32(rs, o.o4 + rofs, (c0 + K4 + j) * 1024u, 0);
-        if constexpr (H2) a.w[i++] = __builtin_amdgcn_raw_buffer_load_b32(rs, o.o2 + rofs, (c0 + K2 + (j >> 1)) * 1024u + 8 * (j & 1), 0);
-        if constexpr (H1) a.w[i++] = __builtin_amdgcn_raw_buffer_load_b32(rs, o.o1 + rofs, (c0 + K1) * 1024u + 4 * j, 0);
-    } else {                                             // int4: 2 chunks per unit, K-step s is chunk s
-        a.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, o.o4 + rofs, (tchunk + (uint32_t)sc) * 1024u, 0);
+    } else if constexpr (FMT == BGL_QNG64) {
+        constexpr int K4 = 8 * P::P8, K2 = K4 + 4 * P::P4, K1 = K2 + 2 * P::P2;
+        const uint32_t u = (uint32_t)s >> 2, j0 = (uint32_t)s & 3, c0 = tchunk + u * NB;
+        if constexpr (P::P8) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const mf_u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, o.op, (c0 + 2 * (j0 + j)) * 1024u, 0);
+                p.w8[4 * j] = v[0]; p.w8[4 * j + 1] = v[1]; p.w8[4 * j + 2] = v[2]; p.w8[4 * j + 3] = v[3];
+            }
+        }
+        if constexpr (P::P4) {
+            const mf_u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, o.op, (c0 + K4 + j0) * 1024u, 0);
+            p.w4[0] = v[0]; p.w4[1] = v[1]; p.w4[2] = v[2]; p.w4[3] = v[3];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const uint32_t jj = j0 + j;
+                if constexpr (P::P2)
+                    p.w2[2 * j + r] = __builtin_amdgcn_raw_buffer_load_b32(rs, o.o2 + 256u * r, (c0 + K2 + (jj >> 1)) * 1024u + 8 * (jj & 1), 0);
+                if constexpr (P::P1)
+                    p.w1[2 * j + r] = __builtin_amdgcn_raw_buffer_load_b32(rs, o.o1 + 256u * r, (c0 + K1) * 1024u + 4 * jj, 0);
+            }
+    } else {                                             // int4: K-step s is chunk s
+        const mf_u4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, o.op, (tchunk + (uint32_t)s) * 1024u, 0);
+        p.w4[0] = v[0]; p.w4[1] = v[1]; p.w4[2] = v[2]; p.w4[3] = v[3];
+    }
+}
+
+// Operand words of both K-steps and row blocks from a loaded pair.  Nibble chunks: a 4x4 transpose
+// of (quarter-wave, word) -- quarter-wave 2j+rb holds rows 16rb..+15 of K-step j -- puts word q of
+// row 16rb + r into lane (r, q), register 2j+rb.  Byte chunks: quarter-wave 2c+rb holds chunk c of
+// rows 16rb..+15; swapping odd with even quarter-waves puts bytes 8q..8q+7 of the row (chunk q/2,
+// words 2(q%2), +1) into lane (r, q), registers (2rb, 2rb+1).
+template <int FMT, int NB>
+__device__ __forceinline__ void exch(const PRaw<FMT, NB> &p, ARaw<FMT, NB> (&a)[2][MF_RBW]) {
+    using P = Planes<FMT, NB>;
+    int i = 0;
+    if constexpr (P::P8) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const auto e = __builtin_amdgcn_permlane16_swap(p.w8[4 * j], p.w8[4 * j + 2], false, false);
+            const auto f = __builtin_amdgcn_permlane16_swap(p.w8[4 * j + 1], p.w8[4 * j + 3], false, false);
+            a[j][0].w[i] = e[0]; a[j][0].w[i + 1] = f[0];
+            a[j][1].w[i] = e[1]; a[j][1].w[i + 1] = f[1];
+        }
+        i += 2;
+    }
+    if constexpr (P::P4) {
+        const auto x = __builtin_amdgcn_permlane32_swap(p.w4[0], p.w4[2], false, false);
+        const auto y = __builtin_amdgcn_permlane32_swap(p.w4[1], p.w4[3], false, false);
+        const auto c = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
+        const auto d = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
+        a[0][0].w[i] = c[0]; a[0][1].w[i] = c[1]; a[1][0].w[i] = d[0]; a[1][1].w[i] = d[1];
+        i += 1;
+    }
+    if constexpr (P::P2) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 2; r++) a[j][r].w[i] = p.w2[2 * j + r];
+        i += 1;
+    }
+    if constexpr (P::P1) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 2; r++) a[j][r].w[i] = p.w1[2 * j + r];
     }
 }
 
@@ -275,222 +296,299 @@ __device__ __forceinline__ int mf_task(const MfmaLaunch &L) {
 template <int FMT, int NB> constexpr int a_words() {
     return FMT == BGL_Q8G64 ? 2 : FMT == BGL_QNG64 ? 2 * ((NB >> 3) & 1) + ((NB >> 2) & 1) + ((NB >> 1) & 1) + (NB & 1) : 1;
 }
+// K-steps of weights a wave keeps in flight: a ring of depth/2 K-step pairs, Planes::WORDS
+// registers each.
+template <int FMT, int NB> constexpr int ring_depth() { return Planes<FMT, NB>::WORDS <= 4 ? 16 : Planes<FMT, NB>::WORDS <= 8 ? 8 : 4; }
+// LDS bytes per staged K-step: activation fragments (CT x hi/lo x 1 KB) + the 4 tiles' scale
+// words in the device layout (512 B for every format).
+constexpr int mf_step_lds(int CT) { return CT * 2048 + 512; }
+// K-steps one workgroup stages (its split's whole K range): as many as fit 144 KB, a multiple of
+// 16 (every ring depth divides it).
+constexpr int mf_kps_max(int CT) { return (147456 / mf_step_lds(CT)) / 16 * 16; }
 
-template <int FMT, int NB, int CT>
-__global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
-    constexpr int NT = MF_WAVES * 64;
-    constexpr int KC = MF_KC;                                      // K-steps per staged block
+template <int FMT, int NB, int CT, int KW>
+__global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) {
+    constexpr int NT = MF_WAVES * KW * 64;
+    constexpr int KPM = mf_kps_max(CT);                             // staged K-steps (max)
     constexpr int SPU = ksteps_per_unit<FMT>();
-    constexpr int UPB = KC / SPU;                                  // units per block
     constexpr int GPU = groups_per_unit<FMT>();
     constexpr int SCW = scale_bytes<FMT>();
     constexpr int SPG = SPU / GPU;                                 // K-steps per scale group
-    constexpr int BF = KC * CT * 2 * 64;                           // activation uint4 per block
-    constexpr int SUT = UPB * 64 * SCW / 16;                       // scale uint4 per tile and block (global layout)
-    constexpr int SF = MF_TILES * SUT;
-    constexpr int SFL = MF_TILES * UPB * GPU * 64 / 4;             // ... in LDS: fp32 [tile][unit][group][row]
-    constexpr int PER_B = BF / NT, PER_S = (SF + NT - 1) / NT;
-    static_assert(BF % NT == 0, "staged block must split evenly over the threads");
-    __shared__ uint4 stage[2][BF + SFL];
+    constexpr int BST = CT * 2 * 64;                               // activation uint4 per K-step
+    constexpr int UMAX = KPM / SPU;                                // staged units (max)
+    constexpr int SUT = 64 * SCW / 16;                             // scale uint4 per tile and unit
+    // ring depth: halved with two slices (each wave runs half the split, and 16 waves share the
+    // registers); at least 4 so that a unit's groups keep their parity pattern
+    constexpr int D = KW == 1 || ring_depth<FMT, NB>() == 4 ? ring_depth<FMT, NB>() : ring_depth<FMT, NB>() / 2;
+    static_assert(KPM % D == 0 && KPM % SPU == 0 && D % SPU == 0, "staged range must hold whole rings and units");
+    static_assert(KW == 1 || KW * MF_WAVES * 64 * CT * MF_RBW * 4 * 4 <= KPM * BST * 16, "slice exchange must fit the stage");
+    __shared__ uint4 xs[KPM * BST];                                // [step][CT][hi/lo][64 lanes]
+    __shared__ uint4 ss[MF_TILES * UMAX * SUT];                    // [tile][unit][64 rows] scale words
 
     const int ti = mf_task(L);
     const MfmaTask &tk = L.t[ti];
     const BglDevTensor &T = tk.T;
     // the wave index is uniform: in a scalar register, every offset derived from it is scalar too
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, q = lane >> 4;
-    const int wt = wave / (4 / MF_RBW), rbase = (wave % (4 / MF_RBW)) * MF_RBW;   // tile in the group, first row block
+    const int kw = wave / MF_WAVES, w8 = wave % MF_WAVES;          // K-slice, wave within the slice
+    const int wt = w8 / (4 / MF_RBW), rbase = (w8 % (4 / MF_RBW)) * MF_RBW;   // tile in the group, first row block
     const int local = (int)blockIdx.x - tk.wg0;
     const int split = local / tk.wgr, tg = local % tk.wgr;
     const int tile0 = tg * MF_TILES, tile = tile0 + wt;
     const int KS = T.K >> 5;
-    const int s0 = split * tk.kps, s1 = min(s0 + tk.kps, KS);
-    const int nblocks = (s1 - s0 + KC - 1) / KC;
-    const int u0 = s0 / SPU;
+    const int s0 = split * tk.kps, ns = min(tk.kps, KS - s0);      // this split: K-steps [s0, s0 + ns)
+    const int nrings = (ns + D - 1) / D;                           // whole rings (steps past ns are zeros)
+    const int nsr = nrings * D;
+    const int u0 = s0 / SPU, nu = nsr / SPU;
+    // slice kw runs rings [r0, r1) of the split
+    const int rsplit = (nrings + KW - 1) / KW;
+    const int ls0 = min(kw * rsplit, nrings) * D, ls1 = min((kw + 1) * rsplit, nrings) * D;
 
     const __amdgpu_buffer_rsrc_t rw = mf_rsrc(T.w, (uint32_t)T.ntiles * T.cpr * 1024u);
-    const __amdgpu_buffer_rsrc_t rx = mf_rsrc(L.xf, (uint32_t)L.xf_steps * CT * 2048u);
+    const __amdgpu_buffer_rsrc_t rx = mf_rsrc(L.x, (uint32_t)L.M * (uint32_t)T.K * 4u);
     const __amdgpu_buffer_rsrc_t rsc = mf_rsrc(T.s0, (uint32_t)T.ntiles * T.nunits * 64 * SCW);
 
-    mf_f4 acc[MF_RBW][CT], cg[MF_RBW][CT];
+    // ---- activations of the split: each wave loads 8-element slots of its columns ----
+    // Column m belongs to wave m % NW; lane l takes slots l, l+64, ... (slot g = K elements
+    // 8g..8g+7 of the split).  Loads are unconditional (clamped) and issued before the weights, so
+    // the conversion below waits for them alone.
+    constexpr int NW = MF_WAVES * KW;                              // waves
+    constexpr int CPW = (16 * CT + NW - 1) / NW;                   // columns per wave
+    constexpr int SPL = KPM / 16;                                  // slots per lane (4 per K-step)
+    float4 xv[CPW][SPL][2];
 #pragma unroll
-    for (int r = 0; r < MF_RBW; r++)
+    for (int ci = 0; ci < CPW; ci++)
 #pragma unroll
-        for (int c = 0; c < CT; c++) { acc[r][c] = mf_f4{0, 0, 0, 0}; cg[r][c] = mf_f4{0, 0, 0, 0}; }
+        for (int j = 0; j < SPL; j++) {
+            const int m = ci * NW + wave, g = lane + 64 * j;
+            const bool ok = m < L.M && g < 4 * ns;
+            const uint32_t off = ((uint32_t)(ok ? m : 0) * (uint32_t)T.K + (uint32_t)s0 * 32u + 8u * (uint32_t)(ok ? g : 0)) * 4u;
+            const mf_u4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+            const mf_u4 b = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16u, 0, 0);
+            xv[ci][j][0] = make_float4(__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3]));
+            xv[ci][j][1] = make_float4(__uint_as_float(b[0]), __uint_as_float(b[1]), __uint_as_float(b[2]), __uint_as_float(b[3]));
+        }
 
-    // ---- staged data of block b (activation fragments + the 4 tiles' scales) ----
-    // Blocks past the split reread its last block (the prefetch runs two ahead); their buffers are
-    // never read.  Fragment K-steps past K are zeros in xf.
-    struct SR { uint4 b[PER_B], s[PER_S]; };
-    const uint32_t xo = threadIdx.x * 16u;
-    // scale uint4 e = threadIdx.x + i*NT: tile st = e / SUT (clamped into the tensor), offset rem
-    uint32_t so[PER_S];
-    int sub[PER_S];
-#pragma unroll
-    for (int i = 0; i < PER_S; i++) {
-        const int e = threadIdx.x + i * NT, ec = e < SF ? e : SF - 1;
-        const int st = ec / SUT, rem = ec % SUT;
-        const int tc = min(tile0 + st, T.ntiles - 1);
-        sub[i] = rem / (64 * SCW / 16);                              // unit within the block
-        so[i] = ((uint32_t)tc * T.nunits) * (64 * SCW) + (uint32_t)(rem % (64 * SCW / 16)) * 16u;
+    // ---- the 4 tiles' scales of the split: LDS (scale units past it are zeroed) ----
+    {
+        const int nsu = nu * SUT;                                  // scale uint4 per tile in this split
+        for (int e = threadIdx.x; e < MF_TILES * nsu; e += NT) {
+            const int st = e / nsu, rem = e % nsu, uu = rem / SUT;
+            const int tc = min(tile0 + st, T.ntiles - 1), uc = min(u0 + uu, T.nunits - 1);
+            const mf_u4 g = __builtin_amdgcn_raw_buffer_load_b128(
+                rsc, ((uint32_t)tc * T.nunits + uc) * (64 * SCW) + (uint32_t)(rem % SUT) * 16u, 0, 0);
+            ss[(st * UMAX + uu) * SUT + rem % SUT] = uu * SPU < ns ? make_uint4(g[0], g[1], g[2], g[3]) : make_uint4(0, 0, 0, 0);
+        }
     }
-    auto load_stage = [&](SR &R, int b) {
-        const int bc = min(b, nblocks - 1);
-        const uint32_t xs = (uint32_t)(s0 + bc * KC) * CT * 2048u;
-#pragma unroll
-        for (int i = 0; i < PER_B; i++) {
-            const mf_u4 g = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + i * NT * 16u, xs, 0);
-            R.b[i] = make_uint4(g[0], g[1], g[2], g[3]);
-        }
-#pragma unroll
-        for (int i = 0; i < PER_S; i++) {
-            const int uc = min(u0 + bc * UPB + sub[i], T.nunits - 1);
-            const mf_u4 g = __builtin_amdgcn_raw_buffer_load_b128(rsc, so[i] + (uint32_t)uc * (64 * SCW), 0, 0);
-            R.s[i] = make_uint4(g[0], g[1], g[2], g[3]);
-        }
-    };
-    // Scales go to LDS as fp32 [tile][unit][group][64 rows], so a lane's 4 rows of one group are
-    // one 16-byte read.
-    auto store_stage = [&](int buf, const SR &R) {
-#pragma unroll
-        for (int i = 0; i < PER_B; i++) stage[buf][threadIdx.x + i * NT] = R.b[i];
-        float *sl = reinterpret_cast<float *>(&stage[buf][BF]);
-#pragma unroll
-        for (int i = 0; i < PER_S; i++) {
-            const int e = threadIdx.x + i * NT;
-            if (e < SF) {
-                const int tu = e / (64 * SCW / 16), rr = e % (64 * SCW / 16);   // (tile, unit) pair, uint4 within its rows
-                float *d = sl + tu * GPU * 64;
-                if constexpr (FMT == BGL_Q4G32H) {              // 4 rows x (fp16 group 0, fp16 group 1)
-                    const uint32_t w[4] = {R.s[i].x, R.s[i].y, R.s[i].z, R.s[i].w};
-                    float4 g0, g1;
-                    g0.x = __half2float(__ushort_as_half((unsigned short)(w[0] & 0xffffu)));
-                    g0.y = __half2float(__ushort_as_half((unsigned short)(w[1] & 0xffffu)));
-                    g0.z = __half2float(__ushort_as_half((unsigned short)(w[2] & 0xffffu)));
-                    g0.w = __half2float(__ushort_as_half((unsigned short)(w[3] & 0xffffu)));
-                    g1.x = __half2float(__ushort_as_half((unsigned short)(w[0] >> 16)));
-                    g1.y = __half2float(__ushort_as_half((unsigned short)(w[1] >> 16)));
-                    g1.z = __half2float(__ushort_as_half((unsigned short)(w[2] >> 16)));
-                    g1.w = __half2float(__ushort_as_half((unsigned short)(w[3] >> 16)));
-                    *reinterpret_cast<float4 *>(d + 4 * rr) = g0;
-                    *reinterpret_cast<float4 *>(d + 64 + 4 * rr) = g1;
-                } else if constexpr (FMT == BGL_QNG64) {        // 2 rows x (group 0, group 1)
-                    *reinterpret_cast<float2 *>(d + 2 * rr) = make_float2(__uint_as_float(R.s[i].x), __uint_as_float(R.s[i].z));
-                    *reinterpret_cast<float2 *>(d + 64 + 2 * rr) = make_float2(__uint_as_float(R.s[i].y), __uint_as_float(R.s[i].w));
-                } else {
-                    reinterpret_cast<uint4 *>(d)[rr] = R.s[i];
-                }
-            }
-        }
-    };
 
-    // ---- weights of block b for this wave: the register ring ----
-    struct WR { ARaw<FMT, NB> a[KC][MF_RBW]; };
+    // ---- the weight ring: local K-step s lives in slot (s - ls0) % D until it is computed ----
     const int tile_c = min(tile, T.ntiles - 1);                    // waves past the tensor read a real tile
     const uint32_t tchunk = (uint32_t)tile_c * T.cpr;
     const AOff ao = a_offsets(rbase, lane);
-    auto load_w = [&](WR &W, int b) {
-        const int bc = min(b, nblocks - 1);
-#pragma unroll
-        for (int j = 0; j < KC; j++) {
-            const int sc = min(s0 + bc * KC + j, KS - 1);
-#pragma unroll
-            for (int r = 0; r < MF_RBW; r++) ld_a<FMT, NB>(W.a[j][r], rw, ao, tchunk, sc, r);
-        }
+    PRaw<FMT, NB> ring[D / 2];
+    auto load_w = [&](PRaw<FMT, NB> &slot, int s) {             // local K-steps s, s+1 (s even)
+        const int sc = min(s0 + s, KS - 2);                        // past the split: reread, multiplied by zeros
+        ld_pair<FMT, NB>(slot, rw, ao, tchunk, sc);
     };
+#pragma unroll
+    for (int d = 0; d < D / 2; d++) load_w(ring[d], ls0 + 2 * d);
 
-    auto compute = [&](const WR &W, int b) {
-        const uint4 *stg = stage[b & 1];
-        const float *scl = reinterpret_cast<const float *>(stg + BF);
+    // ---- activation fragments: each column is scaled by a power of two so its largest magnitude
+    // over the split lies in [2^13, 2^14), then split into hi = fp16(x'), lo = fp16(x' - hi) in the
+    // MFMA operand order; the split's column factor 2^(e-14) is applied to its partial sums ----
+    __shared__ float cinv[16 * MF_MAXCT];
 #pragma unroll
-        for (int j = 0; j < KC; j++) {
-            mf_h8 A[MF_RBW];
+    for (int ci = 0; ci < CPW; ci++) {
+        const int m = ci * NW + wave;
+        if (m >= 16 * CT) break;                                   // uniform
+        float mx = 0.0f;
 #pragma unroll
-            for (int r = 0; r < MF_RBW; r++) A[r] = dec_a<FMT, NB>(W.a[j][r], q);
-            const bool gstart = j % SPG == 0;                       // first K-step of a scale group
+        for (int j = 0; j < SPL; j++)
 #pragma unroll
-            for (int c = 0; c < CT; c++) {
-                const mf_h8 Bh = __builtin_bit_cast(mf_h8, stg[((j * CT + c) * 2 + 0) * 64 + lane]);
-                const mf_h8 Bl = __builtin_bit_cast(mf_h8, stg[((j * CT + c) * 2 + 1) * 64 + lane]);
-#pragma unroll
-                for (int r = 0; r < MF_RBW; r++) {
-                    cg[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], Bh, gstart ? mf_f4{0, 0, 0, 0} : cg[r][c], 0, 0, 0);
-                    cg[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], Bl, cg[r][c], 0, 0, 0);
-                }
+            for (int h = 0; h < 2; h++) {
+                const float4 v = xv[ci][j][h];
+                const float t = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+                mx = m < L.M && lane + 64 * j < 4 * ns ? fmaxf(mx, t) : mx;
             }
-            if ((j + 1) % SPG == 0) {                                // group complete: fold with its scales
-                const int ub = j / SPU, g = (j % SPU) / SPG;
+        mx = wave_max_f32(mx);
+        int e = 0;
+        if (mx > 0.0f) frexpf(mx, &e);                             // mx in [2^(e-1), 2^e)
+        const float sc = mx > 0.0f ? ldexpf(1.0f, 14 - e) : 1.0f;
+        if (lane == 0) cinv[m] = mx > 0.0f ? ldexpf(1.0f, e - 14) : 1.0f;
+        const int ct = m >> 4, ml = m & 15;
 #pragma unroll
-                for (int rb = 0; rb < MF_RBW; rb++) {
-                    const mf_f4 sc = *reinterpret_cast<const mf_f4 *>(scl + ((wt * UPB + ub) * GPU + g) * 64 +
-                                                                     16 * (rbase + rb) + 4 * q);
+        for (int j = 0; j < SPL; j++) {
+            const int g = lane + 64 * j;
+            if (g >= 4 * nsr) break;
+            const bool ok = m < L.M && g < 4 * ns;
+            const float4 a = xv[ci][j][0], b = xv[ci][j][1];
+            const float v8[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};   // element order {0,2,1,3,4,6,5,7}
+            _Float16 hi[8], lo[8];
 #pragma unroll
-                    for (int c = 0; c < CT; c++) {
-#pragma unroll
-                        for (int v = 0; v < 4; v++) acc[rb][c][v] = __fmaf_rn(cg[rb][c][v], sc[v], acc[rb][c][v]);
-                    }
-                }
+            for (int p = 0; p < 8; p++) {
+                const float v = ok ? v8[p] * sc : 0.0f;            // power-of-two scaling: exact
+                const _Float16 hh = (_Float16)v;
+                hi[p] = hh;
+                lo[p] = (_Float16)(v - (float)hh);
             }
-        }
-    };
-
-    // Pipeline: block b is computed while block b+2's weights and staged data are loading and
-    // block b+1's staged data goes to LDS, so both streams have a block of compute between issue
-    // and use.  Weights use a ring of three register sets (block b in w[b%3]); staged data uses
-    // two (the set of block b is free once b is in LDS).  Every load is issued on every path, so
-    // each wait covers only its own block.
-    // With 48-64 columns, or three or more A words per K-step, two weight sets are all that fit
-    // beside the accumulators: the weights then load one block ahead.
-    constexpr int WD = CT <= 2 && a_words<FMT, NB>() <= 2 ? 2 : 1;   // weight prefetch distance in blocks
-    WR w0, w1, w2;
-    SR r0, r1;
-    load_stage(r0, 0);
-    load_w(w0, 0);
-    load_stage(r1, 1);
-    if constexpr (WD == 2) load_w(w1, 1);
-    store_stage(0, r0);
-    __syncthreads();
-    auto iter = [&](WR &wc, WR &wl, SR &rs, SR &rl, int b) {
-        load_stage(rl, b + 2);
-        load_w(wl, b + WD);
-        compute(wc, b);
-        store_stage((b + 1) & 1, rs);                // past the end it fills a buffer nobody reads again
-        __syncthreads();
-        return b + 1 < nblocks;
-    };
-    if constexpr (WD == 2) {
-        for (int b = 0; b < nblocks; b += 6) {
-            if (!iter(w0, w2, r1, r0, b)) break;
-            if (!iter(w1, w0, r0, r1, b + 1)) break;
-            if (!iter(w2, w1, r1, r0, b + 2)) break;
-            if (!iter(w0, w2, r0, r1, b + 3)) break;
-            if (!iter(w1, w0, r1, r0, b + 4)) break;
-            if (!iter(w2, w1, r0, r1, b + 5)) break;
-        }
-    } else {
-        for (int b = 0; b < nblocks; b += 2) {
-            if (!iter(w0, w1, r1, r0, b)) break;
-            if (!iter(w1, w0, r0, r1, b + 1)) break;
+            uint4 H, Lo;
+            memcpy(&H, hi, 16);
+            memcpy(&Lo, lo, 16);
+            uint4 *d = xs + ((g >> 2) * CT + ct) * 128 + ml + 16 * (g & 3);
+            d[0] = H;
+            d[64] = Lo;
         }
     }
+    __syncthreads();
 
-    if (tile >= T.ntiles) return;
-    const int S = (KS + tk.kps - 1) / tk.kps;
+    mf_f4 acc[MF_RBW][CT];
 #pragma unroll
-    for (int rb = 0; rb < MF_RBW; rb++) {
-        const int n0 = tile * BGL_TILE + 16 * (rbase + rb) + 4 * q;
+    for (int r = 0; r < MF_RBW; r++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) acc[r][c] = mf_f4{0, 0, 0, 0};
+
+    // Scale words of this lane's 4 rows (16*(rbase+rb) + 4q .. +3) for staged unit u: one uint4
+    // (4 rows x one fp32, or x an fp16 pair), or for qNg64 the two groups' float2s split into one
+    // mf_f4 per group.
+    struct SW { uint4 w; mf_f4 g0, g1; };
+    auto scale_words = [&](int u, int rb) -> SW {
+        const int row = 16 * (rbase + rb) + 4 * q;
+        const uint4 *base = ss + (wt * UMAX + u) * SUT;
+        SW r;
+        if constexpr (SCW == 8) {
+            const uint4 a = base[row >> 1], b = base[(row >> 1) + 1];
+            r.g0 = mf_f4{__uint_as_float(a.x), __uint_as_float(a.z), __uint_as_float(b.x), __uint_as_float(b.z)};
+            r.g1 = mf_f4{__uint_as_float(a.y), __uint_as_float(a.w), __uint_as_float(b.y), __uint_as_float(b.w)};
+        } else {
+            r.w = base[row >> 2];
+        }
+        return r;
+    };
+    auto scale_of = [&](const SW &r, int g) -> mf_f4 {
+        if constexpr (FMT == BGL_Q4G32H) {                         // fp16 pairs: group g is half g of each word
+            const uint32_t sh = 16 * g;
+            return mf_f4{__half2float(__ushort_as_half((unsigned short)(r.w.x >> sh))),
+                         __half2float(__ushort_as_half((unsigned short)(r.w.y >> sh))),
+                         __half2float(__ushort_as_half((unsigned short)(r.w.z >> sh))),
+                         __half2float(__ushort_as_half((unsigned short)(r.w.w >> sh)))};
+        } else if constexpr (FMT == BGL_QNG64) {
+            return g == 0 ? r.g0 : r.g1;
+        } else {
+            return mf_f4{__uint_as_float(r.w.x), __uint_as_float(r.w.y), __uint_as_float(r.w.z), __uint_as_float(r.w.w)};
+        }
+    };
+    // Activation fragments of local step s (clamped into the staged range).
+    struct BF { mf_h8 h[CT], l[CT]; };
+    auto load_b = [&](int s) -> BF {
+        const uint4 *p = xs + min(s, nsr - 1) * BST + lane;
+        BF r;
 #pragma unroll
         for (int c = 0; c < CT; c++) {
-            const int m = 16 * c + (lane & 15);
-            if (m >= L.M) continue;
-            const float ci = L.colinv[m];
-            float *dst = S > 1 ? tk.part + ((size_t)split * L.M + m) * T.N : tk.y + (size_t)m * tk.ystride;
+            r.h[c] = __builtin_bit_cast(mf_h8, p[c * 128]);
+            r.l[c] = __builtin_bit_cast(mf_h8, p[c * 128 + 64]);
+        }
+        return r;
+    };
+
+    // ---- main loop: no barriers; each wave streams its own weights D K-steps ahead, and the next
+    // step's fragments and the unit's scales are read from LDS a step ahead of their use.  The
+    // fold is software-pipelined: a group's MFMA sums (cg[g % 2]) are folded into acc while the
+    // next group's MFMAs run, so the matrix cores and the vector ALUs work at the same time ----
+    static_assert((D / SPG) % 2 == 0, "group parity must repeat every ring");
+    mf_f4 cg[2][MF_RBW][CT], scp[MF_RBW];
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int n = n0 + v;
-                if (n < T.N) {
-                    float o = acc[rb][c][v] * ci;
-                    if (S == 1 && tk.bias) o += tk.bias[n];
-                    dst[n] = o;
+    for (int r = 0; r < MF_RBW; r++) {
+        scp[r] = mf_f4{0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < CT; c++) { cg[0][r][c] = mf_f4{0, 0, 0, 0}; cg[1][r][c] = mf_f4{0, 0, 0, 0}; }
+    }
+    auto fold = [&](const mf_f4 (&g)[MF_RBW][CT]) {
+#pragma unroll
+        for (int rb = 0; rb < MF_RBW; rb++)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[rb][c][v] = __fmaf_rn(g[rb][c][v], scp[rb][v], acc[rb][c][v]);
+    };
+    BF bnext;
+    if constexpr (KW == 1) bnext = load_b(ls0);
+    for (int sb = ls0; sb < ls1; sb += D) {
+        SW swd[MF_RBW];
+        ARaw<FMT, NB> apair[2][MF_RBW];
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int s = sb + d, par = (d / SPG) & 1;
+            if (d % SPU == 0) {
+#pragma unroll
+                for (int rb = 0; rb < MF_RBW; rb++) swd[rb] = scale_words(s / SPU, rb);
+            }
+            // one slice (2 waves per SIMD) reads the next step's fragments ahead; two slices read
+            // them in place (the other waves cover the LDS latency, and the registers are needed)
+            BF bc;
+            if constexpr (KW == 1) { bc = bnext; bnext = load_b(s + 1); }
+            else bc = load_b(s);
+            if (d % 2 == 0) {                                       // a new K-step pair: exchange, refill the slot
+                exch<FMT, NB>(ring[d / 2], apair);
+                load_w(ring[d / 2], s + D);                         // unconditional, clamped
+            }
+            mf_h8 A[MF_RBW];
+#pragma unroll
+            for (int r = 0; r < MF_RBW; r++) A[r] = dec_a<FMT, NB>(apair[d % 2][r], q);
+            const bool gstart = d % SPG == 0;                       // first K-step of a scale group
+#pragma unroll
+            for (int h = 0; h < 2; h++)                             // all hi products, then the lo ones
+#pragma unroll
+                for (int c = 0; c < CT; c++)
+#pragma unroll
+                    for (int r = 0; r < MF_RBW; r++)
+                        cg[par][r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            A[r], h ? bc.l[c] : bc.h[c], gstart && !h ? mf_f4{0, 0, 0, 0} : cg[par][r][c], 0, 0, 0);
+            if (gstart) fold(cg[par ^ 1]);                          // the previous group, while these run
+            if ((d + 1) % SPG == 0) {                                // group complete: its scales for the next fold
+                const int g = (d % SPU) / SPG;
+#pragma unroll
+                for (int rb = 0; rb < MF_RBW; rb++) scp[rb] = scale_of(swd[rb], g);
+            }
+        }
+    }
+    fold(cg[((D / SPG) - 1) & 1]);                                  // the last group
+
+    // ---- combine the K-slices through LDS: slice k keeps row block k of its wave's pair ----
+    if constexpr (KW == 2) {
+        __syncthreads();                                            // every wave is done with the staged data
+        float *red = reinterpret_cast<float *>(xs);
+        const int give = 1 - kw;
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) red[(((kw * MF_WAVES + w8) * CT + c) * 4 + v) * 64 + lane] = acc[give][c][v];
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < CT; c++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[kw][c][v] += red[((((1 - kw) * MF_WAVES + w8) * CT + c) * 4 + v) * 64 + lane];
+    }
+
+    const int S = (KS + tk.kps - 1) / tk.kps;
+    if (tile < T.ntiles) {
+#pragma unroll
+        for (int rb = 0; rb < MF_RBW; rb++) {
+            if (KW == 2 && rb != kw) continue;
+            const int n0 = tile * BGL_TILE + 16 * (rbase + rb) + 4 * q;
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                const int m = 16 * c + (lane & 15);
+                if (m >= L.M) continue;
+                const float ci = cinv[m];
+                float *dst = S > 1 ? tk.part + ((size_t)split * L.M + m) * T.N : tk.y + (size_t)m * tk.ystride;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int n = n0 + v;
+                    if (n < T.N) {
+                        float o = acc[rb][c][v] * ci;
+                        if (S == 1 && tk.bias) o += tk.bias[n];
+                        dst[n] = o;
+                    }
                 }
             }
         }
@@ -499,7 +597,8 @@ __global__ __launch_bounds__(MF_WAVES * 64) void k_gemm_mfma(MfmaLaunch L) {
 
 // ==================================================================================== K-split reduce
 // y[m][n] = bias[n] + sum_s part[s][m][n], s in order, for every task of a launch with S > 1.  A
-// thread owns 4 consecutive n of one m and loads all S partials before adding them.
+// thread owns 4 consecutive n of one m and keeps MF_RED_BATCH partials in flight.
+#define MF_RED_BATCH 8
 struct MfmaReduceTask {
     const float *part;
     const float *bias;
@@ -523,29 +622,33 @@ __global__ __launch_bounds__(256) void k_mfma_reduce(MfmaReduce R) {
     const int m = lq / nq, n = 4 * (lq % nq);
     const size_t plane = (size_t)R.M * t.N;
     const float *p = t.part + (size_t)m * t.N + n;
-    float v[MF_MAXS][4];
-    if ((t.N & 3) == 0) {
+    const bool vec = (t.N & 3) == 0;
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < t.S; s0 += MF_RED_BATCH) {               // a batch of partials in flight, added in order
+        float v[MF_RED_BATCH][4];
 #pragma unroll
-        for (int s = 0; s < MF_MAXS; s++)
-            if (s < t.S) {
+        for (int i = 0; i < MF_RED_BATCH; i++) {
+            const int s = s0 + i;
+            if (s >= t.S) break;
+            if (vec) {
                 const float4 f = *reinterpret_cast<const float4 *>(p + s * plane);
-                v[s][0] = f.x; v[s][1] = f.y; v[s][2] = f.z; v[s][3] = f.w;
+                v[i][0] = f.x; v[i][1] = f.y; v[i][2] = f.z; v[i][3] = f.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[i][e] = n + e < t.N ? p[s * plane + e] : 0.0f;
             }
-    } else {
+        }
 #pragma unroll
-        for (int s = 0; s < MF_MAXS; s++)
-            if (s < t.S)
+        for (int i = 0; i < MF_RED_BATCH; i++) {
+            if (s0 + i >= t.S) break;
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[s][e] = n + e < t.N ? p[s * plane + e] : 0.0f;
+            for (int e = 0; e < 4; e++) a[e] = s0 + i == 0 ? v[i][e] : a[e] + v[i][e];
+        }
     }
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         if (n + e >= t.N) break;
-        float a = v[0][e];
-#pragma unroll
-        for (int s = 1; s < MF_MAXS; s++)
-            if (s < t.S) a += v[s][e];
-        t.y[(size_t)m * t.ystride + n + e] = (t.bias ? t.bias[n + e] : 0.0f) + a;
+        t.y[(size_t)m * t.ystride + n + e] = (t.bias ? t.bias[n + e] : 0.0f) + a[e];
     }
 }
 
@@ -555,13 +658,28 @@ bool bgl_mfma_ok(int fmt, int bits) {
     return fmt == BGL_QNG64 && bits >= 2 && bits <= MF_MAXN;
 }
 
+// Two K-slices (16 waves, <= 128 VGPRs) where that instance compiles without private memory --
+// which instances fit depends on the register allocator, so it is read from the code object --
+// else one slice (8 waves, <= 256 VGPRs).
+template <int FMT, int NB, int CT>
+static void launch_ct(const MfmaLaunch &L, dim3 grid, hipStream_t st) {
+    static int kw2 = -1;
+    if (kw2 < 0) {
+        hipFuncAttributes a;
+        kw2 = hipFuncGetAttributes(&a, reinterpret_cast<const void *>(&k_gemm_mfma<FMT, NB, CT, 2>)) == hipSuccess &&
+              a.localSizeBytes == 0;
+    }
+    if (kw2) hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, CT, 2>), grid, dim3(MF_WAVES * 2 * 64), 0, st, L);
+    else hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, CT, 1>), grid, dim3(MF_WAVES * 64), 0, st, L);
+}
+
 template <int FMT, int NB>
 static int launch_fmt(const MfmaLaunch &L, int CT, dim3 grid, hipStream_t st) {
     switch (CT) {
-    case 1: hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, 1>), grid, dim3(MF_WAVES * 64), 0, st, L); return 0;
-    case 2: hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, 2>), grid, dim3(MF_WAVES * 64), 0, st, L); return 0;
-    case 3: hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, 3>), grid, dim3(MF_WAVES * 64), 0, st, L); return 0;
-    case 4: hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, 4>), grid, dim3(MF_WAVES * 64), 0, st, L); return 0;
+    case 1: launch_ct<FMT, NB, 1>(L, grid, st); return 0;
+    case 2: launch_ct<FMT, NB, 2>(L, grid, st); return 0;
+    case 3: launch_ct<FMT, NB, 3>(L, grid, st); return 0;
+    case 4: launch_ct<FMT, NB, 4>(L, grid, st); return 0;
     default: return -1;
     }
 }
@@ -612,39 +730,28 @@ int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev,
     for (int m0 = 0; m0 < M; m0 += 16 * MF_MAXCT) {
         const int Mc = M - m0 < 16 * MF_MAXCT ? M - m0 : 16 * MF_MAXCT;
         const int CT = (Mc + 15) / 16;
-        const int KC = MF_KC;
-        const int KSP = (KS + KC - 1) / KC * KC;
-        const size_t fbytes = (size_t)KSP * CT * 2 * 64 * 16;
-        if (dbuf_reserve(c, c->act_w, fbytes, false) || dbuf_reserve(c, c->act_s, (size_t)16 * CT * 4, false)) return BGL_E_NOMEM;
-        int tok = prof_begin(c, 0);
-        hipLaunchKernelGGL(k_act_frag, dim3(16 * CT, (KSP * 4 + MF_PREP_SLOTS - 1) / MF_PREP_SLOTS), dim3(256), 0, c->stream,
-                           x_dev + (size_t)m0 * K, Mc, K, KSP, CT, (uint4 *)c->act_w.p, (float *)c->act_s.p);
-        prof_end(c, tok);
-        HIPCHK(hipGetLastError());
-        c->prep_act = -1;                                 // the activation buffers now hold fragments
-
+        const int kpm = CT == 1 ? mf_kps_max(1) : CT == 2 ? mf_kps_max(2) : CT == 3 ? mf_kps_max(3) : mf_kps_max(4);
         MfmaLaunch L;
         memset(&L, 0, sizeof L);
-        L.ntasks = n; L.M = Mc; L.xf = (const uint4 *)c->act_w.p; L.colinv = (const float *)c->act_s.p; L.xf_steps = KSP;
-        MfmaReduce R;
-        memset(&R, 0, sizeof R);
-        R.M = Mc;
+        L.ntasks = n; L.M = Mc; L.x = x_dev + (size_t)m0 * K;
         int wgs = 0;
         size_t poff[BGL_MAX_TASKS], pfl = 0;              // partial offsets (floats) in the shared buffer
         int S_[BGL_MAX_TASKS];
         for (int i = 0; i < n; i++) {
             const BglDevTensor &T = Ts[i];
             const int wgr = (T.ntiles + MF_TILES - 1) / MF_TILES;
-            int S = (c->min_blocks + wgr - 1) / wgr;     // split K until the grid has ~min_blocks workgroups
-            int maxS = KS / (2 * KC);                     // at least two staged blocks per split
-            if (maxS > MF_MAXS) maxS = MF_MAXS;
-            // the partials (written and read back once each) stay under half the weight bytes
+            // A split's K range must fit the workgroup's LDS (kpm steps); beyond that, split K until
+            // the grid has ~min_blocks workgroups while the partials (written and read back once
+            // each) stay under half the weight bytes.
+            const int smin = (KS + kpm - 1) / kpm;
+            int S = (c->min_blocks + wgr - 1) / wgr;
             const int capS = (int)(0.5 * mf_weight_bytes(T) / (8.0 * Mc * T.N));
-            if (maxS > capS) maxS = capS;
-            if (S > maxS) S = maxS;
+            if (S > capS) S = capS;
+            if (S < smin) S = smin;
             if (S < 1) S = 1;
             int kps = (KS + S - 1) / S;
-            kps = (kps + KC - 1) / KC * KC;               // splits end on block boundaries
+            kps = (kps + MF_KSTEP_PAD - 1) / MF_KSTEP_PAD * MF_KSTEP_PAD;
+            if (kps > kpm) kps = kpm;
             S = (KS + kps - 1) / kps;
             S_[i] = S;
             MfmaTask &t = L.t[i];
@@ -656,6 +763,9 @@ int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev,
             poff[i] = pfl;
             if (S > 1) pfl += (size_t)S * Mc * T.N;
         }
+        MfmaReduce R;
+        memset(&R, 0, sizeof R);
+        R.M = Mc;
         if (pfl) {
             if (dbuf_reserve(c, c->part, pfl * 4, false)) return BGL_E_NOMEM;
             int nq = 0;
@@ -670,13 +780,13 @@ int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev,
             }
             R.nquads = nq;
         }
-        tok = prof_begin(c, 1);
+        int tok = prof_begin(c, 1);
         if (launch_any(L, Ts[0].fmt, Ts[0].bits, CT, dim3(wgs), c->stream)) return bgl_fail(BGL_E_UNSUPPORTED, "MFMA path: format");
         prof_end(c, tok);
         HIPCHK(hipGetLastError());
         if (R.ntasks) {
             tok = prof_begin(c, 2);
-            hipLaunchKernelGGL(k_mfma_reduce, dim3(nblk(R.nquads)), dim3(256), 0, c->stream, R);
+            hipLaunchKernelGGL(k_mfma_reduce, dim3((R.nquads + 255) / 256), dim3(256), 0, c->stream, R);
             prof_end(c, tok);
             HIPCHK(hipGetLastError());
         }
