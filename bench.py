@@ -321,7 +321,8 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 
 def mfma_roofline(ctx, torch, stream, wl, M, reps):
     """k_gemm_mfma's own time: eager steps with an event pair per launch (phase 1 = the GEMM
-    kernel, 0 = activation fragments, 2 = K-split reduce); achieved = step bytes / GEMM time.
+    kernel, which also converts the activations; 2 = K-split reduce); achieved = step bytes / GEMM
+    time.
     Matrix-core rate: the kernel issues 2 (hi, lo) x ceil(M/16)*16 x N_tiles*64 x K x 2 flops per
     call; useful flops are 2*M*N*K."""
     ctx.prof_enable(True)
@@ -333,7 +334,7 @@ def mfma_roofline(ctx, torch, stream, wl, M, reps):
     ph = ctx.prof_read()
     ctx.prof_enable(False)
     g_ms, g_n = ph["gemv"][0] / reps, ph["gemv"][1] // reps
-    p_ms, o_ms = ph["prep"][0] / reps, ph["other"][0] / reps
+    o_ms = ph["other"][0] / reps
     achieved = wl.nbytes() / (g_ms * 1e-3) / 1e9
     useful, issued = 0.0, 0.0
     mp = (M + 15) // 16 * 16
@@ -349,7 +350,7 @@ def mfma_roofline(ctx, torch, stream, wl, M, reps):
             "bytes_per_launch": round(wl.nbytes() / max(g_n, 1)),
             "mfma": {"issued_tflops": round(tflops, 1), "useful_tflops": round(useful / (g_ms * 1e-3) / 1e12, 1),
                      "peak_fp16_tflops": MFMA_F16_PEAK_TFLOPS, "util": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)},
-            "prep_us_per_step": round(p_ms * 1e3, 2), "reduce_us_per_step": round(o_ms * 1e3, 2),
+            "reduce_us_per_step": round(o_ms * 1e3, 2),
             "timing": f"eager, event pair per launch, {reps} steps"}
 
 
