@@ -76,8 +76,8 @@ struct MoeTask {
     const BglDevTensor *tb;      // up table [E] in SwiGLU mode
     BglDevTensor da, db;         // by-value single tensor(s) when ta is null (shared experts)
     int E, tpe;                  // grid = E * tpe workgroups (tpe: 64-row tiles per expert)
-    const int *off;              // [E+1] sorted segment starts; null: one segment [0, ncols)
-    int ncols;
+    const int *off;              // [E+1] sorted segment starts; null: one segment [0, ncols), or with
+    int ncols, seg;              // seg > 0 runs of seg columns (E = ncols / seg rounded up, one tensor)
     const int *cols;             // activation row of sorted position s (null: s)
     const int *ymap;             // output row of sorted position s (null: s)
     GemvAct a;                   // exact-digit activations (k_act_x24 layout)
@@ -156,12 +156,15 @@ __device__ __forceinline__ BglDevTensor ld_tensor(const BglDevTensor *p) {
 
 // WIDE: also the dense fp16 / fp32 cases, whose 64-register units would raise every format's
 // register count (and lower occupancy) if they shared one instantiation.
-template <bool WIDE>
+// SEG: the segments are consecutive runs of Mt.seg columns (the shared experts).  A separate
+// instantiation, so the routed kernel's register allocation (and occupancy) stays its own.
+template <bool WIDE, bool SEG>
 __global__ __launch_bounds__(MOE_MAXW * BGL_TILE) void k_moe_gemv(MoeTask Mt) {
     __shared__ float red[MOE_MAXW][2][MOE_MB][BGL_TILE];
     const int e = blockIdx.x / Mt.tpe, tile = blockIdx.x % Mt.tpe;
     int seg0 = 0, ncols = Mt.ncols;
-    if (Mt.off) { seg0 = uni(Mt.off)[e]; ncols = uni(Mt.off)[e + 1] - seg0; }
+    if constexpr (SEG) { seg0 = e * Mt.seg; ncols = min(Mt.seg, Mt.ncols - seg0); }
+    else if (Mt.off) { seg0 = uni(Mt.off)[e]; ncols = uni(Mt.off)[e + 1] - seg0; }
     if (ncols <= 0) return;                                   // expert not routed to by any pair
     const BglDevTensor Ta = Mt.ta ? ld_tensor(Mt.ta + e) : Mt.da;
     if (tile >= Ta.ntiles) return;
@@ -317,13 +320,27 @@ static bool task_wide(const bgl_tensor *stack, const MoeTask &Mt) {
     return !Mt.ta && (dense_fmt(Mt.da.fmt) || (Mt.swiglu && dense_fmt(Mt.db.fmt)));
 }
 
+// The shared experts' T columns are cut into segments of MOE_SHARED_SEG, one pseudo-expert each
+// (every one reads the same tensor), so the chunks run on separate workgroups instead of one after
+// another on each tile's workgroup; the tiles' rereads come from cache (two small experts).
+// Routed experts keep one workgroup per tile: a second reader of a large expert's tile would go to
+// HBM, while one workgroup walking its segment rereads the tile from L2.
+#define MOE_SHARED_SEG MOE_MB
+
 static int moe_launch(bgl_ctx *c, const MoeTask &Mt, int units, bool wide) {
     int nw = units < c->max_waves ? units : c->max_waves;
     if (nw > MOE_MAXW) nw = MOE_MAXW;
     if (nw < 1) nw = 1;
     int tok = prof_begin(c, 1);
-    if (wide) hipLaunchKernelGGL(k_moe_gemv<true>, dim3(Mt.E * Mt.tpe), dim3(nw * BGL_TILE), 0, c->stream, Mt);
-    else hipLaunchKernelGGL(k_moe_gemv<false>, dim3(Mt.E * Mt.tpe), dim3(nw * BGL_TILE), 0, c->stream, Mt);
+    const bool seg = !Mt.off && Mt.seg > 0;
+    const dim3 g(Mt.E * Mt.tpe), b(nw * BGL_TILE);
+    if (wide) {
+        if (seg) hipLaunchKernelGGL((k_moe_gemv<true, true>), g, b, 0, c->stream, Mt);
+        else hipLaunchKernelGGL((k_moe_gemv<true, false>), g, b, 0, c->stream, Mt);
+    } else {
+        if (seg) hipLaunchKernelGGL((k_moe_gemv<false, true>), g, b, 0, c->stream, Mt);
+        else hipLaunchKernelGGL((k_moe_gemv<false, false>), g, b, 0, c->stream, Mt);
+    }
     prof_end(c, tok);
     HIPCHK(hipGetLastError());
     return 0;
@@ -414,7 +431,8 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
     if ((rc = moe_launch(c, Mr, units, task_wide(gate, Mr)))) return rc;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
-        Ms.a = Mr.a; Ms.da = sg->T; Ms.db = su->T; Ms.E = 1; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
+        Ms.a = Mr.a; Ms.da = sg->T; Ms.db = su->T; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
+        Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
         Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
         if ((rc = moe_launch(c, Ms, sg->T.nunits, task_wide(nullptr, Ms)))) return rc;
     }
@@ -426,7 +444,8 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         if ((rc = moe_prep(c, 0, shh, T, Ish, Ms.a))) return rc;
-        Ms.da = sd->T; Ms.E = 1; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
+        Ms.da = sd->T; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
+        Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
         if ((rc = moe_launch(c, Ms, sd->T.nunits, task_wide(nullptr, Ms)))) return rc;
     }
     int tok = prof_begin(c, 2);
