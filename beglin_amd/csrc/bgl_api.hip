@@ -605,45 +605,55 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
     return 0;
 }
 
-#define BGL_GEMV_Q_LDS_MAX (64 * 1024)
+#define BGL_GEMV_Q_LDS_MAX (64 * 1024)          // one column: two workgroups of the largest shapes per CU
+#define BGL_GEMV_Q_LDS_MAX_MB (128 * 1024)      // 4 or 8 columns: the codes of every column sit in LDS
+#define BGL_GEMV_Q_MAXMB 8
 
-// W4A8 with one activation column: quantization fused into the GEMV workgroups (one launch).
-static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, const float *const *bias,
+static int q_mb(int mc) { return mc <= 1 ? 1 : mc <= 4 ? 4 : 8; }
+static size_t q_lds_max(int MB) { return MB == 1 ? BGL_GEMV_Q_LDS_MAX : BGL_GEMV_Q_LDS_MAX_MB; }
+
+// W4A8 with the quantization fused in, M columns in launches of up to 8 (each launch streams the
+// weights once for its columns; every column's arithmetic is the one-column kernel's).
+static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
                       float *const *y) {
-    GemvLaunch L;
-    memset(&L, 0, sizeof L);
-    int blocks = 0;
-    fill_tasks(L, n, Ts, bias, y, nullptr, blocks);
-    L.x = x_dev;
-    L.m0 = 0;
-    L.mcols = 1;
-    // Rows per workgroup: split 64-row tiles until the launch has >= 512 workgroups (8 rows at the
-    // least), so the weight stream is spread over every CU.  Waves: ceil(passes / 4), at least 3,
-    // since every workgroup quantizes the whole activation row; the waves take the weight units in
-    // turn (the last ones only quantize when there are fewer units than waves).  (Measured on
-    // 1536x1536, 2048x1536, 17920x1536 and 1536x8960 g256sf launches: the best shape found for
-    // each, or within 0.05 us of it.)
-    int TR = 64;
-    while (TR > 8 && (long)blocks * (BGL_TILE / TR) < 512) TR >>= 1;
-    if (c->force_tr) TR = c->force_tr;
-    while (TR > 8 && bgl_gemv_q_lds(Ts[0].fmt, Ts[0].K, TR) > BGL_GEMV_Q_LDS_MAX) TR >>= 1;   // the t[u][row] terms shrink with TR
-    const int KQ = BGL_TILE / TR, NP = (Ts[0].K + 255) / 256;
-    int nw = std::min(16, std::max(3, (NP + 3) / 4));
-    if (nw > c->max_waves) nw = c->max_waves;
-    // every task block of the launch uses the same TR; remap blk0 to workgroup units
-    for (int i = 0; i < n; i++) L.t[i].blk0 *= KQ;
-    int tok = prof_begin(c, 1);
-    int rc = bgl_launch_gemv_q(L, blocks, TR, nw, c->stream);
-    prof_end(c, tok);
-    if (rc) return bgl_fail(BGL_E_UNSUPPORTED, "fused W4A8 path: kind %d", Ts[0].fmt);
-    HIPCHK(hipGetLastError());
+    for (int m0 = 0; m0 < M; m0 += BGL_GEMV_Q_MAXMB) {
+        const int mc = std::min(BGL_GEMV_Q_MAXMB, M - m0), MB = q_mb(mc);
+        GemvLaunch L;
+        memset(&L, 0, sizeof L);
+        int blocks = 0;
+        fill_tasks(L, n, Ts, bias, y, nullptr, blocks);
+        L.x = x_dev;
+        L.m0 = m0;
+        L.mcols = mc;
+        // Rows per workgroup: split 64-row tiles until the launch has >= 512 workgroups (8 rows at
+        // the least), so the weight stream is spread over every CU.  Waves: ceil(passes / 4), at
+        // least 3, since every workgroup quantizes the whole activation; the waves take the weight
+        // units in turn (the last ones only quantize when there are fewer units than waves).
+        // (Measured on 1536x1536, 2048x1536, 17920x1536 and 1536x8960 g256sf launches at one column:
+        // the best shape found for each, or within 0.05 us of it.)
+        int TR = 64;
+        while (TR > 8 && (long)blocks * (BGL_TILE / TR) < 512) TR >>= 1;
+        if (c->force_tr) TR = c->force_tr;
+        while (TR > 8 && bgl_gemv_q_lds(Ts[0].fmt, Ts[0].K, TR, MB) > q_lds_max(MB)) TR >>= 1;   // the t[u][row] terms shrink with TR
+        const int KQ = BGL_TILE / TR, NP = (Ts[0].K + 255) / 256;
+        int nw = std::min(16, std::max(3, (MB * NP + 3) / 4));
+        if (nw > c->max_waves) nw = c->max_waves;
+        // every task block of the launch uses the same TR; remap blk0 to workgroup units
+        for (int i = 0; i < n; i++) L.t[i].blk0 *= KQ;
+        int tok = prof_begin(c, 1);
+        int rc = bgl_launch_gemv_q(L, blocks, TR, nw, MB, c->stream);
+        prof_end(c, tok);
+        if (rc) return bgl_fail(BGL_E_UNSUPPORTED, "fused W4A8 path: kind %d", Ts[0].fmt);
+        HIPCHK(hipGetLastError());
+    }
     return 0;
 }
 
 static bool fused_q_ok(bgl_ctx *c, int kind, int K, int M) {
-    if (M != 1 || c->no_fused) return false;
+    if (c->no_fused) return false;
     if (kind != BGL_Q4G256SF && kind != BGL_Q4G64 && kind != BGL_Q8G64) return false;
-    return bgl_gemv_q_lds(kind, K, 8) <= BGL_GEMV_Q_LDS_MAX;
+    const int MB = q_mb(std::min(M, BGL_GEMV_Q_MAXMB));
+    return bgl_gemv_q_lds(kind, K, 8, MB) <= q_lds_max(MB);
 }
 
 
@@ -666,7 +676,7 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
     if ((kind == BGL_Q4G32H || kind == BGL_QNG64) && act != BGL_ACT_F32)
         return bgl_fail(BGL_E_UNSUPPORTED, "kind %d has fp32-activation kernels only", kind);
     HIPCHK(hipSetDevice(c->device));
-    if (act == BGL_ACT_W4A8 && fused_q_ok(c, kind, Ts[0].K, M)) return run_gemv_q(c, n, Ts, x_dev, bias_dev, y_dev);
+    if (act == BGL_ACT_W4A8 && fused_q_ok(c, kind, Ts[0].K, M)) return run_gemv_q(c, n, Ts, x_dev, M, bias_dev, y_dev);
     if (act == BGL_ACT_F32 && M >= BGL_MFMA_MIN_M && !c->no_mfma) {
         bool ok = true;
         for (int i = 0; i < n; i++) ok = ok && bgl_mfma_ok(Ts[i].fmt, Ts[i].bits);

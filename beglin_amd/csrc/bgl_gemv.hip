@@ -193,16 +193,20 @@ __device__ __forceinline__ uint32_t quant_byte(float x, float inv) {
     return (uint32_t)q & 255u;
 }
 
-// Quantizes QP passes (pass i = values 256*(p0 + i*nw) .. +255; lane l holds values 4l..4l+3 of each
-// in v[i]) into LDS.  The passes are processed in lockstep so their dependency chains interleave.
-// |x| is maximised on its bit pattern (the same order as the float values for non-NaN inputs).
+// Quantizes QP passes into LDS.  The MB columns of a launch are one run of passes: pass p is values
+// 256*(p % NP) .. +255 of column p / NP (NP passes per column, NPT = MB*NP in all); pass i of the
+// call is p0 + i*nw, lane l holding values 4l..4l+3 of it in v[i].  The passes are processed in
+// lockstep so their dependency chains interleave.  Column m's operands live at xq + m*XQS,
+// asc + m*(NGQ+1), xsum + m*(K/64+1); passes past NPT and lanes past K store into each region's dummy
+// slot.  |x| is maximised on its bit pattern (the same order as the float values for non-NaN inputs).
 // GQ=256: one pass is one group; its four row maxima are combined with readlane, and one IEEE
 // division pair serves every pass (lane i computes pass i's scale and reciprocal).  GQ=64: one pass
-// is four groups, one per 16-lane row.  Lanes past K store into the dummy slots.
-template <int FMT, int QP>
-__device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int nw, int K, int NGQ, int U, int lane,
-                                             int8_t *xq, float *asc, int *xsum) {
+// is four groups, one per 16-lane row.
+template <int FMT, int QP, int MB>
+__device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int nw, int K, int NP, int NPT, int NGQ, int U,
+                                             int lane, int8_t *xq, float *asc, int *xsum) {
     using QU = QUnit<FMT>;
+    const int XQS = (U + 1) * QU::STRIDE;
     uint32_t m[QP];
 #pragma unroll
     for (int i = 0; i < QP; i++)
@@ -215,6 +219,23 @@ __device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int 
     for (int i = 0; i < QP; i++) m[i] = umax(m[i], dpp_u<0x141>(m[i]));
 #pragma unroll
     for (int i = 0; i < QP; i++) m[i] = umax(m[i], dpp_u<0x140>(m[i]));   // row maxima in every lane
+    // pass i: column col[i] (clamped), value offset e[i] within the column, whether it is real
+    int col[QP], e[QP];
+    bool ok[QP];
+#pragma unroll
+    for (int i = 0; i < QP; i++) {
+        const int p = p0 + i * nw;
+        if constexpr (MB == 1) {                       // one column: passes past K land past K
+            col[i] = 0;
+            e[i] = 256 * p + 4 * lane;
+            ok[i] = e[i] < K;
+        } else {
+            const int pc = p < NPT ? p : NPT - 1;
+            col[i] = pc / NP;
+            e[i] = 256 * (pc - col[i] * NP) + 4 * lane;
+            ok[i] = p < NPT && e[i] < K;               // K % 64 == 0: whole 16-lane rows are in or out
+        }
+    }
     float inv[QP];
     if constexpr (QU::GQ == 256) {
         float mx = 0.0f;
@@ -230,7 +251,12 @@ __device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int 
         for (int i = 0; i < QP; i++) inv[i] = rlane_f(iv, i);
         if (lane < QP) {
             const int p = p0 + lane * nw;
-            asc[256 * p < K ? p : NGQ] = sc;
+            if constexpr (MB == 1) {
+                asc[256 * p < K ? p : NGQ] = sc;
+            } else {
+                const int pc = p < NPT ? p : NPT - 1, cm = pc / NP, pp = pc - cm * NP;
+                asc[cm * (NGQ + 1) + (p < NPT && 256 * pp < K ? pp : NGQ)] = sc;
+            }
         }
     } else {
         float sc[QP];
@@ -240,10 +266,7 @@ __device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int 
         for (int i = 0; i < QP; i++) inv[i] = __fdiv_rn(1.0f, sc[i]);
         if ((lane & 15) == 0) {
 #pragma unroll
-            for (int i = 0; i < QP; i++) {
-                const int e = 256 * (p0 + i * nw) + 4 * lane;
-                asc[e < K ? e / 64 : NGQ] = sc[i];
-            }
+            for (int i = 0; i < QP; i++) asc[col[i] * (NGQ + 1) + (ok[i] ? e[i] / 64 : NGQ)] = sc[i];
         }
     }
     uint32_t word[QP];
@@ -252,11 +275,8 @@ __device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int 
         word[i] = quant_byte(v[i].x, inv[i]) | (quant_byte(v[i].y, inv[i]) << 8) | (quant_byte(v[i].z, inv[i]) << 16) |
                   (quant_byte(v[i].w, inv[i]) << 24);
 #pragma unroll
-    for (int i = 0; i < QP; i++) {
-        const int e = 256 * (p0 + i * nw) + 4 * lane;
-        const bool ok = e < K;                         // K % 64 == 0: whole 16-lane rows are in or out
-        *reinterpret_cast<uint32_t *>(xq + (ok ? e / QU::ELEMS : U) * QU::STRIDE + e % QU::ELEMS) = word[i];
-    }
+    for (int i = 0; i < QP; i++)
+        *reinterpret_cast<uint32_t *>(xq + col[i] * XQS + (ok[i] ? e[i] / QU::ELEMS : U) * QU::STRIDE + e[i] % QU::ELEMS) = word[i];
     if constexpr (QU::XSUM) {
         int sm[QP];
 #pragma unroll
@@ -268,20 +288,24 @@ __device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int 
         for (int i = 0; i < QP; i++) sm[i] = row_sum_i32(sm[i]);
         if ((lane & 15) == 0) {
 #pragma unroll
-            for (int i = 0; i < QP; i++) {
-                const int e = 256 * (p0 + i * nw) + 4 * lane;
-                xsum[e < K ? e / 64 : K / 64] = sm[i];
-            }
+            for (int i = 0; i < QP; i++) xsum[col[i] * (K / 64 + 1) + (ok[i] ? e[i] / 64 : K / 64)] = sm[i];
         }
     }
 }
 
-template <int QP>
-__device__ __forceinline__ void load_xpass(float4 (&v)[QP], const float *x, int p0, int nw, int K, int lane) {
+// x values of QP passes (see quant_passes); addresses are clamped, so every load is valid.
+template <int QP, int MB>
+__device__ __forceinline__ void load_xpass(float4 (&v)[QP], const float *x, int p0, int nw, int K, int NP, int NPT, int lane) {
 #pragma unroll
     for (int i = 0; i < QP; i++) {
-        const int e = min(256 * (p0 + i * nw) + 4 * lane, K - 4);      // clamped: always a valid address
-        const bgl_f32x4 t = *((const BGL_GLOBAL bgl_f32x4 *)(x + e));
+        const float *xp;
+        if constexpr (MB == 1) {
+            xp = x + min(256 * (p0 + i * nw) + 4 * lane, K - 4);
+        } else {
+            const int p = min(p0 + i * nw, NPT - 1), cm = p / NP;
+            xp = x + (size_t)cm * K + min(256 * (p - cm * NP) + 4 * lane, K - 4);
+        }
+        const bgl_f32x4 t = *((const BGL_GLOBAL bgl_f32x4 *)xp);
         v[i] = make_float4(t.x, t.y, t.z, t.w);
     }
 }
@@ -353,7 +377,7 @@ __device__ __forceinline__ float unit_float(int isum, float s, const float *asc,
     else return __fmul_rn(__fmul_rn((float)isum, s), asc[u]);
 }
 
-template <int FMT, int TR, int QP>
+template <int FMT, int TR, int QP, int MB>
 __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     extern __shared__ __align__(16) unsigned char lds[];
     constexpr int KQ = BGL_TILE / TR, SUBS = BGL_TILE / TR;
@@ -365,16 +389,17 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     const int lb = b - sel.blk0, tile = lb / SUBS, r0 = (lb % SUBS) * TR;
     const int nw = sel.nthreads >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int K = T.K, U = T.nunits, NGQ = K / QU::GQ, NP = (K + 255) / 256;
+    const int K = T.K, U = T.nunits, NGQ = K / QU::GQ, NP = (K + 255) / 256, NPT = MB * NP;
+    const int XQS = (U + 1) * QU::STRIDE;               // LDS bytes of one column's codes
     int8_t *xq = reinterpret_cast<int8_t *>(lds);
-    float *asc = reinterpret_cast<float *>(lds + (size_t)(U + 1) * QU::STRIDE);
-    int *xsum = reinterpret_cast<int *>(asc + NGQ + 1);
-    float *tl = reinterpret_cast<float *>(xsum + K / 64 + 1);
+    float *asc = reinterpret_cast<float *>(lds + (size_t)MB * XQS);
+    int *xsum = reinterpret_cast<int *>(asc + MB * (NGQ + 1));
+    float *tl = reinterpret_cast<float *>(xsum + MB * (K / 64 + 1));
     const float *x = sel.x;
 
     // ---- x loads of the first pass, then the first weight units (unconditional, clamped)
     float4 v[QP];
-    load_xpass<QP>(v, x, wave, nw, K, lane);
+    load_xpass<QP, MB>(v, x, wave, nw, K, NP, NPT, lane);
     __builtin_amdgcn_sched_barrier(0);
     // Waves [0, nwl) own weight units; any further waves of the launch only quantize.  The two
     // roles are separate branches so the weight waves' wait for x is not merged with a path that
@@ -391,17 +416,22 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
         // quantize x (q4gemv.h:177-213 / q4gemv_g256.h:72-99).  The first passes stay outside the
         // loop: a loop header joining the back edge (whose x loads are the newest) would make the
         // compiler wait for the weight loads as well.
-        quant_passes<FMT, QP>(v, wave, nw, K, NGQ, U, lane, xq, asc, xsum);
-        for (int p0 = wave + QP * nw; p0 < NP; p0 += QP * nw) {
-            load_xpass<QP>(v, x, p0, nw, K, lane);
-            quant_passes<FMT, QP>(v, p0, nw, K, NGQ, U, lane, xq, asc, xsum);
+        quant_passes<FMT, QP, MB>(v, wave, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
+        for (int p0 = wave + QP * nw; p0 < NPT; p0 += QP * nw) {
+            load_xpass<QP, MB>(v, x, p0, nw, K, NP, NPT, lane);
+            quant_passes<FMT, QP, MB>(v, p0, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
         }
         __syncthreads();
-        // per-unit fold terms t[u][row]; every lane computes (the partner exchange is wave-wide)
+        // per-unit fold terms t[m][u][row]; every lane computes (the partner exchange is wave-wide).
+        // One unit's weights serve every column.
         auto emit = [&](const RawPart<FMT, H> &c, int u) {
-            int p = unit_part<FMT, H>(c, xq, min(u, U - 1), h);
-            if constexpr (H == 2) p += __shfl_xor(p, TR);
-            if (h == 0 && u < U) tl[u * TR + r] = unit_float<FMT>(p, c.s, asc, xsum, u);
+#pragma unroll
+            for (int m = 0; m < MB; m++) {
+                int p = unit_part<FMT, H>(c, xq + m * XQS, min(u, U - 1), h);
+                if constexpr (H == 2) p += __shfl_xor(p, TR);
+                if (h == 0 && u < U)
+                    tl[(m * U + u) * TR + r] = unit_float<FMT>(p, c.s, asc + m * (NGQ + 1), xsum + m * (K / 64 + 1), u);
+            }
         };
         for (;;) {
             const int un = ub + nwl * UPI, u = ub + kq;
@@ -415,40 +445,48 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
             ub = un;
         }
     } else {
-        quant_passes<FMT, QP>(v, wave, nw, K, NGQ, U, lane, xq, asc, xsum);
-        for (int p0 = wave + QP * nw; p0 < NP; p0 += QP * nw) {
-            load_xpass<QP>(v, x, p0, nw, K, lane);
-            quant_passes<FMT, QP>(v, p0, nw, K, NGQ, U, lane, xq, asc, xsum);
+        quant_passes<FMT, QP, MB>(v, wave, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
+        for (int p0 = wave + QP * nw; p0 < NPT; p0 += QP * nw) {
+            load_xpass<QP, MB>(v, x, p0, nw, K, NP, NPT, lane);
+            quant_passes<FMT, QP, MB>(v, p0, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
         }
         __syncthreads();
     }
     __syncthreads();
-    if (threadIdx.x >= TR) return;
+    // sequential fold of each (column, row) in group order; the LDS reads go out 8 at a time, one
+    // batch ahead of the adds
     const GemvTask &task = L.t[sel.ti];
-    const int row = tile * BGL_TILE + r0 + threadIdx.x;
-    if (row >= task.T.N) return;
-    // sequential fold in group order; the LDS reads go out 8 at a time, one batch ahead of the adds
-    float acc = 0.0f;
-    const float *tr = tl + threadIdx.x;
-    const int U8 = U & ~7;
-    float t8[8], n8[8];
-    if (U8) {
+    auto fold = [&](int m, int rl) {
+        const int row = tile * BGL_TILE + r0 + rl;
+        if (row >= task.T.N) return;
+        float acc = 0.0f;
+        const float *tr = tl + (size_t)m * U * TR + rl;
+        const int U8 = U & ~7;
+        float t8[8], n8[8];
+        if (U8) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) t8[i] = tr[i * TR];
-    }
-    for (int g = 0; g < U8; g += 8) {
-        if (g + 8 < U8) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) n8[i] = tr[(g + 8 + i) * TR];
+            for (int i = 0; i < 8; i++) t8[i] = tr[i * TR];
         }
+        for (int g = 0; g < U8; g += 8) {
+            if (g + 8 < U8) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc = __fadd_rn(acc, t8[i]);
+                for (int i = 0; i < 8; i++) n8[i] = tr[(g + 8 + i) * TR];
+            }
 #pragma unroll
-        for (int i = 0; i < 8; i++) t8[i] = n8[i];
+            for (int i = 0; i < 8; i++) acc = __fadd_rn(acc, t8[i]);
+#pragma unroll
+            for (int i = 0; i < 8; i++) t8[i] = n8[i];
+        }
+        for (int g = U8; g < U; g++) acc = __fadd_rn(acc, tr[g * TR]);
+        const float bb = task.bias ? task.bias[row] : 0.0f;
+        task.y[(size_t)(L.m0 + m) * task.ystride + row] = __fadd_rn(bb, acc);
+    };
+    if constexpr (MB == 1) {
+        if (threadIdx.x < TR) fold(0, threadIdx.x);
+    } else {
+        for (int t = threadIdx.x; t < MB * TR; t += sel.nthreads)
+            if (t / TR < L.mcols) fold(t / TR, t % TR);
     }
-    for (int g = U8; g < U; g++) acc = __fadd_rn(acc, tr[g * TR]);
-    const float bb = task.bias ? task.bias[row] : 0.0f;
-    task.y[(size_t)L.m0 * task.ystride + row] = __fadd_rn(bb, acc);
 }
 
 // ================================================================================== launchers
@@ -501,47 +539,58 @@ int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, int nw, h
     return -2;
 }
 
-size_t bgl_gemv_q_lds(int fmt, int K, int TR) {
+size_t bgl_gemv_q_lds(int fmt, int K, int TR, int MB) {
     const int GQ = fmt == BGL_Q4G256SF ? 256 : 64;
     const int ELEMS = fmt == BGL_Q4G256SF ? 256 : 64;
     const int U = K / ELEMS;
-    return (size_t)(U + 1) * (ELEMS + 16) + 4 * (size_t)(K / GQ + 1) + 4 * (size_t)(K / 64 + 1) + 4 * (size_t)U * TR;
+    return (size_t)MB * ((size_t)(U + 1) * (ELEMS + 16) + 4 * (size_t)(K / GQ + 1) + 4 * (size_t)(K / 64 + 1) + 4 * (size_t)U * TR);
 }
 
-template <int FMT, int QP>
+template <int FMT, int QP, int MB>
 static int launch_q_tr(int TR, const GemvLaunch &L, int nblocks, int nw, size_t lds, hipStream_t st) {
     dim3 g(nblocks), b(nw * BGL_TILE);
     switch (TR) {
-    case 64: hipLaunchKernelGGL((k_gemv_q<FMT, 64, QP>), g, b, lds, st, L); return 0;
-    case 32: hipLaunchKernelGGL((k_gemv_q<FMT, 32, QP>), g, b, lds, st, L); return 0;
-    case 16: hipLaunchKernelGGL((k_gemv_q<FMT, 16, QP>), g, b, lds, st, L); return 0;
-    case 8: hipLaunchKernelGGL((k_gemv_q<FMT, 8, QP>), g, b, lds, st, L); return 0;
+    case 64: hipLaunchKernelGGL((k_gemv_q<FMT, 64, QP, MB>), g, b, lds, st, L); return 0;
+    case 32: hipLaunchKernelGGL((k_gemv_q<FMT, 32, QP, MB>), g, b, lds, st, L); return 0;
+    case 16: hipLaunchKernelGGL((k_gemv_q<FMT, 16, QP, MB>), g, b, lds, st, L); return 0;
+    case 8: hipLaunchKernelGGL((k_gemv_q<FMT, 8, QP, MB>), g, b, lds, st, L); return 0;
     default: return -1;
     }
 }
 
-template <int FMT>
+template <int FMT, int MB>
 static int launch_q_qp(int QP, int TR, const GemvLaunch &L, int nblocks, int nw, size_t lds, hipStream_t st) {
     switch (QP) {
-    case 1: return launch_q_tr<FMT, 1>(TR, L, nblocks, nw, lds, st);
-    case 2: return launch_q_tr<FMT, 2>(TR, L, nblocks, nw, lds, st);
-    default: return launch_q_tr<FMT, 4>(TR, L, nblocks, nw, lds, st);
+    case 1: return launch_q_tr<FMT, 1, MB>(TR, L, nblocks, nw, lds, st);
+    case 2: return launch_q_tr<FMT, 2, MB>(TR, L, nblocks, nw, lds, st);
+    default: return launch_q_tr<FMT, 4, MB>(TR, L, nblocks, nw, lds, st);
     }
 }
 
-// ntiles counts 64-row tiles; each is split into 64/TR workgroups.  QP (quantization passes per
-// wave loaded up front) covers a wave's whole share of the 256-value passes when that is <= 4.
-int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, hipStream_t st) {
+template <int FMT>
+static int launch_q_mb(int MB, int QP, int TR, const GemvLaunch &L, int nblocks, int nw, size_t lds, hipStream_t st) {
+    switch (MB) {
+    case 1: return launch_q_qp<FMT, 1>(QP, TR, L, nblocks, nw, lds, st);
+    case 4: return launch_q_qp<FMT, 4>(QP, TR, L, nblocks, nw, lds, st);
+    case 8: return launch_q_qp<FMT, 8>(QP, TR, L, nblocks, nw, lds, st);
+    default: return -1;
+    }
+}
+
+// ntiles counts 64-row tiles; each is split into 64/TR workgroups.  MB columns (1, 4 or 8) per
+// launch, L.mcols of them real.  QP (quantization passes per wave loaded up front) covers a wave's
+// whole share of the MB*ceil(K/256) passes when that is <= 4.
+int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, int MB, hipStream_t st) {
     const int fmt = L.t[0].T.fmt, K = L.t[0].T.K;
     if (K < 64 || K % 64) return -1;
-    const size_t lds = bgl_gemv_q_lds(fmt, K, TR);
+    const size_t lds = bgl_gemv_q_lds(fmt, K, TR, MB);
     const int nblocks = ntiles * (BGL_TILE / TR);
-    const int pw = ((K + 255) / 256 + nw - 1) / nw;
+    const int pw = (MB * ((K + 255) / 256) + nw - 1) / nw;
     const int QP = pw <= 1 ? 1 : pw <= 2 ? 2 : 4;
     switch (fmt) {
-    case BGL_Q4G256SF: return launch_q_qp<BGL_Q4G256SF>(QP, TR, L, nblocks, nw, lds, st);
-    case BGL_Q4G64: return launch_q_qp<BGL_Q4G64>(QP, TR, L, nblocks, nw, lds, st);
-    case BGL_Q8G64: return launch_q_qp<BGL_Q8G64>(QP, TR, L, nblocks, nw, lds, st);
+    case BGL_Q4G256SF: return launch_q_mb<BGL_Q4G256SF>(MB, QP, TR, L, nblocks, nw, lds, st);
+    case BGL_Q4G64: return launch_q_mb<BGL_Q4G64>(MB, QP, TR, L, nblocks, nw, lds, st);
+    case BGL_Q8G64: return launch_q_mb<BGL_Q8G64>(MB, QP, TR, L, nblocks, nw, lds, st);
     default: return -2;
     }
 }
