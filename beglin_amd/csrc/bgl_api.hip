@@ -606,18 +606,25 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
 }
 
 #define BGL_GEMV_Q_LDS_MAX (64 * 1024)          // one column: two workgroups of the largest shapes per CU
-#define BGL_GEMV_Q_LDS_MAX_MB (128 * 1024)      // 4 or 8 columns: the codes of every column sit in LDS
-#define BGL_GEMV_Q_MAXMB 8
+#define BGL_GEMV_Q_LDS_MAX_MB (160 * 1024)      // 4 or 8 columns: the codes of every column sit in LDS
 
 static int q_mb(int mc) { return mc <= 1 ? 1 : mc <= 4 ? 4 : 8; }
 static size_t q_lds_max(int MB) { return MB == 1 ? BGL_GEMV_Q_LDS_MAX : BGL_GEMV_Q_LDS_MAX_MB; }
+// The widest launch (8, 4 or 1 columns) whose LDS fits at 8 rows per workgroup; 0: none does.
+static int q_mb_max(int kind, int K) {
+    for (int MB : {8, 4, 1})
+        if (bgl_gemv_q_lds(kind, K, 8, MB) <= q_lds_max(MB)) return MB;
+    return 0;
+}
 
-// W4A8 with the quantization fused in, M columns in launches of up to 8 (each launch streams the
-// weights once for its columns; every column's arithmetic is the one-column kernel's).
+// W4A8 with the quantization fused in, M columns in launches of up to 8 -- fewer where the
+// columns' codes would not fit LDS (each launch streams the weights once for its columns; every
+// column's arithmetic is the one-column kernel's).
 static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
                       float *const *y) {
-    for (int m0 = 0; m0 < M; m0 += BGL_GEMV_Q_MAXMB) {
-        const int mc = std::min(BGL_GEMV_Q_MAXMB, M - m0), MB = q_mb(mc);
+    const int mbmax = q_mb_max(Ts[0].fmt, Ts[0].K);
+    for (int m0 = 0; m0 < M; m0 += mbmax) {
+        const int mc = std::min(mbmax, M - m0), MB = q_mb(mc);
         GemvLaunch L;
         memset(&L, 0, sizeof L);
         int blocks = 0;
@@ -650,10 +657,10 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
 }
 
 static bool fused_q_ok(bgl_ctx *c, int kind, int K, int M) {
+    (void)M;
     if (c->no_fused) return false;
     if (kind != BGL_Q4G256SF && kind != BGL_Q4G64 && kind != BGL_Q8G64) return false;
-    const int MB = q_mb(std::min(M, BGL_GEMV_Q_MAXMB));
-    return bgl_gemv_q_lds(kind, K, 8, MB) <= q_lds_max(MB);
+    return q_mb_max(kind, K) > 0;
 }
 
 

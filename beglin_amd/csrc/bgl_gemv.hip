@@ -579,7 +579,8 @@ static int launch_q_mb(int MB, int QP, int TR, const GemvLaunch &L, int nblocks,
 
 // ntiles counts 64-row tiles; each is split into 64/TR workgroups.  MB columns (1, 4 or 8) per
 // launch, L.mcols of them real.  QP (quantization passes per wave loaded up front) covers a wave's
-// whole share of the MB*ceil(K/256) passes when that is <= 4.
+// whole share of the MB*ceil(K/256) passes when that is <= 4.  (8 passes up front for the 4- and
+// 8-column launches measured no faster.)
 int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, int MB, hipStream_t st) {
     const int fmt = L.t[0].T.fmt, K = L.t[0].T.K;
     if (K < 64 || K % 64) return -1;
