@@ -102,6 +102,13 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     c->no_fused = nf && atoi(nf) != 0;
     const char *nm = getenv("BGL_NO_MFMA");
     c->no_mfma = nm && atoi(nm) != 0;
+    const char *nx = getenv("BGL_NO_GEMV_X");
+    c->no_gemv_x = nx && atoi(nx) != 0;
+    const char *xw = getenv("BGL_X_WAVES");
+    c->x_waves = xw ? atoi(xw) : 0;
+    if (c->x_waves < 0 || c->x_waves > 16) c->x_waves = 0;
+    const char *xf = getenv("BGL_X_FUSE");
+    c->x_fuse = xf ? (atoi(xf) != 0) : -1;
     *out = c;
     return 0;
 }
@@ -552,8 +559,58 @@ static void fill_tasks(GemvLaunch &L, int n, const BglDevTensor *Ts, const float
     }
 }
 
+#define BGL_GEMV_X_LDS_MAX (160 * 1024)
+#define BGL_GEMV_X_FUSE_MAX_K 4096            // longer K: one prep kernel beats every workgroup making the digits
+
+// One fp32-activation column through k_gemv_x (bgl_gemv_x.hip): workgroups of TR rows over the whole
+// K range, waves taking slots of 64/TR groups in turn, so no launch needs a K split.  A: the prepared
+// activation operands, or null to have every workgroup make them from the raw column x_dev.
+// Returns 1 when the shape is not taken (the activation records of K would not fit LDS, or a tensor
+// spans 2 GiB).
+static int run_gemv_x(bgl_ctx *c, int n, const BglDevTensor *Ts, const GemvAct *A, const float *x_dev,
+                      const float *const *bias, float *const *y, const int *ystride) {
+    GemvLaunch L;
+    memset(&L, 0, sizeof L);
+    int blocks = 0;
+    fill_tasks(L, n, Ts, bias, y, ystride, blocks);
+    if (A) L.a = *A;
+    L.x = x_dev;
+    L.m0 = 0;
+    L.mcols = 1;
+    L.mtot = 1;
+    // Shapes (measured on the cfg1 / cfg3 Q4G32H and qNg64 launches, n = 2..15): making the digits
+    // costs every workgroup a pass over K, so those launches keep whole 64-row tiles (>= 128
+    // workgroups) with up to 12 waves; with prepared digits the tiles split until >= 256 workgroups,
+    // up to 16 waves.
+    const bool fused = A == nullptr;
+    int TR = 64;
+    while (TR > 8 && (long)blocks * (BGL_TILE / TR) < (fused ? 128 : 256)) TR >>= 1;
+    if (c->force_tr) TR = c->force_tr;
+    const int KQ = BGL_TILE / TR, G = Ts[0].K / 64, S = (G + KQ - 1) / KQ;
+    int nw = std::min({S, c->max_waves, fused ? 12 : 16});
+    if (c->x_waves) nw = std::min(S, c->x_waves);
+    if (bgl_gemv_x_lds(Ts[0].K, TR, nw) > BGL_GEMV_X_LDS_MAX) return 1;
+    for (int i = 0; i < n; i++)            // the kernel addresses each tensor through 32-bit buffer offsets
+        if ((size_t)Ts[i].ntiles * Ts[i].cpr * 1024 >= (1ull << 31) || (size_t)Ts[i].ntiles * Ts[i].nunits * 512 >= (1ull << 31))
+            return 1;
+    for (int i = 0; i < n; i++) L.t[i].blk0 *= KQ;
+    int tok = prof_begin(c, 1);
+    int rc = bgl_launch_gemv_x(L, A == nullptr, blocks * KQ, TR, nw, c->stream);
+    prof_end(c, tok);
+    if (rc == -2) return bgl_fail(BGL_E_UNSUPPORTED, "kind %d bits %d: no fp32-activation kernel", Ts[0].fmt, Ts[0].bits);
+    if (rc) return bgl_fail(BGL_E_ARG, "gemv_x launch: bad shape");
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
+static bool gemv_x_kind(int fmt) { return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64; }
+
 int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &A, int M,
              const float *const *bias, float *const *y, const int *ystride) {
+    if (M == 1 && act == BGL_ACT_F32 && !c->no_gemv_x && gemv_x_kind(Ts[0].fmt)) {
+        int rc = run_gemv_x(c, n, Ts, &A, nullptr, bias, y, ystride);
+        if (rc <= 0) return rc;
+    }
     GemvLaunch L;
     memset(&L, 0, sizeof L);
     int blocks = 0;
@@ -688,6 +745,12 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
         bool ok = true;
         for (int i = 0; i < n; i++) ok = ok && bgl_mfma_ok(Ts[i].fmt, Ts[i].bits);
         if (ok) return run_gemm_mfma(c, n, Ts, x_dev, M, bias_dev, y_dev, nullptr);
+    }
+    // one fp32 column over a short K: the GEMV makes the activation digits itself (no prep launch)
+    if (act == BGL_ACT_F32 && M == 1 && !c->no_gemv_x && gemv_x_kind(kind) &&
+        (c->x_fuse == 1 || (c->x_fuse < 0 && Ts[0].K <= BGL_GEMV_X_FUSE_MAX_K))) {
+        int rc = run_gemv_x(c, n, Ts, nullptr, x_dev, bias_dev, y_dev, nullptr);
+        if (rc <= 0) return rc;
     }
     GemvAct A;
     int rc = prep_act(c, act, act_group(kind), x_dev, M, Ts[0].K, A);

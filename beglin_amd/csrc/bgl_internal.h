@@ -30,6 +30,9 @@ struct bgl_ctx {
     bool no_mfma = false;                 // BGL_NO_MFMA=1: fp32-activation M >= 16 through the dot4 kernels
     int min_blocks = 256;                 // fused W4A8: split tiles until at least this many workgroups
     int force_tr = 0;                     // BGL_FORCE_TR: fixed rows per workgroup (tuning)
+    bool no_gemv_x = false;               // BGL_NO_GEMV_X=1: fp32-activation M=1 through the tile kernel (k_gemv)
+    int x_waves = 0;                      // BGL_X_WAVES: wavefronts per k_gemv_x workgroup (tuning)
+    int x_fuse = -1;                      // BGL_X_FUSE: 0 never / 1 always make the digits inside k_gemv_x; -1 by K
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
     int prep_act = -1, prep_gq = 0, prep_M = 0, prep_K = 0;   // what act_* currently hold
     DevBuf part;                          // K-split partial sums [ks][M][N]

@@ -75,3 +75,6 @@ __global__ void k_splitk_reduce(const float *part, int ks, int M, int N, const f
 int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, int nw, hipStream_t st);
 int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, int MB, hipStream_t st);
 size_t bgl_gemv_q_lds(int fmt, int K, int TR, int MB);
+// ---- bgl_gemv_x.hip: one-column fp32-activation GEMV over prepared digits ----
+int bgl_launch_gemv_x(const GemvLaunch &L, bool fuse, int nblocks, int TR, int nw, hipStream_t st);
+size_t bgl_gemv_x_lds(int K, int TR, int nw);

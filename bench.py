@@ -654,20 +654,32 @@ def main():
         n = wl.ncalls([tag])
         per_call[tag] = {"us": round(ms * 1e3 / n, 2), "GB/s": round(wl.nbytes([tag]) / (ms * 1e-3) / 1e9, 1)}
 
-    # The dominant kernel is the GEMV; for the fused W4A8 path (cfg2, every M) it is the only
-    # kernel of the step, so its average launch duration is the graph-timed step (HIP events on the
-    # context's stream around the timed replays) over the launches per step.  The separate-prep
-    # paths (fp32 activations) add one activation kernel per call; those are timed the same way from
-    # a graph of the prep alone.
+    # The dominant kernel is the GEMV; for the fused W4A8 path (cfg2, every M) and the one-column
+    # fp32 GEMV over a short K it is the only kernel of the step, so its average launch duration is
+    # the graph-timed step (HIP events on the context's stream around the timed replays) over the
+    # launches per step.  The separate-prep paths (fp32 activations otherwise) add one activation
+    # kernel per call; those are timed the same way from a graph of the prep alone.
     launches = wl.ncalls()
     prep_ms = 0.0
+    has_prep = False
     if args.workload != "cfg2":
+        # does the path launch an activation-prep kernel? (one profiled eager step counts them; the
+        # one-column fp32 GEMV over a short K makes its digits itself)
+        ctx.prof_enable(True)
+        ctx.prof_read()
+        with torch.cuda.stream(stream):
+            wl.run()
+        ctx.sync()
+        has_prep = ctx.prof_read()["prep"][1] > 0
+        ctx.prof_enable(False)
+    if has_prep:
         prep_ms = time_prep(ctx, torch, stream, wl, max(5, args.steps // 5))
     k_ms = max(step_ms - prep_ms, 1e-6)
     achieved = nbytes / (k_ms * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemv_q<fmt,TR,QP,MB> (bgl_gemv.hip)" if prep_ms == 0.0 else "k_gemv<fmt,act,n,MB> (bgl_gemv.hip)",
+            "kernel": ("k_gemv_q<fmt,TR,QP,MB> (bgl_gemv.hip)" if args.workload == "cfg2" else
+                       "k_gemv_x<fmt,n,TR,FUSE> (bgl_gemv_x.hip)" if M == 1 else "k_gemv<fmt,act,n,MB> (bgl_gemv.hip)"),
             "launches_per_step": launches, "kernel_us_per_launch": round(k_ms * 1e3 / launches, 3),
             "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3),
             "bytes_per_launch": round(nbytes / launches)}
