@@ -107,6 +107,8 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     const char *xw = getenv("BGL_X_WAVES");
     c->x_waves = xw ? atoi(xw) : 0;
     if (c->x_waves < 0 || c->x_waves > 16) c->x_waves = 0;
+    const char *nmx = getenv("BGL_NO_MOE_X");
+    c->no_moe_x = nmx && atoi(nmx) != 0;
     const char *xf = getenv("BGL_X_FUSE");
     c->x_fuse = xf ? (atoi(xf) != 0) : -1;
     *out = c;

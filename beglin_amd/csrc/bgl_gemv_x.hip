@@ -1,331 +1,17 @@
 // bgl_gemv_x.hip -- the one-column fp32-activation GEMV (q4gemv.h:761-769 gemm_qXg64_mt at M=1,
 // qng64_dense.c:70-79 qng64_matvec_f32; int4 g64, int4 g32 fp16-scale, int8 g64, qNg64 n=2..15).
 //
-// Activations arrive prepared by k_act_x24 (bgl_prep.hip): per 64-group three balanced int8 digits
-// of X = rint(x * 2^(21-e)), the digit sums per 32-element half and the scale 2^(e-21), so every
-// product below is an exact int32 dot4 sum and fp32 only enters in the per-group fold.
-//
 // Work decomposition (the shape of the fused W4A8 kernel): a workgroup owns TR rows of a 64-row
 // tile and the whole K range, so no launch needs a K split or a second reduction kernel.  Lane l
 // of a wave handles row l % TR and group kq = l / TR of each slot of KQ = 64/TR consecutive
 // 64-groups, so each wave-wide weight load is KQ runs of TR*16 >= 128 contiguous bytes.  The
-// workgroup's waves take the slots in turn; a wave's next slot is loaded before the current one is
-// used.
+// workgroup's waves take the slots in turn, each keeping up to D of its slots in flight.
 //
-// The activation operands of the whole K range are copied into LDS once per workgroup (one 240-byte
-// record per group: 48 digit dwords, two 4-dword digit-sum words, the scale), issued before the
-// first weight loads so the copy's latency hides under theirs.  Lanes of one group read the same
-// record (a broadcast); the 60-dword record stride puts the KQ <= 8 records a read touches in
-// disjoint banks.
-//
-// qNg64 bit planes: the 8-bit field (stored as f ^ 0x80, a signed byte f - 128) is one dot4
-// operand; the 4-, 2- and 1-bit fields of an element are merged into one byte (their values sit at
-// bit 0, 4*has4 and 4*has4 + 2*has2 of it, < 128) with one shift and one v_and_or per field, so a
-// group costs two dot4 operands per digit instead of one per field.
-#include "bgl_gemv_impl.h"
-
-#define XREC_DW 60            // LDS dwords per 64-group record
-#define XREC_DSUM 48          // digit sums of the two halves: [half][digit 0..2, pad]
-#define XREC_SCALE 56         // 2^(e-21)
-#define X_PRE 4               // record pieces (16 bytes) per thread loaded ahead of the weights
-
-// (a & m) | o in one v_and_or_b32 (gfx9's three-operand encoding takes no literal constant and
-// reads at most one scalar register: m in a scalar register, o in a vector register).
-__device__ __forceinline__ uint32_t x_and_or(uint32_t a, uint32_t m, uint32_t o) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(o));
-    return r;
-}
-
-// A lane's weights for one 64-group.
-template <int FMT, int NB> struct XRaw;
-template <int NB> struct XRaw<BGL_Q4G64, NB> { uint4 c[2]; float s; };
-template <int NB> struct XRaw<BGL_Q4G32H, NB> { uint4 c[2]; uint32_t s; };
-template <int NB> struct XRaw<BGL_Q8G64, NB> { uint4 c[4]; float s; };
-template <int NB> struct XRaw<BGL_QNG64, NB> {
-    static constexpr int H8 = (NB >> 3) & 1, H4 = (NB >> 2) & 1, H2 = (NB >> 1) & 1, H1 = NB & 1;
-    uint4 p8[H8 ? 4 : 1], p4[H4 ? 2 : 1], p2;
-    uint2 p1;
-    float s;
-};
-
-// Buffer resources over a tensor's chunks and its per-unit scales, and an empty one: every load
-// through it returns zeros without touching memory.  A wave issues the loads of slots it does not
-// have through the empty resource, so every load is unconditional and each wait counts exactly the
-// loads issued after the one it needs.  Offsets: a lane-constant part in a vector register, the
-// slot's part in a scalar one.
-#define X_RSRC_W3 0x00020000  // buffer resource word 3 on gfx9: 32-bit data format, raw addressing
-#define X_OOB 0x80000000u     // a lane offset past any resource (resources are < 2^31 bytes)
-typedef unsigned int x_u32x2 __attribute__((ext_vector_type(2)));
-template <int FMT> constexpr int x_scale_bytes() { return FMT == BGL_QNG64 ? 8 : 4; }
-struct XRes {
-    __amdgpu_buffer_rsrc_t w, s, z;
-    uint32_t wtile, stile;    // byte offsets of this workgroup's tile in w and s
-};
-template <int FMT>
-__device__ __forceinline__ XRes x_res(const BglDevTensor &T, int tile) {
-    XRes r;
-    const uint32_t wb = (uint32_t)T.ntiles * (uint32_t)T.cpr * 1024u;
-    const uint32_t sb = (uint32_t)T.ntiles * (uint32_t)T.nunits * 64u * x_scale_bytes<FMT>();
-    r.w = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(T.w), (short)0, (int)wb, X_RSRC_W3);
-    r.s = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(T.s0), (short)0, (int)sb, X_RSRC_W3);
-    r.z = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(T.w), (short)0, 0, X_RSRC_W3);
-    r.wtile = (uint32_t)tile * (uint32_t)T.cpr * 1024u;
-    r.stile = (uint32_t)tile * (uint32_t)T.nunits * 64u * x_scale_bytes<FMT>();
-    return r;
-}
-
-// Lane-constant byte offsets of a lane's group inside a slot: row rr, group kq of the slot's KQ.
-// qNg64 units are pairs of groups: with KQ >= 2 the lane's half h = kq & 1 is fixed, with KQ == 1
-// it alternates with the slot (and goes into the slot's scalar offset).
-template <int NB> struct XPlanes {
-    static constexpr int H8 = (NB >> 3) & 1, H4 = (NB >> 2) & 1, H2 = (NB >> 1) & 1;
-    static constexpr int K4 = 8 * H8, K2 = K4 + 4 * H4, K1 = K2 + 2 * H2;
-};
-struct XLane {
-    uint32_t p8, p4, p2, p1, s;   // qNg64 fields (p8 is the chunk base of the other formats)
-};
-template <int FMT, int NB, int KQ>
-__device__ __forceinline__ XLane x_lane(int rr, int kq) {
-    constexpr int CPU = chunks_per_unit<FMT>(NB);
-    XLane l;
-    if constexpr (FMT == BGL_QNG64) {
-        using P = XPlanes<NB>;
-        const uint32_t ub = KQ >= 2 ? (uint32_t)kq >> 1 : 0u, h = KQ >= 2 ? (uint32_t)kq & 1u : 0u;
-        const uint32_t base = ub * CPU * 1024u + (uint32_t)rr * 16u;
-        l.p8 = base + 4096u * h;
-        l.p4 = base + 2048u * h + P::K4 * 1024u;
-        l.p2 = base + 1024u * h + P::K2 * 1024u;
-        l.p1 = base + 8u * h + P::K1 * 1024u;
-        l.s = (ub * 64u + (uint32_t)rr) * 8u + 4u * h;
-    } else {
-        l.p8 = (uint32_t)kq * CPU * 1024u + (uint32_t)rr * 16u;
-        l.p4 = l.p2 = l.p1 = 0u;
-        l.s = ((uint32_t)kq * 64u + (uint32_t)rr) * 4u;
-    }
-    return l;
-}
-
-// Slot sl's weights (zeros when !ok).
-template <int FMT, int NB, int KQ>
-__device__ __forceinline__ void x_load(XRaw<FMT, NB> &r, const XRes &R, const XLane &l, int sl, bool ok) {
-    constexpr int CPU = chunks_per_unit<FMT>(NB);
-    const __amdgpu_buffer_rsrc_t W = ok ? R.w : R.z, S = ok ? R.s : R.z;
-    auto ld = [&](uint32_t lane_off, uint32_t soff) {
-        const bgl_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(W, lane_off, soff, 0);
-        return make_uint4(v.x, v.y, v.z, v.w);
-    };
-    uint32_t sv;
-    if constexpr (FMT == BGL_QNG64) {
-        using X = XRaw<FMT, NB>;
-        const uint32_t su = KQ >= 2 ? (uint32_t)sl * (KQ / 2) : (uint32_t)sl >> 1;   // first unit of the slot
-        const uint32_t hh = KQ >= 2 ? 0u : (uint32_t)sl & 1u;                        // KQ == 1: the slot's half
-        const uint32_t wo = R.wtile + su * CPU * 1024u;
-        if constexpr (X::H8) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) r.p8[k] = ld(l.p8, wo + 4096u * hh + 1024u * k);
-        }
-        if constexpr (X::H4) {
-#pragma unroll
-            for (int k = 0; k < 2; k++) r.p4[k] = ld(l.p4, wo + 2048u * hh + 1024u * k);
-        }
-        if constexpr (X::H2) r.p2 = ld(l.p2, wo + 1024u * hh);
-        if constexpr (X::H1) {
-            const x_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(W, l.p1, wo + 8u * hh, 0);
-            r.p1 = make_uint2(v.x, v.y);
-        }
-        sv = __builtin_amdgcn_raw_buffer_load_b32(S, l.s, R.stile + su * 512u + 4u * hh, 0);
-    } else {
-        const uint32_t su = (uint32_t)sl * KQ;
-        const uint32_t wo = R.wtile + su * CPU * 1024u;
-#pragma unroll
-        for (int k = 0; k < CPU; k++) r.c[k] = ld(l.p8, wo + 1024u * k);
-        sv = __builtin_amdgcn_raw_buffer_load_b32(S, l.s, R.stile + su * 256u, 0);
-    }
-    if constexpr (FMT == BGL_Q4G32H) r.s = sv;
-    else r.s = __uint_as_float(sv);
-}
-
-// Slots a wave keeps in flight: as many as fit beside the decode registers.
-template <int FMT, int NB> constexpr int x_depth() {
-    return FMT == BGL_QNG64 ? (NB <= 4 ? 4 : NB <= 8 ? 3 : 2) : FMT == BGL_Q8G64 ? 3 : 4;
-}
-
-// Digit d of the group record as 16 dwords (element 4q..4q+3 in dword q).
-struct XDig {
-    int v[16];
-};
-__device__ __forceinline__ XDig x_digit(const int *rec, int d) {
-    XDig x;
-    const int4 *p = reinterpret_cast<const int4 *>(rec + 16 * d);
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int4 t = p[k];
-        x.v[4 * k] = t.x; x.v[4 * k + 1] = t.y; x.v[4 * k + 2] = t.z; x.v[4 * k + 3] = t.w;
-    }
-    return x;
-}
-
-// The group's fp32 term: the exact integer dot product per digit, folded as
-// s * ((t0 + 256 t1 + 65536 t2) * 2^(e-21)).
-template <int FMT, int NB>
-__device__ __forceinline__ float x_group(const XRaw<FMT, NB> &r, const int *rec) {
-    const int4 ds0 = *reinterpret_cast<const int4 *>(rec + XREC_DSUM);
-    const int4 ds1 = *reinterpret_cast<const int4 *>(rec + XREC_DSUM + 4);
-    const float xs = *reinterpret_cast<const float *>(rec + XREC_SCALE);
-    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H) {
-        const uint32_t raw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w};
-        int lo[8], hi[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) { lo[q] = nib_lo(raw[q]); hi[q] = nib_hi(raw[q]); }
-        int ta[3], tb[3];
-#pragma unroll
-        for (int d = 0; d < 3; d++) {
-            const XDig x = x_digit(rec, d);
-            int a = 0, b = 0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) { a = dot4(lo[q], x.v[2 * q], a); a = dot4(hi[q], x.v[2 * q + 1], a); }
-#pragma unroll
-            for (int q = 4; q < 8; q++) { b = dot4(lo[q], x.v[2 * q], b); b = dot4(hi[q], x.v[2 * q + 1], b); }
-            ta[d] = a; tb[d] = b;
-        }
-        if constexpr (FMT == BGL_Q4G64) {
-            const float V = fold_digits(ta[0] + tb[0] - 8 * (ds0.x + ds1.x), ta[1] + tb[1] - 8 * (ds0.y + ds1.y),
-                                        ta[2] + tb[2] - 8 * (ds0.z + ds1.z));
-            return r.s * (V * xs);
-        } else {
-            const float sa = __half2float(__ushort_as_half((unsigned short)(r.s & 0xffffu)));
-            const float sb = __half2float(__ushort_as_half((unsigned short)(r.s >> 16)));
-            const float Va = fold_digits(ta[0] - 8 * ds0.x, ta[1] - 8 * ds0.y, ta[2] - 8 * ds0.z);
-            const float Vb = fold_digits(tb[0] - 8 * ds1.x, tb[1] - 8 * ds1.y, tb[2] - 8 * ds1.z);
-            return sa * (Va * xs) + sb * (Vb * xs);
-        }
-    } else if constexpr (FMT == BGL_Q8G64) {
-        const int w[16] = {(int)r.c[0].x, (int)r.c[0].y, (int)r.c[0].z, (int)r.c[0].w, (int)r.c[1].x, (int)r.c[1].y,
-                           (int)r.c[1].z, (int)r.c[1].w, (int)r.c[2].x, (int)r.c[2].y, (int)r.c[2].z, (int)r.c[2].w,
-                           (int)r.c[3].x, (int)r.c[3].y, (int)r.c[3].z, (int)r.c[3].w};
-        int t[3];
-#pragma unroll
-        for (int d = 0; d < 3; d++) {
-            const XDig x = x_digit(rec, d);
-            int a = 0;
-#pragma unroll
-            for (int q = 0; q < 16; q++) a = dot4(w[q], x.v[q], a);
-            t[d] = a;
-        }
-        return r.s * (fold_digits(t[0], t[1], t[2]) * xs);
-    } else {
-        using R = XRaw<FMT, NB>;
-        constexpr int H8 = R::H8, H4 = R::H4, H2 = R::H2, H1 = R::H1;
-        constexpr bool HI = H4 || H2 || H1;                  // fields merged into the second operand
-        constexpr int S2 = 4 * H4, S1 = 4 * H4 + 2 * H2;     // their bit offsets inside it
-        constexpr int CORR = 128 * H8 - (1 << (NB - 1));     // code = u - 2^(n-1); the 8-bit field is stored as f - 128
-        int lo[16], hi[16];
-        if constexpr (H8) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                lo[4 * k] = (int)r.p8[k].x; lo[4 * k + 1] = (int)r.p8[k].y; lo[4 * k + 2] = (int)r.p8[k].z; lo[4 * k + 3] = (int)r.p8[k].w;
-            }
-        }
-        if constexpr (HI) {
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                uint32_t h = 0;
-                if constexpr (H4) {
-                    // element 4q+i's 4-bit field: chunk q/8, dword (q/2)%4, byte i, low nibble for even q
-                    const uint4 &c = r.p4[q >> 3];
-                    const uint32_t w = ((q >> 1) & 3) == 0 ? c.x : ((q >> 1) & 3) == 1 ? c.y : ((q >> 1) & 3) == 2 ? c.z : c.w;
-                    h = ((q & 1) ? w >> 4 : w) & 0x0F0F0F0Fu;
-                }
-                if constexpr (H2) {
-                    // element 4q+i's 2-bit field: dword q/4, byte i, bits 2(q%4)..+1
-                    const uint32_t w = (q >> 2) == 0 ? r.p2.x : (q >> 2) == 1 ? r.p2.y : (q >> 2) == 2 ? r.p2.z : r.p2.w;
-                    const int sh = 2 * (q & 3) - S2;
-                    const uint32_t v = sh >= 0 ? w >> sh : w << -sh;
-                    h = H4 ? x_and_or(v, 0x03030303u << S2, h) : (v & (0x03030303u << S2));
-                }
-                if constexpr (H1) {
-                    // element 4q+i's 1-bit field: dword q/8, byte i, bit q%8
-                    const uint32_t w = (q >> 3) ? r.p1.y : r.p1.x;
-                    const int sh = (q & 7) - S1;
-                    const uint32_t v = sh >= 0 ? w >> sh : w << -sh;
-                    h = (H4 || H2) ? x_and_or(v, 0x01010101u << S1, h) : (v & (0x01010101u << S1));
-                }
-                hi[q] = (int)h;
-            }
-        }
-        int t[3];
-#pragma unroll
-        for (int d = 0; d < 3; d++) {
-            const XDig x = x_digit(rec, d);
-            int a = 0, b = 0;
-            if constexpr (H8) {
-#pragma unroll
-                for (int q = 0; q < 16; q++) a = dot4(lo[q], x.v[q], a);
-            }
-            if constexpr (HI) {
-#pragma unroll
-                for (int q = 0; q < 16; q++) b = dot4(hi[q], x.v[q], b);
-            }
-            t[d] = H8 ? a + b * 256 : b;
-        }
-        t[0] += CORR * (ds0.x + ds1.x); t[1] += CORR * (ds0.y + ds1.y); t[2] += CORR * (ds0.z + ds1.z);
-        return r.s * (fold_digits(t[0], t[1], t[2]) * xs);
-    }
-}
-
-// ---- fused activation digits (k_act_x24's arithmetic, bgl_prep.hip): one pass is 256 consecutive
-// values, lane l holding values 4l..4l+3 (one float4), a 16-lane row one 64-group g = 4p + l/16.
-// Per group e = exponent of max|x| (frexp), X = rint(x * 2^(21-e)) split into balanced int8 digits
-// X = d0 + 256 d1 + 65536 d2; the record gets the digits, their sums per 32-element half and 2^(e-21).
-template <int CTRL>
-__device__ __forceinline__ uint32_t x_dpp(uint32_t v) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false); }
-__device__ __forceinline__ uint32_t x_umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
-
-__device__ __forceinline__ float4 x_pass_load(const float *x, int p, int lane, int K) {
-    const bgl_f32x4 t = *((const BGL_GLOBAL bgl_f32x4 *)(x + min(256 * p + 4 * lane, K - 4)));
-    return make_float4(t.x, t.y, t.z, t.w);
-}
-
-__device__ __forceinline__ void x_pass_digits(const float4 &v, int p, int lane, int G, int *xl) {
-    const int g = 4 * p + (lane >> 4), q = lane & 15;
-    uint32_t mb = x_umax(x_umax(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
-                         x_umax(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu));
-    mb = x_umax(mb, x_dpp<0xB1>(mb));
-    mb = x_umax(mb, x_dpp<0x4E>(mb));
-    mb = x_umax(mb, x_dpp<0x141>(mb));
-    mb = x_umax(mb, x_dpp<0x140>(mb));             // the group's max |x| bits in all 16 lanes
-    const float mx = __uint_as_float(mb);
-    int e = 0;
-    if (mx > 0.0f) frexpf(mx, &e);
-    const float f[4] = {v.x, v.y, v.z, v.w};
-    uint32_t D0 = 0, D1 = 0, D2 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int X = mx > 0.0f ? (int)rintf(ldexpf(f[i], 21 - e)) : 0;
-        const int d0 = (int)(int8_t)(X & 255);
-        const int X1 = (X - d0) >> 8;
-        const int d1 = (int)(int8_t)(X1 & 255);
-        const int d2 = (X1 - d1) >> 8;
-        D0 |= ((uint32_t)d0 & 255u) << (8 * i);
-        D1 |= ((uint32_t)d1 & 255u) << (8 * i);
-        D2 |= ((uint32_t)d2 & 255u) << (8 * i);
-    }
-    // digit sums of the lane's 4 values, then of its 8-lane half (32 values)
-    int s0 = dot4((int)D0, 0x01010101, 0), s1 = dot4((int)D1, 0x01010101, 0), s2 = dot4((int)D2, 0x01010101, 0);
-    s0 += (int)x_dpp<0xB1>((uint32_t)s0); s1 += (int)x_dpp<0xB1>((uint32_t)s1); s2 += (int)x_dpp<0xB1>((uint32_t)s2);
-    s0 += (int)x_dpp<0x4E>((uint32_t)s0); s1 += (int)x_dpp<0x4E>((uint32_t)s1); s2 += (int)x_dpp<0x4E>((uint32_t)s2);
-    s0 += (int)x_dpp<0x141>((uint32_t)s0); s1 += (int)x_dpp<0x141>((uint32_t)s1); s2 += (int)x_dpp<0x141>((uint32_t)s2);
-    if (g < G) {
-        int *rec = xl + g * XREC_DW;
-        rec[q] = (int)D0; rec[16 + q] = (int)D1; rec[32 + q] = (int)D2;
-        if ((q & 7) == 0) {
-            int4 *ds = reinterpret_cast<int4 *>(rec + XREC_DSUM + 4 * (q >> 3));
-            *ds = make_int4(s0, s1, s2, 0);
-        }
-        if (q == 0) rec[XREC_SCALE] = __float_as_int(mx > 0.0f ? ldexpf(1.0f, e - 21) : 0.0f);
-    }
-}
+// The activation records of the whole K range (bgl_gemv_x.h) sit in LDS: copied from the prep
+// kernel's output, or (FUSE) made by the workgroup itself from the raw column; the first loads go
+// out before the weights' so their latency hides under the weights'.  Lanes of one group read the
+// same record (a broadcast).
+#include "bgl_gemv_x.h"
 
 template <int FMT, int NB, int TR, bool FUSE>
 __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {

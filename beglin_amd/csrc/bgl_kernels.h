@@ -49,6 +49,22 @@ struct GemvLaunch {
     int mtot;                 // total columns of the call (partial buffer stride)
 };
 
+// One expert-sorted gather launch (bgl_moe.hip, bgl_moe_x.hip).
+struct MoeTask {
+    const BglDevTensor *ta;      // expert table [E] (gate, or the only projection); null: use da
+    const BglDevTensor *tb;      // up table [E] in SwiGLU mode
+    BglDevTensor da, db;         // by-value single tensor(s) when ta is null (shared experts)
+    int E, tpe;                  // grid = E * tpe workgroups (tpe: 64-row tiles per expert)
+    const int *off;              // [E+1] sorted segment starts; null: one segment [0, ncols), or with
+    int ncols, seg;              // seg > 0 runs of seg columns (E = ncols / seg rounded up, one tensor)
+    const int *cols;             // activation row of sorted position s (null: s)
+    const int *ymap;             // output row of sorted position s (null: s)
+    GemvAct a;                   // k_moe_gemv: exact-digit activations (k_act_x24 layout); k_moe_x: a.xf, the raw rows
+    float *y;
+    int ystride;
+    int swiglu;                  // y = silu(A x) * (B x)
+};
+
 // ---- kernels (bgl_prep.hip) ----
 __global__ void k_act_w4a8(const float *x, int M, int K, int gsize, int8_t *xq, float *ascale, int *xqsum64);
 __global__ void k_act_x24(const float *x, int M, int K, int8_t *xd, float *xs, int *dsum);
@@ -78,3 +94,8 @@ size_t bgl_gemv_q_lds(int fmt, int K, int TR, int MB);
 // ---- bgl_gemv_x.hip: one-column fp32-activation GEMV over prepared digits ----
 int bgl_launch_gemv_x(const GemvLaunch &L, bool fuse, int nblocks, int TR, int nw, hipStream_t st);
 size_t bgl_gemv_x_lds(int K, int TR, int nw);
+// ---- bgl_moe_x.hip: the MoE gather over records made in the kernel ----
+bool bgl_moe_x_fmt(int fmt);
+size_t bgl_moe_x_lds(int K);
+int bgl_moe_x_waves(int K);
+int bgl_launch_moe_x(const MoeTask &Mt, int K, int nw, hipStream_t st);

@@ -71,20 +71,7 @@ __global__ __launch_bounds__(1024) void k_moe_bucket(const int32_t *__restrict__
 }
 
 // ====================================================================================== gather GEMV
-struct MoeTask {
-    const BglDevTensor *ta;      // expert table [E] (gate, or the only projection); null: use da
-    const BglDevTensor *tb;      // up table [E] in SwiGLU mode
-    BglDevTensor da, db;         // by-value single tensor(s) when ta is null (shared experts)
-    int E, tpe;                  // grid = E * tpe workgroups (tpe: 64-row tiles per expert)
-    const int *off;              // [E+1] sorted segment starts; null: one segment [0, ncols), or with
-    int ncols, seg;              // seg > 0 runs of seg columns (E = ncols / seg rounded up, one tensor)
-    const int *cols;             // activation row of sorted position s (null: s)
-    const int *ymap;             // output row of sorted position s (null: s)
-    GemvAct a;                   // exact-digit activations (k_act_x24 layout)
-    float *y;
-    int ystride;
-    int swiglu;                  // y = silu(A x) * (B x)
-};
+
 
 template <int FMT, int NB, int MB>
 __device__ __forceinline__ void moe_chunk(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
@@ -346,6 +333,52 @@ static int moe_launch(bgl_ctx *c, const MoeTask &Mt, int units, bool wide) {
     return 0;
 }
 
+// Whether a gather launch can run k_moe_x (bgl_moe_x.hip): every tensor it meets in a format that
+// kernel takes, addressable through 32-bit buffer offsets, and the chunk's records fit LDS.
+static bool x_tensor_ok(const BglDevTensor &T) {
+    return bgl_moe_x_fmt(T.fmt) && (size_t)T.ntiles * T.cpr * 1024 < (1ull << 31) && (size_t)T.ntiles * T.nunits * 512 < (1ull << 31);
+}
+static bool moe_x_ok(bgl_ctx *c, const bgl_tensor *sa, const bgl_tensor *sb, const MoeTask &Mt, int K) {
+    if (c->no_moe_x || bgl_moe_x_lds(K) > 160 * 1024) return false;
+    for (const bgl_tensor *st : {sa, sb})
+        if (st)
+            for (const bgl_tensor *e : st->experts)
+                if (!x_tensor_ok(e->T)) return false;
+    if (!Mt.ta && (!x_tensor_ok(Mt.da) || (Mt.swiglu && !x_tensor_ok(Mt.db)))) return false;
+    return true;
+}
+
+// Activation digits already made in this call (reused by the launches that read the same rows).
+struct PrepMemo {
+    const float *x = nullptr;
+    int K = 0;
+    GemvAct A{};
+};
+
+// One gather launch over the activation rows x_rows ([nrows][K]): through k_moe_x, which makes the
+// records from the raw rows itself, when every tensor takes it; else k_act_x24 into digit slot
+// `slot` (once per rows) and k_moe_gemv.
+static int moe_run(bgl_ctx *c, MoeTask &Mt, const bgl_tensor *sa, const bgl_tensor *sb, int units, int slot,
+                   PrepMemo &memo, const float *x_rows, int nrows, int K) {
+    if (moe_x_ok(c, sa, sb, Mt, K)) {
+        memset(&Mt.a, 0, sizeof Mt.a);
+        Mt.a.xf = x_rows;
+        int tok = prof_begin(c, 1);
+        int rc = bgl_launch_moe_x(Mt, K, bgl_moe_x_waves(K), c->stream);
+        prof_end(c, tok);
+        if (rc) return bgl_fail(BGL_E_ARG, "k_moe_x launch: in=%d", K);
+        HIPCHK(hipGetLastError());
+        return 0;
+    }
+    if (memo.x != x_rows || memo.K != K) {
+        int rc = moe_prep(c, slot, x_rows, nrows, K, memo.A);
+        if (rc) return rc;
+        memo.x = x_rows; memo.K = K;
+    }
+    Mt.a = memo.A;
+    return moe_launch(c, Mt, units, task_wide(sa, Mt) || task_wide(sb, Mt));
+}
+
 static int expert_check(const bgl_tensor *t, const char *what) {
     if (!t || t->experts.empty() || !t->dev_table)
         return bgl_fail(BGL_E_ARG, "%s must be an expert tensor (bgl_bind_experts / bgl_experts_from_tensors)", what);
@@ -372,12 +405,12 @@ extern "C" int bgl_gather_matvec_dev(bgl_ctx *c, const bgl_tensor *experts, cons
     if ((rc = moe_bucket(c, idx_dev, N, 1, E, S))) return rc;
     MoeTask Mt;
     memset(&Mt, 0, sizeof Mt);
-    if ((rc = moe_prep(c, 0, x_dev, N, experts->T.K, Mt.a))) return rc;
     int units;
     max_units(experts, Mt.tpe, units);
     Mt.ta = (const BglDevTensor *)experts->dev_table; Mt.E = E; Mt.off = S.off;
     Mt.cols = S.perm; Mt.ymap = S.perm; Mt.y = y_dev; Mt.ystride = experts->T.N;
-    return moe_launch(c, Mt, units, task_wide(experts, Mt));
+    PrepMemo memo;
+    return moe_run(c, Mt, experts, nullptr, units, 0, memo, x_dev, N, experts->T.K);
 }
 
 extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down,
@@ -422,31 +455,29 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
     float *h = (float *)c->moe_g.p, *shh = h + nh, *dd = shh + nsh_h, *sdd = dd + nd;
 
     MoeTask Mr, Ms;
+    PrepMemo mx, mh, ms;                      // digits of x (slot 0), of h (slot 1), of the shared h (slot 0)
     memset(&Mr, 0, sizeof Mr);
-    if ((rc = moe_prep(c, 0, x_dev, T, H, Mr.a))) return rc;
     int units;
     max_units(gate, Mr.tpe, units);
     Mr.ta = (const BglDevTensor *)gate->dev_table; Mr.tb = (const BglDevTensor *)up->dev_table;
     Mr.E = E; Mr.off = S.off; Mr.cols = S.tok; Mr.y = h; Mr.ystride = I; Mr.swiglu = 1;
-    if ((rc = moe_launch(c, Mr, units, task_wide(gate, Mr)))) return rc;
+    if ((rc = moe_run(c, Mr, gate, up, units, 0, mx, x_dev, T, H))) return rc;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
-        Ms.a = Mr.a; Ms.da = sg->T; Ms.db = su->T; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
+        Ms.da = sg->T; Ms.db = su->T; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
         Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
         Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
-        if ((rc = moe_launch(c, Ms, sg->T.nunits, task_wide(nullptr, Ms)))) return rc;
+        if ((rc = moe_run(c, Ms, nullptr, nullptr, sg->T.nunits, 0, mx, x_dev, T, H))) return rc;
     }
     memset(&Mr, 0, sizeof Mr);
-    if ((rc = moe_prep(c, 1, h, P, I, Mr.a))) return rc;
     max_units(down, Mr.tpe, units);
     Mr.ta = (const BglDevTensor *)down->dev_table; Mr.E = E; Mr.off = S.off; Mr.y = dd; Mr.ystride = H;
-    if ((rc = moe_launch(c, Mr, units, task_wide(down, Mr)))) return rc;
+    if ((rc = moe_run(c, Mr, down, nullptr, units, 1, mh, h, P, I))) return rc;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
-        if ((rc = moe_prep(c, 0, shh, T, Ish, Ms.a))) return rc;
         Ms.da = sd->T; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
         Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
-        if ((rc = moe_launch(c, Ms, sd->T.nunits, task_wide(nullptr, Ms)))) return rc;
+        if ((rc = moe_run(c, Ms, nullptr, nullptr, sd->T.nunits, 0, ms, shh, T, Ish))) return rc;
     }
     int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_moe_combine, dim3(nblk((long)T * H)), dim3(256), 0, c->stream, dd, S.pos, idx_dev, w_dev, T, K, H,

@@ -1,0 +1,186 @@
+// bgl_moe_x.hip -- the expert-sorted MoE gather GEMV over LDS activation records (the gate+up with
+// SwiGLU and down projections of moe_ffn_batched, qwen_infer.c:5238-5350, and the routed gather
+// of mlx_moe.cpp's gather_qmm), for experts in int4 g64, int4 g32 fp16-scale, int8 g64 or qNg64.
+//
+// A workgroup owns one 64-row tile of one expert (gate and up rows together in SwiGLU mode; lane =
+// row) and walks the expert's sorted segment in chunks of up to MB = 4 token columns.  Per chunk it
+// makes the columns' activation records (bgl_gemv_x.h) from the raw fp32 rows itself -- so a routed
+// FFN needs no activation-prep launches -- while its waves' first weight loads are in flight; then
+// the waves take the 64-groups in turn (each group once per tensor, two in flight): each lane
+// decodes its row's group once and folds it against every column (the records are read as
+// broadcasts).  Row sums go over the waves in order; SwiGLU
+// (moe_swiglu_inplace, qwen_infer.c:3475-3481) is applied before the store.
+#include "bgl_gemv_x.h"
+
+#define MX_MB 4                  // token columns per chunk
+#define MX_MAXW 8                // waves per workgroup
+
+bool bgl_moe_x_fmt(int fmt) { return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64; }
+
+// LDS: MB columns of records and the wave partials.
+size_t bgl_moe_x_lds(int K) {
+    return (size_t)MX_MB * (K / 64) * XREC_DW * 4 + (size_t)MX_MAXW * 2 * MX_MB * BGL_TILE * 4;
+}
+
+template <int FMT, int NB, int MB>
+__device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
+                                            int tile, int base, int mc, int *xl) {
+    const int nthr = blockDim.x, nw = nthr >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int K = Ta.K, G = K >> 6, RC = G * XREC_DW, NPX = (K + 255) >> 8;
+
+    // ---- a wave's items: its groups wave, wave + nw, ... -- each once per tensor in SwiGLU mode
+    // (gate then up) -- two in flight; the first two go out ahead of the activation work
+    const XRes Ra = x_res<FMT>(Ta, tile), Rb = x_res<FMT>(Tb, tile);
+    const XLane xlane = x_lane<FMT, NB, 1>(lane, 0);
+    const int ns = (G - 1 - wave) / nw + 1, NI = glu ? 2 * ns : ns;     // nw <= G: every wave has a group
+    auto item_load = [&](XRaw<FMT, NB> &r, int j) {
+        const int g = wave + (glu ? j >> 1 : j) * nw;
+        x_load<FMT, NB, 1>(r, glu && (j & 1) ? Rb : Ra, xlane, g, j < NI);
+    };
+    XRaw<FMT, NB> c[2];
+    item_load(c[0], 0);
+    item_load(c[1], 1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- the chunk's records, made from the raw rows: pass pi = column pi / NPX, values
+    // 256 * (pi % NPX) ..
+    for (int pi = wave; pi < mc * NPX; pi += nw) {
+        const int m = pi / NPX, p = pi - m * NPX;
+        const int row = Mt.cols ? uni(Mt.cols)[base + m] : base + m;
+        const float4 v = x_pass_load(Mt.a.xf + (size_t)row * K, p, lane, K);
+        x_pass_digits(v, p, lane, G, xl + m * RC);
+    }
+    __syncthreads();
+
+    float acc[MB], accb[MB];
+#pragma unroll
+    for (int m = 0; m < MB; m++) { acc[m] = 0.0f; accb[m] = 0.0f; }
+    for (int j0 = 0; j0 < NI; j0 += 2) {
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+            const int j = j0 + jj;
+            if (j < NI) {
+                const bool up = glu && (j & 1);
+                const int *rec = xl + (wave + (glu ? j >> 1 : j) * nw) * XREC_DW;
+                const XDec<FMT, NB> d = x_decode<FMT, NB>(c[jj]);
+                // columns one loop iteration at a time (not unrolled: the scheduler would hoist every
+                // column's record reads, and their registers, to the front); the accumulator is
+                // picked by wave-uniform branches
+#pragma unroll 1
+                for (int m = 0; m < mc; m++) {
+                    const float v = x_dot<FMT, NB>(d, rec + m * RC);
+#pragma unroll
+                    for (int q = 0; q < MB; q++) {
+                        if (q == m && !up) acc[q] += v;
+                        if (q == m && up) accb[q] += v;
+                    }
+                }
+            }
+            item_load(c[jj], j + 2);
+        }
+    }
+
+    // ---- row sums over the waves in order (lane = row)
+    float *red = reinterpret_cast<float *>(xl + MX_MB * RC);      // [wave][2][MB][64]
+#pragma unroll
+    for (int m = 0; m < MB; m++) {
+        red[((wave * 2 + 0) * MB + m) * BGL_TILE + lane] = acc[m];
+        red[((wave * 2 + 1) * MB + m) * BGL_TILE + lane] = accb[m];
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < mc * BGL_TILE; t += nthr) {
+        const int m = t / BGL_TILE, rl = t % BGL_TILE, row = tile * BGL_TILE + rl;
+        if (row < Ta.N) {
+            float va = red[(0 * MB + m) * BGL_TILE + rl], vb = red[(1 * MB + m) * BGL_TILE + rl];
+            for (int w = 1; w < nw; w++) {
+                va += red[((w * 2 + 0) * MB + m) * BGL_TILE + rl];
+                vb += red[((w * 2 + 1) * MB + m) * BGL_TILE + rl];
+            }
+            const float out = glu ? (va / (1.0f + expf(-va))) * vb : va;
+            const int yr = Mt.ymap ? Mt.ymap[base + m] : base + m;
+            Mt.y[(size_t)yr * Mt.ystride + row] = out;
+        }
+    }
+    __syncthreads();                                               // the next chunk reuses the LDS
+}
+
+template <int FMT, int NB>
+__device__ __forceinline__ void moe_x_tile(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
+                                           int tile, int seg0, int ncols, int *xl) {
+    int c0 = 0;
+    for (; ncols - c0 >= 2; c0 += MX_MB) {
+        const int rem = ncols - c0;
+        moe_x_chunk<FMT, NB, MX_MB>(Mt, Ta, Tb, glu, tile, seg0 + c0, rem < MX_MB ? rem : MX_MB, xl);
+    }
+    if (c0 < ncols) moe_x_chunk<FMT, NB, 1>(Mt, Ta, Tb, glu, tile, seg0 + c0, 1, xl);
+}
+
+// Expert record through the constant address space (scalar loads, wave-uniform addresses).
+__device__ __forceinline__ BglDevTensor mx_tensor(const BglDevTensor *p) {
+    static_assert(sizeof(BglDevTensor) % 4 == 0, "BglDevTensor is loaded as dwords");
+    int w[sizeof(BglDevTensor) / 4];
+    ucint q = uni(reinterpret_cast<const int *>(p));
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(BglDevTensor) / 4); i++) w[i] = q[i];
+    BglDevTensor t;
+    __builtin_memcpy(&t, w, sizeof t);
+    return t;
+}
+
+// Grid: E x tpe workgroups.  SEG: the segments are consecutive runs of Mt.seg columns of
+// one by-value tensor (the shared experts).  At least 3 waves per SIMD: the widest formats then fit
+// 168 registers without spilling.
+template <bool SEG>
+__global__ __launch_bounds__(MX_MAXW * BGL_TILE, 3) void k_moe_x(MoeTask Mt) {
+    extern __shared__ __align__(16) int xl[];
+    const int e = blockIdx.x / Mt.tpe, tile = blockIdx.x % Mt.tpe;
+    int seg0 = 0, ncols = Mt.ncols;
+    if constexpr (SEG) { seg0 = e * Mt.seg; ncols = min(Mt.seg, Mt.ncols - seg0); }
+    else if (Mt.off) { seg0 = uni(Mt.off)[e]; ncols = uni(Mt.off)[e + 1] - seg0; }
+    if (ncols <= 0) return;                                   // expert not routed to by any pair
+    const BglDevTensor Ta = Mt.ta ? mx_tensor(Mt.ta + e) : Mt.da;
+    if (tile >= Ta.ntiles) return;
+    const bool glu = Mt.swiglu != 0;
+    const BglDevTensor Tb = glu ? (Mt.tb ? mx_tensor(Mt.tb + e) : Mt.db) : Ta;
+    switch (Ta.fmt) {
+    case BGL_Q4G32H: moe_x_tile<BGL_Q4G32H, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+    case BGL_Q4G64: moe_x_tile<BGL_Q4G64, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+    case BGL_Q8G64: moe_x_tile<BGL_Q8G64, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+    case BGL_QNG64:
+        switch (Ta.bits) {
+        case 2: moe_x_tile<BGL_QNG64, 2>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 3: moe_x_tile<BGL_QNG64, 3>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 4: moe_x_tile<BGL_QNG64, 4>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 5: moe_x_tile<BGL_QNG64, 5>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 6: moe_x_tile<BGL_QNG64, 6>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 7: moe_x_tile<BGL_QNG64, 7>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 8: moe_x_tile<BGL_QNG64, 8>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 9: moe_x_tile<BGL_QNG64, 9>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 10: moe_x_tile<BGL_QNG64, 10>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 11: moe_x_tile<BGL_QNG64, 11>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 12: moe_x_tile<BGL_QNG64, 12>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 13: moe_x_tile<BGL_QNG64, 13>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 14: moe_x_tile<BGL_QNG64, 14>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 15: moe_x_tile<BGL_QNG64, 15>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        default: break;
+        }
+        break;
+    default: break;
+    }
+}
+
+// Mt.a.xf: the raw fp32 activation rows (row stride K = the tensors' in).  nw waves (<= 8, and at
+// most one per 64-group).
+int bgl_launch_moe_x(const MoeTask &Mt, int K, int nw, hipStream_t st) {
+    if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW) return -1;
+    const size_t lds = bgl_moe_x_lds(K);
+    if (lds > 160 * 1024) return -1;
+    const dim3 g(Mt.E * Mt.tpe), b(nw * BGL_TILE);
+    const bool seg = !Mt.off && Mt.seg > 0;
+    if (seg) hipLaunchKernelGGL(k_moe_x<true>, g, b, lds, st, Mt);
+    else hipLaunchKernelGGL(k_moe_x<false>, g, b, lds, st, Mt);
+    return 0;
+}
+
+int bgl_moe_x_waves(int K) { return K / 64 < MX_MAXW ? K / 64 : MX_MAXW; }

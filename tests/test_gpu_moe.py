@@ -408,3 +408,27 @@ def test_moe_error_paths(ctx, torch_dev, oracle):
     ctx.sync()
     for t in (g, u, d, single, t256):
         t.free()
+
+
+@pytest.mark.parametrize("T", [1, 6, 21])
+def test_moe_x_matches_prep_path(torch_dev, oracle, monkeypatch, T):
+    """The gather that makes its activation records in the kernel (k_moe_x) against the prep
+    kernel + k_moe_gemv path and the oracle: few experts so segments run 1..12 columns (chunks of
+    4 and a single last column), hidden 320 (a partial last pass of 256 values), inter 192 (a
+    partly filled slot), shared experts over T > 4 columns in segments."""
+    import beglin_amd
+    torch = torch_dev
+    E, H, I, K, Ish = 4, 320, 192, 2, 320
+    say("moe_x vs prep", T)
+    fm = [(5, 0), (2, 0), (4, 7), (4, 15)]
+    gate, up, down, shared = moe_setup(oracle, 6000 + T, E, H, I, Ish, fm, down_fmts=fm[::-1], sh_fmt=(4, 12))
+    x = seeded_normal(90 + T, (T, H))
+    idx, w = oracle.route(seeded_normal(91 + T, (T, E)), K, True)
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("BGL_NO_MOE_X", flag)
+        c = beglin_amd.Context(0)
+        outs.append(run_moe(c, torch, gate, up, down, shared, x, idx, w))
+        c.close()
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    assert relerr(outs[0], ref) <= TOL and relerr(outs[1], ref) <= TOL and relerr(outs[0], outs[1]) <= 2 * TOL
