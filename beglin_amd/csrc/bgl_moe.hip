@@ -15,6 +15,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "bgl_gemv_impl.h"
@@ -339,7 +340,7 @@ static bool x_tensor_ok(const BglDevTensor &T) {
     return bgl_moe_x_fmt(T.fmt) && (size_t)T.ntiles * T.cpr * 1024 < (1ull << 31) && (size_t)T.ntiles * T.nunits * 512 < (1ull << 31);
 }
 static bool moe_x_ok(bgl_ctx *c, const bgl_tensor *sa, const bgl_tensor *sb, const MoeTask &Mt, int K) {
-    if (c->no_moe_x || bgl_moe_x_lds(K) > 160 * 1024) return false;
+    if (c->no_moe_x || bgl_moe_x_lds(K, 16) > 160 * 1024) return false;
     for (const bgl_tensor *st : {sa, sb})
         if (st)
             for (const bgl_tensor *e : st->experts)
@@ -359,12 +360,12 @@ struct PrepMemo {
 // records from the raw rows itself, when every tensor takes it; else k_act_x24 into digit slot
 // `slot` (once per rows) and k_moe_gemv.
 static int moe_run(bgl_ctx *c, MoeTask &Mt, const bgl_tensor *sa, const bgl_tensor *sb, int units, int slot,
-                   PrepMemo &memo, const float *x_rows, int nrows, int K) {
+                   PrepMemo &memo, const float *x_rows, int nrows, int K, long active_wgs) {
     if (moe_x_ok(c, sa, sb, Mt, K)) {
         memset(&Mt.a, 0, sizeof Mt.a);
         Mt.a.xf = x_rows;
         int tok = prof_begin(c, 1);
-        int rc = bgl_launch_moe_x(Mt, K, bgl_moe_x_waves(K), c->stream);
+        int rc = bgl_launch_moe_x(Mt, K, bgl_moe_x_waves(K, active_wgs, c->x_waves), c->stream);
         prof_end(c, tok);
         if (rc) return bgl_fail(BGL_E_ARG, "k_moe_x launch: in=%d", K);
         HIPCHK(hipGetLastError());
@@ -410,7 +411,7 @@ extern "C" int bgl_gather_matvec_dev(bgl_ctx *c, const bgl_tensor *experts, cons
     Mt.ta = (const BglDevTensor *)experts->dev_table; Mt.E = E; Mt.off = S.off;
     Mt.cols = S.perm; Mt.ymap = S.perm; Mt.y = y_dev; Mt.ystride = experts->T.N;
     PrepMemo memo;
-    return moe_run(c, Mt, experts, nullptr, units, 0, memo, x_dev, N, experts->T.K);
+    return moe_run(c, Mt, experts, nullptr, units, 0, memo, x_dev, N, experts->T.K, (long)std::min(E, N) * Mt.tpe);
 }
 
 extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down,
@@ -461,23 +462,25 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
     max_units(gate, Mr.tpe, units);
     Mr.ta = (const BglDevTensor *)gate->dev_table; Mr.tb = (const BglDevTensor *)up->dev_table;
     Mr.E = E; Mr.off = S.off; Mr.cols = S.tok; Mr.y = h; Mr.ystride = I; Mr.swiglu = 1;
-    if ((rc = moe_run(c, Mr, gate, up, units, 0, mx, x_dev, T, H))) return rc;
+    // workgroups with work: at most one expert per pair, every tile of it
+    const long act_r = (long)std::min(E, P);
+    if ((rc = moe_run(c, Mr, gate, up, units, 0, mx, x_dev, T, H, act_r * Mr.tpe))) return rc;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         Ms.da = sg->T; Ms.db = su->T; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
         Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
         Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
-        if ((rc = moe_run(c, Ms, nullptr, nullptr, sg->T.nunits, 0, mx, x_dev, T, H))) return rc;
+        if ((rc = moe_run(c, Ms, nullptr, nullptr, sg->T.nunits, 0, mx, x_dev, T, H, (long)Ms.E * Ms.tpe))) return rc;
     }
     memset(&Mr, 0, sizeof Mr);
     max_units(down, Mr.tpe, units);
     Mr.ta = (const BglDevTensor *)down->dev_table; Mr.E = E; Mr.off = S.off; Mr.y = dd; Mr.ystride = H;
-    if ((rc = moe_run(c, Mr, down, nullptr, units, 1, mh, h, P, I))) return rc;
+    if ((rc = moe_run(c, Mr, down, nullptr, units, 1, mh, h, P, I, act_r * Mr.tpe))) return rc;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         Ms.da = sd->T; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
         Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
-        if ((rc = moe_run(c, Ms, nullptr, nullptr, sd->T.nunits, 0, ms, shh, T, Ish))) return rc;
+        if ((rc = moe_run(c, Ms, nullptr, nullptr, sd->T.nunits, 0, ms, shh, T, Ish, (long)Ms.E * Ms.tpe))) return rc;
     }
     int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_moe_combine, dim3(nblk((long)T * H)), dim3(256), 0, c->stream, dd, S.pos, idx_dev, w_dev, T, K, H,

@@ -13,13 +13,14 @@
 #include "bgl_gemv_x.h"
 
 #define MX_MB 4                  // token columns per chunk
-#define MX_MAXW 8                // waves per workgroup
+#define MX_DEPTH 2               // items (a group of one tensor) a wave keeps in flight
+#define MX_MAXW 16               // waves per workgroup (instances of 8 and 16)
 
 bool bgl_moe_x_fmt(int fmt) { return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64; }
 
 // LDS: MB columns of records and the wave partials.
-size_t bgl_moe_x_lds(int K) {
-    return (size_t)MX_MB * (K / 64) * XREC_DW * 4 + (size_t)MX_MAXW * 2 * MX_MB * BGL_TILE * 4;
+size_t bgl_moe_x_lds(int K, int nw) {
+    return (size_t)MX_MB * (K / 64) * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * BGL_TILE * 4;
 }
 
 template <int FMT, int NB, int MB>
@@ -30,7 +31,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
     const int K = Ta.K, G = K >> 6, RC = G * XREC_DW, NPX = (K + 255) >> 8;
 
     // ---- a wave's items: its groups wave, wave + nw, ... -- each once per tensor in SwiGLU mode
-    // (gate then up) -- two in flight; the first two go out ahead of the activation work
+    // (gate then up) -- MX_DEPTH in flight; the first ones go out ahead of the activation work
     const XRes Ra = x_res<FMT>(Ta, tile), Rb = x_res<FMT>(Tb, tile);
     const XLane xlane = x_lane<FMT, NB, 1>(lane, 0);
     const int ns = (G - 1 - wave) / nw + 1, NI = glu ? 2 * ns : ns;     // nw <= G: every wave has a group
@@ -38,9 +39,9 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
         const int g = wave + (glu ? j >> 1 : j) * nw;
         x_load<FMT, NB, 1>(r, glu && (j & 1) ? Rb : Ra, xlane, g, j < NI);
     };
-    XRaw<FMT, NB> c[2];
-    item_load(c[0], 0);
-    item_load(c[1], 1);
+    XRaw<FMT, NB> c[MX_DEPTH];
+#pragma unroll
+    for (int j = 0; j < MX_DEPTH; j++) item_load(c[j], j);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- the chunk's records, made from the raw rows: pass pi = column pi / NPX, values
@@ -56,9 +57,9 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
     float acc[MB], accb[MB];
 #pragma unroll
     for (int m = 0; m < MB; m++) { acc[m] = 0.0f; accb[m] = 0.0f; }
-    for (int j0 = 0; j0 < NI; j0 += 2) {
+    for (int j0 = 0; j0 < NI; j0 += MX_DEPTH) {
 #pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
+        for (int jj = 0; jj < MX_DEPTH; jj++) {
             const int j = j0 + jj;
             if (j < NI) {
                 const bool up = glu && (j & 1);
@@ -77,7 +78,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
                     }
                 }
             }
-            item_load(c[jj], j + 2);
+            item_load(c[jj], j + MX_DEPTH);
         }
     }
 
@@ -131,8 +132,8 @@ __device__ __forceinline__ BglDevTensor mx_tensor(const BglDevTensor *p) {
 // Grid: E x tpe workgroups.  SEG: the segments are consecutive runs of Mt.seg columns of
 // one by-value tensor (the shared experts).  At least 3 waves per SIMD: the widest formats then fit
 // 168 registers without spilling.
-template <bool SEG>
-__global__ __launch_bounds__(MX_MAXW * BGL_TILE, 3) void k_moe_x(MoeTask Mt) {
+template <bool SEG, int NWMAX>
+__global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(MoeTask Mt) {
     extern __shared__ __align__(16) int xl[];
     const int e = blockIdx.x / Mt.tpe, tile = blockIdx.x % Mt.tpe;
     int seg0 = 0, ncols = Mt.ncols;
@@ -174,13 +175,26 @@ __global__ __launch_bounds__(MX_MAXW * BGL_TILE, 3) void k_moe_x(MoeTask Mt) {
 // most one per 64-group).
 int bgl_launch_moe_x(const MoeTask &Mt, int K, int nw, hipStream_t st) {
     if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW) return -1;
-    const size_t lds = bgl_moe_x_lds(K);
+    const size_t lds = bgl_moe_x_lds(K, nw);
     if (lds > 160 * 1024) return -1;
     const dim3 g(Mt.E * Mt.tpe), b(nw * BGL_TILE);
     const bool seg = !Mt.off && Mt.seg > 0;
-    if (seg) hipLaunchKernelGGL(k_moe_x<true>, g, b, lds, st, Mt);
-    else hipLaunchKernelGGL(k_moe_x<false>, g, b, lds, st, Mt);
+    if (nw <= 8) {
+        if (seg) hipLaunchKernelGGL((k_moe_x<true, 8>), g, b, lds, st, Mt);
+        else hipLaunchKernelGGL((k_moe_x<false, 8>), g, b, lds, st, Mt);
+    } else {
+        if (seg) hipLaunchKernelGGL((k_moe_x<true, 16>), g, b, lds, st, Mt);
+        else hipLaunchKernelGGL((k_moe_x<false, 16>), g, b, lds, st, Mt);
+    }
     return 0;
 }
 
-int bgl_moe_x_waves(int K) { return K / 64 < MX_MAXW ? K / 64 : MX_MAXW; }
+// Waves per workgroup: 12 when the launch has few active workgroups (every CU then holds at most
+// one, so more waves keep more loads in flight), else 8 (two workgroups per CU); never more than
+// one per 64-group.  (Measured on the DeepSeek-V2-Lite layer: T=1 72.8 vs 81.3 us with 12 waves,
+// T=8 and T=64 slower with 12 or 16.)
+int bgl_moe_x_waves(int K, long active_wgs, int cap) {
+    int w = active_wgs < 256 ? 12 : 8;
+    if (cap > 0) w = cap < MX_MAXW ? cap : MX_MAXW;
+    return K / 64 < w ? K / 64 : w;
+}
