@@ -293,7 +293,7 @@ def time_prep(ctx, torch, stream, wl, steps):
 
 
 def moe_roofline(ctx, torch, stream, wl, reps):
-    """k_moe_gemv's own time: eager steps with an event pair around every launch (bgl_prof_*),
+    """The gather kernel's own time: eager steps with an event pair around every launch (bgl_prof_*),
     summed per phase on the context's stream; achieved = step bytes / gather-GEMV time."""
     ctx.prof_enable(True)
     ctx.prof_read()
@@ -308,7 +308,7 @@ def moe_roofline(ctx, torch, stream, wl, reps):
     o_ms, o_n = ph["other"][0] / reps, ph["other"][1] // reps
     achieved = wl.nbytes() / (g_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_moe_gemv (bgl_moe.hip)",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_moe_x (bgl_moe_x.hip)",
             "launches_per_step": g_n, "kernel_us_per_launch": round(g_ms * 1e3 / max(g_n, 1), 3),
             "bytes_per_launch": round(wl.nbytes() / max(g_n, 1)),
             "prep_us_per_step": round(p_ms * 1e3, 2), "prep_launches": p_n,
