@@ -49,6 +49,8 @@ struct GemvLaunch {
     int mtot;                 // total columns of the call (partial buffer stride)
 };
 
+#define MOE_MAX_K 16        // top-K limit of the combine
+
 // One expert-sorted gather launch (bgl_moe.hip, bgl_moe_x.hip).
 struct MoeTask {
     const BglDevTensor *ta;      // expert table [E] (gate, or the only projection); null: use da
@@ -63,6 +65,14 @@ struct MoeTask {
     float *y;
     int ystride;
     int swiglu;                  // y = silu(A x) * (B x)
+    // k_moe_x only (the shared down projection of a routed FFN, column = token): when cout is set,
+    // the store is the whole combine, cout[t] = sum over t's experts in ascending id of
+    // w * cdown[pos] + this launch's value (k_moe_combine's arithmetic)
+    float *cout;
+    const float *cdown, *cw;
+    const int *cpos;
+    const int32_t *cidx;
+    int ck;
 };
 
 // ---- kernels (bgl_prep.hip) ----

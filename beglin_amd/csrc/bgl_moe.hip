@@ -29,7 +29,6 @@
 
 #define MOE_MB 4            // token columns per weight pass of one tile
 #define MOE_MAXW 8          // waves per workgroup: 512 threads leave 256 VGPRs for the widest formats
-#define MOE_MAX_K 16        // top-K limit of the combine kernel
 
 static inline unsigned nblk(long n, int bs = 256) { return (unsigned)((n + bs - 1) / bs); }
 
@@ -265,13 +264,21 @@ struct MoeScratch {
     int *off, *perm, *pos, *tok;
 };
 
-static int moe_bucket(bgl_ctx *c, const int32_t *idx_dev, int P, int K, int E, MoeScratch &S) {
+// The bucketing outputs in the context's scratch: off [E+1], perm [P], pos [P], tok [P].
+static int moe_scratch(bgl_ctx *c, int P, int E, MoeScratch &S) {
     const size_t lds = ((size_t)E + 1 + P) * 4;
     if (lds > 64 * 1024)
         return bgl_fail(BGL_E_ARG, "MoE bucketing: %d pairs over %d experts exceed one workgroup's LDS", P, E);
     if (dbuf_reserve(c, c->moe_meta, ((size_t)E + 1 + 3 * (size_t)P) * 4, false)) return BGL_E_NOMEM;
     int *b = (int *)c->moe_meta.p;
     S.off = b; S.perm = b + E + 1; S.pos = S.perm + P; S.tok = S.pos + P;
+    return 0;
+}
+
+static int moe_bucket(bgl_ctx *c, const int32_t *idx_dev, int P, int K, int E, MoeScratch &S) {
+    int rc = moe_scratch(c, P, E, S);
+    if (rc) return rc;
+    const size_t lds = ((size_t)E + 1 + P) * 4;
     int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_moe_bucket, dim3(1), dim3(1024), lds, c->stream, idx_dev, P, K, E, S.off, S.perm, S.pos, S.tok);
     prof_end(c, tok);
@@ -361,6 +368,7 @@ struct PrepMemo {
 // `slot` (once per rows) and k_moe_gemv.
 static int moe_run(bgl_ctx *c, MoeTask &Mt, const bgl_tensor *sa, const bgl_tensor *sb, int units, int slot,
                    PrepMemo &memo, const float *x_rows, int nrows, int K, long active_wgs) {
+    if (Mt.cout && !moe_x_ok(c, sa, sb, Mt, K)) return bgl_fail(BGL_E_ARG, "internal: a fused combine needs k_moe_x");
     if (moe_x_ok(c, sa, sb, Mt, K)) {
         memset(&Mt.a, 0, sizeof Mt.a);
         Mt.a.xf = x_rows;
@@ -414,9 +422,10 @@ extern "C" int bgl_gather_matvec_dev(bgl_ctx *c, const bgl_tensor *experts, cons
     return moe_run(c, Mt, experts, nullptr, units, 0, memo, x_dev, N, experts->T.K, (long)std::min(E, N) * Mt.tpe);
 }
 
-extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down,
-                               const bgl_tensor *sg, const bgl_tensor *su, const bgl_tensor *sd, const float *x_dev,
-                               const int32_t *idx_dev, const float *w_dev, int T, int K, float *out_dev) {
+// The routed FFN; pre: the pairs' bucketing when the caller already made it (the whole-layer entry).
+static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down, const bgl_tensor *sg,
+                   const bgl_tensor *su, const bgl_tensor *sd, const float *x_dev, const int32_t *idx_dev, const float *w_dev,
+                   int T, int K, float *out_dev, const MoeScratch *pre) {
     if (!c || !x_dev || !idx_dev || !w_dev || !out_dev || T < 1 || K < 1 || K > MOE_MAX_K)
         return bgl_fail(BGL_E_ARG, "bgl_moe_ffn_dev: bad argument (T=%d, K=%d; 1 <= K <= %d)", T, K, MOE_MAX_K);
     int rc;
@@ -449,7 +458,8 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
     HIPCHK(hipSetDevice(c->device));
     const int P = T * K;
     MoeScratch S;
-    if ((rc = moe_bucket(c, idx_dev, P, K, E, S))) return rc;
+    if (pre) S = *pre;
+    else if ((rc = moe_bucket(c, idx_dev, P, K, E, S))) return rc;
     // fp32 work rows: h [P][I], shared h [T][Ish], routed down [P][H], shared down [T][H]
     const size_t nh = (size_t)P * I, nsh_h = (size_t)T * Ish, nd = (size_t)P * H, nsd = (size_t)T * H;
     if (dbuf_reserve(c, c->moe_g, (nh + nsh_h + nd + nsd) * 4, false)) return BGL_E_NOMEM;
@@ -476,18 +486,30 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
     max_units(down, Mr.tpe, units);
     Mr.ta = (const BglDevTensor *)down->dev_table; Mr.E = E; Mr.off = S.off; Mr.y = dd; Mr.ystride = H;
     if ((rc = moe_run(c, Mr, down, nullptr, units, 1, mh, h, P, I, act_r * Mr.tpe))) return rc;
+    bool combined = false;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         Ms.da = sd->T; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
         Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
+        if (moe_x_ok(c, nullptr, nullptr, Ms, Ish)) {      // the combine rides on the shared down's store
+            Ms.cout = out_dev; Ms.cdown = dd; Ms.cw = w_dev; Ms.cpos = S.pos; Ms.cidx = idx_dev; Ms.ck = K;
+            combined = true;
+        }
         if ((rc = moe_run(c, Ms, nullptr, nullptr, sd->T.nunits, 0, ms, shh, T, Ish, (long)Ms.E * Ms.tpe))) return rc;
     }
+    if (combined) return 0;
     int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_moe_combine, dim3(nblk((long)T * H)), dim3(256), 0, c->stream, dd, S.pos, idx_dev, w_dev, T, K, H,
                        nsh ? sdd : nullptr, out_dev);
     prof_end(c, tok);
     HIPCHK(hipGetLastError());
     return 0;
+}
+
+extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down,
+                               const bgl_tensor *sg, const bgl_tensor *su, const bgl_tensor *sd, const float *x_dev,
+                               const int32_t *idx_dev, const float *w_dev, int T, int K, float *out_dev) {
+    return moe_ffn(c, gate, up, down, sg, su, sd, x_dev, idx_dev, w_dev, T, K, out_dev, nullptr);
 }
 
 // ================================================================================== router
@@ -524,39 +546,34 @@ __global__ __launch_bounds__(ROUTE_EPW * 64) void k_moe_router_scores(const floa
     if (lane == 0) scores[(size_t)t * E + e] = bias ? __fadd_rn((float)acc, bias[e]) : (float)acc;
 }
 
-// softmax, top-K and renorm of one token per wave (grid T, 64 threads).
-__global__ __launch_bounds__(64) void k_moe_route_topk(const float *__restrict__ scores, int E, int K, int renorm,
-                                                       int32_t *__restrict__ idx_out, float *__restrict__ w_out) {
-    __shared__ float sc[ROUTE_MAXE];
-    const int t = blockIdx.x, lane = threadIdx.x;
+// Softmax, top-K and renorm of one token's E scores by one wave; lane 0 returns the K picks.
+__device__ __forceinline__ void route_topk_wave(const float *__restrict__ sc_t, int E, int K, int renorm, int lane,
+                                                int *sel_i, float *sel_w) {
     constexpr int PL = ROUTE_MAXE / 64;                      // scores per lane: expert lane + 64j
     float v[PL];
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < PL; j++) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? scores[(size_t)t * E + e] : 0.0f;
+        v[j] = e < E ? sc_t[e] : 0.0f;
         if (e < E) mx = fmaxf(mx, v[j]);
     }
     for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
 #pragma unroll
     for (int j = 0; j < PL; j++) {
         const int e = lane + 64 * j;
-        if (e < E) {
-            v[j] = (float)exp((double)__fsub_rn(v[j], mx));
-            sc[e] = v[j];
-        }
+        if (e < E) v[j] = (float)exp((double)__fsub_rn(v[j], mx));
     }
-    __syncthreads();                                         // the workgroup is this one wave
+    // the double sum in expert order, every lane reading the values across the wave
     double sum = 0.0;
-    if (lane == 0)
-        for (int e = 0; e < E; e++) sum += (double)sc[e];
-    sum = __shfl(sum, 0);
+    for (int e = 0; e < E; e++) {
+        const int j = e >> 6;
+        const float ve = j == 0 ? v[0] : j == 1 ? v[PL > 1 ? 1 : 0] : j == 2 ? v[PL > 2 ? 2 : 0] : v[PL > 3 ? 3 : 0];
+        sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ve), e & 63));
+    }
     unsigned used = 0;                                       // bit j: expert lane + 64j selected
 #pragma unroll
     for (int j = 0; j < PL; j++) v[j] = (float)((double)v[j] / sum);
-    float sel_w[MOE_MAX_K];
-    int sel_i[MOE_MAX_K];
     for (int k = 0; k < K; k++) {
         // this lane's best unselected expert (lowest id first among equal values), then the wave's
         float bv = -1.0f;
@@ -575,36 +592,98 @@ __global__ __launch_bounds__(64) void k_moe_route_topk(const float *__restrict__
         sel_w[k] = bv;
         sel_i[k] = bi;
     }
-    if (lane != 0) return;
-    if (renorm) {
+    if (lane == 0 && renorm) {
         double s = 0.0;
         for (int k = 0; k < K; k++) s += (double)sel_w[k];
         if (s > 0.0)
             for (int k = 0; k < K; k++) sel_w[k] = (float)((double)sel_w[k] / s);
     }
+}
+
+// softmax, top-K and renorm of one token per wave (grid T, 64 threads).
+__global__ __launch_bounds__(64) void k_moe_route_topk(const float *__restrict__ scores, int E, int K, int renorm,
+                                                       int32_t *__restrict__ idx_out, float *__restrict__ w_out) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    float sel_w[MOE_MAX_K];
+    int sel_i[MOE_MAX_K];
+    route_topk_wave(scores + (size_t)t * E, E, K, renorm, lane, sel_i, sel_w);
+    if (lane != 0) return;
     for (int k = 0; k < K; k++) {
         idx_out[(size_t)t * K + k] = sel_i[k];
         w_out[(size_t)t * K + k] = sel_w[k];
     }
 }
 
-extern "C" int bgl_moe_route_dev(bgl_ctx *c, const float *rw_dev, const float *rb_dev, int E, int in, const float *x_dev,
-                                 int T, int K, int renorm, int32_t *idx_dev, float *w_dev) {
-    if (!c || !rw_dev || !x_dev || !idx_dev || !w_dev || T < 1)
-        return bgl_fail(BGL_E_ARG, "bgl_moe_route_dev: bad argument");
+// The top-K of every token (one wave per token in turn) and the bucketing of the T*K pairs by
+// expert (k_moe_bucket's outputs, stable in pair order) in one workgroup: the whole routing after
+// the scores is one launch.
+__global__ __launch_bounds__(1024) void k_moe_route_bucket(const float *__restrict__ scores, int T, int E, int K, int renorm,
+                                                           int32_t *__restrict__ idx_out, float *__restrict__ w_out,
+                                                           int *__restrict__ off, int *__restrict__ perm,
+                                                           int *__restrict__ pos, int *__restrict__ tok) {
+    extern __shared__ int sm[];
+    int *start = sm;               // [E + 1]
+    int *ids = sm + E + 1;         // [P]
+    const int P = T * K, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) start[e] = 0;
+    for (int t = wave; t < T; t += nw) {
+        float sel_w[MOE_MAX_K];
+        int sel_i[MOE_MAX_K];
+        route_topk_wave(scores + (size_t)t * E, E, K, renorm, lane, sel_i, sel_w);
+        if (lane == 0)
+            for (int k = 0; k < K; k++) {
+                idx_out[(size_t)t * K + k] = sel_i[k];
+                w_out[(size_t)t * K + k] = sel_w[k];
+                ids[t * K + k] = sel_i[k];
+            }
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += blockDim.x) atomicAdd(&start[ids[p]], 1);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int e = 0; e < E; e++) { const int n = start[e]; start[e] = run; run += n; }
+        start[E] = run;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) off[e] = start[e];
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        const int e = ids[p];
+        int rank = 0;
+        for (int q = 0; q < p; q++) rank += ids[q] == e;
+        const int s = start[e] + rank;
+        perm[s] = p;
+        pos[p] = s;
+        tok[s] = p / K;
+    }
+}
+
+// The router's checks and its scores kernel; *scores: the [T][E] scores in the context's scratch.
+static int route_scores(bgl_ctx *c, const char *who, const float *rw_dev, const float *rb_dev, int E, int in,
+                        const float *x_dev, int T, int K, float **scores) {
+    if (!c || !rw_dev || !x_dev || T < 1) return bgl_fail(BGL_E_ARG, "%s: bad argument", who);
     if (E < 1 || E > ROUTE_MAXE || K < 1 || K > E || K > MOE_MAX_K)
-        return bgl_fail(BGL_E_ARG, "bgl_moe_route_dev: need 1 <= K <= min(E, %d) and E <= %d (E=%d, K=%d)", MOE_MAX_K, ROUTE_MAXE, E, K);
+        return bgl_fail(BGL_E_ARG, "%s: need 1 <= K <= min(E, %d) and E <= %d (E=%d, K=%d)", who, MOE_MAX_K, ROUTE_MAXE, E, K);
     if (in < 4 || in % 4 || ((uintptr_t)rw_dev | (uintptr_t)x_dev) % 16)
-        return bgl_fail(BGL_E_ARG, "bgl_moe_route_dev: in=%d must be a multiple of 4 with 16-byte aligned rows", in);
+        return bgl_fail(BGL_E_ARG, "%s: in=%d must be a multiple of 4 with 16-byte aligned rows", who, in);
     HIPCHK(hipSetDevice(c->device));
     if (dbuf_reserve(c, c->moe_scores, (size_t)T * E * 4, false)) return BGL_E_NOMEM;
-    float *scores = (float *)c->moe_scores.p;
+    *scores = (float *)c->moe_scores.p;
     int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_moe_router_scores, dim3(T, (E + ROUTE_EPW - 1) / ROUTE_EPW), dim3(ROUTE_EPW * 64), 0, c->stream, rw_dev,
-                       rb_dev, E, in, x_dev, scores);
+                       rb_dev, E, in, x_dev, *scores);
     prof_end(c, tok);
     HIPCHK(hipGetLastError());
-    tok = prof_begin(c, 2);
+    return 0;
+}
+
+extern "C" int bgl_moe_route_dev(bgl_ctx *c, const float *rw_dev, const float *rb_dev, int E, int in, const float *x_dev,
+                                 int T, int K, int renorm, int32_t *idx_dev, float *w_dev) {
+    if (!idx_dev || !w_dev) return bgl_fail(BGL_E_ARG, "bgl_moe_route_dev: bad argument");
+    float *scores = nullptr;
+    int rc = route_scores(c, "bgl_moe_route_dev", rw_dev, rb_dev, E, in, x_dev, T, K, &scores);
+    if (rc) return rc;
+    int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_moe_route_topk, dim3(T), dim3(64), 0, c->stream, (const float *)scores, E, K, renorm ? 1 : 0, idx_dev, w_dev);
     prof_end(c, tok);
     HIPCHK(hipGetLastError());
@@ -622,6 +701,24 @@ extern "C" int bgl_moe_layer_dev(bgl_ctx *c, const float *rw_dev, const float *r
     if (dbuf_reserve(c, c->moe_route, (size_t)T * K * 8, false)) return BGL_E_NOMEM;
     int32_t *idx = (int32_t *)c->moe_route.p;
     float *w = (float *)(idx + (size_t)T * K);
-    if ((rc = bgl_moe_route_dev(c, rw_dev, rb_dev, E, H, x_dev, T, K, renorm, idx, w))) return rc;
-    return bgl_moe_ffn_dev(c, gate, up, down, sg, su, sd, x_dev, idx, w, T, K, out_dev);
+    float *scores = nullptr;
+    if ((rc = route_scores(c, "bgl_moe_layer_dev", rw_dev, rb_dev, E, H, x_dev, T, K, &scores))) return rc;
+    // up to 16 tokens (one per wave): top-K and bucketing in one launch, then the FFN without its
+    // own bucketing; more tokens: a wave per token in parallel (one workgroup walking 64 tokens'
+    // top-K measured 35 us slower per layer at T = 64)
+    if (T > 16) {
+        int tok = prof_begin(c, 2);
+        hipLaunchKernelGGL(k_moe_route_topk, dim3(T), dim3(64), 0, c->stream, (const float *)scores, E, K, renorm ? 1 : 0, idx, w);
+        prof_end(c, tok);
+        HIPCHK(hipGetLastError());
+        return moe_ffn(c, gate, up, down, sg, su, sd, x_dev, idx, w, T, K, out_dev, nullptr);
+    }
+    MoeScratch S;
+    if ((rc = moe_scratch(c, T * K, E, S))) return rc;
+    int tok = prof_begin(c, 2);
+    hipLaunchKernelGGL(k_moe_route_bucket, dim3(1), dim3(1024), ((size_t)E + 1 + (size_t)T * K) * 4, c->stream,
+                       (const float *)scores, T, E, K, renorm ? 1 : 0, idx, w, S.off, S.perm, S.pos, S.tok);
+    prof_end(c, tok);
+    HIPCHK(hipGetLastError());
+    return moe_ffn(c, gate, up, down, sg, su, sd, x_dev, idx, w, T, K, out_dev, &S);
 }

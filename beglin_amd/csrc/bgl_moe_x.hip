@@ -23,6 +23,27 @@ size_t bgl_moe_x_lds(int K, int nw) {
     return (size_t)MX_MB * (K / 64) * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * BGL_TILE * 4;
 }
 
+// out[t][c] = (((0 + w_a d_a) + w_b d_b) + ...) over t's experts in ascending expert id (then k), then
+// + the shared value: k_moe_combine's order (bgl_moe.hip), the order in which moe_ffn_batched's
+// bucket loop adds into mlp_out_batch.
+__device__ __forceinline__ void moe_x_combine(const MoeTask &Mt, int t, int c, float shared) {
+    const int K = Mt.ck;
+    const int32_t *it = Mt.cidx + (size_t)t * K;
+    int order[MOE_MAX_K];
+    for (int k = 0; k < K; k++) order[k] = k;
+    for (int a = 1; a < K; a++)
+        for (int b = a; b > 0 && it[order[b]] < it[order[b - 1]]; b--) {
+            const int tmp = order[b]; order[b] = order[b - 1]; order[b - 1] = tmp;
+        }
+    float acc = 0.0f;
+    for (int a = 0; a < K; a++) {
+        const int p = t * K + order[a];
+        const int s = Mt.cpos[p];
+        if (s >= 0) acc += Mt.cw[p] * Mt.cdown[(size_t)s * Mt.ystride + c];
+    }
+    Mt.cout[(size_t)t * Mt.ystride + c] = acc + shared;
+}
+
 template <int FMT, int NB, int MB>
 __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
                                             int tile, int base, int mc, int *xl) {
@@ -100,7 +121,8 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
             }
             const float out = glu ? (va / (1.0f + expf(-va))) * vb : va;
             const int yr = Mt.ymap ? Mt.ymap[base + m] : base + m;
-            Mt.y[(size_t)yr * Mt.ystride + row] = out;
+            if (Mt.cout) moe_x_combine(Mt, yr, row, out);
+            else Mt.y[(size_t)yr * Mt.ystride + row] = out;
         }
     }
     __syncthreads();                                               // the next chunk reuses the LDS
