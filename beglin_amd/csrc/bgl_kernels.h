@@ -106,6 +106,6 @@ int bgl_launch_gemv_x(const GemvLaunch &L, bool fuse, int nblocks, int TR, int n
 size_t bgl_gemv_x_lds(int K, int TR, int nw);
 // ---- bgl_moe_x.hip: the MoE gather over records made in the kernel ----
 bool bgl_moe_x_fmt(int fmt);
-size_t bgl_moe_x_lds(int K, int nw);
-int bgl_moe_x_waves(int K, long active_wgs, int cap);
-int bgl_launch_moe_x(const MoeTask &Mt, int K, int nw, hipStream_t st);
+size_t bgl_moe_x_lds(int K, int nw, int TR);
+void bgl_moe_x_shape(int K, long active_wgs, int tr_force, int nw_cap, int *TR, int *nw);
+int bgl_launch_moe_x(const MoeTask &Mt, int K, int TR, int nw, hipStream_t st);

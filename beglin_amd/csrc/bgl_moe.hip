@@ -347,7 +347,7 @@ static bool x_tensor_ok(const BglDevTensor &T) {
     return bgl_moe_x_fmt(T.fmt) && (size_t)T.ntiles * T.cpr * 1024 < (1ull << 31) && (size_t)T.ntiles * T.nunits * 512 < (1ull << 31);
 }
 static bool moe_x_ok(bgl_ctx *c, const bgl_tensor *sa, const bgl_tensor *sb, const MoeTask &Mt, int K) {
-    if (c->no_moe_x || bgl_moe_x_lds(K, 16) > 160 * 1024) return false;
+    if (c->no_moe_x || bgl_moe_x_lds(K, 16, 64) > 160 * 1024 || bgl_moe_x_lds(K, 8, 16) > 160 * 1024) return false;
     for (const bgl_tensor *st : {sa, sb})
         if (st)
             for (const bgl_tensor *e : st->experts)
@@ -373,7 +373,9 @@ static int moe_run(bgl_ctx *c, MoeTask &Mt, const bgl_tensor *sa, const bgl_tens
         memset(&Mt.a, 0, sizeof Mt.a);
         Mt.a.xf = x_rows;
         int tok = prof_begin(c, 1);
-        int rc = bgl_launch_moe_x(Mt, K, bgl_moe_x_waves(K, active_wgs, c->x_waves), c->stream);
+        int TR, nw;
+        bgl_moe_x_shape(K, active_wgs, c->force_tr, c->x_waves, &TR, &nw);
+        int rc = bgl_launch_moe_x(Mt, K, TR, nw, c->stream);
         prof_end(c, tok);
         if (rc) return bgl_fail(BGL_E_ARG, "k_moe_x launch: in=%d", K);
         HIPCHK(hipGetLastError());

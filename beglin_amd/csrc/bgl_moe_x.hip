@@ -18,9 +18,10 @@
 
 bool bgl_moe_x_fmt(int fmt) { return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64; }
 
-// LDS: MB columns of records and the wave partials.
-size_t bgl_moe_x_lds(int K, int nw) {
-    return (size_t)MX_MB * (K / 64) * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * BGL_TILE * 4;
+// LDS: MB columns of records (K/64 rounded up to whole slots of 64/TR groups) and the wave partials.
+size_t bgl_moe_x_lds(int K, int nw, int TR) {
+    const int KQ = BGL_TILE / TR, S = (K / 64 + KQ - 1) / KQ;
+    return (size_t)MX_MB * S * KQ * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * TR * 4;
 }
 
 // out[t][c] = (((0 + w_a d_a) + w_b d_b) + ...) over t's experts in ascending expert id (then k), then
@@ -44,21 +45,26 @@ __device__ __forceinline__ void moe_x_combine(const MoeTask &Mt, int t, int c, f
     Mt.cout[(size_t)t * Mt.ystride + c] = acc + shared;
 }
 
-template <int FMT, int NB, int MB>
+template <int FMT, int NB, int MB, int TR>
 __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
-                                            int tile, int base, int mc, int *xl) {
+                                            int tile, int r0, int base, int mc, int *xl) {
+    constexpr int KQ = BGL_TILE / TR;              // groups per slot: lane = (row lane % TR, group lane / TR)
     const int nthr = blockDim.x, nw = nthr >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int K = Ta.K, G = K >> 6, RC = G * XREC_DW, NPX = (K + 255) >> 8;
+    const int K = Ta.K, G = K >> 6, S = (G + KQ - 1) / KQ, RC = S * KQ * XREC_DW, NPX = (K + 255) >> 8;
+    const int r = lane % TR, kq = lane / TR;
 
-    // ---- a wave's items: its groups wave, wave + nw, ... -- each once per tensor in SwiGLU mode
-    // (gate then up) -- MX_DEPTH in flight; the first ones go out ahead of the activation work
+    // ---- a wave's items: its slots wave, wave + nw, ... -- each once per tensor in SwiGLU mode
+    // (gate then up) -- MX_DEPTH in flight; the first ones go out ahead of the activation work.
+    // Lanes whose group of the last slot lies past K read nothing there; their records are zero.
     const XRes Ra = x_res<FMT>(Ta, tile), Rb = x_res<FMT>(Tb, tile);
-    const XLane xlane = x_lane<FMT, NB, 1>(lane, 0);
-    const int ns = (G - 1 - wave) / nw + 1, NI = glu ? 2 * ns : ns;     // nw <= G: every wave has a group
-    auto item_load = [&](XRaw<FMT, NB> &r, int j) {
-        const int g = wave + (glu ? j >> 1 : j) * nw;
-        x_load<FMT, NB, 1>(r, glu && (j & 1) ? Rb : Ra, xlane, g, j < NI);
+    const XLane xlane = x_lane<FMT, NB, KQ>(r0 + r, kq);
+    XLane xlast = xlane;
+    if (kq >= G - (S - 1) * KQ) xlast = XLane{X_OOB, X_OOB, X_OOB, X_OOB, X_OOB};
+    const int ns = (S - 1 - wave) / nw + 1, NI = glu ? 2 * ns : ns;     // nw <= S: every wave has a slot
+    auto item_load = [&](XRaw<FMT, NB> &rw, int j) {
+        const int sl = wave + (glu ? j >> 1 : j) * nw;
+        x_load<FMT, NB, KQ>(rw, glu && (j & 1) ? Rb : Ra, sl == S - 1 ? xlast : xlane, sl, j < NI);
     };
     XRaw<FMT, NB> c[MX_DEPTH];
 #pragma unroll
@@ -73,18 +79,26 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
         const float4 v = x_pass_load(Mt.a.xf + (size_t)row * K, p, lane, K);
         x_pass_digits(v, p, lane, G, xl + m * RC);
     }
+    if (KQ > 1) {
+        const int per = (S * KQ - G) * XREC_DW;
+        for (int i = threadIdx.x; i < mc * per; i += nthr) {
+            const int m = i / per;
+            xl[m * RC + G * XREC_DW + (i - m * per)] = 0;
+        }
+    }
     __syncthreads();
 
     float acc[MB], accb[MB];
 #pragma unroll
     for (int m = 0; m < MB; m++) { acc[m] = 0.0f; accb[m] = 0.0f; }
+    const int *xk = xl + kq * XREC_DW;
     for (int j0 = 0; j0 < NI; j0 += MX_DEPTH) {
 #pragma unroll
         for (int jj = 0; jj < MX_DEPTH; jj++) {
             const int j = j0 + jj;
             if (j < NI) {
                 const bool up = glu && (j & 1);
-                const int *rec = xl + (wave + (glu ? j >> 1 : j) * nw) * XREC_DW;
+                const int *rec = xk + (wave + (glu ? j >> 1 : j) * nw) * (KQ * XREC_DW);
                 const XDec<FMT, NB> d = x_decode<FMT, NB>(c[jj]);
                 // columns one loop iteration at a time (not unrolled: the scheduler would hoist every
                 // column's record reads, and their registers, to the front); the accumulator is
@@ -103,21 +117,31 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
         }
     }
 
-    // ---- row sums over the waves in order (lane = row)
-    float *red = reinterpret_cast<float *>(xl + MX_MB * RC);      // [wave][2][MB][64]
+    // ---- row sums: over the KQ lanes of a row, then over the waves in order
 #pragma unroll
     for (int m = 0; m < MB; m++) {
-        red[((wave * 2 + 0) * MB + m) * BGL_TILE + lane] = acc[m];
-        red[((wave * 2 + 1) * MB + m) * BGL_TILE + lane] = accb[m];
+#pragma unroll
+        for (int o = TR; o < BGL_TILE; o <<= 1) {
+            acc[m] += __shfl_xor(acc[m], o);
+            accb[m] += __shfl_xor(accb[m], o);
+        }
+    }
+    float *red = reinterpret_cast<float *>(xl + MX_MB * RC);      // [wave][2][MB][TR]
+    if (lane < TR) {
+#pragma unroll
+        for (int m = 0; m < MB; m++) {
+            red[((wave * 2 + 0) * MB + m) * TR + lane] = acc[m];
+            red[((wave * 2 + 1) * MB + m) * TR + lane] = accb[m];
+        }
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < mc * BGL_TILE; t += nthr) {
-        const int m = t / BGL_TILE, rl = t % BGL_TILE, row = tile * BGL_TILE + rl;
+    for (int t = threadIdx.x; t < mc * TR; t += nthr) {
+        const int m = t / TR, rl = t % TR, row = tile * BGL_TILE + r0 + rl;
         if (row < Ta.N) {
-            float va = red[(0 * MB + m) * BGL_TILE + rl], vb = red[(1 * MB + m) * BGL_TILE + rl];
+            float va = red[(0 * MB + m) * TR + rl], vb = red[(1 * MB + m) * TR + rl];
             for (int w = 1; w < nw; w++) {
-                va += red[((w * 2 + 0) * MB + m) * BGL_TILE + rl];
-                vb += red[((w * 2 + 1) * MB + m) * BGL_TILE + rl];
+                va += red[((w * 2 + 0) * MB + m) * TR + rl];
+                vb += red[((w * 2 + 1) * MB + m) * TR + rl];
             }
             const float out = glu ? (va / (1.0f + expf(-va))) * vb : va;
             const int yr = Mt.ymap ? Mt.ymap[base + m] : base + m;
@@ -128,15 +152,15 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
     __syncthreads();                                               // the next chunk reuses the LDS
 }
 
-template <int FMT, int NB>
+template <int FMT, int NB, int TR>
 __device__ __forceinline__ void moe_x_tile(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
-                                           int tile, int seg0, int ncols, int *xl) {
+                                           int tile, int r0, int seg0, int ncols, int *xl) {
     int c0 = 0;
     for (; ncols - c0 >= 2; c0 += MX_MB) {
         const int rem = ncols - c0;
-        moe_x_chunk<FMT, NB, MX_MB>(Mt, Ta, Tb, glu, tile, seg0 + c0, rem < MX_MB ? rem : MX_MB, xl);
+        moe_x_chunk<FMT, NB, MX_MB, TR>(Mt, Ta, Tb, glu, tile, r0, seg0 + c0, rem < MX_MB ? rem : MX_MB, xl);
     }
-    if (c0 < ncols) moe_x_chunk<FMT, NB, 1>(Mt, Ta, Tb, glu, tile, seg0 + c0, 1, xl);
+    if (c0 < ncols) moe_x_chunk<FMT, NB, 1, TR>(Mt, Ta, Tb, glu, tile, r0, seg0 + c0, 1, xl);
 }
 
 // Expert record through the constant address space (scalar loads, wave-uniform addresses).
@@ -154,10 +178,12 @@ __device__ __forceinline__ BglDevTensor mx_tensor(const BglDevTensor *p) {
 // Grid: E x tpe workgroups.  SEG: the segments are consecutive runs of Mt.seg columns of
 // one by-value tensor (the shared experts).  At least 3 waves per SIMD: the widest formats then fit
 // 168 registers without spilling.
-template <bool SEG, int NWMAX>
+template <bool SEG, int NWMAX, int TR>
 __global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(MoeTask Mt) {
     extern __shared__ __align__(16) int xl[];
-    const int e = blockIdx.x / Mt.tpe, tile = blockIdx.x % Mt.tpe;
+    constexpr int SUBS = BGL_TILE / TR;
+    const int e = blockIdx.x / (Mt.tpe * SUBS), rem = blockIdx.x - e * Mt.tpe * SUBS;
+    const int tile = rem / SUBS, r0 = (rem % SUBS) * TR;
     int seg0 = 0, ncols = Mt.ncols;
     if constexpr (SEG) { seg0 = e * Mt.seg; ncols = min(Mt.seg, Mt.ncols - seg0); }
     else if (Mt.off) { seg0 = uni(Mt.off)[e]; ncols = uni(Mt.off)[e + 1] - seg0; }
@@ -167,25 +193,25 @@ __global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(
     const bool glu = Mt.swiglu != 0;
     const BglDevTensor Tb = glu ? (Mt.tb ? mx_tensor(Mt.tb + e) : Mt.db) : Ta;
     switch (Ta.fmt) {
-    case BGL_Q4G32H: moe_x_tile<BGL_Q4G32H, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-    case BGL_Q4G64: moe_x_tile<BGL_Q4G64, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-    case BGL_Q8G64: moe_x_tile<BGL_Q8G64, 0>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+    case BGL_Q4G32H: moe_x_tile<BGL_Q4G32H, 0, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+    case BGL_Q4G64: moe_x_tile<BGL_Q4G64, 0, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+    case BGL_Q8G64: moe_x_tile<BGL_Q8G64, 0, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
     case BGL_QNG64:
         switch (Ta.bits) {
-        case 2: moe_x_tile<BGL_QNG64, 2>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 3: moe_x_tile<BGL_QNG64, 3>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 4: moe_x_tile<BGL_QNG64, 4>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 5: moe_x_tile<BGL_QNG64, 5>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 6: moe_x_tile<BGL_QNG64, 6>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 7: moe_x_tile<BGL_QNG64, 7>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 8: moe_x_tile<BGL_QNG64, 8>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 9: moe_x_tile<BGL_QNG64, 9>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 10: moe_x_tile<BGL_QNG64, 10>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 11: moe_x_tile<BGL_QNG64, 11>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 12: moe_x_tile<BGL_QNG64, 12>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 13: moe_x_tile<BGL_QNG64, 13>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 14: moe_x_tile<BGL_QNG64, 14>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
-        case 15: moe_x_tile<BGL_QNG64, 15>(Mt, Ta, Tb, glu, tile, seg0, ncols, xl); break;
+        case 2: moe_x_tile<BGL_QNG64, 2, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 3: moe_x_tile<BGL_QNG64, 3, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 4: moe_x_tile<BGL_QNG64, 4, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 5: moe_x_tile<BGL_QNG64, 5, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 6: moe_x_tile<BGL_QNG64, 6, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 7: moe_x_tile<BGL_QNG64, 7, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 8: moe_x_tile<BGL_QNG64, 8, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 9: moe_x_tile<BGL_QNG64, 9, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 10: moe_x_tile<BGL_QNG64, 10, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 11: moe_x_tile<BGL_QNG64, 11, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 12: moe_x_tile<BGL_QNG64, 12, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 13: moe_x_tile<BGL_QNG64, 13, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 14: moe_x_tile<BGL_QNG64, 14, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+        case 15: moe_x_tile<BGL_QNG64, 15, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
         default: break;
         }
         break;
@@ -193,30 +219,36 @@ __global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(
     }
 }
 
-// Mt.a.xf: the raw fp32 activation rows (row stride K = the tensors' in).  nw waves (<= 8, and at
-// most one per 64-group).
-int bgl_launch_moe_x(const MoeTask &Mt, int K, int nw, hipStream_t st) {
-    if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW) return -1;
-    const size_t lds = bgl_moe_x_lds(K, nw);
+// Mt.a.xf: the raw fp32 activation rows (row stride K = the tensors' in).  TR rows per workgroup
+// (64 or 16), nw waves (<= 16, at most one per slot of 64/TR groups).
+int bgl_launch_moe_x(const MoeTask &Mt, int K, int TR, int nw, hipStream_t st) {
+    if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW || (TR != 64 && TR != 16)) return -1;
+    const size_t lds = bgl_moe_x_lds(K, nw, TR);
     if (lds > 160 * 1024) return -1;
-    const dim3 g(Mt.E * Mt.tpe), b(nw * BGL_TILE);
+    const dim3 g(Mt.E * Mt.tpe * (BGL_TILE / TR)), b(nw * BGL_TILE);
     const bool seg = !Mt.off && Mt.seg > 0;
-    if (nw <= 8) {
-        if (seg) hipLaunchKernelGGL((k_moe_x<true, 8>), g, b, lds, st, Mt);
-        else hipLaunchKernelGGL((k_moe_x<false, 8>), g, b, lds, st, Mt);
+#define MX_GO(S_, W_, T_) hipLaunchKernelGGL((k_moe_x<S_, W_, T_>), g, b, lds, st, Mt)
+    if (TR == 64) {
+        if (nw <= 8) { if (seg) MX_GO(true, 8, 64); else MX_GO(false, 8, 64); }
+        else { if (seg) MX_GO(true, 16, 64); else MX_GO(false, 16, 64); }
     } else {
-        if (seg) hipLaunchKernelGGL((k_moe_x<true, 16>), g, b, lds, st, Mt);
-        else hipLaunchKernelGGL((k_moe_x<false, 16>), g, b, lds, st, Mt);
+        if (seg) MX_GO(true, 8, 16); else MX_GO(false, 8, 16);
     }
+#undef MX_GO
     return 0;
 }
 
-// Waves per workgroup: 12 when the launch has few active workgroups (every CU then holds at most
-// one, so more waves keep more loads in flight), else 8 (two workgroups per CU); never more than
-// one per 64-group.  (Measured on the DeepSeek-V2-Lite layer: T=1 72.8 vs 81.3 us with 12 waves,
-// T=8 and T=64 slower with 12 or 16.)
-int bgl_moe_x_waves(int K, long active_wgs, int cap) {
+// Shape of a launch with active_wgs workgroups of whole tiles: very few (< 128: the shared experts
+// at a few tokens) -> 16-row workgroups (4x as many) of up to 8 waves; few (< 256: the routed
+// experts of one token) -> whole tiles of 12 waves; else whole tiles of 8 waves.  tr_force /
+// nw_cap: tuning overrides.
+void bgl_moe_x_shape(int K, long active_wgs, int tr_force, int nw_cap, int *TR, int *nw) {
+    int tr = active_wgs < 128 ? 16 : 64;
+    if (tr_force == 16 || tr_force == 64) tr = tr_force;
+    const int KQ = BGL_TILE / tr, S = (K / 64 + KQ - 1) / KQ;
     int w = active_wgs < 256 ? 12 : 8;
-    if (cap > 0) w = cap < MX_MAXW ? cap : MX_MAXW;
-    return K / 64 < w ? K / 64 : w;
+    if (nw_cap > 0) w = nw_cap < MX_MAXW ? nw_cap : MX_MAXW;
+    if (tr == 16 && w > 8) w = 8;
+    *TR = tr;
+    *nw = S < w ? S : w;
 }

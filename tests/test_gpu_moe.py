@@ -410,16 +410,17 @@ def test_moe_error_paths(ctx, torch_dev, oracle):
         t.free()
 
 
-@pytest.mark.parametrize("T", [1, 6, 21])
-def test_moe_x_matches_prep_path(torch_dev, oracle, monkeypatch, T):
+@pytest.mark.parametrize("T,tr", [(1, 0), (6, 0), (21, 0), (6, 16), (21, 16), (1, 64)])
+def test_moe_x_matches_prep_path(torch_dev, oracle, monkeypatch, T, tr):
     """The gather that makes its activation records in the kernel (k_moe_x) against the prep
     kernel + k_moe_gemv path and the oracle: few experts so segments run 1..12 columns (chunks of
     4 and a single last column), hidden 320 (a partial last pass of 256 values), inter 192 (a
-    partly filled slot), shared experts over T > 4 columns in segments."""
+    partly filled slot), shared experts over T > 4 columns in segments; workgroups of whole tiles
+    and of 16 rows (tr: forced width, 0 = the launch's own choice)."""
     import beglin_amd
     torch = torch_dev
     E, H, I, K, Ish = 4, 320, 192, 2, 320
-    say("moe_x vs prep", T)
+    say("moe_x vs prep", T, tr)
     fm = [(5, 0), (2, 0), (4, 7), (4, 15)]
     gate, up, down, shared = moe_setup(oracle, 6000 + T, E, H, I, Ish, fm, down_fmts=fm[::-1], sh_fmt=(4, 12))
     x = seeded_normal(90 + T, (T, H))
@@ -427,6 +428,10 @@ def test_moe_x_matches_prep_path(torch_dev, oracle, monkeypatch, T):
     outs = []
     for flag in ("0", "1"):
         monkeypatch.setenv("BGL_NO_MOE_X", flag)
+        if tr:
+            monkeypatch.setenv("BGL_FORCE_TR", str(tr))
+        else:
+            monkeypatch.delenv("BGL_FORCE_TR", raising=False)
         c = beglin_amd.Context(0)
         outs.append(run_moe(c, torch, gate, up, down, shared, x, idx, w))
         c.close()
