@@ -107,6 +107,8 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     const char *xw = getenv("BGL_X_WAVES");
     c->x_waves = xw ? atoi(xw) : 0;
     if (c->x_waves < 0 || c->x_waves > 16) c->x_waves = 0;
+    const char *qp = getenv("BGL_Q_PREP");
+    c->q_prep = qp ? (atoi(qp) != 0) : -1;
     const char *nmx = getenv("BGL_NO_MOE_X");
     c->no_moe_x = nmx && atoi(nmx) != 0;
     const char *xf = getenv("BGL_X_FUSE");
@@ -665,6 +667,7 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
 }
 
 #define BGL_GEMV_Q_LDS_MAX (64 * 1024)          // one column: two workgroups of the largest shapes per CU
+#define BGL_Q_PREP_MIN_PASSES 64                // W4A8 calls with this many passes of 256 values per launch quantize up front
 #define BGL_GEMV_Q_LDS_MAX_MB (160 * 1024)      // 4 or 8 columns: the codes of every column sit in LDS
 
 static int q_mb(int mc) { return mc <= 1 ? 1 : mc <= 4 ? 4 : 8; }
@@ -682,6 +685,18 @@ static int q_mb_max(int kind, int K) {
 static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
                       float *const *y) {
     const int mbmax = q_mb_max(Ts[0].fmt, Ts[0].K);
+    // Several columns over a long K: one k_act_w4a8 launch quantizes them all (the same codes)
+    // instead of every workgroup quantizing every column of its launch.  (Measured on Qwen2.5-1.5B
+    // g256sf: the down projection, 4 x 35 and 8 x 35 passes per workgroup, 10.95 -> 9.57 and
+    // 17.75 -> 11.38 us; for 8 x 6 passes and fewer the extra launch costs more than it saves.)
+    GemvAct A;
+    memset(&A, 0, sizeof A);
+    const int passes = std::min(M, mbmax) * ((Ts[0].K + 255) / 256);
+    const bool prep = M > 1 && (c->q_prep == 1 || (c->q_prep < 0 && passes >= BGL_Q_PREP_MIN_PASSES));
+    if (prep) {
+        int rc = prep_act(c, BGL_ACT_W4A8, act_group(Ts[0].fmt), x_dev, M, Ts[0].K, A);
+        if (rc) return rc;
+    }
     for (int m0 = 0; m0 < M; m0 += mbmax) {
         const int mc = std::min(mbmax, M - m0), MB = q_mb(mc);
         GemvLaunch L;
@@ -689,6 +704,7 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
         int blocks = 0;
         fill_tasks(L, n, Ts, bias, y, nullptr, blocks);
         L.x = x_dev;
+        if (prep && MB > 1) L.a = A;
         L.m0 = m0;
         L.mcols = mc;
         // Rows per workgroup: split 64-row tiles until the launch has >= 512 workgroups (8 rows at

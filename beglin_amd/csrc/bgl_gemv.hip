@@ -377,7 +377,7 @@ __device__ __forceinline__ float unit_float(int isum, float s, const float *asc,
     else return __fmul_rn(__fmul_rn((float)isum, s), asc[u]);
 }
 
-template <int FMT, int TR, int QP, int MB>
+template <int FMT, int TR, int QP, int MB, bool PREP>
 __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     extern __shared__ __align__(16) unsigned char lds[];
     constexpr int KQ = BGL_TILE / TR, SUBS = BGL_TILE / TR;
@@ -389,7 +389,8 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     const int lb = b - sel.blk0, tile = lb / SUBS, r0 = (lb % SUBS) * TR;
     const int nw = sel.nthreads >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int K = T.K, U = T.nunits, NGQ = K / QU::GQ, NP = (K + 255) / 256, NPT = MB * NP;
+    // passes run over the launch's real columns only (a launch of MB columns may carry fewer)
+    const int K = T.K, U = T.nunits, NGQ = K / QU::GQ, NP = (K + 255) / 256, NPT = (MB == 1 ? 1 : L.mcols) * NP;
     const int XQS = (U + 1) * QU::STRIDE;               // LDS bytes of one column's codes
     int8_t *xq = reinterpret_cast<int8_t *>(lds);
     float *asc = reinterpret_cast<float *>(lds + (size_t)MB * XQS);
@@ -397,10 +398,44 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
     float *tl = reinterpret_cast<float *>(xsum + MB * (K / 64 + 1));
     const float *x = sel.x;
 
-    // ---- x loads of the first pass, then the first weight units (unconditional, clamped)
+    // ---- x loads of the first pass (PREP: of the first prepared codes), then the first weight
+    // units (unconditional, clamped)
     float4 v[QP];
-    load_xpass<QP, MB>(v, x, wave, nw, K, NP, NPT, lane);
+    const int8_t *pq = L.a.xw ? reinterpret_cast<const int8_t *>(L.a.xw) + (size_t)L.m0 * K : nullptr;
+    const int npq = L.mcols * (K >> 4);           // PREP: 16-byte pieces of the columns' codes
+    bgl_u32x4 pre[4];
+    if constexpr (PREP) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = min((int)threadIdx.x + j * sel.nthreads, npq - 1);
+            pre[j] = *(const BGL_GLOBAL bgl_u32x4 *)(pq + (size_t)(i / (K >> 4)) * K + (size_t)(i % (K >> 4)) * 16);
+        }
+    } else {
+        load_xpass<QP, MB>(v, x, wave, nw, K, NP, NPT, lane);
+    }
     __builtin_amdgcn_sched_barrier(0);
+    // PREP: the prepared codes, scales and code sums into the per-column LDS regions
+    auto copy_prep = [&]() {
+        const int nthr = sel.nthreads;
+        auto dst = [&](int i) {
+            const int m = i / (K >> 4), o = (i % (K >> 4)) * 16;
+            return reinterpret_cast<bgl_u32x4 *>(xq + m * XQS + (o / QU::ELEMS) * QU::STRIDE + o % QU::ELEMS);
+        };
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = threadIdx.x + j * nthr;
+            if (i < npq) *dst(i) = pre[j];
+        }
+        for (int i = threadIdx.x + 4 * nthr; i < npq; i += nthr)
+            *dst(i) = *(const BGL_GLOBAL bgl_u32x4 *)(pq + (size_t)(i / (K >> 4)) * K + (size_t)(i % (K >> 4)) * 16);
+        for (int i = threadIdx.x; i < L.mcols * NGQ; i += nthr)
+            asc[(i / NGQ) * (NGQ + 1) + i % NGQ] = L.a.xs[(size_t)(L.m0 + i / NGQ) * NGQ + i % NGQ];
+        if constexpr (QU::XSUM) {
+            const int n64 = K / 64;
+            for (int i = threadIdx.x; i < L.mcols * n64; i += nthr)
+                xsum[(i / n64) * (n64 + 1) + i % n64] = L.a.xsum[(size_t)(L.m0 + i / n64) * n64 + i % n64];
+        }
+    };
     // Waves [0, nwl) own weight units; any further waves of the launch only quantize.  The two
     // roles are separate branches so the weight waves' wait for x is not merged with a path that
     // issued no weight loads.
@@ -416,10 +451,14 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
         // quantize x (q4gemv.h:177-213 / q4gemv_g256.h:72-99).  The first passes stay outside the
         // loop: a loop header joining the back edge (whose x loads are the newest) would make the
         // compiler wait for the weight loads as well.
-        quant_passes<FMT, QP, MB>(v, wave, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
-        for (int p0 = wave + QP * nw; p0 < NPT; p0 += QP * nw) {
-            load_xpass<QP, MB>(v, x, p0, nw, K, NP, NPT, lane);
-            quant_passes<FMT, QP, MB>(v, p0, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
+        if constexpr (PREP) {
+            copy_prep();
+        } else {
+            quant_passes<FMT, QP, MB>(v, wave, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
+            for (int p0 = wave + QP * nw; p0 < NPT; p0 += QP * nw) {
+                load_xpass<QP, MB>(v, x, p0, nw, K, NP, NPT, lane);
+                quant_passes<FMT, QP, MB>(v, p0, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
+            }
         }
         __syncthreads();
         // per-unit fold terms t[m][u][row]; every lane computes (the partner exchange is wave-wide).
@@ -445,10 +484,14 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
             ub = un;
         }
     } else {
-        quant_passes<FMT, QP, MB>(v, wave, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
-        for (int p0 = wave + QP * nw; p0 < NPT; p0 += QP * nw) {
-            load_xpass<QP, MB>(v, x, p0, nw, K, NP, NPT, lane);
-            quant_passes<FMT, QP, MB>(v, p0, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
+        if constexpr (PREP) {
+            copy_prep();
+        } else {
+            quant_passes<FMT, QP, MB>(v, wave, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
+            for (int p0 = wave + QP * nw; p0 < NPT; p0 += QP * nw) {
+                load_xpass<QP, MB>(v, x, p0, nw, K, NP, NPT, lane);
+                quant_passes<FMT, QP, MB>(v, p0, nw, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
+            }
         }
         __syncthreads();
     }
@@ -546,14 +589,14 @@ size_t bgl_gemv_q_lds(int fmt, int K, int TR, int MB) {
     return (size_t)MB * ((size_t)(U + 1) * (ELEMS + 16) + 4 * (size_t)(K / GQ + 1) + 4 * (size_t)(K / 64 + 1) + 4 * (size_t)U * TR);
 }
 
-template <int FMT, int QP, int MB>
+template <int FMT, int QP, int MB, bool PREP = false>
 static int launch_q_tr(int TR, const GemvLaunch &L, int nblocks, int nw, size_t lds, hipStream_t st) {
     dim3 g(nblocks), b(nw * BGL_TILE);
     switch (TR) {
-    case 64: hipLaunchKernelGGL((k_gemv_q<FMT, 64, QP, MB>), g, b, lds, st, L); return 0;
-    case 32: hipLaunchKernelGGL((k_gemv_q<FMT, 32, QP, MB>), g, b, lds, st, L); return 0;
-    case 16: hipLaunchKernelGGL((k_gemv_q<FMT, 16, QP, MB>), g, b, lds, st, L); return 0;
-    case 8: hipLaunchKernelGGL((k_gemv_q<FMT, 8, QP, MB>), g, b, lds, st, L); return 0;
+    case 64: hipLaunchKernelGGL((k_gemv_q<FMT, 64, QP, MB, PREP>), g, b, lds, st, L); return 0;
+    case 32: hipLaunchKernelGGL((k_gemv_q<FMT, 32, QP, MB, PREP>), g, b, lds, st, L); return 0;
+    case 16: hipLaunchKernelGGL((k_gemv_q<FMT, 16, QP, MB, PREP>), g, b, lds, st, L); return 0;
+    case 8: hipLaunchKernelGGL((k_gemv_q<FMT, 8, QP, MB, PREP>), g, b, lds, st, L); return 0;
     default: return -1;
     }
 }
@@ -569,6 +612,13 @@ static int launch_q_qp(int QP, int TR, const GemvLaunch &L, int nblocks, int nw,
 
 template <int FMT>
 static int launch_q_mb(int MB, int QP, int TR, const GemvLaunch &L, int nblocks, int nw, size_t lds, hipStream_t st) {
+    if (L.a.xw) {                                  // prepared codes (QP is unused)
+        switch (MB) {
+        case 4: return launch_q_tr<FMT, 1, 4, true>(TR, L, nblocks, nw, lds, st);
+        case 8: return launch_q_tr<FMT, 1, 8, true>(TR, L, nblocks, nw, lds, st);
+        default: return -1;
+        }
+    }
     switch (MB) {
     case 1: return launch_q_qp<FMT, 1>(QP, TR, L, nblocks, nw, lds, st);
     case 4: return launch_q_qp<FMT, 4>(QP, TR, L, nblocks, nw, lds, st);
@@ -578,7 +628,9 @@ static int launch_q_mb(int MB, int QP, int TR, const GemvLaunch &L, int nblocks,
 }
 
 // ntiles counts 64-row tiles; each is split into 64/TR workgroups.  MB columns (1, 4 or 8) per
-// launch, L.mcols of them real.  QP (quantization passes per wave loaded up front) covers a wave's
+// launch, L.mcols of them real.  With L.a.xw set (MB 4 or 8) the workgroups copy the columns' int8
+// codes, scales and code sums prepared by k_act_w4a8 (the same codes the fused quantization makes)
+// instead of quantizing every column themselves.  QP (quantization passes per wave loaded up front) covers a wave's
 // whole share of the MB*ceil(K/256) passes when that is <= 4.  (8 passes up front for the 4- and
 // 8-column launches measured no faster.)
 int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, int MB, hipStream_t st) {

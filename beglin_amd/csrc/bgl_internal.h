@@ -32,6 +32,7 @@ struct bgl_ctx {
     int force_tr = 0;                     // BGL_FORCE_TR: fixed rows per workgroup (tuning)
     bool no_gemv_x = false;               // BGL_NO_GEMV_X=1: fp32-activation M=1 through the tile kernel (k_gemv)
     int x_waves = 0;                      // BGL_X_WAVES: wavefronts per k_gemv_x workgroup (tuning)
+    int q_prep = -1;                      // BGL_Q_PREP: 0 never / 1 always quantize W4A8 columns up front; -1 by M and K
     bool no_moe_x = false;                // BGL_NO_MOE_X=1: MoE gathers through the prep kernel + k_moe_gemv
     int x_fuse = -1;                      // BGL_X_FUSE: 0 never / 1 always make the digits inside k_gemv_x; -1 by K
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call

@@ -283,11 +283,13 @@ def time_graph(torch, stream, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall, g
 
 
-def time_prep(ctx, torch, stream, wl, steps):
-    """Graph-timed activation-prep kernels alone (one per call), for paths that have them."""
+def time_prep(ctx, torch, stream, wl, steps, tags):
+    """Graph-timed activation-prep kernels alone (one per call of the given call types: the ones
+    whose path launches a prep kernel)."""
     def prep_only():
         for group, x, ys, act, _, tag in wl.calls:
-            ctx.prep_only(x, act, group[0])
+            if tag in tags:
+                ctx.prep_only(x, act, group[0])
     ms, _, _ = time_graph(torch, stream, prep_only, steps, 2)
     return ms
 
@@ -654,26 +656,28 @@ def main():
         n = wl.ncalls([tag])
         per_call[tag] = {"us": round(ms * 1e3 / n, 2), "GB/s": round(wl.nbytes([tag]) / (ms * 1e-3) / 1e9, 1)}
 
-    # The dominant kernel is the GEMV; for the fused W4A8 path (cfg2, every M) and the one-column
-    # fp32 GEMV over a short K it is the only kernel of the step, so its average launch duration is
-    # the graph-timed step (HIP events on the context's stream around the timed replays) over the
-    # launches per step.  The separate-prep paths (fp32 activations otherwise) add one activation
-    # kernel per call; those are timed the same way from a graph of the prep alone.
+    # The dominant kernel is the GEMV; where it is the only kernel of the step (W4A8 at M=1, the
+    # one-column fp32 GEMV over a short K) its average launch duration is the graph-timed step (HIP
+    # events on the context's stream around the timed replays) over the launches per step.  Call
+    # types whose path adds an activation-prep kernel have those timed the same way from a graph of
+    # the prep alone, subtracted from the step.
     launches = wl.ncalls()
     prep_ms = 0.0
-    has_prep = False
-    if args.workload != "cfg2":
-        # does the path launch an activation-prep kernel? (one profiled eager step counts them; the
-        # one-column fp32 GEMV over a short K makes its digits itself)
+    # which call types launch an activation-prep kernel? (one profiled eager run of each counts
+    # them: the fused W4A8 kernel and the one-column fp32 GEMV over a short K make their operands
+    # themselves; several W4A8 columns over a long K and long fp32 K are quantized up front)
+    prep_tags = []
+    for tag in tags:
         ctx.prof_enable(True)
         ctx.prof_read()
         with torch.cuda.stream(stream):
-            wl.run()
+            wl.run([tag])
         ctx.sync()
-        has_prep = ctx.prof_read()["prep"][1] > 0
+        if ctx.prof_read()["prep"][1] > 0:
+            prep_tags.append(tag)
         ctx.prof_enable(False)
-    if has_prep:
-        prep_ms = time_prep(ctx, torch, stream, wl, max(5, args.steps // 5))
+    if prep_tags:
+        prep_ms = time_prep(ctx, torch, stream, wl, max(5, args.steps // 5), set(prep_tags))
     k_ms = max(step_ms - prep_ms, 1e-6)
     achieved = nbytes / (k_ms * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -681,7 +685,7 @@ def main():
             "kernel": ("k_gemv_q<fmt,TR,QP,MB> (bgl_gemv.hip)" if args.workload == "cfg2" else
                        "k_gemv_x<fmt,n,TR,FUSE> (bgl_gemv_x.hip)" if M == 1 else "k_gemv<fmt,act,n,MB> (bgl_gemv.hip)"),
             "launches_per_step": launches, "kernel_us_per_launch": round(k_ms * 1e3 / launches, 3),
-            "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3),
+            "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3), "prep_call_types": prep_tags,
             "bytes_per_launch": round(nbytes / launches)}
 
     # HBM traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this

@@ -349,3 +349,34 @@ def test_prepped_activation_reuse(ctx, torch_dev, oracle):
             assert relerr(y.cpu().numpy(), ref) <= TOL
         for t in ts:
             t.free()
+
+
+@pytest.mark.parametrize("kind", [1, 2, 3])
+def test_w4a8_batched_prep_equals_fused(torch_dev, oracle, monkeypatch, kind):
+    """Several W4A8 columns quantized once up front (k_act_w4a8, then workgroups copying the codes)
+    == every workgroup quantizing its launch's columns: both bit-identical to the oracle, at column
+    counts that leave a launch of 4 or 8 partly filled."""
+    import beglin_amd
+    torch = torch_dev
+    for inn in (320, 1408, 8960):
+        if kind == 3 and inn % 256:
+            continue
+        out = 136
+        w = weights(1200 + kind + inn, out, inn)
+        pk, sc, sub = ref_quant(oracle, kind, w, 0)
+        for M in (2, 5, 8, 12):
+            say("w4a8 prep vs fused", kind, inn, M)
+            x = seeded_normal(1210 + M, (M, inn))
+            ref = oracle.matmul_sdot(kind, pk, sc, x, sub=sub)
+            outs = []
+            for flag in ("0", "1"):
+                monkeypatch.setenv("BGL_Q_PREP", flag)
+                c = beglin_amd.Context(0)
+                t = c.bind(kind, pk, sc, out, inn, sub=sub)
+                y = torch.full((M, out), float("nan"), dtype=torch.float32, device="cuda")
+                c.matmul(t, torch.from_numpy(x).cuda(), y, act=1)
+                torch.cuda.synchronize()
+                outs.append(y.cpu().numpy())
+                t.free(); c.close()
+            assert np.array_equal(outs[0].view(np.uint32), ref.view(np.uint32)), (inn, M)
+            assert np.array_equal(outs[1].view(np.uint32), ref.view(np.uint32)), (inn, M)
