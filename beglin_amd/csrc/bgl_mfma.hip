@@ -140,6 +140,10 @@ __device__ __forceinline__ AOff a_offsets(int rb0, int lane) {
 template <int FMT, int NB>
 __device__ __forceinline__ void ld_pair(PRaw<FMT, NB> &p, __amdgpu_buffer_rsrc_t rs, const AOff &o, uint32_t tchunk, int s) {
     using P = Planes<FMT, NB>;
+    // both are wave-uniform; said so explicitly, so every offset below is a scalar operand (a value
+    // the compiler cannot prove uniform would wrap each load in a loop over the lanes' values)
+    tchunk = __builtin_amdgcn_readfirstlane(tchunk);
+    s = __builtin_amdgcn_readfirstlane(s);
     if constexpr (FMT == BGL_Q8G64) {                    // K-step s is chunks 2s, 2s+1
 #pragma unroll
         for (int j = 0; j < 2; j++) {
