@@ -33,6 +33,39 @@
 static inline unsigned nblk(long n, int bs = 256) { return (unsigned)((n + bs - 1) / bs); }
 
 // ====================================================================================== bucketing
+// start[0..E) holds per-expert counts; rewrites them as exclusive segment starts and sets
+// start[E] to the total.  The first wave scans 256 experts per round (4 per lane, then a wave
+// prefix over the lanes); the caller synchronizes before and after.
+__device__ __forceinline__ void bucket_scan(int *start, int E) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 256) {
+        int c[4], sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = e0 + 4 * lane + j;
+            c[j] = e < E ? start[e] : 0;
+            sum += c[j];
+        }
+        int incl = sum;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int n = __shfl_up(incl, o);
+            if (lane >= o) incl += n;
+        }
+        int run = carry + incl - sum;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = e0 + 4 * lane + j;
+            if (e < E) start[e] = run;
+            run += c[j];
+        }
+        carry += __shfl(incl, 63);
+    }
+    if (lane == 0) start[E] = carry;
+}
+
 // One workgroup.  off[E+1]: segment starts in sorted order; perm[s]: pair at sorted position s;
 // pos[p]: sorted position of pair p (-1 for an expert id outside [0, E), which is skipped);
 // tok[s] = perm[s] / K, the token row that feeds sorted position s.
@@ -51,11 +84,7 @@ __global__ __launch_bounds__(1024) void k_moe_bucket(const int32_t *__restrict__
         if (e >= 0) atomicAdd(&start[e], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int e = 0; e < E; e++) { const int n = start[e]; start[e] = run; run += n; }
-        start[E] = run;
-    }
+    bucket_scan(start, E);
     __syncthreads();
     for (int e = threadIdx.x; e <= E; e += blockDim.x) off[e] = start[e];
     for (int p = threadIdx.x; p < P; p += blockDim.x) {
@@ -529,20 +558,35 @@ extern "C" int bgl_moe_ffn_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_ten
 #define ROUTE_EPW 4          // experts per scores workgroup: one per wave
 
 // scores[t][e] = (float)(sum_c (double)W[e][c] * x[t][c]) (+ b[e]); grid (T, ceil(E/4)), one wave
-// per expert so the router matrix is read by many CUs at once.
+// per expert so the router matrix is read by many CUs at once.  Each lane sums its elements
+// 4*lane + 256*i in ascending order; a round's 8 row and 8 x loads all go out before the first fma
+// (buffer loads: the ones past H return zero, so none is conditional and one round trip serves
+// H <= 2048).
+#define ROUTE_RND 8
 __global__ __launch_bounds__(ROUTE_EPW * 64) void k_moe_router_scores(const float *__restrict__ W, const float *__restrict__ bias,
                                                                       int E, int H, const float *__restrict__ x,
                                                                       float *__restrict__ scores) {
     const int t = blockIdx.x, e = blockIdx.y * ROUTE_EPW + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (e >= E) return;
-    const float *we = W + (size_t)e * H, *xt = x + (size_t)t * H;
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(W + (size_t)e * H), (short)0, H * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(x + (size_t)t * H), (short)0, H * 4, 0x00020000);
+    typedef float rf4 __attribute__((ext_vector_type(4)));
     double acc = 0.0;
-    for (int c = 4 * lane; c < H; c += 256) {
-        const float4 wv = *reinterpret_cast<const float4 *>(we + c), xv = *reinterpret_cast<const float4 *>(xt + c);
-        acc = fma((double)wv.x, (double)xv.x, acc);
-        acc = fma((double)wv.y, (double)xv.y, acc);
-        acc = fma((double)wv.z, (double)xv.z, acc);
-        acc = fma((double)wv.w, (double)xv.w, acc);
+    for (int c0 = 0; c0 < H; c0 += ROUTE_RND * 256) {
+        rf4 wv[ROUTE_RND], xv[ROUTE_RND];
+#pragma unroll
+        for (int i = 0; i < ROUTE_RND; i++) {
+            const int off = (c0 + 256 * i + 4 * lane) * 4;
+            wv[i] = __builtin_bit_cast(rf4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+            xv[i] = __builtin_bit_cast(rf4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < ROUTE_RND; i++) {
+            acc = fma((double)wv[i].x, (double)xv[i].x, acc);
+            acc = fma((double)wv[i].y, (double)xv[i].y, acc);
+            acc = fma((double)wv[i].z, (double)xv[i].z, acc);
+            acc = fma((double)wv[i].w, (double)xv[i].w, acc);
+        }
     }
     for (int o = 32; o; o >>= 1) acc += __shfl_xor(acc, o);
     if (lane == 0) scores[(size_t)t * E + e] = bias ? __fadd_rn((float)acc, bias[e]) : (float)acc;
@@ -568,10 +612,15 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ sc_t, 
     }
     // the double sum in expert order, every lane reading the values across the wave
     double sum = 0.0;
-    for (int e = 0; e < E; e++) {
-        const int j = e >> 6;
-        const float ve = j == 0 ? v[0] : j == 1 ? v[PL > 1 ? 1 : 0] : j == 2 ? v[PL > 2 ? 2 : 0] : v[PL > 3 ? 3 : 0];
-        sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ve), e & 63));
+#pragma unroll
+    for (int j = 0; j < PL; j++) {
+        const int n = min(64, E - 64 * j);
+        if (n == 64) {                                       // constant lanes: the reads pipeline
+#pragma unroll
+            for (int l = 0; l < 64; l++) sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
+        } else {
+            for (int l = 0; l < n; l++) sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
+        }
     }
     unsigned used = 0;                                       // bit j: expert lane + 64j selected
 #pragma unroll
@@ -636,21 +685,19 @@ __global__ __launch_bounds__(1024) void k_moe_route_bucket(const float *__restri
             for (int k = 0; k < K; k++) {
                 idx_out[(size_t)t * K + k] = sel_i[k];
                 w_out[(size_t)t * K + k] = sel_w[k];
-                ids[t * K + k] = sel_i[k];
+                ids[t * K + k] = sel_i[k] < E ? sel_i[k] : -1;   // a slot no score filled
             }
     }
     __syncthreads();
-    for (int p = threadIdx.x; p < P; p += blockDim.x) atomicAdd(&start[ids[p]], 1);
+    for (int p = threadIdx.x; p < P; p += blockDim.x)
+        if (ids[p] >= 0) atomicAdd(&start[ids[p]], 1);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int e = 0; e < E; e++) { const int n = start[e]; start[e] = run; run += n; }
-        start[E] = run;
-    }
+    bucket_scan(start, E);
     __syncthreads();
     for (int e = threadIdx.x; e <= E; e += blockDim.x) off[e] = start[e];
     for (int p = threadIdx.x; p < P; p += blockDim.x) {
         const int e = ids[p];
+        if (e < 0) { pos[p] = -1; continue; }
         int rank = 0;
         for (int q = 0; q < p; q++) rank += ids[q] == e;
         const int s = start[e] + rank;

@@ -364,6 +364,73 @@ def test_moe_layer_parity(ctx, torch_dev, oracle, T, renorm):
         t.free()
 
 
+def test_moe_layer_fused_router_ties_and_wide(ctx, torch_dev, oracle):
+    """The whole-layer entry's router for up to 16 tokens (top-K and bucketing in one workgroup)
+    over E = 160 experts (a partly
+    filled third block of 64 scores per lane), K = 8, renorm, and tied router rows (identical
+    probabilities: the lowest expert id is picked first) -- the outputs equal the oracle's layer,
+    whose FFN differs for every expert, so a wrong pick or tie order shows."""
+    torch = torch_dev
+    E, H, I, K, Ish, T = 160, 256, 64, 8, 64, 3
+    say("moe_layer fused router", E, K, T)
+    gate, up, down, shared = moe_setup(oracle, 6200, E, H, I, Ish, [(5, 0), (2, 0), (4, 7)])
+    x = seeded_normal(6201, (T, H))
+    rwt = seeded_normal(6202, (E, H), 0.05)
+    rwt[3] = x[0] * np.float32(0.03)                     # token 0's top scores, tied three ways
+    rwt[140] = rwt[3]; rwt[77] = rwt[3]
+    rwt[150] = rwt[9]; rwt[21] = rwt[9]
+    idx, w = oracle.route(oracle.router_logits(rwt, x), K, True)
+    assert list(idx[0][:3]) == [3, 77, 140]
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    g, u, d = ctx.bind_experts(gate), ctx.bind_experts(up), ctx.bind_experts(down)
+    sh = tuple(bind_one(ctx, dd) for dd in shared)
+    out = torch.full((T, H), float("nan"), device="cuda")
+    ctx.moe_layer(dev(torch, rwt), g, u, d, sh, dev(torch, x), K, out, renorm=True)
+    ctx.sync()
+    assert relerr(out.cpu().numpy(), ref) <= TOL
+    for t in (g, u, d) + sh:
+        t.free()
+
+
+def test_moe_layer_graph_replays_match_eager(torch_dev, oracle):
+    """The whole layer (router, top-K + bucketing, FFN, shared experts) replayed
+    from a graph: every replay, with eager calls in between, equals the eager result bit for bit."""
+    import beglin_amd
+    torch = torch_dev
+    E, H, I, K, Ish, T = 16, 256, 128, 4, 128, 5
+    say("moe_layer graph")
+    gate, up, down, shared = moe_setup(oracle, 6300, E, H, I, Ish, [(5, 0), (4, 9)])
+    x = dev(torch, seeded_normal(6301, (T, H)))
+    rwt = dev(torch, seeded_normal(6302, (E, H), 0.05))
+    s = torch.cuda.Stream()
+    gc = beglin_amd.Context(0, stream=s.cuda_stream)
+    g, u, d = gc.bind_experts(gate), gc.bind_experts(up), gc.bind_experts(down)
+    sh = tuple(bind_one(gc, dd) for dd in shared)
+    out = torch.zeros((T, H), dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(s):
+        gc.moe_layer(rwt, g, u, d, sh, x, K, out)
+    gc.sync()
+    eager = out.cpu().numpy().copy()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        gc.moe_layer(rwt, g, u, d, sh, x, K, out)
+    for r in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager), f"replay {r}"
+        with torch.cuda.stream(s):
+            gc.moe_layer(rwt, g, u, d, sh, x, K, out)
+        gc.sync()
+    idx, w = oracle.route(oracle.router_logits(rwt.cpu().numpy(), x.cpu().numpy()), K, False)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x.cpu().numpy(), idx, w)
+    assert relerr(eager, ref) <= TOL
+    for t in (g, u, d) + sh:
+        t.free()
+    gc.close()
+
+
 def test_moe_route_error_paths(ctx, torch_dev):
     import beglin_amd
     torch = torch_dev
