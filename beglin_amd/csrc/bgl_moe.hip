@@ -594,7 +594,7 @@ __global__ __launch_bounds__(ROUTE_EPW * 64) void k_moe_router_scores(const floa
 
 // Softmax, top-K and renorm of one token's E scores by one wave; lane 0 returns the K picks.
 __device__ __forceinline__ void route_topk_wave(const float *__restrict__ sc_t, int E, int K, int renorm, int lane,
-                                                int *sel_i, float *sel_w) {
+                                                int *sel_i, float *sel_w, float *lbuf) {
     constexpr int PL = ROUTE_MAXE / 64;                      // scores per lane: expert lane + 64j
     float v[PL];
     float mx = -INFINITY;
@@ -610,18 +610,25 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ sc_t, 
         const int e = lane + 64 * j;
         if (e < E) v[j] = (float)exp((double)__fsub_rn(v[j], mx));
     }
-    // the double sum in expert order, every lane reading the values across the wave
+    // the double sum in expert order: the values go through the wave's LDS row (lbuf, 16-byte
+    // aligned, ROUTE_MAXE floats) and every lane reads them all at the same addresses (broadcast
+    // reads, 16 values per round); a wave's LDS accesses complete in order
+#pragma unroll
+    for (int j = 0; j < PL; j++)
+        if (lane + 64 * j < E) lbuf[lane + 64 * j] = v[j];
+    __builtin_amdgcn_wave_barrier();
+    typedef float lf4 __attribute__((ext_vector_type(4)));
+    const lf4 *l4 = reinterpret_cast<const lf4 *>(lbuf);
     double sum = 0.0;
-#pragma unroll
-    for (int j = 0; j < PL; j++) {
-        const int n = min(64, E - 64 * j);
-        if (n == 64) {                                       // constant lanes: the reads pipeline
-#pragma unroll
-            for (int l = 0; l < 64; l++) sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
-        } else {
-            for (int l = 0; l < n; l++) sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
-        }
+    int e16 = 0;
+    for (; e16 + 16 <= E; e16 += 16) {
+        const lf4 q0 = l4[e16 / 4], q1 = l4[e16 / 4 + 1], q2 = l4[e16 / 4 + 2], q3 = l4[e16 / 4 + 3];
+        sum += (double)q0.x; sum += (double)q0.y; sum += (double)q0.z; sum += (double)q0.w;
+        sum += (double)q1.x; sum += (double)q1.y; sum += (double)q1.z; sum += (double)q1.w;
+        sum += (double)q2.x; sum += (double)q2.y; sum += (double)q2.z; sum += (double)q2.w;
+        sum += (double)q3.x; sum += (double)q3.y; sum += (double)q3.z; sum += (double)q3.w;
     }
+    for (; e16 < E; e16++) sum += (double)lbuf[e16];
     unsigned used = 0;                                       // bit j: expert lane + 64j selected
 #pragma unroll
     for (int j = 0; j < PL; j++) v[j] = (float)((double)v[j] / sum);
@@ -654,10 +661,11 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ sc_t, 
 // softmax, top-K and renorm of one token per wave (grid T, 64 threads).
 __global__ __launch_bounds__(64) void k_moe_route_topk(const float *__restrict__ scores, int E, int K, int renorm,
                                                        int32_t *__restrict__ idx_out, float *__restrict__ w_out) {
+    __shared__ __align__(16) float lbuf[ROUTE_MAXE];
     const int t = blockIdx.x, lane = threadIdx.x;
     float sel_w[MOE_MAX_K];
     int sel_i[MOE_MAX_K];
-    route_topk_wave(scores + (size_t)t * E, E, K, renorm, lane, sel_i, sel_w);
+    route_topk_wave(scores + (size_t)t * E, E, K, renorm, lane, sel_i, sel_w, lbuf);
     if (lane != 0) return;
     for (int k = 0; k < K; k++) {
         idx_out[(size_t)t * K + k] = sel_i[k];
@@ -673,6 +681,7 @@ __global__ __launch_bounds__(1024) void k_moe_route_bucket(const float *__restri
                                                            int *__restrict__ off, int *__restrict__ perm,
                                                            int *__restrict__ pos, int *__restrict__ tok) {
     extern __shared__ int sm[];
+    __shared__ __align__(16) float lbuf[16][ROUTE_MAXE];   // a row per wave
     int *start = sm;               // [E + 1]
     int *ids = sm + E + 1;         // [P]
     const int P = T * K, wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
@@ -680,7 +689,7 @@ __global__ __launch_bounds__(1024) void k_moe_route_bucket(const float *__restri
     for (int t = wave; t < T; t += nw) {
         float sel_w[MOE_MAX_K];
         int sel_i[MOE_MAX_K];
-        route_topk_wave(scores + (size_t)t * E, E, K, renorm, lane, sel_i, sel_w);
+        route_topk_wave(scores + (size_t)t * E, E, K, renorm, lane, sel_i, sel_w, lbuf[wave]);
         if (lane == 0)
             for (int k = 0; k < K; k++) {
                 idx_out[(size_t)t * K + k] = sel_i[k];
