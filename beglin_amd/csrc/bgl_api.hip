@@ -113,6 +113,8 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     c->no_moe_x = nmx && atoi(nmx) != 0;
     const char *xf = getenv("BGL_X_FUSE");
     c->x_fuse = xf ? (atoi(xf) != 0) : -1;
+    const char *mm = getenv("BGL_MOE_MERGE");
+    c->moe_merge = mm ? (atoi(mm) != 0) : -1;
     *out = c;
     return 0;
 }

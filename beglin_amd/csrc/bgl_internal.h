@@ -35,6 +35,7 @@ struct bgl_ctx {
     int q_prep = -1;                      // BGL_Q_PREP: 0 never / 1 always quantize W4A8 columns up front; -1 by M and K
     bool no_moe_x = false;                // BGL_NO_MOE_X=1: MoE gathers through the prep kernel + k_moe_gemv
     int x_fuse = -1;                      // BGL_X_FUSE: 0 never / 1 always make the digits inside k_gemv_x; -1 by K
+    int moe_merge = -1;                   // BGL_MOE_MERGE: 0 never / 1 always run the routed and shared gate+up in one launch; -1 by shape
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
     int prep_act = -1, prep_gq = 0, prep_M = 0, prep_K = 0;   // what act_* currently hold
     DevBuf part;                          // K-split partial sums [ks][M][N]

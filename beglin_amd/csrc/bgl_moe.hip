@@ -505,13 +505,34 @@ static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, con
     Mr.E = E; Mr.off = S.off; Mr.cols = S.tok; Mr.y = h; Mr.ystride = I; Mr.swiglu = 1;
     // workgroups with work: at most one expert per pair, every tile of it
     const long act_r = (long)std::min(E, P);
-    if ((rc = moe_run(c, Mr, gate, up, units, 0, mx, x_dev, T, H, act_r * Mr.tpe))) return rc;
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         Ms.da = sg->T; Ms.db = su->T; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
         Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
         Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
-        if ((rc = moe_run(c, Ms, nullptr, nullptr, sg->T.nunits, 0, mx, x_dev, T, H, (long)Ms.E * Ms.tpe))) return rc;
+    }
+    // Up to MOE_SHARED_SEG tokens the shared gate+up joins the routed launch when that launch runs
+    // whole-tile workgroups (BGL_MOE_MERGE=1 forces whole tiles, 0 keeps two launches).
+    bool merged = false;
+    if (nsh && Ms.seg == 0 && c->moe_merge != 0 && moe_x_ok(c, gate, up, Mr, H) && moe_x_ok(c, nullptr, nullptr, Ms, H)) {
+        int TR, nw;
+        bgl_moe_x_shape(H, act_r * Mr.tpe + Ms.tpe, c->moe_merge == 1 ? BGL_TILE : c->force_tr, c->x_waves, &TR, &nw);
+        if (TR == BGL_TILE) {
+            memset(&Mr.a, 0, sizeof Mr.a);
+            memset(&Ms.a, 0, sizeof Ms.a);
+            Mr.a.xf = x_dev;
+            Ms.a.xf = x_dev;
+            int tok = prof_begin(c, 1);
+            rc = bgl_launch_moe_x2(Mr, Ms, H, nw, c->stream);
+            prof_end(c, tok);
+            if (rc) return bgl_fail(BGL_E_ARG, "k_moe_x2 launch: in=%d", H);
+            HIPCHK(hipGetLastError());
+            merged = true;
+        }
+    }
+    if (!merged) {
+        if ((rc = moe_run(c, Mr, gate, up, units, 0, mx, x_dev, T, H, act_r * Mr.tpe))) return rc;
+        if (nsh && (rc = moe_run(c, Ms, nullptr, nullptr, sg->T.nunits, 0, mx, x_dev, T, H, (long)Ms.E * Ms.tpe))) return rc;
     }
     memset(&Mr, 0, sizeof Mr);
     max_units(down, Mr.tpe, units);

@@ -178,11 +178,10 @@ __device__ __forceinline__ BglDevTensor mx_tensor(const BglDevTensor *p) {
 // Grid: E x tpe workgroups.  SEG: the segments are consecutive runs of Mt.seg columns of
 // one by-value tensor (the shared experts).  At least 3 waves per SIMD: the widest formats then fit
 // 168 registers without spilling.
-template <bool SEG, int NWMAX, int TR>
-__global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(MoeTask Mt) {
-    extern __shared__ __align__(16) int xl[];
+template <bool SEG, int TR>
+__device__ __forceinline__ void moe_x_body(const MoeTask &Mt, int bid, int *xl) {
     constexpr int SUBS = BGL_TILE / TR;
-    const int e = blockIdx.x / (Mt.tpe * SUBS), rem = blockIdx.x - e * Mt.tpe * SUBS;
+    const int e = bid / (Mt.tpe * SUBS), rem = bid - e * Mt.tpe * SUBS;
     const int tile = rem / SUBS, r0 = (rem % SUBS) * TR;
     int seg0 = 0, ncols = Mt.ncols;
     if constexpr (SEG) { seg0 = e * Mt.seg; ncols = min(Mt.seg, Mt.ncols - seg0); }
@@ -217,6 +216,35 @@ __global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(
         break;
     default: break;
     }
+}
+
+template <bool SEG, int NWMAX, int TR>
+__global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(MoeTask Mt) {
+    extern __shared__ __align__(16) int xl[];
+    moe_x_body<SEG, TR>(Mt, blockIdx.x, xl);
+}
+
+// The routed experts' and the shared experts' gate+up of the same token rows in one launch: the
+// shared tiles run beside the routed ones instead of after them.
+template <int NWMAX>
+__global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x2(MoePair P) {
+    extern __shared__ __align__(16) int xl[];
+    if ((int)blockIdx.x < P.nb0) moe_x_body<false, BGL_TILE>(P.t[0], blockIdx.x, xl);
+    else moe_x_body<false, BGL_TILE>(P.t[1], (int)blockIdx.x - P.nb0, xl);
+}
+
+int bgl_launch_moe_x2(const MoeTask &a, const MoeTask &b, int K, int nw, hipStream_t st) {
+    if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW) return -1;
+    if ((a.seg > 0 && !a.off) || (b.seg > 0 && !b.off)) return -1;
+    const size_t lds = bgl_moe_x_lds(K, nw, BGL_TILE);
+    if (lds > 160 * 1024) return -1;
+    MoePair P;
+    P.t[0] = a; P.t[1] = b;
+    P.nb0 = a.E * a.tpe;
+    const dim3 g(P.nb0 + b.E * b.tpe), bl(nw * BGL_TILE);
+    if (nw <= 8) hipLaunchKernelGGL((k_moe_x2<8>), g, bl, lds, st, P);
+    else hipLaunchKernelGGL((k_moe_x2<16>), g, bl, lds, st, P);
+    return 0;
 }
 
 // Mt.a.xf: the raw fp32 activation rows (row stride K = the tensors' in).  TR rows per workgroup

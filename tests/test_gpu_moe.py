@@ -505,3 +505,32 @@ def test_moe_x_matches_prep_path(torch_dev, oracle, monkeypatch, T, tr):
         c.close()
     ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
     assert relerr(outs[0], ref) <= TOL and relerr(outs[1], ref) <= TOL and relerr(outs[0], outs[1]) <= 2 * TOL
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_merged_gate_up_equals_two_launches(torch_dev, oracle, monkeypatch, T):
+    """Up to 4 tokens, the routed and the shared gate+up run in one launch (k_moe_x2).  With the
+    workgroup shape pinned (whole tiles, 4 waves) the merged launch gives the same bits as the two
+    separate launches, and both equal the oracle's FFN."""
+    import beglin_amd
+    torch = torch_dev
+    E, H, I, K, Ish = 4, 320, 192, 2, 320
+    say("moe merged gate+up", T)
+    fm = [(5, 0), (2, 0), (4, 7), (4, 15)]
+    gate, up, down, shared = moe_setup(oracle, 6400 + T, E, H, I, Ish, fm, down_fmts=fm[::-1], sh_fmt=(4, 12))
+    x = seeded_normal(6410 + T, (T, H))
+    idx, w = oracle.route(seeded_normal(6420 + T, (T, E)), K, True)
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("BGL_MOE_MERGE", flag)
+        monkeypatch.setenv("BGL_FORCE_TR", "64")
+        monkeypatch.setenv("BGL_X_WAVES", "4")
+        c = beglin_amd.Context(0)
+        outs.append(run_moe(c, torch, gate, up, down, shared, x, idx, w))
+        c.close()
+    monkeypatch.delenv("BGL_MOE_MERGE", raising=False)
+    monkeypatch.delenv("BGL_FORCE_TR", raising=False)
+    monkeypatch.delenv("BGL_X_WAVES", raising=False)
+    assert np.array_equal(np.asarray(outs[0]).view(np.uint32), np.asarray(outs[1]).view(np.uint32))
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    assert relerr(outs[0], ref) <= TOL
