@@ -110,7 +110,7 @@ size_t bgl_moe_x_lds(int K, int nw, int TR);
 void bgl_moe_x_shape(int K, long active_wgs, int tr_force, int nw_cap, int *TR, int *nw);
 int bgl_launch_moe_x(const MoeTask &Mt, int K, int TR, int nw, hipStream_t st);
 // Two gathers over the same activation rows in one launch (workgroups [0, nb0) run t[0], the rest
-// t[1]); both unsegmented, whole 64-row tiles.
+// t[1]); whole 64-row tiles; t[1] may be segmented (seg > 0 without off).
 struct MoePair {
     MoeTask t[2];
     int nb0;

@@ -511,12 +511,13 @@ static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, con
         Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
         Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
     }
-    // Up to MOE_SHARED_SEG tokens the shared gate+up joins the routed launch when that launch runs
-    // whole-tile workgroups (BGL_MOE_MERGE=1 forces whole tiles, 0 keeps two launches).
+    // The shared gate+up joins the routed launch when that launch runs whole-tile workgroups
+    // (BGL_MOE_MERGE=1 forces whole tiles, 0 keeps two launches).
     bool merged = false;
-    if (nsh && Ms.seg == 0 && c->moe_merge != 0 && moe_x_ok(c, gate, up, Mr, H) && moe_x_ok(c, nullptr, nullptr, Ms, H)) {
+    if (nsh && c->moe_merge != 0 && moe_x_ok(c, gate, up, Mr, H) && moe_x_ok(c, nullptr, nullptr, Ms, H)) {
         int TR, nw;
-        bgl_moe_x_shape(H, act_r * Mr.tpe + Ms.tpe, c->moe_merge == 1 ? BGL_TILE : c->force_tr, c->x_waves, &TR, &nw);
+        bgl_moe_x_shape(H, act_r * Mr.tpe + (long)Ms.E * Ms.tpe, c->moe_merge == 1 ? BGL_TILE : c->force_tr, c->x_waves, &TR,
+                        &nw);
         if (TR == BGL_TILE) {
             memset(&Mr.a, 0, sizeof Mr.a);
             memset(&Ms.a, 0, sizeof Ms.a);

@@ -225,25 +225,32 @@ __global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(
 }
 
 // The routed experts' and the shared experts' gate+up of the same token rows in one launch: the
-// shared tiles run beside the routed ones instead of after them.
-template <int NWMAX>
+// shared tiles run beside the routed ones instead of after them.  SEG1: the second task's columns
+// are cut into segments (the shared experts over more than 4 tokens).
+template <int NWMAX, bool SEG1>
 __global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x2(MoePair P) {
     extern __shared__ __align__(16) int xl[];
     if ((int)blockIdx.x < P.nb0) moe_x_body<false, BGL_TILE>(P.t[0], blockIdx.x, xl);
-    else moe_x_body<false, BGL_TILE>(P.t[1], (int)blockIdx.x - P.nb0, xl);
+    else moe_x_body<SEG1, BGL_TILE>(P.t[1], (int)blockIdx.x - P.nb0, xl);
 }
 
 int bgl_launch_moe_x2(const MoeTask &a, const MoeTask &b, int K, int nw, hipStream_t st) {
     if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW) return -1;
-    if ((a.seg > 0 && !a.off) || (b.seg > 0 && !b.off)) return -1;
+    if (a.seg > 0 && !a.off) return -1;                     // the first task is never segmented
+    const bool seg1 = !b.off && b.seg > 0;
     const size_t lds = bgl_moe_x_lds(K, nw, BGL_TILE);
     if (lds > 160 * 1024) return -1;
     MoePair P;
     P.t[0] = a; P.t[1] = b;
     P.nb0 = a.E * a.tpe;
     const dim3 g(P.nb0 + b.E * b.tpe), bl(nw * BGL_TILE);
-    if (nw <= 8) hipLaunchKernelGGL((k_moe_x2<8>), g, bl, lds, st, P);
-    else hipLaunchKernelGGL((k_moe_x2<16>), g, bl, lds, st, P);
+    if (nw <= 8) {
+        if (seg1) hipLaunchKernelGGL((k_moe_x2<8, true>), g, bl, lds, st, P);
+        else hipLaunchKernelGGL((k_moe_x2<8, false>), g, bl, lds, st, P);
+    } else {
+        if (seg1) hipLaunchKernelGGL((k_moe_x2<16, true>), g, bl, lds, st, P);
+        else hipLaunchKernelGGL((k_moe_x2<16, false>), g, bl, lds, st, P);
+    }
     return 0;
 }
 

@@ -507,11 +507,12 @@ def test_moe_x_matches_prep_path(torch_dev, oracle, monkeypatch, T, tr):
     assert relerr(outs[0], ref) <= TOL and relerr(outs[1], ref) <= TOL and relerr(outs[0], outs[1]) <= 2 * TOL
 
 
-@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("T", [1, 3, 6, 13])
 def test_moe_merged_gate_up_equals_two_launches(torch_dev, oracle, monkeypatch, T):
-    """Up to 4 tokens, the routed and the shared gate+up run in one launch (k_moe_x2).  With the
-    workgroup shape pinned (whole tiles, 4 waves) the merged launch gives the same bits as the two
-    separate launches, and both equal the oracle's FFN."""
+    """The routed and the shared gate+up in one launch (k_moe_x2; past 4 tokens the shared columns
+    run in segments of 4, the last one partial at T = 6 and 13).  With the workgroup shape pinned
+    (whole tiles, 4 waves) the merged launch gives the same bits as the two separate launches, and
+    both equal the oracle's FFN."""
     import beglin_amd
     torch = torch_dev
     E, H, I, K, Ish = 4, 320, 192, 2, 320
