@@ -5,8 +5,9 @@
  * repository root).  Conventions:
  *   - return 0 on success, a negative BGL_E_* code on failure (bgl_last_error() has the text).
  *     The reference's GEMV entries FATAL+exit(1) on misuse (q4gemv.h:675, :704, :783;
- *     q4gemv_g256.h:342-343); the engine-side shim in INTEGRATION.md turns a non-zero return into
- *     that same FATAL, so behaviour at the engine boundary is unchanged.
+ *     q4gemv_g256.h:342-343); an engine-side shim that turns a non-zero return into that same
+ *     FATAL keeps the behaviour at the engine boundary unchanged.  The bgl_gpu_* (MLX boundary)
+ *     functions below keep MLX's convention instead: 1 = ok, 0 = failure.
  *   - weights: "kind" ids 1..4 are the engine's WT kinds (qwen_infer.c:207): 1 K_Q4G64, 2 K_Q8G64,
  *     3 K_Q4G256SF, 4 K_QNG64; 5 is BGL_K_Q4G32H (int4 group-32, fp16 scale, q4gemv nibble pairing).
  *     6..8 are the AF expert kinds the MoE boundary binds (mlx_gpu_bind_af bits=4/16/32,
