@@ -721,6 +721,10 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
         while (TR > 8 && bgl_gemv_q_lds(Ts[0].fmt, Ts[0].K, TR, MB) > q_lds_max(MB)) TR >>= 1;   // the t[u][row] terms shrink with TR
         const int KQ = BGL_TILE / TR, NP = (Ts[0].K + 255) / 256;
         int nw = std::min(16, std::max(3, (MB * NP + 3) / 4));
+        // 8 columns quantized in the kernel by >= 512 workgroups: 4 waves (Qwen2.5-1.5B gate+up,
+        // 560 workgroups x 48 passes: 18.2 us with 12 waves, 15.7 with 4; the 256- and 192-
+        // workgroup q/k/v and o launches run best with 12)
+        if (MB == 8 && !(prep && MB > 1) && (long)blocks * KQ >= 512) nw = std::min(nw, 4);
         if (nw > c->max_waves) nw = c->max_waves;
         // every task block of the launch uses the same TR; remap blk0 to workgroup units
         for (int i = 0; i < n; i++) L.t[i].blk0 *= KQ;
