@@ -393,13 +393,19 @@ def test_moe_layer_fused_router_ties_and_wide(ctx, torch_dev, oracle):
         t.free()
 
 
-def test_moe_layer_graph_replays_match_eager(torch_dev, oracle):
+@pytest.mark.parametrize("merge", ["auto", "1"])
+def test_moe_layer_graph_replays_match_eager(torch_dev, oracle, monkeypatch, merge):
     """The whole layer (router, top-K + bucketing, FFN, shared experts) replayed
-    from a graph: every replay, with eager calls in between, equals the eager result bit for bit."""
+    from a graph: every replay, with eager calls in between, equals the eager result bit for bit
+    (merge "1": the routed and shared gate+up in one launch, k_moe_x2)."""
     import beglin_amd
     torch = torch_dev
     E, H, I, K, Ish, T = 16, 256, 128, 4, 128, 5
-    say("moe_layer graph")
+    say("moe_layer graph", merge)
+    if merge == "auto":
+        monkeypatch.delenv("BGL_MOE_MERGE", raising=False)
+    else:
+        monkeypatch.setenv("BGL_MOE_MERGE", merge)
     gate, up, down, shared = moe_setup(oracle, 6300, E, H, I, Ish, [(5, 0), (4, 9)])
     x = dev(torch, seeded_normal(6301, (T, H)))
     rwt = dev(torch, seeded_normal(6302, (E, H), 0.05))
