@@ -501,12 +501,24 @@ extern "C" int bgl_dequant_dev(bgl_ctx *c, const bgl_tensor *t, int row0, int nr
 // ------------------------------------------------------------------ activation prep
 static int act_group(int kind) { return kind == BGL_Q4G256SF ? 256 : 64; }
 
+// The fp32-activation operands of M prepared columns of length K: k_act_x24 writes level 0 of all
+// M columns and then level 1 into each of the three buffers.
+void f32_act_ptrs(const void *xw, const void *xs, const void *xsum, int M, int K, const float *x_dev, GemvAct &A) {
+    const size_t ng = (size_t)K / 64;
+    A.xw = (const int *)xw; A.xs = (const float *)xs; A.xsum = (const int *)xsum;
+    A.xw1 = A.xw + (size_t)M * ng * BGL_XD_DW;
+    A.xs1 = A.xs + (size_t)M * ng;
+    A.xsum1 = A.xsum + (size_t)M * (K / 32) * 4;
+    A.xf = x_dev;
+    A.gq = 64;
+}
+
 int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, GemvAct &A) {
     memset(&A, 0, sizeof A);
     if (act == BGL_ACT_F32) {
         int ng = K / 64;
-        if (dbuf_reserve(c, c->act_w, (size_t)M * ng * 192, false) || dbuf_reserve(c, c->act_s, (size_t)M * ng * 4, false) ||
-            dbuf_reserve(c, c->act_sum, (size_t)M * (K / 32) * 16, false))
+        if (dbuf_reserve(c, c->act_w, (size_t)2 * M * ng * 192, false) || dbuf_reserve(c, c->act_s, (size_t)2 * M * ng * 4, false) ||
+            dbuf_reserve(c, c->act_sum, (size_t)2 * M * (K / 32) * 16, false))
             return BGL_E_NOMEM;
         int tok = prof_begin(c, 0);
         hipLaunchKernelGGL(k_act_x24, dim3(nblk((long)M * ng * 64)), dim3(256), 0, c->stream, x_dev, M, K,
@@ -522,11 +534,15 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
         prof_end(c, tok);
     }
     HIPCHK(hipGetLastError());
-    c->prep_act = act; c->prep_gq = gq; c->prep_M = M; c->prep_K = K;
-    A.xw = (const int *)c->act_w.p;
-    A.xs = (const float *)c->act_s.p;
-    A.xsum = (const int *)c->act_sum.p;
-    A.gq = gq;
+    c->prep_act = act; c->prep_gq = gq; c->prep_M = M; c->prep_K = K; c->prep_x = x_dev;
+    if (act == BGL_ACT_F32) {
+        f32_act_ptrs(c->act_w.p, c->act_s.p, c->act_sum.p, M, K, x_dev, A);
+    } else {
+        A.xw = (const int *)c->act_w.p;
+        A.xs = (const float *)c->act_s.p;
+        A.xsum = (const int *)c->act_sum.p;
+        A.gq = gq;
+    }
     return 0;
 }
 
@@ -804,7 +820,8 @@ extern "C" int bgl_matmul_prepped_dev(bgl_ctx *c, const bgl_tensor *w, int act, 
     HIPCHK(hipSetDevice(c->device));
     GemvAct A;
     memset(&A, 0, sizeof A);
-    A.xw = (const int *)c->act_w.p; A.xs = (const float *)c->act_s.p; A.xsum = (const int *)c->act_sum.p; A.gq = c->prep_gq;
+    if (act == BGL_ACT_F32) f32_act_ptrs(c->act_w.p, c->act_s.p, c->act_sum.p, c->prep_M, T.K, c->prep_x, A);
+    else { A.xw = (const int *)c->act_w.p; A.xs = (const float *)c->act_s.p; A.xsum = (const int *)c->act_sum.p; A.gq = c->prep_gq; }
     const float *b[1] = {bias_dev};
     float *y[1] = {y_dev};
     return run_gemv(c, 1, &T, act, A, M, b, y, nullptr);

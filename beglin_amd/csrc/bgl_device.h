@@ -29,12 +29,23 @@
 #define BGL_F16 BGL_K_F16
 #define BGL_F32 BGL_K_F32
 
-// fp32 activations are represented exactly enough for the 1e-5 bar as X = rint(x * 2^(21-e)) per
-// 64-group (e = exponent of the group's max |x|, so |X| <= 2^21), split into three balanced
-// base-256 int8 digits X = d0 + 256*d1 + 65536*d2.  Per column the prep kernel writes
-// [group][digit][64 bytes] (48 dwords per group), the power-of-two scale 2^(e-21) per group and
-// the exact integer sum of X per 32-element half-group.
+// fp32 activations as exact integers, per 64-group:
+//   level 0: X = rint(x * 2^(21-e)), e = exponent of the group's largest finite |x| (|X| <= 2^21),
+//            as three balanced base-256 int8 digits X = d0 + 256*d1 + 65536*d2;
+//   level 1: only in groups where fewer than half of the nonzero elements lie within 2^6 of that
+//            maximum (an outlier would otherwise leave the rest of the group with few bits): the
+//            residual r = x * 2^(21-e) - X (exact) as X1 = rint(r * 2^(21-e1)), e1 = exponent of the
+//            group's largest |r|, in the same three digits.  x = (X + X1 * 2^(e1-21)) * 2^(e-21) to
+//            about 2^-44 of the group maximum.
+// Non-finite elements (NaN, +-Inf) enter both levels as 0; the group is flagged and the GEMVs add
+// their products code * scale * x one element at a time, so NaN and +-Inf propagate as in IEEE
+// arithmetic.  Per column the prep kernel writes [group][digit][64 bytes] (48 dwords per group),
+// the power-of-two scale 2^(e-21) per group and the exact integer sum of the digits per
+// 32-element half-group; level 1 the same beside it, plus the ratio 2^(e1-21) (0 without level 1).
 #define BGL_XD_DW 48
+#define BGL_XF_L1 1            // group flags: the group has level-1 digits
+#define BGL_XF_NF 2            //              the group holds a non-finite element
+#define BGL_X_SPIKE_BITS 6     // level 1 when fewer than half the nonzero |x| are >= 2^(e-6)
 
 // Wave-uniform read-only operands (activations, column maps) are read through the constant address
 // space so the compiler emits scalar loads (s_load_dwordx16) and feeds v_dot4 from SGPRs.

@@ -91,6 +91,20 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv(GemvLaunch L) {
         }
         u = un;
     }
+    // groups whose fp32 activations carry a level-1 residual or non-finite values (cold path)
+    if constexpr (ACT == BGL_ACT_F32 && FMT != BGL_F16 && FMT != BGL_F32 && FMT != BGL_Q4G256SF) {
+        const WRow W{&T, tile * BGL_TILE + lane};
+        for (int uu = ubeg + wave; uu < U; uu += nw) {
+            int fl = 0;
+#pragma unroll
+            for (int m = 0; m < MB; m++) fl |= unit_flags<FMT, NB>(L.a, C.am[m], K, uu);
+            if (fl) {
+                Raw<FMT, NB> rf;
+                load_raw<FMT, NB>(rf, T, tile, lane, uu);
+                comp_fix<FMT, NB, MB>(rf, W, uu, L.a, C, acc);
+            }
+        }
+    }
 
 #pragma unroll
     for (int m = 0; m < MB; m++) red[wave][m][lane] = acc[m];

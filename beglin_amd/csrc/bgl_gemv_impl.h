@@ -23,11 +23,36 @@ __device__ __forceinline__ Cols<MB> col_rows(const GemvAct &A, int m0, int mcols
     return c;
 }
 
-// digit sums of one 32-element half (3 ints, padded to 4)
-__device__ __forceinline__ int4 ld_dsum(const GemvAct &A, int am, int K, int half) {
-    ucint p = uni(A.xsum) + ((size_t)am * (K >> 5) + half) * 4;
+// digit sums of one 32-element half (3 ints; the 4th: the group's BGL_XF_* flags in its first half)
+__device__ __forceinline__ int4 ld_dsum(const int *xsum, int am, int K, int half) {
+    ucint p = uni(xsum) + ((size_t)am * (K >> 5) + half) * 4;
     return make_int4(p[0], p[1], p[2], p[3]);
 }
+__device__ __forceinline__ int4 ld_dsum(const GemvAct &A, int am, int K, int half) { return ld_dsum(A.xsum, am, K, half); }
+// the BGL_XF_* flags of group g of prepared column am
+__device__ __forceinline__ int ld_xflags(const GemvAct &A, int am, int K, int g) {
+    return uni(A.xsum)[((size_t)am * (K >> 5) + 2 * g) * 4 + 3];
+}
+
+// The products code * scale * x of a group's non-finite activations, one element at a time
+// (IEEE: NaN and +-Inf propagate as in the reference's fp32-product sums).  Only groups flagged
+// BGL_XF_NF take this path; their finite part comes from the digits.
+template <int FMT, int NB>
+__device__ __forceinline__ float x_nonfinite(const BglDevTensor &T, int row, int g, const float *xr) {
+    float acc = 0.0f;
+#pragma unroll 1
+    for (int j = 0; j < 64; j++) {
+        const float v = xr[g * 64 + j];
+        if (!isfinite(v)) acc += w_at_t<FMT, NB>(T, row, g * 64 + j) * v;
+    }
+    return acc;
+}
+
+// The weight row a lane computes (for the non-finite slow path).
+struct WRow {
+    const BglDevTensor *T;
+    int row;
+};
 
 __device__ __forceinline__ float fold_digits(int t0, int t1, int t2) {
     return (float)t0 + 256.0f * (float)t1 + 65536.0f * (float)t2;
@@ -368,6 +393,125 @@ __device__ __forceinline__ void comp_dense(const Raw<FMT, NB> &r, int K, int u, 
     }
 #pragma unroll
     for (int m = 0; m < MB; m++) acc[m] += a[m];
+}
+
+// ======================================================================== flagged groups (cold path)
+// The terms the level-0 digits leave out, for the groups of unit u flagged in some column of the
+// launch: the level-1 residual s * ((V1 * 2^(e1-21)) * 2^(e-21)) and the non-finite products.  Run
+// after the main loop over units whose flags are set (the unit's weights are loaded again), so the
+// hot loop keeps its registers.
+template <int FMT, int NB>
+__device__ __forceinline__ int unit_flags(const GemvAct &A, int am, int K, int u) {
+    if constexpr (FMT == BGL_QNG64) {
+        const int g = 2 * u;
+        return ld_xflags(A, am, K, g) | (g + 1 < (K >> 6) ? ld_xflags(A, am, K, g + 1) : 0);
+    } else {
+        return ld_xflags(A, am, K, u);
+    }
+}
+
+template <int FMT, int NB, int MB>
+__device__ __forceinline__ void comp_fix(const Raw<FMT, NB> &r, const WRow &W, int u, const GemvAct &A, const Cols<MB> &C,
+                                         float (&acc)[MB]) {
+    const int K = W.T->K, ng = K >> 6;
+    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H || FMT == BGL_Q4G64A) {
+        int lo[8], hi[8];
+        const uint32_t raw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) { lo[q] = nib_lo(raw[q]); hi[q] = nib_hi(raw[q]); }
+#pragma unroll 1
+        for (int m = 0; m < MB; m++) {
+            const int am = C.am[m];
+            const size_t gi = (size_t)am * ng + u;
+            const int fl = ld_xflags(A, am, K, u);
+            if (!fl) continue;
+            float t = 0.0f;
+            if (fl & BGL_XF_L1) {
+                ucint xg = uni(A.xw1) + gi * BGL_XD_DW;
+                int a[3] = {0, 0, 0}, b[3] = {0, 0, 0};
+#pragma unroll
+                for (int d = 0; d < 3; d++) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) { a[d] = dot4(lo[q], xg[16 * d + 2 * q], a[d]); a[d] = dot4(hi[q], xg[16 * d + 2 * q + 1], a[d]); }
+#pragma unroll
+                    for (int q = 4; q < 8; q++) { b[d] = dot4(lo[q], xg[16 * d + 2 * q], b[d]); b[d] = dot4(hi[q], xg[16 * d + 2 * q + 1], b[d]); }
+                }
+                const int4 d0 = ld_dsum(A.xsum1, am, K, 2 * u), d1 = ld_dsum(A.xsum1, am, K, 2 * u + 1);
+                const float rt = uni(A.xs1)[gi], xs = uni(A.xs)[gi];
+                if constexpr (FMT == BGL_Q4G64) {
+                    const float V = fold_digits(a[0] + b[0] - 8 * (d0.x + d1.x), a[1] + b[1] - 8 * (d0.y + d1.y),
+                                                a[2] + b[2] - 8 * (d0.z + d1.z));
+                    t = r.s * ((V * rt) * xs);
+                } else if constexpr (FMT == BGL_Q4G32H) {
+                    const float sa = __half2float(__ushort_as_half((unsigned short)(r.s & 0xffffu)));
+                    const float sb = __half2float(__ushort_as_half((unsigned short)(r.s >> 16)));
+                    const float Va = fold_digits(a[0] - 8 * d0.x, a[1] - 8 * d0.y, a[2] - 8 * d0.z);
+                    const float Vb = fold_digits(b[0] - 8 * d1.x, b[1] - 8 * d1.y, b[2] - 8 * d1.z);
+                    t = sa * ((Va * rt) * xs) + sb * ((Vb * rt) * xs);
+                } else {                                         // affine: s * sum(nib X1) + b * sum(X1)
+                    const float V = fold_digits(a[0] + b[0], a[1] + b[1], a[2] + b[2]);
+                    const float sx = fold_digits(d0.x + d1.x, d0.y + d1.y, d0.z + d1.z);
+                    t = r.s * ((V * rt) * xs) + r.b * ((sx * rt) * xs);
+                }
+            }
+            if (fl & BGL_XF_NF) t += x_nonfinite<FMT, NB>(*W.T, W.row, u, A.xf + (size_t)am * K);
+            acc[m] += t;
+        }
+    } else if constexpr (FMT == BGL_Q8G64) {
+        int w[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            w[4 * k] = (int)r.c[k].x; w[4 * k + 1] = (int)r.c[k].y; w[4 * k + 2] = (int)r.c[k].z; w[4 * k + 3] = (int)r.c[k].w;
+        }
+#pragma unroll 1
+        for (int m = 0; m < MB; m++) {
+            const int am = C.am[m];
+            const size_t gi = (size_t)am * ng + u;
+            const int fl = ld_xflags(A, am, K, u);
+            if (!fl) continue;
+            float t = 0.0f;
+            if (fl & BGL_XF_L1) {
+                ucint xg = uni(A.xw1) + gi * BGL_XD_DW;
+                int t0 = 0, t1 = 0, t2 = 0;
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    t0 = dot4(w[q], xg[q], t0); t1 = dot4(w[q], xg[16 + q], t1); t2 = dot4(w[q], xg[32 + q], t2);
+                }
+                t = r.s * ((fold_digits(t0, t1, t2) * uni(A.xs1)[gi]) * uni(A.xs)[gi]);
+            }
+            if (fl & BGL_XF_NF) t += x_nonfinite<FMT, NB>(*W.T, W.row, u, A.xf + (size_t)am * K);
+            acc[m] += t;
+        }
+    } else if constexpr (FMT == BGL_QNG64) {
+        // per element: the row's code (read from the tiled layout) times each level-1 digit (cold path)
+#pragma unroll 1
+        for (int h = 0; h < 2; h++) {
+            const int g = 2 * u + h;
+            if (g >= ng) break;
+            const float s = h ? r.s.y : r.s.x;
+#pragma unroll 1
+            for (int m = 0; m < MB; m++) {
+                const int am = C.am[m];
+                const size_t gi = (size_t)am * ng + g;
+                const int fl = ld_xflags(A, am, K, g);
+                if (!fl) continue;
+                float t = 0.0f;
+                if (fl & BGL_XF_L1) {
+                    ucint xg = uni(A.xw1) + gi * BGL_XD_DW;
+                    int td[3] = {0, 0, 0};
+#pragma unroll 1
+                    for (int j = 0; j < 64; j++) {
+                        const int code = (int)qng_u_at(*W.T, W.row, g * 64 + j) - (1 << (NB - 1));
+#pragma unroll
+                        for (int d = 0; d < 3; d++) td[d] += code * (int)(int8_t)(xg[16 * d + (j >> 2)] >> (8 * (j & 3)));
+                    }
+                    t = s * ((fold_digits(td[0], td[1], td[2]) * uni(A.xs1)[gi]) * uni(A.xs)[gi]);
+                }
+                if (fl & BGL_XF_NF) t += x_nonfinite<FMT, NB>(*W.T, W.row, g, A.xf + (size_t)am * K);
+                acc[m] += t;
+            }
+        }
+    }
 }
 
 template <int FMT, int ACT, int NB, int MB>

@@ -4,10 +4,14 @@
 // the fp32 fold, and the in-kernel making of the records from raw fp32 values.
 //
 // A record (one per 64-group and activation column, 240 bytes in LDS): the three balanced int8
-// digits of X = rint(x * 2^(21-e)) (e = exponent of the group's max |x|) as 48 dwords, the digit
-// sums of the two 32-element halves, the scale 2^(e-21) -- k_act_x24's operands (bgl_prep.hip), so
-// every product is an exact int32 dot4 sum and fp32 only enters in the per-group fold.  The 60-dword
-// stride puts the <= 8 records one read touches in disjoint banks.
+// digits of X = rint(x * 2^(21-e)) (e = exponent of the group's largest finite |x|) as 48 dwords,
+// the digit sums of the two 32-element halves (the first half's 4th int holds the group's BGL_XF_*
+// flags), the scale 2^(e-21) and the level-1 ratio 2^(e1-21) -- k_act_x24's operands
+// (bgl_prep.hip), so every product is an exact int32 dot4 sum and fp32 only enters in the
+// per-group fold.  A group flagged BGL_XF_L1 also has a level-1 record (the residual's digits and
+// sums) at a fixed dword offset l1 from its level-0 record; its ratio is 0 otherwise, so a level-1
+// fold over a stale record adds exactly 0.  The 60-dword stride puts the <= 8 records one read
+// touches in disjoint banks.
 //
 // qNg64 bit planes: the 8-bit field (stored as f ^ 0x80, a signed byte f - 128) is one dot4
 // operand; the 4-, 2- and 1-bit fields of an element are merged into one byte (their values sit at
@@ -17,8 +21,8 @@
 #include "bgl_gemv_impl.h"
 
 #define XREC_DW 60            // LDS dwords per 64-group record
-#define XREC_DSUM 48          // digit sums of the two halves: [half][digit 0..2, pad]
-#define XREC_SCALE 56         // 2^(e-21)
+#define XREC_DSUM 48          // digit sums of the two halves: [half][digit 0..2, flags / pad]
+#define XREC_SCALE 56         // 2^(e-21), then the level-1 ratio 2^(e1-21)
 #define X_PRE 4               // record pieces (16 bytes) per thread loaded ahead of the weights
 
 // (a & m) | o in one v_and_or_b32 (gfx9's three-operand encoding takes no literal constant and
@@ -230,6 +234,67 @@ __device__ __forceinline__ XDec<FMT, NB> x_decode(const XRaw<FMT, NB> &r) {
     return d;
 }
 
+// The exact integer dot products of a lane's decoded group with one record's digits, bias
+// corrections included: o[0..2] per digit (Q4G32H: the first half; o[3..5] the second).
+template <int FMT, int NB>
+__device__ __forceinline__ void x_ints(const XDec<FMT, NB> &w, const int *rec, const int4 &ds0, const int4 &ds1, int (&o)[6]) {
+    // cold path only: one digit at a time (unrolled, the three digits' LDS reads are hoisted together)
+    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H) {
+        int ta[3], tb[3];
+#pragma unroll 1
+        for (int d = 0; d < 3; d++) {
+            const XDig x = x_digit(rec, d);
+            int a = 0, b = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) { a = dot4(w.lo[q], x.v[2 * q], a); a = dot4(w.hi[q], x.v[2 * q + 1], a); }
+#pragma unroll
+            for (int q = 4; q < 8; q++) { b = dot4(w.lo[q], x.v[2 * q], b); b = dot4(w.hi[q], x.v[2 * q + 1], b); }
+            ta[d] = a; tb[d] = b;
+        }
+        if constexpr (FMT == BGL_Q4G64) {
+            o[0] = ta[0] + tb[0] - 8 * (ds0.x + ds1.x); o[1] = ta[1] + tb[1] - 8 * (ds0.y + ds1.y);
+            o[2] = ta[2] + tb[2] - 8 * (ds0.z + ds1.z);
+        } else {
+            o[0] = ta[0] - 8 * ds0.x; o[1] = ta[1] - 8 * ds0.y; o[2] = ta[2] - 8 * ds0.z;
+            o[3] = tb[0] - 8 * ds1.x; o[4] = tb[1] - 8 * ds1.y; o[5] = tb[2] - 8 * ds1.z;
+        }
+    } else if constexpr (FMT == BGL_Q8G64) {
+#pragma unroll 1
+        for (int d = 0; d < 3; d++) {
+            const XDig x = x_digit(rec, d);
+            int a = 0;
+#pragma unroll
+            for (int q = 0; q < 16; q++) a = dot4(w.w[q], x.v[q], a);
+            o[d] = a;
+        }
+    } else {
+        using X = XDec<FMT, NB>;
+        constexpr int CORR = 128 * X::H8 - (1 << (NB - 1));     // code = u - 2^(n-1); the 8-bit field is stored as f - 128
+#pragma unroll 1
+        for (int d = 0; d < 3; d++) {
+            const XDig x = x_digit(rec, d);
+            int a = 0, b = 0;
+            if constexpr (X::H8) {
+#pragma unroll
+                for (int q = 0; q < 16; q++) a = dot4(w.lo[q], x.v[q], a);
+            }
+            if constexpr (X::HI) {
+#pragma unroll
+                for (int q = 0; q < 16; q++) b = dot4(w.hi[q], x.v[q], b);
+            }
+            o[d] = X::H8 ? a + b * 256 : b;
+        }
+        o[0] += CORR * (ds0.x + ds1.x); o[1] += CORR * (ds0.y + ds1.y); o[2] += CORR * (ds0.z + ds1.z);
+    }
+}
+
+// Where the raw values of a lane's group are, for the non-finite slow path.
+struct XRow {
+    const BglDevTensor *T;
+    int row;                  // the lane's weight row
+    const float *xr;          // the activation column's raw values
+};
+
 // The group's fp32 term against one record: the exact integer dot product per digit, folded as
 // s * ((t0 + 256 t1 + 65536 t2) * 2^(e-21)).
 template <int FMT, int NB>
@@ -292,59 +357,146 @@ __device__ __forceinline__ float x_dot(const XDec<FMT, NB> &w, const int *rec) {
     }
 }
 
+// The terms the level-0 digits leave out, for a lane's group flagged BGL_XF_L1 or BGL_XF_NF (0 for
+// the lanes of the wave whose groups are not): the level-1 residual
+// s * ((V1 * 2^(e1-21)) * 2^(e-21)) and the non-finite products.  Cold path: the GEMVs run it after
+// their main loop for the slots whose records carry flags, with the weights loaded again.
+template <int FMT, int NB>
+__device__ __forceinline__ float x_fix(const XDec<FMT, NB> &w, const int *rec, int l1, const XRow &xrow, int g) {
+    const int fl = rec[XREC_DSUM + 3];
+    const float2 xs = *reinterpret_cast<const float2 *>(rec + XREC_SCALE);
+    float t = 0.0f;
+    if (__builtin_amdgcn_ballot_w64(fl & BGL_XF_L1)) {
+        const int *r1 = rec + l1;
+        const int4 e0 = *reinterpret_cast<const int4 *>(r1 + XREC_DSUM);
+        const int4 e1 = *reinterpret_cast<const int4 *>(r1 + XREC_DSUM + 4);
+        int p[6];
+        x_ints<FMT, NB>(w, r1, e0, e1, p);
+        const float rt = (fl & BGL_XF_L1) ? xs.y : 0.0f;      // a stale record of an unflagged lane adds 0
+        if constexpr (FMT == BGL_Q4G32H)
+            t = w.sa * ((fold_digits(p[0], p[1], p[2]) * rt) * xs.x) + w.sb * ((fold_digits(p[3], p[4], p[5]) * rt) * xs.x);
+        else
+            t = w.s * ((fold_digits(p[0], p[1], p[2]) * rt) * xs.x);
+    }
+    if (fl & BGL_XF_NF) t += x_nonfinite<FMT, NB>(*xrow.T, xrow.row, g, xrow.xr);
+    return t;
+}
+
 template <int FMT, int NB>
 __device__ __forceinline__ float x_group(const XRaw<FMT, NB> &r, const int *rec) { return x_dot<FMT, NB>(x_decode<FMT, NB>(r), rec); }
 
 // ---- fused activation digits (k_act_x24's arithmetic, bgl_prep.hip): one pass is 256 consecutive
 // values, lane l holding values 4l..4l+3 (one float4), a 16-lane row one 64-group g = 4p + l/16.
-// Per group e = exponent of max|x| (frexp), X = rint(x * 2^(21-e)) split into balanced int8 digits
-// X = d0 + 256 d1 + 65536 d2; the record gets the digits, their sums per 32-element half and 2^(e-21).
+// Per group e = exponent of the largest finite |x| (frexp), X = rint(x * 2^(21-e)) split into
+// balanced int8 digits X = d0 + 256 d1 + 65536 d2; the record gets the digits, their sums per
+// 32-element half, the flags, 2^(e-21) and the level-1 ratio.  Groups with an outlier (fewer than
+// half the nonzero elements within 2^BGL_X_SPIKE_BITS of the max) also get the level-1 record of
+// the residual at rec + l1; non-finite elements count as 0 and flag the group.
 template <int CTRL>
 __device__ __forceinline__ uint32_t x_dpp(uint32_t v) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false); }
 __device__ __forceinline__ uint32_t x_umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t x_row_umax(uint32_t v) {
+    v = x_umax(v, x_dpp<0xB1>(v));
+    v = x_umax(v, x_dpp<0x4E>(v));
+    v = x_umax(v, x_dpp<0x141>(v));
+    return x_umax(v, x_dpp<0x140>(v));            // the 16-lane row's max in all its lanes
+}
 
 __device__ __forceinline__ float4 x_pass_load(const float *x, int p, int lane, int K) {
     const bgl_f32x4 t = *((const BGL_GLOBAL bgl_f32x4 *)(x + min(256 * p + 4 * lane, K - 4)));
     return make_float4(t.x, t.y, t.z, t.w);
 }
 
-__device__ __forceinline__ void x_pass_digits(const float4 &v, int p, int lane, int G, int *xl) {
-    const int g = 4 * p + (lane >> 4), q = lane & 15;
-    uint32_t mb = x_umax(x_umax(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
-                         x_umax(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu));
-    mb = x_umax(mb, x_dpp<0xB1>(mb));
-    mb = x_umax(mb, x_dpp<0x4E>(mb));
-    mb = x_umax(mb, x_dpp<0x141>(mb));
-    mb = x_umax(mb, x_dpp<0x140>(mb));             // the group's max |x| bits in all 16 lanes
-    const float mx = __uint_as_float(mb);
-    int e = 0;
-    if (mx > 0.0f) frexpf(mx, &e);
-    const float f[4] = {v.x, v.y, v.z, v.w};
-    uint32_t D0 = 0, D1 = 0, D2 = 0;
+// Three balanced digits of 4 integers |X| <= 2^21, packed one byte per element, and their sums
+// over the lane's 8-lane half of the row (32 elements).
+struct XPack {
+    uint32_t D[3];
+    int s[3];
+};
+__device__ __forceinline__ XPack x_pack3(const int (&X)[4]) {
+    XPack p;
+    p.D[0] = p.D[1] = p.D[2] = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int X = mx > 0.0f ? (int)rintf(ldexpf(f[i], 21 - e)) : 0;
-        const int d0 = (int)(int8_t)(X & 255);
-        const int X1 = (X - d0) >> 8;
+        const int d0 = (int)(int8_t)(X[i] & 255);
+        const int X1 = (X[i] - d0) >> 8;
         const int d1 = (int)(int8_t)(X1 & 255);
         const int d2 = (X1 - d1) >> 8;
-        D0 |= ((uint32_t)d0 & 255u) << (8 * i);
-        D1 |= ((uint32_t)d1 & 255u) << (8 * i);
-        D2 |= ((uint32_t)d2 & 255u) << (8 * i);
+        p.D[0] |= ((uint32_t)d0 & 255u) << (8 * i);
+        p.D[1] |= ((uint32_t)d1 & 255u) << (8 * i);
+        p.D[2] |= ((uint32_t)d2 & 255u) << (8 * i);
     }
-    // digit sums of the lane's 4 values, then of its 8-lane half (32 values)
-    int s0 = dot4((int)D0, 0x01010101, 0), s1 = dot4((int)D1, 0x01010101, 0), s2 = dot4((int)D2, 0x01010101, 0);
-    s0 += (int)x_dpp<0xB1>((uint32_t)s0); s1 += (int)x_dpp<0xB1>((uint32_t)s1); s2 += (int)x_dpp<0xB1>((uint32_t)s2);
-    s0 += (int)x_dpp<0x4E>((uint32_t)s0); s1 += (int)x_dpp<0x4E>((uint32_t)s1); s2 += (int)x_dpp<0x4E>((uint32_t)s2);
-    s0 += (int)x_dpp<0x141>((uint32_t)s0); s1 += (int)x_dpp<0x141>((uint32_t)s1); s2 += (int)x_dpp<0x141>((uint32_t)s2);
-    if (g < G) {
-        int *rec = xl + g * XREC_DW;
-        rec[q] = (int)D0; rec[16 + q] = (int)D1; rec[32 + q] = (int)D2;
-        if ((q & 7) == 0) {
-            int4 *ds = reinterpret_cast<int4 *>(rec + XREC_DSUM + 4 * (q >> 3));
-            *ds = make_int4(s0, s1, s2, 0);
-        }
-        if (q == 0) rec[XREC_SCALE] = __float_as_int(mx > 0.0f ? ldexpf(1.0f, e - 21) : 0.0f);
+#pragma unroll
+    for (int d = 0; d < 3; d++) {
+        int t = dot4((int)p.D[d], 0x01010101, 0);
+        t += (int)x_dpp<0xB1>((uint32_t)t);
+        t += (int)x_dpp<0x4E>((uint32_t)t);
+        t += (int)x_dpp<0x141>((uint32_t)t);
+        p.s[d] = t;
+    }
+    return p;
+}
+__device__ __forceinline__ void x_store3(int *rec, int q, const XPack &p, int flags) {
+    rec[q] = (int)p.D[0]; rec[16 + q] = (int)p.D[1]; rec[32 + q] = (int)p.D[2];
+    if ((q & 7) == 0) {
+        int4 *ds = reinterpret_cast<int4 *>(rec + XREC_DSUM + 4 * (q >> 3));
+        *ds = make_int4(p.s[0], p.s[1], p.s[2], q == 0 ? flags : 0);
     }
 }
 
+__device__ __forceinline__ void x_pass_digits(const float4 &v, int p, int lane, int G, int *xl, int l1) {
+    const int g = 4 * p + (lane >> 4), q = lane & 15;
+    float f[4] = {v.x, v.y, v.z, v.w};
+    uint32_t b[4];
+    int nnf = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        b[i] = __float_as_uint(f[i]) & 0x7fffffffu;
+        if (b[i] >= 0x7f800000u) { f[i] = 0.0f; b[i] = 0u; nnf++; }     // NaN / +-Inf: 0 in the digits
+    }
+    const uint32_t mb = x_row_umax(x_umax(x_umax(b[0], b[1]), x_umax(b[2], b[3])));   // the group's max |x| bits
+    const float mx = __uint_as_float(mb);
+    int e = 0;
+    if (mx > 0.0f) frexpf(mx, &e);
+    const uint32_t thr = mx > 0.0f ? __float_as_uint(ldexpf(1.0f, e - BGL_X_SPIKE_BITS)) : 0u;
+    int cnt = 65536 * nnf;
+#pragma unroll
+    for (int i = 0; i < 4; i++) cnt += (b[i] != 0u ? 256 : 0) + (b[i] != 0u && b[i] >= thr ? 1 : 0);
+    cnt = row_sum_i32(cnt);
+    const bool spiky = 2 * (cnt & 255) < ((cnt >> 8) & 255);
+    int X[4];
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float xp = mx > 0.0f ? ldexpf(f[i], 21 - e) : 0.0f;
+        const float Xf = rintf(xp);
+        X[i] = (int)Xf;
+        r[i] = xp - Xf;                           // exact residual, |r| <= 1/2
+    }
+    const XPack P0 = x_pack3(X);
+    int flags = (cnt >> 16) ? BGL_XF_NF : 0;
+    float ratio = 0.0f;
+    XPack P1;
+    P1.D[0] = P1.D[1] = P1.D[2] = 0; P1.s[0] = P1.s[1] = P1.s[2] = 0;
+    if (__builtin_amdgcn_ballot_w64(spiky)) {       // uniform branch: some row of the wave has an outlier
+        const uint32_t rb = x_row_umax(x_umax(x_umax(__float_as_uint(r[0]) & 0x7fffffffu, __float_as_uint(r[1]) & 0x7fffffffu),
+                                              x_umax(__float_as_uint(r[2]) & 0x7fffffffu, __float_as_uint(r[3]) & 0x7fffffffu)));
+        const float mr = __uint_as_float(rb);
+        if (spiky && mr > 0.0f) {
+            int e1 = 0;
+            frexpf(mr, &e1);
+            int X1[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) X1[i] = (int)rintf(ldexpf(r[i], 21 - e1));
+            ratio = ldexpf(1.0f, e1 - 21);
+            flags |= BGL_XF_L1;
+            P1 = x_pack3(X1);                     // row-uniform branch: the row's DPP sums stay in the row
+        }
+    }
+    if (g < G) {
+        int *rec = xl + g * XREC_DW;
+        x_store3(rec, q, P0, flags);
+        if (flags & BGL_XF_L1) x_store3(rec + l1, q, P1, 0);
+        if (q == 0) *reinterpret_cast<float2 *>(rec + XREC_SCALE) = make_float2(mx > 0.0f ? ldexpf(1.0f, e - 21) : 0.0f, ratio);
+    }
+}

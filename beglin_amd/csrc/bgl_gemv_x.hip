@@ -32,7 +32,7 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
     const int *xw = L.a.xw + (size_t)m * G * BGL_XD_DW;
     const int *xsum = L.a.xsum + (size_t)m * (K >> 5) * 4;
     const float *xsc = L.a.xs + (size_t)m * G;
-    const float *xr = L.x + (size_t)m * K;
+    const float *xr = (FUSE ? L.x : L.a.xf) + (size_t)m * K;
     const int NPX = (K + 255) >> 8;               // fused: passes of 256 values
 
     // ---- activation records (or the raw values they are made from): the first loads go out ahead
@@ -64,6 +64,7 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
     // ---- the first slots' weights: a wave's slots are wave, wave + nw, ...; D of them in flight
     const int r = lane % TR, kq = lane / TR, rr = r0 + r;
     const int S = (G + KQ - 1) / KQ;               // slots of KQ groups (records past G are zero)
+    const int L1 = S * KQ * XREC_DW;              // level-1 records follow the level-0 ones
     constexpr int D = x_depth<FMT, NB>();
     const int ns = (S - 1 - wave) / nw + 1;        // nw <= S: every wave has a slot
     XRaw<FMT, NB> c[D];
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
     if constexpr (FUSE) {
         for (int p = wave; p < NPX; p += nw) {
             if (p != wave) xv = x_pass_load(xr, p, lane, K);
-            x_pass_digits(xv, p, lane, G, xl);
+            x_pass_digits(xv, p, lane, G, xl, L1);
         }
     } else {
         if ((int)threadIdx.x < npc) *piece_dst(threadIdx.x) = pre0;
@@ -91,8 +92,21 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
         if ((int)threadIdx.x < G) xl[threadIdx.x * XREC_DW + XREC_SCALE] = __float_as_int(xs0);
         for (int i = threadIdx.x + X_PRE * nthr; i < npc; i += nthr) *piece_dst(i) = *piece_src(i);
         for (int g = threadIdx.x + nthr; g < G; g += nthr) xl[g * XREC_DW + XREC_SCALE] = __float_as_int(xsc[g]);
+        // level 1: the ratio of every group, the records of the flagged ones
+        const float *xsc1 = L.a.xs1 + (size_t)m * G;
+        const int *xw1 = L.a.xw1 + (size_t)m * G * BGL_XD_DW, *xsum1 = L.a.xsum1 + (size_t)m * (K >> 5) * 4;
+        for (int g = threadIdx.x; g < G; g += nthr) xl[g * XREC_DW + XREC_SCALE + 1] = __float_as_int(xsc1[g]);
+        for (int i = threadIdx.x; i < npc; i += nthr) {
+            const int g = i / 14, p = i - g * 14;
+            if (xsum[(size_t)g * 8 + 3] & BGL_XF_L1) {
+                const bgl_u32x4 v = p < 12 ? *reinterpret_cast<const bgl_u32x4 *>(xw1 + (size_t)g * BGL_XD_DW + 4 * p)
+                                           : *reinterpret_cast<const bgl_u32x4 *>(xsum1 + ((size_t)2 * g + (p - 12)) * 4);
+                *reinterpret_cast<bgl_u32x4 *>(xl + L1 + g * XREC_DW + (p < 12 ? 4 * p : XREC_DSUM + 4 * (p - 12))) = v;
+            }
+        }
     }
-    // records of the last slot's groups past K: zero digits, sums and scale (a zero term for any weight)
+    // records of the last slot's groups past K: zero digits, sums, flags and scales (a zero term for
+    // any weight)
     for (int i = G * XREC_DW + threadIdx.x; i < S * KQ * XREC_DW; i += nthr) xl[i] = 0;
     __syncthreads();
 
@@ -106,10 +120,27 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
             x_load<FMT, NB, KQ>(c[j], R, lane_of(sl + D * nw), sl + D * nw, i + D < ns);
         }
     }
+    // slots whose records carry a level-1 residual or non-finite values: their weights again (cold)
+    {
+        int fl = 0;
+        for (int i = 0; i < ns; i++) fl |= xk[(wave + i * nw) * (KQ * XREC_DW) + XREC_DSUM + 3];
+        if (__builtin_amdgcn_ballot_w64(fl != 0)) {
+            const XRow xrow{&T, tile * BGL_TILE + rr, xr};
+            for (int i = 0; i < ns; i++) {
+                const int sl = wave + i * nw;
+                const int *rec = xk + sl * (KQ * XREC_DW);
+                if (__builtin_amdgcn_ballot_w64(rec[XREC_DSUM + 3] != 0)) {
+                    XRaw<FMT, NB> rf;
+                    x_load<FMT, NB, KQ>(rf, R, lane_of(sl), sl, true);
+                    acc += x_fix<FMT, NB>(x_decode<FMT, NB>(rf), rec, L1, xrow, sl * KQ + kq);
+                }
+            }
+        }
+    }
     // rows' partials: over the KQ lanes of a row, then over the waves in order
 #pragma unroll
     for (int o = TR; o < BGL_TILE; o <<= 1) acc += __shfl_xor(acc, o);
-    float *red = reinterpret_cast<float *>(xl + S * KQ * XREC_DW);
+    float *red = reinterpret_cast<float *>(xl + 2 * L1);
     if (lane < TR) red[wave * TR + lane] = acc;
     __syncthreads();
     if (threadIdx.x < TR) {
@@ -122,10 +153,11 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
     }
 }
 
-// Records of every slot's groups (K/64 rounded up to the slot width 64/TR) and the row partials.
+// Level-0 and level-1 records of every slot's groups (K/64 rounded up to the slot width 64/TR) and
+// the row partials.
 size_t bgl_gemv_x_lds(int K, int TR, int nw) {
     const int KQ = 64 / TR, S = (K / 64 + KQ - 1) / KQ;
-    return (size_t)S * KQ * XREC_DW * 4 + (size_t)nw * TR * 4;
+    return (size_t)2 * S * KQ * XREC_DW * 4 + (size_t)nw * TR * 4;
 }
 
 template <int FMT, int NB, bool FUSE>

@@ -38,6 +38,7 @@ struct bgl_ctx {
     int moe_merge = -1;                   // BGL_MOE_MERGE: 0 never / 1 always run the routed and shared gate+up in one launch; -1 by shape
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
     int prep_act = -1, prep_gq = 0, prep_M = 0, prep_K = 0;   // what act_* currently hold
+    const float *prep_x = nullptr;        // the raw fp32 columns they were made from (non-finite slow path)
     DevBuf part;                          // K-split partial sums [ks][M][N]
     DevBuf hx, hy, hb;                    // staging for the host-pointer entry points
     DevBuf moe_a, moe_b, moe_c, moe_d, moe_e, moe_f, moe_g, moe_meta;   // MoE digits x2, fp32 h/down, bucket scratch
@@ -65,6 +66,7 @@ int dbuf_reserve(bgl_ctx *c, DevBuf &b, size_t bytes, bool zero);
 size_t ctx_scratch(bgl_ctx *c, bool release);
 int check_wt(int kind, int bits, int out, int in);
 int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, GemvAct &A);
+void f32_act_ptrs(const void *xw, const void *xs, const void *xsum, int M, int K, const float *x_dev, GemvAct &A);
 int pick_waves(bgl_ctx *c, int nunits);
 int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &A, int M,
              const float *const *bias, float *const *y, const int *ystride);

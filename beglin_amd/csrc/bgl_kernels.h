@@ -16,6 +16,116 @@ struct BglDevTensor {
     const uint32_t *s1;
 };
 
+// The biased code u = code + 2^(n-1) of qNg64 weight (r, c) in the tiled layout (fields widest first,
+// device nibble / crumb / bit orders: bgl_prep.hip k_repack_qng).
+__device__ __forceinline__ uint32_t qng_u_at(const BglDevTensor &T, int r, int c) {
+    const int tile = r / BGL_TILE, lane = r % BGL_TILE;
+    const QngFields f = qng_fields(T.bits);
+    const int pr = c / 128, e = c % 128, h = e / 64, p64 = e % 64;
+    const size_t base = (size_t)tile * T.cpr + (size_t)pr * T.bits;
+    auto chunkp = [&](int k) { return T.w + ((base + k) * BGL_TILE + lane) * 16; };
+    uint32_t u = 0;
+    int k = 0;
+    if (f.has8) { u |= (uint32_t)((chunkp(k + e / 16)[e % 16] ^ 0x80) & 255); k += 8; }
+    if (f.has4) {
+        const int ck = e / 32, el = e % 32, j = el / 8, q = el % 8;
+        const uint8_t *b = chunkp(k + ck) + 4 * j;
+        const uint32_t nib = q < 4 ? (b[q] & 15) : (b[q - 4] >> 4);
+        u |= nib << f.sh4; k += 4;
+    }
+    if (f.has2) {
+        const int j = p64 / 16, rem = p64 % 16, q = rem / 4, i = rem % 4;
+        const uint8_t *b = chunkp(k + h) + 4 * j;
+        u |= (uint32_t)((b[i] >> (2 * q)) & 3) << f.sh2; k += 2;
+    }
+    if (f.has1) {
+        const int j = e / 32, rem = e % 32, q = rem / 4, i = rem % 4;
+        const uint8_t *b = chunkp(k) + 4 * j;
+        u |= (uint32_t)((b[i] >> q) & 1) << f.sh1;
+    }
+    return u;
+}
+
+// The fp32 value of weight (r, c) of a bound tensor in the tiled layout: code * scale (nib * s + b for
+// the affine int4 kind), the product the reference decoders form (moe_decode_af, qwen_infer.c:2554-2655;
+// dequant_row_q4_0, gguf_quants.c:118-130; qng64_decode_code, qng64_dense.c:19-27).  One element per
+// call: used by k_dequant and by the GEMVs' slow path for non-finite activations.
+__device__ __forceinline__ float w_at(const BglDevTensor &T, int r, int c) {
+    int tile = r / BGL_TILE, lane = r % BGL_TILE;
+    float v = 0.0f;
+    if (T.fmt == BGL_F16 || T.fmt == BGL_F32) {
+        const int esz = T.fmt == BGL_F16 ? 2 : 4, per = 16 / esz;
+        const uint8_t *p = T.w + (((size_t)tile * T.cpr + c / per) * BGL_TILE + lane) * 16 + (c % per) * esz;
+        if (T.fmt == BGL_F16) v = __half2float(__ushort_as_half(*reinterpret_cast<const unsigned short *>(p)));
+        else v = *reinterpret_cast<const float *>(p);
+    } else if (T.fmt == BGL_Q4G64 || T.fmt == BGL_Q4G32H || T.fmt == BGL_Q4G256SF || T.fmt == BGL_Q4G64A) {
+        int chunk = c / 32, e = c % 32, j = e / 8, q = e % 8;
+        const uint8_t *p = T.w + (((size_t)tile * T.cpr + chunk) * BGL_TILE + lane) * 16 + 4 * j;
+        int nib = q < 4 ? (p[q] & 15) : (p[q - 4] >> 4);
+        if (T.fmt == BGL_Q4G256SF) nib ^= 8;                 // stored as signed nibbles
+        if (T.fmt == BGL_Q4G64A) {
+            // moe_decode_af's affine arm (qwen_infer.c:2649-2652): (float)nib * s + b
+            size_t o = ((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane;
+            v = __fadd_rn(__fmul_rn((float)nib, reinterpret_cast<const float *>(T.s0)[o]),
+                          reinterpret_cast<const float *>(T.s1)[o]);
+        } else if (T.fmt == BGL_Q4G64) {
+            float s = reinterpret_cast<const float *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
+            v = (float)(nib - 8) * s;
+        } else if (T.fmt == BGL_Q4G32H) {
+            uint32_t s2 = reinterpret_cast<const uint32_t *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
+            uint16_t h = (uint16_t)(((c / 32) & 1) ? (s2 >> 16) : (s2 & 0xffff));
+            v = (float)(nib - 8) * __half2float(__ushort_as_half(h));
+        } else {
+            size_t o = ((size_t)tile * T.nunits + c / 256) * BGL_TILE + lane;
+            const uint2 wsub = reinterpret_cast<const uint2 *>(T.s0)[o];
+            float ws = __uint_as_float(wsub.x);
+            uint32_t sub4 = wsub.y;
+            float sc = (float)((sub4 >> (8 * ((c / 64) & 3))) & 255);
+            v = (float)(nib - 8) * __fmul_rn(ws, __fdiv_rn(sc, 63.0f));
+        }
+    } else if (T.fmt == BGL_Q8G64) {
+        const int8_t *p = reinterpret_cast<const int8_t *>(T.w) + (((size_t)tile * T.cpr + c / 16) * BGL_TILE + lane) * 16;
+        float s = reinterpret_cast<const float *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
+        v = (float)p[c % 16] * s;
+    } else {
+        const int n = T.bits, pr = c / 128, h = (c % 128) / 64;
+        const uint32_t u = qng_u_at(T, r, c);
+        float2 s2 = reinterpret_cast<const float2 *>(T.s0)[((size_t)tile * T.nunits + pr) * BGL_TILE + lane];
+        float s = h ? s2.y : s2.x;
+        v = (float)((int)u - (1 << (n - 1))) * s;
+    }
+    return v;
+}
+
+// w_at for a format known at compile time (the GEMVs' cold paths): 32-bit offsets, no format switch.
+template <int FMT, int NB>
+__device__ __forceinline__ float w_at_t(const BglDevTensor &T, int r, int c) {
+    const uint32_t tile = (uint32_t)r / BGL_TILE, lane = (uint32_t)r % BGL_TILE;
+    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H || FMT == BGL_Q4G64A) {
+        const uint32_t e = (uint32_t)c % 32u, j = e / 8u, q = e % 8u;
+        const uint8_t b = T.w[((tile * (uint32_t)T.cpr + (uint32_t)c / 32u) * BGL_TILE + lane) * 16u + 4u * j + (q & 3u)];
+        const int nib = q < 4 ? (b & 15) : (b >> 4);
+        const uint32_t so = (tile * (uint32_t)T.nunits + (uint32_t)c / 64u) * BGL_TILE + lane;
+        if constexpr (FMT == BGL_Q4G64A)
+            return __fadd_rn(__fmul_rn((float)nib, reinterpret_cast<const float *>(T.s0)[so]), reinterpret_cast<const float *>(T.s1)[so]);
+        else if constexpr (FMT == BGL_Q4G64)
+            return (float)(nib - 8) * reinterpret_cast<const float *>(T.s0)[so];
+        else {
+            const uint32_t s2 = reinterpret_cast<const uint32_t *>(T.s0)[so];
+            return (float)(nib - 8) * __half2float(__ushort_as_half((unsigned short)((((uint32_t)c / 32u) & 1u) ? (s2 >> 16) : (s2 & 0xffffu))));
+        }
+    } else if constexpr (FMT == BGL_Q8G64) {
+        const int8_t v = reinterpret_cast<const int8_t *>(T.w)[((tile * (uint32_t)T.cpr + (uint32_t)c / 16u) * BGL_TILE + lane) * 16u + (uint32_t)c % 16u];
+        return (float)v * reinterpret_cast<const float *>(T.s0)[(tile * (uint32_t)T.nunits + (uint32_t)c / 64u) * BGL_TILE + lane];
+    } else if constexpr (FMT == BGL_QNG64) {
+        const uint32_t u = qng_u_at(T, r, c);
+        const float2 s2 = reinterpret_cast<const float2 *>(T.s0)[(tile * (uint32_t)T.nunits + (uint32_t)c / 128u) * BGL_TILE + lane];
+        return (float)((int)u - (1 << (NB - 1))) * (((c % 128) / 64) ? s2.y : s2.x);
+    } else {
+        return w_at(T, r, c);
+    }
+}
+
 #define BGL_MAX_TASKS 4
 
 // One GEMV "task" = one tensor of a (possibly fused) launch.  Blocks [blk0, blk0 + ntiles) of the
@@ -34,9 +144,14 @@ struct GemvTask {
 struct GemvAct {
     const int *xw;            // W4A8: xq dwords [M][K/4];       F32: digits [M][K/64][48]
     const float *xs;          // W4A8: ascale [M][K/gq];          F32: 2^(e-21) [M][K/64]
-    const int *xsum;          // W4A8: sum xq per 64 [M][K/64];   F32: digit sums [M][K/32][4]
+    const int *xsum;          // W4A8: sum xq per 64 [M][K/64];   F32: digit sums [M][K/32][4], the
+                              //   4th int of a group's first half = its flags (BGL_XF_*)
+    const int *xw1;           // F32 level 1 (groups flagged BGL_XF_L1): residual digits [M][K/64][48]
+    const float *xs1;         // F32 level 1: 2^(e1-21) relative to the level-0 scale, 0 without level 1 [M][K/64]
+    const int *xsum1;         // F32 level 1: digit sums [M][K/32][4]
     const int *colmap;        // optional: column m of this launch reads activation row colmap[m]
-    const float *xf;          // F32: the raw rows [M][K] (dense fp16 / fp32 weights read these)
+    const float *xf;          // F32: the raw rows [M][K] (dense fp16 / fp32 weights and the non-finite
+                              //   slow path read these)
     int gq;                   // W4A8 activation group (64 or 256)
 };
 

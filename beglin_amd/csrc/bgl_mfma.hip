@@ -310,6 +310,19 @@ constexpr int mf_step_lds(int CT) { return CT * 2048 + 512; }
 // 16 (every ring depth divides it).
 constexpr int mf_kps_max(int CT) { return (147456 / mf_step_lds(CT)) / 16 * 16; }
 
+// Sum of code * scale * x over the non-finite x[k], k in [k0, k1), for weight row n (the rare path
+// of a column that holds NaN or +-Inf).
+template <int FMT, int NB>
+__device__ __forceinline__ float mf_nonfinite(const BglDevTensor &T, int n, const float *x, int k0, int k1) {
+    float acc = 0.0f;
+#pragma unroll 1
+    for (int k = k0; k < k1; k++) {
+        const float v = x[k];
+        if (!isfinite(v)) acc += w_at_t<FMT, NB>(T, n, k) * v;
+    }
+    return acc;
+}
+
 template <int FMT, int NB, int CT, int KW>
 __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) {
     constexpr int NT = MF_WAVES * KW * 64;
@@ -400,21 +413,34 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
     // ---- activation fragments: each column is scaled by a power of two so its largest magnitude
     // over the split lies in [2^13, 2^14), then split into hi = fp16(x'), lo = fp16(x' - hi) in the
     // MFMA operand order; the split's column factor 2^(e-14) is applied to its partial sums ----
+    // Non-finite values (NaN, +-Inf) enter the fragments as 0 and flag the column; the store adds
+    // their products code * scale * x one element at a time (IEEE propagation, as the reference's
+    // fp32-product sums).
     __shared__ float cinv[16 * MF_MAXCT];
+    __shared__ int cnf[16 * MF_MAXCT];
 #pragma unroll
     for (int ci = 0; ci < CPW; ci++) {
         const int m = ci * NW + wave;
         if (m >= 16 * CT) break;                                   // uniform
-        float mx = 0.0f;
+        uint32_t mb = 0u, nf = 0u;
 #pragma unroll
         for (int j = 0; j < SPL; j++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const float4 v = xv[ci][j][h];
-                const float t = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-                mx = m < L.M && lane + 64 * j < 4 * ns ? fmaxf(mx, t) : mx;
+                float4 &v = xv[ci][j][h];
+                const bool in = m < L.M && lane + 64 * j < 4 * ns;
+                auto screen = [&](float &e) {
+                    const uint32_t ab = __float_as_uint(e) & 0x7fffffffu;
+                    const bool bad = ab >= 0x7f800000u;
+                    e = bad ? 0.0f : e;
+                    nf |= (bad && in) ? 1u : 0u;
+                    mb = (!bad && in && ab > mb) ? ab : mb;
+                };
+                screen(v.x); screen(v.y); screen(v.z); screen(v.w);
             }
-        mx = wave_max_f32(mx);
+        float mx = wave_max_f32(__uint_as_float(mb));
+        if (lane == 0) cnf[m] = 0;
+        if (__builtin_amdgcn_ballot_w64(nf != 0u) != 0 && lane == 0) cnf[m] = 1;
         int e = 0;
         if (mx > 0.0f) frexpf(mx, &e);                             // mx in [2^(e-1), 2^e)
         const float sc = mx > 0.0f ? ldexpf(1.0f, 14 - e) : 1.0f;
@@ -590,6 +616,7 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
                     const int n = n0 + v;
                     if (n < T.N) {
                         float o = acc[rb][c][v] * ci;
+                        if (cnf[m]) o += mf_nonfinite<FMT, NB>(T, n, L.x + (size_t)m * T.K, 32 * s0, min(32 * (s0 + ns), T.K));
                         if (S == 1 && tk.bias) o += tk.bias[n];
                         dst[n] = o;
                     }

@@ -126,6 +126,24 @@ __device__ __forceinline__ void moe_chunk(const MoeTask &Mt, const BglDevTensor 
             comp_dispatch<FMT, BGL_ACT_F32, NB, MB>(r, K, u, Mt.a, C, accb);
         }
     }
+    // groups whose activations carry a level-1 residual or non-finite values (cold path)
+    if constexpr (FMT != BGL_F16 && FMT != BGL_F32) {
+        const WRow Wa{&Ta, tile * BGL_TILE + lane}, Wb{&Tb, tile * BGL_TILE + lane};
+        for (int u = wave; u < U; u += nw) {
+            int fl = 0;
+#pragma unroll
+            for (int m = 0; m < MB; m++) fl |= unit_flags<FMT, NB>(Mt.a, C.am[m], K, u);
+            if (fl) {
+                Raw<FMT, NB> r;
+                load_raw<FMT, NB>(r, Ta, tile, lane, u);
+                comp_fix<FMT, NB, MB>(r, Wa, u, Mt.a, C, acc);
+                if (glu) {
+                    load_raw<FMT, NB>(r, Tb, tile, lane, u);
+                    comp_fix<FMT, NB, MB>(r, Wb, u, Mt.a, C, accb);
+                }
+            }
+        }
+    }
 #pragma unroll
     for (int m = 0; m < MB; m++) { red[wave][0][m][lane] = acc[m]; red[wave][1][m][lane] = accb[m]; }
     __syncthreads();
@@ -321,8 +339,8 @@ static int moe_prep(bgl_ctx *c, int slot, const float *x_dev, int M, int K, Gemv
     DevBuf &s = slot ? c->moe_e : c->moe_b;
     DevBuf &d = slot ? c->moe_f : c->moe_c;
     const int ng = K / 64;
-    if (dbuf_reserve(c, w, (size_t)M * ng * 192, false) || dbuf_reserve(c, s, (size_t)M * ng * 4, false) ||
-        dbuf_reserve(c, d, (size_t)M * (K / 32) * 16, false))
+    if (dbuf_reserve(c, w, (size_t)2 * M * ng * 192, false) || dbuf_reserve(c, s, (size_t)2 * M * ng * 4, false) ||
+        dbuf_reserve(c, d, (size_t)2 * M * (K / 32) * 16, false))
         return BGL_E_NOMEM;
     int tok = prof_begin(c, 0);
     hipLaunchKernelGGL(k_act_x24, dim3(nblk((long)M * ng * 64)), dim3(256), 0, c->stream, x_dev, M, K, (int8_t *)w.p,
@@ -330,7 +348,7 @@ static int moe_prep(bgl_ctx *c, int slot, const float *x_dev, int M, int K, Gemv
     prof_end(c, tok);
     HIPCHK(hipGetLastError());
     memset(&A, 0, sizeof A);
-    A.xw = (const int *)w.p; A.xs = (const float *)s.p; A.xsum = (const int *)d.p; A.xf = x_dev; A.gq = 64;
+    f32_act_ptrs(w.p, s.p, d.p, M, K, x_dev, A);
     return 0;
 }
 

@@ -18,10 +18,11 @@
 
 bool bgl_moe_x_fmt(int fmt) { return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64; }
 
-// LDS: MB columns of records (K/64 rounded up to whole slots of 64/TR groups) and the wave partials.
+// LDS: MB columns of level-0 records (K/64 rounded up to whole slots of 64/TR groups), the same for
+// level 1, and the wave partials.
 size_t bgl_moe_x_lds(int K, int nw, int TR) {
     const int KQ = BGL_TILE / TR, S = (K / 64 + KQ - 1) / KQ;
-    return (size_t)MX_MB * S * KQ * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * TR * 4;
+    return (size_t)2 * MX_MB * S * KQ * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * TR * 4;
 }
 
 // out[t][c] = (((0 + w_a d_a) + w_b d_b) + ...) over t's experts in ascending expert id (then k), then
@@ -52,6 +53,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
     const int nthr = blockDim.x, nw = nthr >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int K = Ta.K, G = K >> 6, S = (G + KQ - 1) / KQ, RC = S * KQ * XREC_DW, NPX = (K + 255) >> 8;
+    const int L1 = MX_MB * RC;                     // level-1 records follow the MB columns' level-0 ones
     const int r = lane % TR, kq = lane / TR;
 
     // ---- a wave's items: its slots wave, wave + nw, ... -- each once per tensor in SwiGLU mode
@@ -77,7 +79,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
         const int m = pi / NPX, p = pi - m * NPX;
         const int row = Mt.cols ? uni(Mt.cols)[base + m] : base + m;
         const float4 v = x_pass_load(Mt.a.xf + (size_t)row * K, p, lane, K);
-        x_pass_digits(v, p, lane, G, xl + m * RC);
+        x_pass_digits(v, p, lane, G, xl + m * RC, L1);
     }
     if (KQ > 1) {
         const int per = (S * KQ - G) * XREC_DW;
@@ -116,6 +118,37 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
             item_load(c[jj], j + MX_DEPTH);
         }
     }
+    // items whose records carry a level-1 residual or non-finite values in some column: their
+    // weights again (cold path)
+    {
+        int fl = 0;
+        for (int i = 0; i < ns; i++)
+            for (int m = 0; m < mc; m++) fl |= xk[(wave + i * nw) * (KQ * XREC_DW) + m * RC + XREC_DSUM + 3];
+        if (__builtin_amdgcn_ballot_w64(fl != 0)) {
+            for (int j = 0; j < NI; j++) {
+                const int sl = wave + (glu ? j >> 1 : j) * nw;
+                const bool up = glu && (j & 1);
+                const int *rec = xk + sl * (KQ * XREC_DW);
+                int f2 = 0;
+                for (int m = 0; m < mc; m++) f2 |= rec[m * RC + XREC_DSUM + 3];
+                if (!__builtin_amdgcn_ballot_w64(f2 != 0)) continue;
+                XRaw<FMT, NB> rf;
+                x_load<FMT, NB, KQ>(rf, up ? Rb : Ra, sl == S - 1 ? xlast : xlane, sl, true);
+                const XDec<FMT, NB> d = x_decode<FMT, NB>(rf);
+#pragma unroll 1
+                for (int m = 0; m < mc; m++) {
+                    const int xrow_m = Mt.cols ? uni(Mt.cols)[base + m] : base + m;
+                    const XRow xrow{up ? &Tb : &Ta, tile * BGL_TILE + r0 + r, Mt.a.xf + (size_t)xrow_m * K};
+                    const float v = x_fix<FMT, NB>(d, rec + m * RC, L1, xrow, sl * KQ + kq);
+#pragma unroll
+                    for (int q = 0; q < MB; q++) {
+                        if (q == m && !up) acc[q] += v;
+                        if (q == m && up) accb[q] += v;
+                    }
+                }
+            }
+        }
+    }
 
     // ---- row sums: over the KQ lanes of a row, then over the waves in order
 #pragma unroll
@@ -126,7 +159,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
             accb[m] += __shfl_xor(accb[m], o);
         }
     }
-    float *red = reinterpret_cast<float *>(xl + MX_MB * RC);      // [wave][2][MB][TR]
+    float *red = reinterpret_cast<float *>(xl + 2 * L1);          // [wave][2][MB][TR]
     if (lane < TR) {
 #pragma unroll
         for (int m = 0; m < MB; m++) {

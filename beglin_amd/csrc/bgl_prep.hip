@@ -42,9 +42,22 @@ __global__ __launch_bounds__(256) void k_act_w4a8(const float *__restrict__ x, i
 }
 
 // ------------------------------------------------------------------ fp32 activation digits
-// One wave per (column, 64-group), lane = element.  e = exponent of the group max (frexp), so
-// X = rint(x * 2^(21-e)) has |X| <= 2^21; X = d0 + 256*d1 + 65536*d2 with balanced int8 digits.
-// xd: [m][g][digit][64] bytes; xs: [m][g] = 2^(e-21); dsum: [m][K/32][4] per-half digit sums.
+// One wave per (column, 64-group), lane = element.  Level 0: e = exponent of the group's largest
+// finite |x| (frexp), X = rint(x * 2^(21-e)), |X| <= 2^21, as X = d0 + 256*d1 + 65536*d2 with
+// balanced int8 digits.  Level 1 (groups with an outlier: fewer than half the nonzero elements
+// within 2^BGL_X_SPIKE_BITS of the max): the exact residual r = x * 2^(21-e) - X in the same form
+// relative to its own maximum, X1 = rint(r * 2^(21-e1)).  Non-finite elements count as 0 and flag
+// the group.  Each buffer holds level 0 for all M columns, then level 1:
+//   xd   [m][g][digit][64] bytes, then the level-1 digits;
+//   xs   [m][g] = 2^(e-21), then [m][g] = 2^(e1-21) (0 without level 1);
+//   dsum [m][K/32][4] per-half digit sums (the 4th int: the group's BGL_XF_* flags), then level 1's.
+__device__ __forceinline__ int x_balanced3(int X, int &d0, int &d1) {
+    d0 = (int)(int8_t)(X & 255);
+    const int X1 = (X - d0) >> 8;
+    d1 = (int)(int8_t)(X1 & 255);
+    return (X1 - d1) >> 8;
+}
+
 __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, int M, int K,
                                                  int8_t *__restrict__ xd, float *__restrict__ xs,
                                                  int *__restrict__ dsum) {
@@ -53,22 +66,52 @@ __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, in
     if (wid >= M * ng) return;
     int m = wid / ng, g = wid % ng;
     float v = x[(size_t)m * K + (size_t)g * 64 + lane];
-    float mx = wave_max_f32(fabsf(v));
+    uint32_t ab = __float_as_uint(v) & 0x7fffffffu;
+    const bool nf = ab >= 0x7f800000u;                     // NaN or +-Inf: 0 in the digits
+    if (nf) { v = 0.0f; ab = 0u; }
+    float mx = wave_max_f32(__uint_as_float(ab));
     int e = 0;
     if (mx > 0.0f) frexpf(mx, &e);
-    int X = (mx > 0.0f) ? (int)rintf(ldexpf(v, 21 - e)) : 0;
-    int d0 = (int)(int8_t)(X & 255);
-    int X1 = (X - d0) >> 8;
-    int d1 = (int)(int8_t)(X1 & 255);
-    int d2 = (X1 - d1) >> 8;
+    const float thr = mx > 0.0f ? ldexpf(1.0f, e - BGL_X_SPIKE_BITS) : 0.0f;
+    const int cnt = wave_sum_i32((ab != 0u && __uint_as_float(ab) >= thr ? 1 : 0) + (ab != 0u ? 256 : 0) + (nf ? 65536 : 0));
+    const int nlarge = cnt & 255, nnz = (cnt >> 8) & 255, nnf = cnt >> 16;
+    const float xp = mx > 0.0f ? ldexpf(v, 21 - e) : 0.0f;  // power-of-two scaling: exact
+    const float Xf = rintf(xp);
+    int d0, d1;
+    int d2 = x_balanced3((int)Xf, d0, d1);
     int8_t *dst = xd + ((size_t)m * ng + g) * 192;
     dst[lane] = (int8_t)d0; dst[64 + lane] = (int8_t)d1; dst[128 + lane] = (int8_t)d2;
-    if (lane == 0) xs[(size_t)m * ng + g] = (mx > 0.0f) ? ldexpf(1.0f, e - 21) : 0.0f;
+    int flags = nnf ? BGL_XF_NF : 0;
+    float ratio = 0.0f;
+    if (2 * nlarge < nnz) {                                // wave-uniform: one group per wave
+        const float r = xp - Xf;                           // exact: xp and rint(xp) differ by <= 1/2
+        const float mr = wave_max_f32(fabsf(r));
+        if (mr > 0.0f) {
+            int e1 = 0;
+            frexpf(mr, &e1);
+            int c0, c1;
+            const int c2 = x_balanced3((int)rintf(ldexpf(r, 21 - e1)), c0, c1);
+            int8_t *d1p = xd + ((size_t)M * ng + (size_t)m * ng + g) * 192;
+            d1p[lane] = (int8_t)c0; d1p[64 + lane] = (int8_t)c1; d1p[128 + lane] = (int8_t)c2;
+            const int2 t0 = half_sums_i32(c0), t1 = half_sums_i32(c1), t2 = half_sums_i32(c2);
+            if ((lane & 31) == 0) {
+                const int h = lane >> 5;
+                int *ds = dsum + ((size_t)M * (K >> 5) + (size_t)m * (K >> 5) + (size_t)g * 2 + h) * 4;
+                ds[0] = h ? t0.y : t0.x; ds[1] = h ? t1.y : t1.x; ds[2] = h ? t2.y : t2.x; ds[3] = 0;
+            }
+            ratio = ldexpf(1.0f, e1 - 21);
+            flags |= BGL_XF_L1;
+        }
+    }
+    if (lane == 0) {
+        xs[(size_t)m * ng + g] = (mx > 0.0f) ? ldexpf(1.0f, e - 21) : 0.0f;
+        xs[(size_t)M * ng + (size_t)m * ng + g] = ratio;
+    }
     int2 s0 = half_sums_i32(d0), s1 = half_sums_i32(d1), s2 = half_sums_i32(d2);
     if ((lane & 31) == 0) {
         const int h = lane >> 5;
         int *ds = dsum + ((size_t)m * (K >> 5) + (size_t)g * 2 + h) * 4;
-        ds[0] = h ? s0.y : s0.x; ds[1] = h ? s1.y : s1.x; ds[2] = h ? s2.y : s2.x; ds[3] = 0;
+        ds[0] = h ? s0.y : s0.x; ds[1] = h ? s1.y : s1.x; ds[2] = h ? s2.y : s2.x; ds[3] = flags;
     }
 }
 
@@ -444,71 +487,5 @@ __global__ void k_repack_qng_scales(const float *__restrict__ src, int N, int ng
 __global__ void k_dequant(BglDevTensor T, int row0, int nrows, float *__restrict__ out) {
     long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (long)nrows * T.K) return;
-    int r = row0 + (int)(t / T.K), c = (int)(t % T.K);
-    int tile = r / BGL_TILE, lane = r % BGL_TILE;
-    float v = 0.0f;
-    if (T.fmt == BGL_F16 || T.fmt == BGL_F32) {
-        const int esz = T.fmt == BGL_F16 ? 2 : 4, per = 16 / esz;
-        const uint8_t *p = T.w + (((size_t)tile * T.cpr + c / per) * BGL_TILE + lane) * 16 + (c % per) * esz;
-        if (T.fmt == BGL_F16) v = __half2float(__ushort_as_half(*reinterpret_cast<const unsigned short *>(p)));
-        else v = *reinterpret_cast<const float *>(p);
-    } else if (T.fmt == BGL_Q4G64 || T.fmt == BGL_Q4G32H || T.fmt == BGL_Q4G256SF || T.fmt == BGL_Q4G64A) {
-        int chunk = c / 32, e = c % 32, j = e / 8, q = e % 8;
-        const uint8_t *p = T.w + (((size_t)tile * T.cpr + chunk) * BGL_TILE + lane) * 16 + 4 * j;
-        int nib = q < 4 ? (p[q] & 15) : (p[q - 4] >> 4);
-        if (T.fmt == BGL_Q4G256SF) nib ^= 8;                 // stored as signed nibbles
-        if (T.fmt == BGL_Q4G64A) {
-            // moe_decode_af's affine arm (qwen_infer.c:2649-2652): (float)nib * s + b
-            size_t o = ((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane;
-            v = __fadd_rn(__fmul_rn((float)nib, reinterpret_cast<const float *>(T.s0)[o]),
-                          reinterpret_cast<const float *>(T.s1)[o]);
-        } else if (T.fmt == BGL_Q4G64) {
-            float s = reinterpret_cast<const float *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
-            v = (float)(nib - 8) * s;
-        } else if (T.fmt == BGL_Q4G32H) {
-            uint32_t s2 = reinterpret_cast<const uint32_t *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
-            uint16_t h = (uint16_t)(((c / 32) & 1) ? (s2 >> 16) : (s2 & 0xffff));
-            v = (float)(nib - 8) * __half2float(__ushort_as_half(h));
-        } else {
-            size_t o = ((size_t)tile * T.nunits + c / 256) * BGL_TILE + lane;
-            const uint2 wsub = reinterpret_cast<const uint2 *>(T.s0)[o];
-            float ws = __uint_as_float(wsub.x);
-            uint32_t sub4 = wsub.y;
-            float sc = (float)((sub4 >> (8 * ((c / 64) & 3))) & 255);
-            v = (float)(nib - 8) * __fmul_rn(ws, __fdiv_rn(sc, 63.0f));
-        }
-    } else if (T.fmt == BGL_Q8G64) {
-        const int8_t *p = reinterpret_cast<const int8_t *>(T.w) + (((size_t)tile * T.cpr + c / 16) * BGL_TILE + lane) * 16;
-        float s = reinterpret_cast<const float *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
-        v = (float)p[c % 16] * s;
-    } else {
-        int n = T.bits;
-        QngFields f = qng_fields(n);
-        int pr = c / 128, e = c % 128, h = e / 64, p64 = e % 64;
-        size_t base = (size_t)tile * T.cpr + (size_t)pr * n;
-        auto chunkp = [&](int k) { return T.w + ((base + k) * BGL_TILE + lane) * 16; };
-        uint32_t u = 0;
-        int k = 0;
-        if (f.has8) { u |= (uint32_t)((chunkp(k + e / 16)[e % 16] ^ 0x80) & 255); k += 8; }
-        if (f.has4) {
-            int ck = e / 32, el = e % 32, j = el / 8, q = el % 8;
-            const uint8_t *b = chunkp(k + ck) + 4 * j;
-            uint32_t nib = q < 4 ? (b[q] & 15) : (b[q - 4] >> 4);
-            u |= nib << f.sh4; k += 4;
-        }
-        if (f.has2) {
-            int j = p64 / 16, rem = p64 % 16, q = rem / 4, i = rem % 4;
-            const uint8_t *b = chunkp(k + h) + 4 * j;
-            u |= (uint32_t)((b[i] >> (2 * q)) & 3) << f.sh2; k += 2;
-        }
-        if (f.has1) {
-            int j = e / 32, rem = e % 32, q = rem / 4, i = rem % 4;
-            const uint8_t *b = chunkp(k) + 4 * j;
-            u |= (uint32_t)((b[i] >> q) & 1) << f.sh1;
-        }
-        float2 s2 = reinterpret_cast<const float2 *>(T.s0)[((size_t)tile * T.nunits + pr) * BGL_TILE + lane];
-        float s = h ? s2.y : s2.x;
-        v = (float)((int)u - (1 << (n - 1))) * s;
-    }
-    out[t] = v;
+    out[t] = w_at(T, row0 + (int)(t / T.K), (int)(t % T.K));
 }
