@@ -611,7 +611,7 @@ static int run_gemv_x(bgl_ctx *c, int n, const BglDevTensor *Ts, const GemvAct *
     const int KQ = BGL_TILE / TR, G = Ts[0].K / 64, S = (G + KQ - 1) / KQ;
     int nw = std::min({S, c->max_waves, fused ? 12 : 16});
     if (c->x_waves) nw = std::min(S, c->x_waves);
-    if (bgl_gemv_x_lds(Ts[0].K, TR, nw) > BGL_GEMV_X_LDS_MAX) return 1;
+    if (bgl_gemv_x_lds(Ts[0].K, TR, nw, fused) > BGL_GEMV_X_LDS_MAX) return 1;
     for (int i = 0; i < n; i++)            // the kernel addresses each tensor through 32-bit buffer offsets
         if ((size_t)Ts[i].ntiles * Ts[i].cpr * 1024 >= (1ull << 31) || (size_t)Ts[i].ntiles * Ts[i].nunits * 512 >= (1ull << 31))
             return 1;

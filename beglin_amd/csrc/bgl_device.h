@@ -69,6 +69,15 @@ __device__ __forceinline__ float wave_max_f32(float v) {
     v = fmaxf(v, dpp_f<0x140>(v));
     return fmaxf(fmaxf(rlane_f(v, 0), rlane_f(v, 16)), fmaxf(rlane_f(v, 32), rlane_f(v, 48)));
 }
+// unsigned max over the wave (NaN bit patterns compare as large integers, unlike fmaxf)
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x141>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x140>((int)v));
+    return max(max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
+               max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
+}
 // returns the per-row (16-lane) sums in every lane of that row
 __device__ __forceinline__ int row_sum_i32(int v) {
     v += dpp_i<0xB1>(v);

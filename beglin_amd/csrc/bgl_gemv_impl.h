@@ -419,7 +419,7 @@ __device__ __forceinline__ void comp_fix(const Raw<FMT, NB> &r, const WRow &W, i
         const uint32_t raw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w};
 #pragma unroll
         for (int q = 0; q < 8; q++) { lo[q] = nib_lo(raw[q]); hi[q] = nib_hi(raw[q]); }
-#pragma unroll 1
+#pragma unroll
         for (int m = 0; m < MB; m++) {
             const int am = C.am[m];
             const size_t gi = (size_t)am * ng + u;
@@ -463,7 +463,7 @@ __device__ __forceinline__ void comp_fix(const Raw<FMT, NB> &r, const WRow &W, i
         for (int k = 0; k < 4; k++) {
             w[4 * k] = (int)r.c[k].x; w[4 * k + 1] = (int)r.c[k].y; w[4 * k + 2] = (int)r.c[k].z; w[4 * k + 3] = (int)r.c[k].w;
         }
-#pragma unroll 1
+#pragma unroll
         for (int m = 0; m < MB; m++) {
             const int am = C.am[m];
             const size_t gi = (size_t)am * ng + u;
@@ -489,7 +489,7 @@ __device__ __forceinline__ void comp_fix(const Raw<FMT, NB> &r, const WRow &W, i
             const int g = 2 * u + h;
             if (g >= ng) break;
             const float s = h ? r.s.y : r.s.x;
-#pragma unroll 1
+#pragma unroll
             for (int m = 0; m < MB; m++) {
                 const int am = C.am[m];
                 const size_t gi = (size_t)am * ng + g;

@@ -359,20 +359,19 @@ __device__ __forceinline__ float x_dot(const XDec<FMT, NB> &w, const int *rec) {
 
 // The terms the level-0 digits leave out, for a lane's group flagged BGL_XF_L1 or BGL_XF_NF (0 for
 // the lanes of the wave whose groups are not): the level-1 residual
-// s * ((V1 * 2^(e1-21)) * 2^(e-21)) and the non-finite products.  Cold path: the GEMVs run it after
+// s * ((V1 * 2^(e1-21)) * 2^(e-21)) against the level-1 digits at r1 (48 dwords, LDS or global)
+// with their half sums e0 / e1, and the non-finite products.  Cold path: the GEMVs run it after
 // their main loop for the slots whose records carry flags, with the weights loaded again.
 template <int FMT, int NB>
-__device__ __forceinline__ float x_fix(const XDec<FMT, NB> &w, const int *rec, int l1, const XRow &xrow, int g) {
+__device__ __forceinline__ float x_fix(const XDec<FMT, NB> &w, const int *rec, const int *r1, int4 e0, int4 e1,
+                                       const XRow &xrow, int g) {
     const int fl = rec[XREC_DSUM + 3];
     const float2 xs = *reinterpret_cast<const float2 *>(rec + XREC_SCALE);
     float t = 0.0f;
     if (__builtin_amdgcn_ballot_w64(fl & BGL_XF_L1)) {
-        const int *r1 = rec + l1;
-        const int4 e0 = *reinterpret_cast<const int4 *>(r1 + XREC_DSUM);
-        const int4 e1 = *reinterpret_cast<const int4 *>(r1 + XREC_DSUM + 4);
         int p[6];
         x_ints<FMT, NB>(w, r1, e0, e1, p);
-        const float rt = (fl & BGL_XF_L1) ? xs.y : 0.0f;      // a stale record of an unflagged lane adds 0
+        const float rt = (fl & BGL_XF_L1) ? xs.y : 0.0f;      // other lanes' level-1 data is not theirs: 0
         if constexpr (FMT == BGL_Q4G32H)
             t = w.sa * ((fold_digits(p[0], p[1], p[2]) * rt) * xs.x) + w.sb * ((fold_digits(p[3], p[4], p[5]) * rt) * xs.x);
         else
@@ -444,59 +443,90 @@ __device__ __forceinline__ void x_store3(int *rec, int q, const XPack &p, int fl
     }
 }
 
-__device__ __forceinline__ void x_pass_digits(const float4 &v, int p, int lane, int G, int *xl, int l1) {
-    const int g = 4 * p + (lane >> 4), q = lane & 15;
+// A 16-lane row's 64-group (4 values per lane): non-finite values zeroed (rare: only when the
+// row's largest |x| bits are Inf/NaN), e = exponent of the largest finite |x| (frexp), whether the
+// group has an outlier, and the level-0 integers X = rint(x * 2^(21-e)) with their exact residuals.
+struct XStat {
+    float mx;                  // the group's largest finite |x|
+    int e, nnf;                // exponent of mx; non-finite values in the row
+    bool spiky;                // fewer than half the nonzero |x| are >= 2^(e - BGL_X_SPIKE_BITS)
+    int X[4];
+    float r[4];                // x * 2^(21-e) - X, exact, |r| <= 1/2
+};
+__device__ __forceinline__ XStat x_stat(const float4 &v) {
+    XStat st;
     float f[4] = {v.x, v.y, v.z, v.w};
     uint32_t b[4];
-    int nnf = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        b[i] = __float_as_uint(f[i]) & 0x7fffffffu;
-        if (b[i] >= 0x7f800000u) { f[i] = 0.0f; b[i] = 0u; nnf++; }     // NaN / +-Inf: 0 in the digits
+    for (int i = 0; i < 4; i++) b[i] = __float_as_uint(f[i]) & 0x7fffffffu;
+    uint32_t mb = x_row_umax(x_umax(x_umax(b[0], b[1]), x_umax(b[2], b[3])));   // the group's max |x| bits
+    st.nnf = 0;
+    if (__builtin_amdgcn_ballot_w64(mb >= 0x7f800000u)) {   // NaN / +-Inf somewhere in the wave: 0 in the digits
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (b[i] >= 0x7f800000u) { f[i] = 0.0f; b[i] = 0u; st.nnf++; }
+        mb = x_row_umax(x_umax(x_umax(b[0], b[1]), x_umax(b[2], b[3])));
+        st.nnf = row_sum_i32(st.nnf);
     }
-    const uint32_t mb = x_row_umax(x_umax(x_umax(b[0], b[1]), x_umax(b[2], b[3])));   // the group's max |x| bits
-    const float mx = __uint_as_float(mb);
-    int e = 0;
-    if (mx > 0.0f) frexpf(mx, &e);
-    const uint32_t thr = mx > 0.0f ? __float_as_uint(ldexpf(1.0f, e - BGL_X_SPIKE_BITS)) : 0u;
-    int cnt = 65536 * nnf;
+    st.mx = __uint_as_float(mb);
+    st.e = 0;
+    if (st.mx > 0.0f) frexpf(st.mx, &st.e);
+    const uint32_t thr = st.mx > 0.0f ? __float_as_uint(ldexpf(1.0f, st.e - BGL_X_SPIKE_BITS)) : 0u;
+    int cnt = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) cnt += (b[i] != 0u ? 256 : 0) + (b[i] != 0u && b[i] >= thr ? 1 : 0);
+    for (int i = 0; i < 4; i++) cnt += (b[i] != 0u ? 256 : 0) + (b[i] >= thr ? 1 : 0);
     cnt = row_sum_i32(cnt);
-    const bool spiky = 2 * (cnt & 255) < ((cnt >> 8) & 255);
-    int X[4];
-    float r[4];
+    st.spiky = 2 * (cnt & 255) < (cnt >> 8);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float xp = mx > 0.0f ? ldexpf(f[i], 21 - e) : 0.0f;
+        const float xp = st.mx > 0.0f ? ldexpf(f[i], 21 - st.e) : 0.0f;   // power-of-two scaling: exact
         const float Xf = rintf(xp);
-        X[i] = (int)Xf;
-        r[i] = xp - Xf;                           // exact residual, |r| <= 1/2
+        st.X[i] = (int)Xf;
+        st.r[i] = xp - Xf;
     }
-    const XPack P0 = x_pack3(X);
-    int flags = (cnt >> 16) ? BGL_XF_NF : 0;
+    return st;
+}
+// exponent e1 of the row's largest |residual| (0 when all are 0), in every lane of the row
+__device__ __forceinline__ int x_resid_exp(const XStat &st, float &mr) {
+    const uint32_t rb = x_row_umax(x_umax(x_umax(__float_as_uint(st.r[0]) & 0x7fffffffu, __float_as_uint(st.r[1]) & 0x7fffffffu),
+                                          x_umax(__float_as_uint(st.r[2]) & 0x7fffffffu, __float_as_uint(st.r[3]) & 0x7fffffffu)));
+    mr = __uint_as_float(rb);
+    int e1 = 0;
+    if (mr > 0.0f) frexpf(mr, &e1);
+    return e1;
+}
+
+// Pass p's level-0 records: digits, sums, flags, the scale 2^(e-21) and the level-1 ratio
+// 2^(e1-21) (0 unless the group has an outlier).  The level-1 digits themselves are made only where
+// a GEMV needs them (x_pass_l1, cold path).
+__device__ __forceinline__ void x_pass_digits(const float4 &v, int p, int lane, int G, int *xl) {
+    const int g = 4 * p + (lane >> 4), q = lane & 15;
+    const XStat st = x_stat(v);
+    const XPack P0 = x_pack3(st.X);
+    int flags = st.nnf ? BGL_XF_NF : 0;
     float ratio = 0.0f;
-    XPack P1;
-    P1.D[0] = P1.D[1] = P1.D[2] = 0; P1.s[0] = P1.s[1] = P1.s[2] = 0;
-    if (__builtin_amdgcn_ballot_w64(spiky)) {       // uniform branch: some row of the wave has an outlier
-        const uint32_t rb = x_row_umax(x_umax(x_umax(__float_as_uint(r[0]) & 0x7fffffffu, __float_as_uint(r[1]) & 0x7fffffffu),
-                                              x_umax(__float_as_uint(r[2]) & 0x7fffffffu, __float_as_uint(r[3]) & 0x7fffffffu)));
-        const float mr = __uint_as_float(rb);
-        if (spiky && mr > 0.0f) {
-            int e1 = 0;
-            frexpf(mr, &e1);
-            int X1[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) X1[i] = (int)rintf(ldexpf(r[i], 21 - e1));
-            ratio = ldexpf(1.0f, e1 - 21);
-            flags |= BGL_XF_L1;
-            P1 = x_pack3(X1);                     // row-uniform branch: the row's DPP sums stay in the row
-        }
+    if (__builtin_amdgcn_ballot_w64(st.spiky)) {    // uniform branch: some row of the wave has an outlier
+        float mr;
+        const int e1 = x_resid_exp(st, mr);
+        if (st.spiky && mr > 0.0f) { ratio = ldexpf(1.0f, e1 - 21); flags |= BGL_XF_L1; }
     }
     if (g < G) {
         int *rec = xl + g * XREC_DW;
         x_store3(rec, q, P0, flags);
-        if (flags & BGL_XF_L1) x_store3(rec + l1, q, P1, 0);
-        if (q == 0) *reinterpret_cast<float2 *>(rec + XREC_SCALE) = make_float2(mx > 0.0f ? ldexpf(1.0f, e - 21) : 0.0f, ratio);
+        if (q == 0) *reinterpret_cast<float2 *>(rec + XREC_SCALE) = make_float2(st.mx > 0.0f ? ldexpf(1.0f, st.e - 21) : 0.0f, ratio);
     }
+}
+
+// The level-1 records (the residual's digits and sums) of pass p's groups in [g0, g1), written to
+// dst + (g - g0) * XREC_DW: the same arithmetic as x_pass_digits, so they match its ratios.
+__device__ __forceinline__ void x_pass_l1(const float4 &v, int p, int lane, int g0, int g1, int *dst) {
+    const int g = 4 * p + (lane >> 4), q = lane & 15;
+    const XStat st = x_stat(v);
+    float mr;
+    const int e1 = x_resid_exp(st, mr);
+    int X1[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) X1[i] = mr > 0.0f ? (int)rintf(ldexpf(st.r[i], 21 - e1)) : 0;
+    const XPack P1 = x_pack3(X1);
+    if (g >= g0 && g < g1) x_store3(dst + (g - g0) * XREC_DW, q, P1, 0);
 }

@@ -13,6 +13,9 @@
 // same record (a broadcast).
 #include "bgl_gemv_x.h"
 
+// dwords of the row-partial area: nw waves x TR rows, rounded to 4 (16-byte alignment after it)
+__host__ __device__ constexpr int x_red_dw(int TR, int nw) { return (nw * TR + 3) & ~3; }
+
 template <int FMT, int NB, int TR, bool FUSE>
 __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
     extern __shared__ __align__(16) int xl[];
@@ -64,7 +67,6 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
     // ---- the first slots' weights: a wave's slots are wave, wave + nw, ...; D of them in flight
     const int r = lane % TR, kq = lane / TR, rr = r0 + r;
     const int S = (G + KQ - 1) / KQ;               // slots of KQ groups (records past G are zero)
-    const int L1 = S * KQ * XREC_DW;              // level-1 records follow the level-0 ones
     constexpr int D = x_depth<FMT, NB>();
     const int ns = (S - 1 - wave) / nw + 1;        // nw <= S: every wave has a slot
     XRaw<FMT, NB> c[D];
@@ -82,7 +84,7 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
     if constexpr (FUSE) {
         for (int p = wave; p < NPX; p += nw) {
             if (p != wave) xv = x_pass_load(xr, p, lane, K);
-            x_pass_digits(xv, p, lane, G, xl, L1);
+            x_pass_digits(xv, p, lane, G, xl);
         }
     } else {
         if ((int)threadIdx.x < npc) *piece_dst(threadIdx.x) = pre0;
@@ -92,18 +94,9 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
         if ((int)threadIdx.x < G) xl[threadIdx.x * XREC_DW + XREC_SCALE] = __float_as_int(xs0);
         for (int i = threadIdx.x + X_PRE * nthr; i < npc; i += nthr) *piece_dst(i) = *piece_src(i);
         for (int g = threadIdx.x + nthr; g < G; g += nthr) xl[g * XREC_DW + XREC_SCALE] = __float_as_int(xsc[g]);
-        // level 1: the ratio of every group, the records of the flagged ones
+        // the level-1 ratio of every group (its digits stay in global memory: only the cold path reads them)
         const float *xsc1 = L.a.xs1 + (size_t)m * G;
-        const int *xw1 = L.a.xw1 + (size_t)m * G * BGL_XD_DW, *xsum1 = L.a.xsum1 + (size_t)m * (K >> 5) * 4;
         for (int g = threadIdx.x; g < G; g += nthr) xl[g * XREC_DW + XREC_SCALE + 1] = __float_as_int(xsc1[g]);
-        for (int i = threadIdx.x; i < npc; i += nthr) {
-            const int g = i / 14, p = i - g * 14;
-            if (xsum[(size_t)g * 8 + 3] & BGL_XF_L1) {
-                const bgl_u32x4 v = p < 12 ? *reinterpret_cast<const bgl_u32x4 *>(xw1 + (size_t)g * BGL_XD_DW + 4 * p)
-                                           : *reinterpret_cast<const bgl_u32x4 *>(xsum1 + ((size_t)2 * g + (p - 12)) * 4);
-                *reinterpret_cast<bgl_u32x4 *>(xl + L1 + g * XREC_DW + (p < 12 ? 4 * p : XREC_DSUM + 4 * (p - 12))) = v;
-            }
-        }
     }
     // records of the last slot's groups past K: zero digits, sums, flags and scales (a zero term for
     // any weight)
@@ -126,21 +119,43 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
         for (int i = 0; i < ns; i++) fl |= xk[(wave + i * nw) * (KQ * XREC_DW) + XREC_DSUM + 3];
         if (__builtin_amdgcn_ballot_w64(fl != 0)) {
             const XRow xrow{&T, tile * BGL_TILE + rr, xr};
+            int *scr = xl + S * KQ * XREC_DW + x_red_dw(TR, nw) + wave * KQ * XREC_DW;   // this wave's level-1 records
             for (int i = 0; i < ns; i++) {
-                const int sl = wave + i * nw;
+                const int sl = wave + i * nw, gl = min(sl * KQ + kq, G - 1);
                 const int *rec = xk + sl * (KQ * XREC_DW);
-                if (__builtin_amdgcn_ballot_w64(rec[XREC_DSUM + 3] != 0)) {
-                    XRaw<FMT, NB> rf;
-                    x_load<FMT, NB, KQ>(rf, R, lane_of(sl), sl, true);
-                    acc += x_fix<FMT, NB>(x_decode<FMT, NB>(rf), rec, L1, xrow, sl * KQ + kq);
+                const int f2 = rec[XREC_DSUM + 3];
+                if (!__builtin_amdgcn_ballot_w64(f2 != 0)) continue;
+                const int *r1;
+                int4 e0, e1;
+                if constexpr (FUSE) {
+                    // the slot's level-1 records, made from the raw column into this wave's scratch
+                    if (__builtin_amdgcn_ballot_w64(f2 & BGL_XF_L1)) {
+                        const int g0 = sl * KQ, g1 = min(g0 + KQ, G);
+                        for (int p = g0 >> 2; p <= (g1 - 1) >> 2; p++) x_pass_l1(x_pass_load(xr, p, lane, K), p, lane, g0, g1, scr);
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    }
+                    r1 = scr + kq * XREC_DW;
+                    e0 = *reinterpret_cast<const int4 *>(r1 + XREC_DSUM);
+                    e1 = *reinterpret_cast<const int4 *>(r1 + XREC_DSUM + 4);
+                } else {
+                    // the prep kernel's level-1 digits, read from global memory
+                    r1 = L.a.xw1 + ((size_t)m * G + gl) * BGL_XD_DW;
+                    const int *d1 = L.a.xsum1 + ((size_t)m * (K >> 5) + 2 * gl) * 4;
+                    e0 = *reinterpret_cast<const int4 *>(d1);
+                    e1 = *reinterpret_cast<const int4 *>(d1 + 4);
                 }
+                XRaw<FMT, NB> rf;
+                x_load<FMT, NB, KQ>(rf, R, lane_of(sl), sl, true);
+                acc += x_fix<FMT, NB>(x_decode<FMT, NB>(rf), rec, r1, e0, e1, xrow, gl);
             }
         }
     }
     // rows' partials: over the KQ lanes of a row, then over the waves in order
 #pragma unroll
     for (int o = TR; o < BGL_TILE; o <<= 1) acc += __shfl_xor(acc, o);
-    float *red = reinterpret_cast<float *>(xl + 2 * L1);
+    float *red = reinterpret_cast<float *>(xl + S * KQ * XREC_DW);
     if (lane < TR) red[wave * TR + lane] = acc;
     __syncthreads();
     if (threadIdx.x < TR) {
@@ -153,17 +168,17 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_x(GemvLaunch L) {
     }
 }
 
-// Level-0 and level-1 records of every slot's groups (K/64 rounded up to the slot width 64/TR) and
-// the row partials.
-size_t bgl_gemv_x_lds(int K, int TR, int nw) {
+// Records of every slot's groups (K/64 rounded up to the slot width 64/TR), the row partials, and
+// with in-kernel digits one slot of level-1 records per wave (cold path).
+size_t bgl_gemv_x_lds(int K, int TR, int nw, bool fuse) {
     const int KQ = 64 / TR, S = (K / 64 + KQ - 1) / KQ;
-    return (size_t)2 * S * KQ * XREC_DW * 4 + (size_t)nw * TR * 4;
+    return ((size_t)S * KQ * XREC_DW + x_red_dw(TR, nw) + (fuse ? (size_t)nw * KQ * XREC_DW : 0)) * 4;
 }
 
 template <int FMT, int NB, bool FUSE>
 static int launch_x_tr(int TR, const GemvLaunch &L, int nblocks, int nw, hipStream_t st) {
     dim3 g(nblocks), b(nw * BGL_TILE);
-    const size_t lds = bgl_gemv_x_lds(L.t[0].T.K, TR, nw);
+    const size_t lds = bgl_gemv_x_lds(L.t[0].T.K, TR, nw, FUSE);
     switch (TR) {
     case 8: hipLaunchKernelGGL((k_gemv_x<FMT, NB, 8, FUSE>), g, b, lds, st, L); return 0;
     case 16: hipLaunchKernelGGL((k_gemv_x<FMT, NB, 16, FUSE>), g, b, lds, st, L); return 0;

@@ -218,7 +218,7 @@ int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, int MB, h
 size_t bgl_gemv_q_lds(int fmt, int K, int TR, int MB);
 // ---- bgl_gemv_x.hip: one-column fp32-activation GEMV over prepared digits ----
 int bgl_launch_gemv_x(const GemvLaunch &L, bool fuse, int nblocks, int TR, int nw, hipStream_t st);
-size_t bgl_gemv_x_lds(int K, int TR, int nw);
+size_t bgl_gemv_x_lds(int K, int TR, int nw, bool fuse);
 // ---- bgl_moe_x.hip: the MoE gather over records made in the kernel ----
 bool bgl_moe_x_fmt(int fmt);
 size_t bgl_moe_x_lds(int K, int nw, int TR);

@@ -422,25 +422,40 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
     for (int ci = 0; ci < CPW; ci++) {
         const int m = ci * NW + wave;
         if (m >= 16 * CT) break;                                   // uniform
-        uint32_t mb = 0u, nf = 0u;
+        // the column's largest |x| bits over the split; Inf / NaN bits exceed every finite value's, so
+        // only then (rare) are they zeroed and the maximum taken again
+        uint32_t mb = 0u;
 #pragma unroll
         for (int j = 0; j < SPL; j++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                float4 &v = xv[ci][j][h];
-                const bool in = m < L.M && lane + 64 * j < 4 * ns;
-                auto screen = [&](float &e) {
-                    const uint32_t ab = __float_as_uint(e) & 0x7fffffffu;
-                    const bool bad = ab >= 0x7f800000u;
-                    e = bad ? 0.0f : e;
-                    nf |= (bad && in) ? 1u : 0u;
-                    mb = (!bad && in && ab > mb) ? ab : mb;
-                };
-                screen(v.x); screen(v.y); screen(v.z); screen(v.w);
+                const float4 v = xv[ci][j][h];
+                const uint32_t t = max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
+                                       max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu));
+                mb = m < L.M && lane + 64 * j < 4 * ns ? max(mb, t) : mb;
             }
-        float mx = wave_max_f32(__uint_as_float(mb));
+        mb = wave_max_u32(mb);
         if (lane == 0) cnf[m] = 0;
-        if (__builtin_amdgcn_ballot_w64(nf != 0u) != 0 && lane == 0) cnf[m] = 1;
+        if (mb >= 0x7f800000u) {                                   // uniform: Inf or NaN in this column's split
+            mb = 0u;
+#pragma unroll
+            for (int j = 0; j < SPL; j++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    float4 &v = xv[ci][j][h];
+                    const bool in = m < L.M && lane + 64 * j < 4 * ns;
+                    auto screen = [&](float &e) {
+                        const uint32_t ab = __float_as_uint(e) & 0x7fffffffu;
+                        const bool bad = ab >= 0x7f800000u;
+                        e = bad ? 0.0f : e;
+                        mb = (!bad && in && ab > mb) ? ab : mb;
+                    };
+                    screen(v.x); screen(v.y); screen(v.z); screen(v.w);
+                }
+            mb = wave_max_u32(mb);
+            if (lane == 0) cnf[m] = 1;
+        }
+        const float mx = __uint_as_float(mb);
         int e = 0;
         if (mx > 0.0f) frexpf(mx, &e);                             // mx in [2^(e-1), 2^e)
         const float sc = mx > 0.0f ? ldexpf(1.0f, 14 - e) : 1.0f;

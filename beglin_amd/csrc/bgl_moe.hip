@@ -193,7 +193,7 @@ __device__ __forceinline__ BglDevTensor ld_tensor(const BglDevTensor *p) {
 // SEG: the segments are consecutive runs of Mt.seg columns (the shared experts).  A separate
 // instantiation, so the routed kernel's register allocation (and occupancy) stays its own.
 template <bool WIDE, bool SEG>
-__global__ __launch_bounds__(MOE_MAXW * BGL_TILE) void k_moe_gemv(MoeTask Mt) {
+__global__ __launch_bounds__(MOE_MAXW * BGL_TILE, WIDE || SEG ? 2 : 4) void k_moe_gemv(MoeTask Mt) {
     __shared__ float red[MOE_MAXW][2][MOE_MB][BGL_TILE];
     const int e = blockIdx.x / Mt.tpe, tile = blockIdx.x % Mt.tpe;
     int seg0 = 0, ncols = Mt.ncols;

@@ -18,11 +18,11 @@
 
 bool bgl_moe_x_fmt(int fmt) { return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64; }
 
-// LDS: MB columns of level-0 records (K/64 rounded up to whole slots of 64/TR groups), the same for
-// level 1, and the wave partials.
+// LDS: MB columns of records (K/64 rounded up to whole slots of 64/TR groups), the wave partials,
+// and one slot of level-1 records per wave (cold path).
 size_t bgl_moe_x_lds(int K, int nw, int TR) {
     const int KQ = BGL_TILE / TR, S = (K / 64 + KQ - 1) / KQ;
-    return (size_t)2 * MX_MB * S * KQ * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * TR * 4;
+    return (size_t)MX_MB * S * KQ * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * TR * 4 + (size_t)nw * KQ * XREC_DW * 4;
 }
 
 // out[t][c] = (((0 + w_a d_a) + w_b d_b) + ...) over t's experts in ascending expert id (then k), then
@@ -53,7 +53,6 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
     const int nthr = blockDim.x, nw = nthr >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int K = Ta.K, G = K >> 6, S = (G + KQ - 1) / KQ, RC = S * KQ * XREC_DW, NPX = (K + 255) >> 8;
-    const int L1 = MX_MB * RC;                     // level-1 records follow the MB columns' level-0 ones
     const int r = lane % TR, kq = lane / TR;
 
     // ---- a wave's items: its slots wave, wave + nw, ... -- each once per tensor in SwiGLU mode
@@ -79,7 +78,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
         const int m = pi / NPX, p = pi - m * NPX;
         const int row = Mt.cols ? uni(Mt.cols)[base + m] : base + m;
         const float4 v = x_pass_load(Mt.a.xf + (size_t)row * K, p, lane, K);
-        x_pass_digits(v, p, lane, G, xl + m * RC, L1);
+        x_pass_digits(v, p, lane, G, xl + m * RC);
     }
     if (KQ > 1) {
         const int per = (S * KQ - G) * XREC_DW;
@@ -119,27 +118,42 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
         }
     }
     // items whose records carry a level-1 residual or non-finite values in some column: their
-    // weights again (cold path)
+    // weights again, and the column's level-1 records made from its raw row (cold path)
     {
         int fl = 0;
         for (int i = 0; i < ns; i++)
             for (int m = 0; m < mc; m++) fl |= xk[(wave + i * nw) * (KQ * XREC_DW) + m * RC + XREC_DSUM + 3];
         if (__builtin_amdgcn_ballot_w64(fl != 0)) {
+            int *scr = xl + MX_MB * RC + nw * 2 * MX_MB * TR + wave * KQ * XREC_DW;   // this wave's level-1 records
+            const int *r1 = scr + kq * XREC_DW;
             for (int j = 0; j < NI; j++) {
-                const int sl = wave + (glu ? j >> 1 : j) * nw;
+                const int sl = wave + (glu ? j >> 1 : j) * nw, gl = min(sl * KQ + kq, G - 1);
                 const bool up = glu && (j & 1);
                 const int *rec = xk + sl * (KQ * XREC_DW);
                 int f2 = 0;
                 for (int m = 0; m < mc; m++) f2 |= rec[m * RC + XREC_DSUM + 3];
                 if (!__builtin_amdgcn_ballot_w64(f2 != 0)) continue;
-                XRaw<FMT, NB> rf;
-                x_load<FMT, NB, KQ>(rf, up ? Rb : Ra, sl == S - 1 ? xlast : xlane, sl, true);
-                const XDec<FMT, NB> d = x_decode<FMT, NB>(rf);
 #pragma unroll 1
                 for (int m = 0; m < mc; m++) {
+                    const int f3 = rec[m * RC + XREC_DSUM + 3];
+                    if (!__builtin_amdgcn_ballot_w64(f3 != 0)) continue;
                     const int xrow_m = Mt.cols ? uni(Mt.cols)[base + m] : base + m;
-                    const XRow xrow{up ? &Tb : &Ta, tile * BGL_TILE + r0 + r, Mt.a.xf + (size_t)xrow_m * K};
-                    const float v = x_fix<FMT, NB>(d, rec + m * RC, L1, xrow, sl * KQ + kq);
+                    const float *xr = Mt.a.xf + (size_t)xrow_m * K;
+                    // the column's level-1 records first, then the weights: the two never hold
+                    // registers at the same time
+                    if (__builtin_amdgcn_ballot_w64(f3 & BGL_XF_L1)) {
+                        __builtin_amdgcn_wave_barrier();      // the previous column's reads of scr are done
+                        const int g0 = sl * KQ, g1 = min(g0 + KQ, G);
+                        for (int p = g0 >> 2; p <= (g1 - 1) >> 2; p++) x_pass_l1(x_pass_load(xr, p, lane, K), p, lane, g0, g1, scr);
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                        __builtin_amdgcn_wave_barrier();
+                        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    }
+                    XRaw<FMT, NB> rf;
+                    x_load<FMT, NB, KQ>(rf, up ? Rb : Ra, sl == S - 1 ? xlast : xlane, sl, true);
+                    const XRow xrow{up ? &Tb : &Ta, tile * BGL_TILE + r0 + r, xr};
+                    const float v = x_fix<FMT, NB>(x_decode<FMT, NB>(rf), rec + m * RC, r1, *reinterpret_cast<const int4 *>(r1 + XREC_DSUM),
+                                                   *reinterpret_cast<const int4 *>(r1 + XREC_DSUM + 4), xrow, gl);
 #pragma unroll
                     for (int q = 0; q < MB; q++) {
                         if (q == m && !up) acc[q] += v;
@@ -159,7 +173,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
             accb[m] += __shfl_xor(accb[m], o);
         }
     }
-    float *red = reinterpret_cast<float *>(xl + 2 * L1);          // [wave][2][MB][TR]
+    float *red = reinterpret_cast<float *>(xl + MX_MB * RC);      // [wave][2][MB][TR]
     if (lane < TR) {
 #pragma unroll
         for (int m = 0; m < MB; m++) {
@@ -209,8 +223,7 @@ __device__ __forceinline__ BglDevTensor mx_tensor(const BglDevTensor *p) {
 }
 
 // Grid: E x tpe workgroups.  SEG: the segments are consecutive runs of Mt.seg columns of
-// one by-value tensor (the shared experts).  At least 3 waves per SIMD: the widest formats then fit
-// 168 registers without spilling.
+// one by-value tensor (the shared experts).
 template <bool SEG, int TR>
 __device__ __forceinline__ void moe_x_body(const MoeTask &Mt, int bid, int *xl) {
     constexpr int SUBS = BGL_TILE / TR;
@@ -251,8 +264,11 @@ __device__ __forceinline__ void moe_x_body(const MoeTask &Mt, int bid, int *xl) 
     }
 }
 
+// Whole-tile instances are held to 4 waves per SIMD (128 VGPRs: two 8-wave workgroups per CU, the
+// occupancy the hot loop fits in); the 16-row instance runs only where fewer workgroups than CUs
+// have work, so 3 waves per SIMD leave its widest formats room without spilling.
 template <bool SEG, int NWMAX, int TR>
-__global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(MoeTask Mt) {
+__global__ __launch_bounds__(NWMAX * BGL_TILE, TR == BGL_TILE ? 4 : 3) void k_moe_x(MoeTask Mt) {
     extern __shared__ __align__(16) int xl[];
     moe_x_body<SEG, TR>(Mt, blockIdx.x, xl);
 }
@@ -261,7 +277,7 @@ __global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x(
 // shared tiles run beside the routed ones instead of after them.  SEG1: the second task's columns
 // are cut into segments (the shared experts over more than 4 tokens).
 template <int NWMAX, bool SEG1>
-__global__ __launch_bounds__(NWMAX * BGL_TILE, NWMAX == 8 ? 3 : 4) void k_moe_x2(MoePair P) {
+__global__ __launch_bounds__(NWMAX * BGL_TILE, 4) void k_moe_x2(MoePair P) {
     extern __shared__ __align__(16) int xl[];
     if ((int)blockIdx.x < P.nb0) moe_x_body<false, BGL_TILE>(P.t[0], blockIdx.x, xl);
     else moe_x_body<SEG1, BGL_TILE>(P.t[1], (int)blockIdx.x - P.nb0, xl);
