@@ -20,8 +20,11 @@
  *     Accelerate library) is parity unpinned beyond the 1e-5 tolerance.
  *   - or_quant_act_i8, or_gemm_*_sdot, or_matmul_sdot: reference rounding cases + the identity
  *     against the de-quantized product + batched == per-column.
- *   - or_quantize_g256sf: parity unpinned (the reference ships no g256sf emitter); held to its
- *     invariants (sub codes in [1,63], effective scale >= group max / 7, decode error bound).
+ *   - or_quantize_g256sf: build-defined (the reference ships no g256sf emitter).  Pinned where
+ *     it reduces to the reference: with the four 64-subgroups of every 256-group sharing their
+ *     max |w| it must be gguf_quantize_q4g64_error_feedback (oracle/_ref) byte for byte, sub = 63;
+ *     plus the minimality of sub (smallest code whose effective scale covers max|w|/7) and
+ *     wsuper = the largest subgroup scale.
  *   - or_moe_router_logits: a pure-Python sequential double loop (the reference order), bit for bit.
  *   - or_decode_qng64_mixed: equal to or_decode_qng64 when every cell has the same n, and to an
  *     independent Python bit-plane decode for random per-cell widths.

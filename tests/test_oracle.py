@@ -332,6 +332,57 @@ def test_g256sf_packer_roundtrip(oracle):
     assert _rel_l2_decode(d, w) < 1.2 * _rel_l2_decode(d4, w)
 
 
+def _equal_subgroup_max(w):
+    """Every 64-subgroup of each 256-group gets the same max |w|: the subgroup's largest element is
+    set (sign kept) to the largest magnitude of its 256-group."""
+    w = w.copy()
+    out, inn = w.shape
+    g = w.reshape(out, inn // 256, 4, 64)
+    a = np.abs(g)
+    big = a.max(axis=(2, 3))                                   # [out][n256]
+    idx = a.argmax(axis=3)                                     # [out][n256][4]
+    o, s, k = np.meshgrid(np.arange(out), np.arange(inn // 256), np.arange(4), indexing="ij")
+    sign = np.where(g[o, s, k, idx] < 0, -1.0, 1.0).astype(np.float32)
+    g[o, s, k, idx] = sign * big[:, :, None]
+    return g.reshape(out, inn)
+
+
+@pytest.mark.parametrize("shape", [(5, 256), (24, 1536), (9, 8960)])
+def test_g256sf_packer_reduces_to_reference_q4g64(oracle, ref, shape):
+    """Where the four 64-subgroups of every 256-group share their max |w|, the g256sf packer must
+    be the reference's q4g64 error-feedback packer (gguf_transcode.c:24-68, built from the
+    reference's own C in oracle/_ref): sub = 63 everywhere, the codes byte for byte and wsuper
+    equal to its per-64 scales bit for bit.  A dropped error-feedback step, a wrong rounding or
+    nibble order, or a sub-code off by one fails here."""
+    w = _equal_subgroup_max(_weights(95, *shape, outliers=True, zero_rows=False))
+    p, ws, sub = oracle.quantize_g256sf(w)
+    rp = np.zeros_like(p)
+    rs = np.zeros((shape[0], shape[1] // 64), np.float32)
+    ref.gguf_quantize_q4g64_error_feedback(_ptr(w), shape[0], shape[1], _ptr(rp), _ptr(rs))
+    assert np.all(sub == 63)
+    assert np.array_equal(p, rp)
+    rs4 = rs.reshape(shape[0], -1, 4)
+    assert np.all(rs4 == rs4[:, :, :1])                       # the reference's four scales agree
+    assert np.array_equal(ws.view(np.uint32), np.ascontiguousarray(rs4[:, :, 0]).view(np.uint32))
+
+
+def test_g256sf_sub_code_is_minimal(oracle):
+    """sub is the smallest integer in [1, 63] whose effective scale wsuper * sub / 63 covers the
+    subgroup's max |w| / 7 (up to one fp32 rounding), and wsuper is the largest subgroup scale."""
+    w = _weights(96, 40, 2048, outliers=True, zero_rows=False)
+    w[3, :256] *= np.float32(1e-3)                             # a 256-group of tiny subgroups
+    w[4, 64:128] = 0.0                                         # one all-zero subgroup
+    p, ws, sub = oracle.quantize_g256sf(w)
+    s64 = (np.abs(w).reshape(40, -1, 64).max(axis=2) / np.float32(7.0)).astype(np.float32).astype(np.float64)
+    wsb = np.repeat(ws.astype(np.float64), 4, axis=1)
+    assert np.array_equal(ws.astype(np.float64), s64.reshape(40, -1, 4).max(axis=2))
+    eff = wsb * sub / 63.0
+    assert np.all(eff >= s64 * (1 - 2.0 ** -22))
+    lower = wsb * (sub.astype(np.float64) - 1) / 63.0
+    assert np.all((sub == 1) | (lower < s64 * (1 + 2.0 ** -22)))
+    assert sub.min() >= 1 and sub.max() <= 63
+
+
 # ---------------------------------------------------------------- MoE
 def test_mixed_qng64_decode_uniform_equals_dense(oracle):
     """A mixed tensor whose cells all have the same n is the qng64_dense layout (qng64_dense.c:19-27
