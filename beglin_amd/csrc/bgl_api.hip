@@ -41,11 +41,20 @@ extern "C" int bgl_available(void) {
 }
 
 // ------------------------------------------------------------------ device buffers
+// Per-call scratch grows on demand.  A graph captured from the context's stream keeps the raw
+// addresses of the scratch its calls used, so a buffer that has to grow is not freed: it is
+// retired and freed with the context (bgl_ctx_destroy) or an epoch reset.  Growing inside a
+// stream capture would put allocation into the captured region: refused with BGL_E_CAPTURE
+// (the caller runs the call once eagerly at that size first).
 int dbuf_reserve(bgl_ctx *c, DevBuf &b, size_t bytes, bool zero) {
     if (b.bytes >= bytes) return 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIPCHK(hipStreamIsCapturing(c->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return bgl_fail(BGL_E_CAPTURE, "per-call scratch would have to grow to %zu B inside a stream capture: run the call "
+                        "once without capture at this size (or larger) first", bytes);
     if (b.p) {
-        HIPCHK(hipStreamSynchronize(c->stream));
-        HIPCHK(hipFree(b.p));
+        c->retired.push_back(b.p);          // a captured graph may still use it
         b.p = nullptr; b.bytes = 0;
     }
     size_t want = bytes + bytes / 4 + 4096;
@@ -72,7 +81,11 @@ size_t ctx_scratch(bgl_ctx *c, bool release) {
         total += b->bytes;
         if (release) dbuf_free(*b);
     }
-    if (release) { c->prep_act = -1; c->prep_M = 0; c->prep_K = 0; }
+    if (release) {
+        for (void *p : c->retired) (void)hipFree(p);
+        c->retired.clear();
+        c->prep_act = -1; c->prep_M = 0; c->prep_K = 0;
+    }
     return total;
 }
 

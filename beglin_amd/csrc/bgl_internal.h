@@ -44,6 +44,7 @@ struct bgl_ctx {
     DevBuf moe_a, moe_b, moe_c, moe_d, moe_e, moe_f, moe_g, moe_meta;   // MoE digits x2, fp32 h/down, bucket scratch
     DevBuf moe_route;                     // routing of bgl_moe_layer_dev: idx [T][K] + w [T][K]
     DevBuf moe_scores;                    // router scores [T][E]
+    std::vector<void *> retired;          // outgrown scratch, kept for captured graphs until destroy / epoch reset
     bool prof = false;                    // bracket launches with events (bgl_prof_enable)
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> prof_ev;
     std::vector<hipEvent_t> ev_pool;

@@ -18,6 +18,12 @@
  *     x in and y out and return after y is on the host.
  *   - one context = one HIP stream; calls on one context are serialised by that stream.  Two
  *     threads must not use the same context concurrently (the q4pool contract, q4gemv.h:721).
+ *   - graph capture: the *_dev calls may be captured from the context's stream once the same
+ *     call has run outside a capture at the same or larger sizes (that sizes the context's
+ *     per-call scratch).  A captured call that would need more scratch returns BGL_E_CAPTURE and
+ *     enqueues nothing.  Scratch a graph uses stays allocated until bgl_ctx_destroy or
+ *     bgl_gpu_reset_runtime_epoch (after which graphs must be captured again), even when a
+ *     later, larger call outgrows it.
  */
 #ifndef BEGLIN_QGEMV_H
 #define BEGLIN_QGEMV_H
@@ -31,7 +37,8 @@ extern "C" {
 enum { BGL_K_Q4G64 = 1, BGL_K_Q8G64 = 2, BGL_K_Q4G256SF = 3, BGL_K_QNG64 = 4, BGL_K_Q4G32H = 5,
        BGL_K_Q4G64A = 6, BGL_K_F16 = 7, BGL_K_F32 = 8 };
 enum { BGL_ACT_F32 = 0, BGL_ACT_W4A8 = 1 };
-enum { BGL_OK = 0, BGL_E_ARG = -1, BGL_E_UNSUPPORTED = -2, BGL_E_HIP = -3, BGL_E_NODEV = -4, BGL_E_NOMEM = -5 };
+enum { BGL_OK = 0, BGL_E_ARG = -1, BGL_E_UNSUPPORTED = -2, BGL_E_HIP = -3, BGL_E_NODEV = -4, BGL_E_NOMEM = -5,
+       BGL_E_CAPTURE = -6 /* per-call scratch would have to grow inside a stream capture */ };
 
 typedef struct bgl_ctx bgl_ctx;
 typedef struct bgl_tensor bgl_tensor;
