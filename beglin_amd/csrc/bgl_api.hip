@@ -16,8 +16,12 @@
 #include "bgl_internal.h"
 
 static thread_local char g_err[512];
+static thread_local int g_code;
+
+int bgl_last_code(void) { return g_code ? g_code : BGL_E_NOMEM; }
 
 int bgl_fail(int code, const char *fmt, ...) {
+    g_code = code;
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(g_err, sizeof g_err, fmt, ap);
@@ -47,6 +51,17 @@ extern "C" int bgl_available(void) {
 // stream capture would put allocation into the captured region: refused with BGL_E_CAPTURE
 // (the caller runs the call once eagerly at that size first).
 int dbuf_reserve(bgl_ctx *c, DevBuf &b, size_t bytes, bool zero) {
+    if (c->fixed_base) {                    // bgl_matmul_group_noalloc_dev: a slice of the fixed array, never an allocation
+        const size_t off = (c->fixed_used + 255) & ~(size_t)255;
+        if (zero) return bgl_fail(BGL_E_UNSUPPORTED, "no-alloc call: no path here needs zeroed scratch");
+        if (off + bytes > c->fixed_cap)
+            return bgl_fail(BGL_E_NOMEM, "no-alloc call needs more than the fixed %zu B of device scratch (BGL_NOALLOC_SCRATCH_BYTES): "
+                            "use fewer columns or the allocating entry point", c->fixed_cap);
+        b.p = c->fixed_base + off;
+        b.bytes = bytes;
+        c->fixed_used = off + bytes;
+        return 0;
+    }
     if (b.bytes >= bytes) return 0;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     HIPCHK(hipStreamIsCapturing(c->stream, &cs));
@@ -89,12 +104,36 @@ size_t ctx_scratch(bgl_ctx *c, bool release) {
     return total;
 }
 
+// ------------------------------------------------------------------ fixed scratch (no-alloc entry)
+// The scratch of bgl_matmul_group_noalloc_dev: a file-scope device array, so the call allocates
+// nothing.  Each GPU the library runs on holds its own copy (BGL_NOALLOC_SCRATCH_BYTES) until the
+// process ends.  In host code `scratch` names a host-side stand-in, not the device array: its
+// device address comes from hipGetSymbolAddress, once per device, and only that address is used.
+static __device__ __align__(256) uint8_t scratch[BGL_NOALLOC_SCRATCH_BYTES];
+#define BGL_MAX_DEVICES 64
+static std::mutex g_scratch_mu;
+static uint8_t *g_scratch_ptr[BGL_MAX_DEVICES];
+
+// The device address of this device's fixed scratch (the caller has made `device` current).
+static int scratch_setup(int device) {
+    if (device < 0 || device >= BGL_MAX_DEVICES) return bgl_fail(BGL_E_NODEV, "fixed scratch: device %d out of range", device);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return 0;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return bgl_fail(BGL_E_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[device] = (uint8_t *)ptr;
+    return 0;
+}
+
 extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     if (!out) return bgl_fail(BGL_E_ARG, "bgl_ctx_create: out is NULL");
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
         return bgl_fail(BGL_E_NODEV, "bgl_ctx_create: no HIP device %d", device);
     HIPCHK(hipSetDevice(device));
+    int rc = scratch_setup(device);
+    if (rc) return rc;
     bgl_ctx *c = new bgl_ctx();
     c->device = device;
     if (hip_stream) { c->stream = (hipStream_t)hip_stream; c->own_stream = false; }
@@ -532,7 +571,7 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
         int ng = K / 64;
         if (dbuf_reserve(c, c->act_w, (size_t)2 * M * ng * 192, false) || dbuf_reserve(c, c->act_s, (size_t)2 * M * ng * 4, false) ||
             dbuf_reserve(c, c->act_sum, (size_t)2 * M * (K / 32) * 16, false))
-            return BGL_E_NOMEM;
+            return bgl_last_code();
         int tok = prof_begin(c, 0);
         hipLaunchKernelGGL(k_act_x24, dim3(nblk((long)M * ng * 64)), dim3(256), 0, c->stream, x_dev, M, K,
                            (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
@@ -540,7 +579,7 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
     } else {
         if (dbuf_reserve(c, c->act_w, (size_t)M * K, false) || dbuf_reserve(c, c->act_s, (size_t)M * (K / gq) * 4, false) ||
             dbuf_reserve(c, c->act_sum, (size_t)M * (K / 64) * 4, false))
-            return BGL_E_NOMEM;
+            return bgl_last_code();
         int tok = prof_begin(c, 0);
         hipLaunchKernelGGL(k_act_w4a8, dim3(nblk((long)M * (K / gq) * 64)), dim3(256), 0, c->stream, x_dev, M, K, gq,
                            (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
@@ -562,7 +601,7 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
 extern "C" int bgl_quant_act_i8_dev(bgl_ctx *c, const float *x_dev, int M, int in, int gsize, int8_t *xq_dev, float *ascale_dev) {
     if (!c || !x_dev || !xq_dev || !ascale_dev || M <= 0) return bgl_fail(BGL_E_ARG, "bgl_quant_act_i8_dev: bad argument");
     if ((gsize != 64 && gsize != 256) || in % gsize) return bgl_fail(BGL_E_ARG, "bgl_quant_act_i8_dev: in=%d gsize=%d", in, gsize);
-    if (dbuf_reserve(c, c->act_sum, (size_t)M * (in / 64) * 4, false)) return BGL_E_NOMEM;
+    if (dbuf_reserve(c, c->act_sum, (size_t)M * (in / 64) * 4, false)) return bgl_last_code();
     hipLaunchKernelGGL(k_act_w4a8, dim3(nblk((long)M * (in / gsize) * 64)), dim3(256), 0, c->stream, x_dev, M, in, gsize, xq_dev,
                        ascale_dev, (int *)c->act_sum.p);
     HIPCHK(hipGetLastError());
@@ -666,7 +705,7 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
         GemvTask &t = L.t[0];
         t.gpb = (Ts[0].nunits + ks - 1) / ks;
         t.ks = (Ts[0].nunits + t.gpb - 1) / t.gpb;
-        if (dbuf_reserve(c, c->part, (size_t)t.ks * M * Ts[0].N * 4, false)) return BGL_E_NOMEM;
+        if (dbuf_reserve(c, c->part, (size_t)t.ks * M * Ts[0].N * 4, false)) return bgl_last_code();
         t.part = (float *)c->part.p;
         blocks *= t.ks;
     }
@@ -811,6 +850,36 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
     return run_gemv(c, n, Ts, act, A, M, bias_dev, y_dev, nullptr);
 }
 
+// bgl_matmul_group_dev with every per-call scratch buffer (activation digits and codes, K-split
+// partials) carved from this GPU's fixed array instead of the context's allocations: no hipMalloc,
+// hipFree or memset.  The context's own scratch and prepared-activation state are left as they
+// were.  Every call on one GPU shares the array and leaves its contents behind (no path here
+// reads scratch it has not written in the same call); calls that overlap on one GPU -- two
+// contexts or streams at once -- race on it.
+extern "C" int bgl_matmul_group_noalloc_dev(bgl_ctx *c, int n, const bgl_tensor *const *w, int act, const float *x_dev,
+                                            const float *const *bias_dev, float *const *y_dev, int M) {
+    if (!c) return bgl_fail(BGL_E_ARG, "bgl_matmul_group_noalloc_dev: NULL context");
+    uint8_t *base = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        base = c->device >= 0 && c->device < BGL_MAX_DEVICES ? g_scratch_ptr[c->device] : nullptr;
+    }
+    if (!base) return bgl_fail(BGL_E_HIP, "bgl_matmul_group_noalloc_dev: no fixed scratch on device %d", c->device);
+    const DevBuf aw = c->act_w, as = c->act_s, asum = c->act_sum, part = c->part;
+    const int pa = c->prep_act, pg = c->prep_gq, pm = c->prep_M, pk = c->prep_K;
+    const float *px = c->prep_x;
+    const bool prof = c->prof;
+    c->act_w = c->act_s = c->act_sum = c->part = DevBuf{};
+    c->fixed_base = base; c->fixed_cap = BGL_NOALLOC_SCRATCH_BYTES; c->fixed_used = 0;
+    c->prof = false;                        // event brackets would create events
+    const int rc = bgl_matmul_group_dev(c, n, w, act, x_dev, bias_dev, y_dev, M);
+    c->fixed_base = nullptr; c->fixed_cap = 0; c->fixed_used = 0;
+    c->act_w = aw; c->act_s = as; c->act_sum = asum; c->part = part;
+    c->prep_act = pa; c->prep_gq = pg; c->prep_M = pm; c->prep_K = pk; c->prep_x = px;
+    c->prof = prof;
+    return rc;
+}
+
 extern "C" int bgl_prep_act_dev(bgl_ctx *c, int act, int kind, const float *x_dev, int M, int in) {
     if (!c || !x_dev || M < 1) return bgl_fail(BGL_E_ARG, "bgl_prep_act_dev: bad argument");
     if (act != BGL_ACT_F32 && act != BGL_ACT_W4A8) return bgl_fail(BGL_E_ARG, "unknown activation mode %d", act);
@@ -880,7 +949,7 @@ static int host_call(bgl_ctx *c, const bgl_wt &wt, int act, const float *x, cons
     if (rc) return rc;
     size_t xb = (size_t)M * wt.in * 4, yb = (size_t)M * wt.out * 4;
     if (dbuf_reserve(c, c->hx, xb, false) || dbuf_reserve(c, c->hy, yb, false) || dbuf_reserve(c, c->hb, (size_t)wt.out * 4, false))
-        return BGL_E_NOMEM;
+        return bgl_last_code();
     HIPCHK(hipMemcpyAsync(c->hx.p, x, xb, hipMemcpyHostToDevice, c->stream));
     if (bias) HIPCHK(hipMemcpyAsync(c->hb.p, bias, (size_t)wt.out * 4, hipMemcpyHostToDevice, c->stream));
     rc = bgl_matmul_dev(c, t, act, (const float *)c->hx.p, bias ? (const float *)c->hb.p : nullptr, (float *)c->hy.p, M);
@@ -910,7 +979,7 @@ static int host_call_i8(bgl_ctx *c, const bgl_wt &wt, const int8_t *xq, const fl
     if (dbuf_reserve(c, c->hx, qpad + ab, false) || dbuf_reserve(c, c->hy, yb, false) ||
         dbuf_reserve(c, c->hb, (size_t)wt.out * 4, false) || dbuf_reserve(c, c->act_w, qb, false) ||
         dbuf_reserve(c, c->act_s, ab, false) || dbuf_reserve(c, c->act_sum, (size_t)M * (K / 64) * 4, false))
-        return BGL_E_NOMEM;
+        return bgl_last_code();
     HIPCHK(hipMemcpyAsync(c->hx.p, xq, qb, hipMemcpyHostToDevice, c->stream));
     HIPCHK(hipMemcpyAsync((char *)c->hx.p + qpad, ascale, ab, hipMemcpyHostToDevice, c->stream));
     if (bias) HIPCHK(hipMemcpyAsync(c->hb.p, bias, (size_t)wt.out * 4, hipMemcpyHostToDevice, c->stream));

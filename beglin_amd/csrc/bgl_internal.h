@@ -45,6 +45,8 @@ struct bgl_ctx {
     DevBuf moe_route;                     // routing of bgl_moe_layer_dev: idx [T][K] + w [T][K]
     DevBuf moe_scores;                    // router scores [T][E]
     std::vector<void *> retired;          // outgrown scratch, kept for captured graphs until destroy / epoch reset
+    uint8_t *fixed_base = nullptr;        // set during bgl_matmul_group_noalloc_dev: scratch comes from here
+    size_t fixed_cap = 0, fixed_used = 0;
     bool prof = false;                    // bracket launches with events (bgl_prof_enable)
     std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> prof_ev;
     std::vector<hipEvent_t> ev_pool;
@@ -53,6 +55,7 @@ struct bgl_ctx {
 };
 
 int bgl_fail(int code, const char *fmt, ...);
+int bgl_last_code(void);             // the code of this thread's last bgl_fail (BGL_E_NOMEM if none)
 // The device layout's version: bump when any format's device bytes change, so caches of the
 // repacked layout written before the change are rejected.  (2: signed-nibble g256sf with one
 // 8-byte scale word per unit.)

@@ -813,7 +813,7 @@ int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev,
         memset(&R, 0, sizeof R);
         R.M = Mc;
         if (pfl) {
-            if (dbuf_reserve(c, c->part, pfl * 4, false)) return BGL_E_NOMEM;
+            if (dbuf_reserve(c, c->part, pfl * 4, false)) return bgl_last_code();
             int nq = 0;
             for (int i = 0; i < n; i++) {
                 if (S_[i] == 1) continue;

@@ -316,7 +316,7 @@ static int moe_scratch(bgl_ctx *c, int P, int E, MoeScratch &S) {
     const size_t lds = ((size_t)E + 1 + P) * 4;
     if (lds > 64 * 1024)
         return bgl_fail(BGL_E_ARG, "MoE bucketing: %d pairs over %d experts exceed one workgroup's LDS", P, E);
-    if (dbuf_reserve(c, c->moe_meta, ((size_t)E + 1 + 3 * (size_t)P) * 4, false)) return BGL_E_NOMEM;
+    if (dbuf_reserve(c, c->moe_meta, ((size_t)E + 1 + 3 * (size_t)P) * 4, false)) return bgl_last_code();
     int *b = (int *)c->moe_meta.p;
     S.off = b; S.perm = b + E + 1; S.pos = S.perm + P; S.tok = S.pos + P;
     return 0;
@@ -341,7 +341,7 @@ static int moe_prep(bgl_ctx *c, int slot, const float *x_dev, int M, int K, Gemv
     const int ng = K / 64;
     if (dbuf_reserve(c, w, (size_t)2 * M * ng * 192, false) || dbuf_reserve(c, s, (size_t)2 * M * ng * 4, false) ||
         dbuf_reserve(c, d, (size_t)2 * M * (K / 32) * 16, false))
-        return BGL_E_NOMEM;
+        return bgl_last_code();
     int tok = prof_begin(c, 0);
     hipLaunchKernelGGL(k_act_x24, dim3(nblk((long)M * ng * 64)), dim3(256), 0, c->stream, x_dev, M, K, (int8_t *)w.p,
                        (float *)s.p, (int *)d.p);
@@ -511,7 +511,7 @@ static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, con
     else if ((rc = moe_bucket(c, idx_dev, P, K, E, S))) return rc;
     // fp32 work rows: h [P][I], shared h [T][Ish], routed down [P][H], shared down [T][H]
     const size_t nh = (size_t)P * I, nsh_h = (size_t)T * Ish, nd = (size_t)P * H, nsd = (size_t)T * H;
-    if (dbuf_reserve(c, c->moe_g, (nh + nsh_h + nd + nsd) * 4, false)) return BGL_E_NOMEM;
+    if (dbuf_reserve(c, c->moe_g, (nh + nsh_h + nd + nsd) * 4, false)) return bgl_last_code();
     float *h = (float *)c->moe_g.p, *shh = h + nh, *dd = shh + nsh_h, *sdd = dd + nd;
 
     MoeTask Mr, Ms;
@@ -765,7 +765,7 @@ static int route_scores(bgl_ctx *c, const char *who, const float *rw_dev, const 
     if (in < 4 || in % 4 || ((uintptr_t)rw_dev | (uintptr_t)x_dev) % 16)
         return bgl_fail(BGL_E_ARG, "%s: in=%d must be a multiple of 4 with 16-byte aligned rows", who, in);
     HIPCHK(hipSetDevice(c->device));
-    if (dbuf_reserve(c, c->moe_scores, (size_t)T * E * 4, false)) return BGL_E_NOMEM;
+    if (dbuf_reserve(c, c->moe_scores, (size_t)T * E * 4, false)) return bgl_last_code();
     *scores = (float *)c->moe_scores.p;
     int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_moe_router_scores, dim3(T, (E + ROUTE_EPW - 1) / ROUTE_EPW), dim3(ROUTE_EPW * 64), 0, c->stream, rw_dev,
@@ -796,7 +796,7 @@ extern "C" int bgl_moe_layer_dev(bgl_ctx *c, const float *rw_dev, const float *r
     if ((rc = expert_check(gate, "bgl_moe_layer_dev: gate"))) return rc;
     const int E = (int)gate->experts.size(), H = gate->T.K;
     HIPCHK(hipSetDevice(c->device));
-    if (dbuf_reserve(c, c->moe_route, (size_t)T * K * 8, false)) return BGL_E_NOMEM;
+    if (dbuf_reserve(c, c->moe_route, (size_t)T * K * 8, false)) return bgl_last_code();
     int32_t *idx = (int32_t *)c->moe_route.p;
     float *w = (float *)(idx + (size_t)T * K);
     float *scores = nullptr;

@@ -113,6 +113,16 @@ int  bgl_matmul_dev(bgl_ctx *ctx, const bgl_tensor *w, int act, const float *x_d
  * qwen_infer.c:1276-1306) in ONE launch.  All must have the same `in` and kind; n <= 4. */
 int  bgl_matmul_group_dev(bgl_ctx *ctx, int n, const bgl_tensor *const *w, int act, const float *x_dev,
                           const float *const *bias_dev, float *const *y_dev, int M);
+/* bgl_matmul_group_dev that allocates nothing: no counterpart in the reference.  For callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  The same kernels and results as bgl_matmul_group_dev; the per-call
+ * scratch (activation digits / codes, K-split partials) comes from a fixed per-GPU device array of
+ * BGL_NOALLOC_SCRATCH_BYTES, held until the process ends.  A call that needs more returns
+ * BGL_E_NOMEM (e.g. fp32 activations: about 116 KB per column at K = 16384).  The array is shared
+ * by every call on the GPU: calls that overlap on one GPU (two contexts or streams) race. */
+#define BGL_NOALLOC_SCRATCH_BYTES (32u << 20)
+int  bgl_matmul_group_noalloc_dev(bgl_ctx *ctx, int n, const bgl_tensor *const *w, int act, const float *x_dev,
+                                  const float *const *bias_dev, float *const *y_dev, int M);
 /* Prepare activation operands once and reuse them for several GEMVs with the same input (the
  * caller-side quantization of matmul_sdot, qwen_infer.c:1870-1889, feeding gemm_qXg64_sdot_mt's
  * xq/ascale arguments, q4gemv.h:779-791).  `kind` selects the activation grouping (g256sf: 256).
