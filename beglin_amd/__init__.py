@@ -158,6 +158,11 @@ class Context:
         B = (C.c_void_p * n)(*[(b.data_ptr() if b is not None else None) for b in (biases or [None] * n)])
         _check(lib().bgl_matmul_group_dev(self.h, n, W, act, _p(x_dev), B, Y, M), "bgl_matmul_group_dev")
 
+    def read_probe(self, ts, nblocks=0, nthreads=0):
+        """Plain streaming read of the tensors' device bytes (the memory floor for a call)."""
+        W = (C.c_void_p * len(ts))(*[t.h.value for t in ts])
+        _check(lib().bgl_read_probe_dev(self.h, len(ts), W, nblocks, nthreads), "bgl_read_probe_dev")
+
     def prep_only(self, x_dev, act, t):
         """Prepare activation operands for tensor t's kind (kept in the context)."""
         M = 1 if x_dev.dim() == 1 else x_dev.shape[0]

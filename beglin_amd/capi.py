@@ -42,6 +42,7 @@ SIGNATURES = [
     ("bgl_matmul_dev", _I, [_P, _P, _I, _P, _P, _P, _I]),
     ("bgl_matmul_group_dev", _I, [_P, _I, C.POINTER(_P), _I, _P, C.POINTER(_P), C.POINTER(_P), _I]),
     ("bgl_matmul_group_noalloc_dev", _I, [_P, _I, C.POINTER(_P), _I, _P, C.POINTER(_P), C.POINTER(_P), _I]),
+    ("bgl_read_probe_dev", _I, [_P, _I, C.POINTER(_P), _I, _I]),
     ("bgl_prep_act_dev", _I, [_P, _I, _I, _P, _I, _I]),
     ("bgl_matmul_prepped_dev", _I, [_P, _P, _I, _P, _P, _I]),
     ("bgl_quant_act_i8_dev", _I, [_P, _P, _I, _I, _I, _P, _P]),

@@ -916,6 +916,61 @@ extern "C" int bgl_matmul_dev(bgl_ctx *c, const bgl_tensor *w, int act, const fl
     return bgl_matmul_group_dev(c, 1, &w, act, x_dev, b, y, M);
 }
 
+// ------------------------------------------------------------------ streaming-read probe
+// A plain read of bound tensors' device bytes (chunks, scales, biases): the memory system's floor
+// for the bytes a GEMV launch streams, measured beside it.  Grid-stride 16-byte loads, four in
+// flight per thread; the xor of everything read is kept alive by an empty asm statement.
+typedef unsigned int rp_u32x4 __attribute__((ext_vector_type(4)));
+struct ReadSeg {
+    const uint8_t *p;
+    uint64_t n16;                       // 16-byte words
+};
+struct ReadProbe {
+    ReadSeg s[3 * BGL_MAX_TASKS];
+    int nseg;
+};
+__global__ __launch_bounds__(1024) void k_read_probe(ReadProbe P) {
+    const uint64_t nt = (uint64_t)gridDim.x * blockDim.x, tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (int k = 0; k < P.nseg; k++) {
+        const __attribute__((address_space(1))) rp_u32x4 *q = (const __attribute__((address_space(1))) rp_u32x4 *)P.s[k].p;
+        const uint64_t n = P.s[k].n16;
+        uint64_t i = tid;
+        for (; i + 3 * nt < n; i += 4 * nt) {
+            const rp_u32x4 a = q[i], b = q[i + nt], c = q[i + 2 * nt], d = q[i + 3 * nt];
+            acc ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^ (d.x ^ d.y ^ d.z ^ d.w);
+        }
+        for (; i < n; i += nt) {
+            const rp_u32x4 a = q[i];
+            acc ^= a.x ^ a.y ^ a.z ^ a.w;
+        }
+    }
+    asm volatile("" ::"v"(acc));
+}
+
+extern "C" int bgl_read_probe_dev(bgl_ctx *c, int n, const bgl_tensor *const *w, int nblocks, int nthreads) {
+    if (!c || n < 1 || n > BGL_MAX_TASKS || !w) return bgl_fail(BGL_E_ARG, "bgl_read_probe_dev: bad argument");
+    if (nblocks <= 0) nblocks = 1024;
+    if (nthreads <= 0) nthreads = 256;
+    if (nthreads > 1024 || nthreads % 64) return bgl_fail(BGL_E_ARG, "bgl_read_probe_dev: nthreads %d", nthreads);
+    ReadProbe P;
+    memset(&P, 0, sizeof P);
+    for (int i = 0; i < n; i++) {
+        if (!w[i] || !w[i]->experts.empty()) return bgl_fail(BGL_E_ARG, "bgl_read_probe_dev: tensor %d invalid", i);
+        const BglDevTensor &T = w[i]->T;
+        BglDevTensor L;
+        size_t b[3];
+        device_layout(T.fmt, T.bits, T.N, T.K, L, b);
+        const void *ptr[3] = {T.w, T.s0, T.s1};
+        for (int k = 0; k < 3; k++)
+            if (b[k] && ptr[k]) P.s[P.nseg++] = ReadSeg{(const uint8_t *)ptr[k], (uint64_t)(b[k] / 16)};
+    }
+    HIPCHK(hipSetDevice(c->device));
+    hipLaunchKernelGGL(k_read_probe, dim3(nblocks), dim3(nthreads), 0, c->stream, P);
+    HIPCHK(hipGetLastError());
+    return 0;
+}
+
 // ------------------------------------------------------------------ host-pointer drop-ins
 // The device copy of a host weight, bound on first use and cached by its packed pointer.
 static int host_tensor(bgl_ctx *c, const bgl_wt &wt, bgl_tensor **res) {

@@ -35,6 +35,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "quantized GEMV / MoE-gather achieved HBM GB/s (% of peak) + µs per call at M=1"
+# the arithmetic each path computes in
+DT_W4A8 = "int8 (W4A8: int4 codes x int8 activations, exact int32 dot4 sums, fp32 fold)"
+DT_F32ACT = "fp32 activations as exact integer digits (int32 dot4 sums over int8 digits, fp32 fold)"
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 
@@ -52,12 +55,23 @@ def alg_bytes(kind, out, inn, bits, M):
     return w + 4 * M * inn + 4 * M * out
 
 
-def host_threads():
+def host_nproc():
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except Exception:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return os.cpu_count() or 1
+
+
+# The GPU box allots 16 host cores to a one-GPU job (its worker pools are to be sized to that
+# share, whatever nproc shows); the CPU leg uses all of them and records nproc beside.
+HOST_SHARE = 16
+
+
+def host_threads():
+    return max(1, min(HOST_SHARE, host_nproc()))
+
+
+ROTATE_BYTES = 512 << 20       # CPU legs cycle through weight copies of at least this footprint (2x the MALL)
 
 
 # ------------------------------------------------------------------------------------- GPU side
@@ -283,6 +297,27 @@ def time_graph(torch, stream, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps, wall, g
 
 
+def plain_read(ctx, torch, stream, wl, steps):
+    """The same step with every call replaced by a plain streaming read of exactly its tensors'
+    device bytes (bgl_read_probe_dev, 1024 workgroups x 256 threads, 16-byte loads), graph-timed
+    the same way: the memory system's floor for this sequence of launches."""
+    def reads():
+        for group, *_ in wl.calls:
+            ctx.read_probe(group)
+    ms, _, _ = time_graph(torch, stream, reads, steps, 3)
+    return ms
+
+
+def kernel_sources_sha16():
+    """Hash of the GEMV kernel sources: a committed counter reading is used only while it matches."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in ("bgl_gemv.hip", "bgl_gemv_impl.h", "bgl_device.h", "bgl_kernels.h"):
+        with open(os.path.join(ROOT, "beglin_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def time_prep(ctx, torch, stream, wl, steps, tags):
     """Graph-timed activation-prep kernels alone (one per call of the given call types: the ones
     whose path launches a prep kernel)."""
@@ -397,25 +432,30 @@ def cpu_baseline_cfg5(M, budget_s, seed):
     el = time.perf_counter() - t0
     dt = el / cols * M                                    # one layer at M columns
     orc.lib.or_pool_destroy(pool)
-    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": T, "kind": "port",
+    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": T, "host_nproc": host_nproc(), "kind": "port",
             "us_per_layer": round(dt * 1e6, 1),
             "sample": f"one Llama-3.1-8B layer (7 tensors, same precision map), {cols} of {M} columns timed "
                       f"({el:.1f} s) and scaled to {M}, per column through the row-block pool, {T} threads"}
 
 
 def cpu_baseline_cfg4(wl, budget_s, seed):
-    """moe_ffn_batched's portable C restatement (router scores, routing and or_moe_ffn_bucketed,
-    one thread) on layer 0's router and formats, for min(T, 2) tokens; only the experts those tokens
-    touch are quantized (the others are never read)."""
+    """moe_ffn_batched's portable C restatement (router scores, routing and the bucketed FFN with
+    every expert matvec's rows split over the row-block pool, moe_matvec_af_mt) on layer 0's router
+    and formats, for min(T, 8) tokens; only the experts those tokens touch are quantized (the others
+    are never read)."""
+    import ctypes as C
+
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from oracle_ffi import Oracle, moe_ffn
+    from oracle_ffi import Oracle, expert_array
     orc = Oracle()
     rng = np.random.default_rng(seed + 1)
     E, H, I, K, Ish = (DSV2[k] for k in ("E", "H", "I", "K", "Ish"))
     fm, shf = wl.formats[0]
     rw = wl.layers[0][7].cpu().numpy()
-    T = min(wl.T, 2)
+    T = min(wl.T, 8)
+    NT = host_threads()
+    pool = orc.lib.or_pool_create(NT, 1)
     x = rng.standard_normal((T, H), dtype=np.float32)
     idx, w = orc.route(orc.router_logits(rw, x), K)
     touched = sorted(set(idx.flatten().tolist()))
@@ -440,21 +480,26 @@ def cpu_baseline_cfg4(wl, budget_s, seed):
         nb += 2 * wbytes(k, I, H, b) + wbytes(k, H, I, b)
     shared = (q(shf[0], shf[1], Ish, H), q(shf[0], shf[1], Ish, H), q(shf[0], shf[1], H, Ish))
     nb += 2 * wbytes(shf[0], Ish, H, shf[1]) + wbytes(shf[0], H, Ish, shf[1]) + 4 * E * H + 2 * 4 * T * H
+    (ga, gk), (ua, uk), (da, dk), (sa, sk) = expert_array(gate), expert_array(up), expert_array(down), expert_array(list(shared))
+    out = np.zeros((T, H), np.float32)
+    P = lambda a: C.c_void_p(a.ctypes.data)
     t0 = time.perf_counter()
     reps = 0
     while True:
         idx, w = orc.route(orc.router_logits(rw, x), K)
-        moe_ffn(orc, gate, up, down, shared, H, I, x, idx, w)
+        z = C.sizeof(sa[0])
+        orc.lib.or_pool_moe_ffn_bucketed(C.c_void_p(pool), ga, ua, da, E, C.byref(sa, 0), C.byref(sa, z), C.byref(sa, 2 * z),
+                                         H, I, Ish, T, K, P(x), P(idx), P(w), P(out))
         reps += 1
         if time.perf_counter() - t0 >= budget_s or reps >= 1000:
             break
     dt = (time.perf_counter() - t0) / reps
-    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+    orc.lib.or_pool_destroy(pool)
+    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": NT, "host_nproc": host_nproc(), "kind": "port",
             "us_per_layer": round(dt * 1e6, 1),
             "sample": f"layer 0, {T} token(s), router + {len(touched)} experts touched + shared ({nb / 1e6:.1f} MB), "
-                      f"or_moe_router_logits + or_moe_route + or_moe_ffn_bucketed single-threaded, {reps} calls over "
-                      f"{dt * reps:.1f} s"}
-
+                      f"or_moe_router_logits + or_moe_route + or_pool_moe_ffn_bucketed (rows over {NT} threads), "
+                      f"{reps} calls over {dt * reps:.1f} s"}
 
 
 def cpu_baseline_cfg2(M, budget_s, layers=2, seed=7):
@@ -469,15 +514,21 @@ def cpu_baseline_cfg2(M, budget_s, layers=2, seed=7):
     rng = np.random.default_rng(seed)
     T = host_threads()
     pool = orc.lib.or_pool_create(T, 8960)
-    mats = []
-    nbytes = 0
+    one, lb = [], 0
+    for _, shapes in qwen_layer_shapes():
+        for out, inn in shapes:
+            w = (rng.standard_normal((out, inn), dtype=np.float32) * np.float32(0.02))
+            pk, ws, sub = orc.quantize_g256sf(w)
+            one.append((pk, ws, sub, out, inn))
+            lb += alg_bytes(3, out, inn, 4, 1)
+    # distinct copies of one quantized layer until the footprint passes ROTATE_BYTES, so every pass
+    # streams its weights from memory rather than the host caches
+    layers = max(layers, -(-ROTATE_BYTES // int(lb)))
+    mats, nbytes = [], 0
     for _ in range(layers):
-        for _, shapes in qwen_layer_shapes():
-            for out, inn in shapes:
-                w = (rng.standard_normal((out, inn), dtype=np.float32) * np.float32(0.02))
-                pk, ws, sub = orc.quantize_g256sf(w)
-                mats.append((pk, ws, sub, out, inn, np.zeros(out, np.float32)))
-                nbytes += alg_bytes(3, out, inn, 4, 1)
+        for pk, ws, sub, out, inn in one:
+            mats.append((pk.copy(), ws.copy(), sub.copy(), out, inn, np.zeros(out, np.float32)))
+        nbytes += lb
     xs = {k: rng.standard_normal(k, dtype=np.float32) for k in (1536, 8960)}
     P = lambda a: C.c_void_p(a.ctypes.data)
 
@@ -495,10 +546,10 @@ def cpu_baseline_cfg2(M, budget_s, layers=2, seed=7):
             break
     dt = (time.perf_counter() - t0) / reps
     orc.lib.or_pool_destroy(pool)
-    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": T, "kind": "port",
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": T, "host_nproc": host_nproc(), "kind": "port",
             "us_per_layer": round(dt / layers * 1e6, 1),
-            "sample": f"{layers} Qwen2.5-1.5B layers of q4g256sf (7 projections each, {nbytes / 1e6:.1f} MB), "
-                      f"M=1 W4A8, {reps} passes over {dt * reps:.1f} s, {T} threads"}
+            "sample": f"{layers} copies of one Qwen2.5-1.5B layer of q4g256sf (7 projections each, {nbytes / 1e6:.1f} MB "
+                      f"rotated), M=1 W4A8, {reps} passes over {dt * reps:.1f} s, {T} threads (the box's 16-core share)"}
 
 
 def cpu_baseline_rotated(kind, bits, out, inn, budget_s, seed=7):
@@ -520,17 +571,21 @@ def cpu_baseline_rotated(kind, bits, out, inn, budget_s, seed=7):
     y = np.zeros(out, np.float32)
     P = lambda a: C.c_void_p(a.ctypes.data)
     nb = alg_bytes(kind, out, inn, bits, 1)
+    ncopy = max(1, -(-ROTATE_BYTES // int(nb)))               # distinct copies: >= ROTATE_BYTES in all
+    copies = [(pk.copy(), sc.copy()) for _ in range(ncopy)]
     orc.lib.or_pool_gemv_f32(pool, kind, bits, P(pk), P(sc), P(x), None, P(y), out, inn)
     t0 = time.perf_counter()
     reps = 0
-    while time.perf_counter() - t0 < budget_s and reps < 1000:
-        orc.lib.or_pool_gemv_f32(pool, kind, bits, P(pk), P(sc), P(x), None, P(y), out, inn)
+    while time.perf_counter() - t0 < budget_s and reps < 100000:
+        cpk, csc = copies[reps % ncopy]
+        orc.lib.or_pool_gemv_f32(pool, kind, bits, P(cpk), P(csc), P(x), None, P(y), out, inn)
         reps += 1
     dt = (time.perf_counter() - t0) / reps
     orc.lib.or_pool_destroy(pool)
-    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": T, "kind": "port",
+    return {"value": round(nb / dt / 1e9, 3), "unit": "GB/s", "cores": T, "host_nproc": host_nproc(), "kind": "port",
             "us_per_call": round(dt * 1e6, 1),
-            "sample": f"one {out}x{inn} tensor (kind {kind}, n={bits}), {reps} calls over {dt * reps:.1f} s, {T} threads"}
+            "sample": f"{ncopy} rotated copies of one {out}x{inn} tensor (kind {kind}, n={bits}; {ncopy * nb / 1e6:.0f} MB), "
+                      f"{reps} calls over {dt * reps:.1f} s, {T} threads (the box's 16-core share)"}
 
 
 def copy_calib(mib):
@@ -603,14 +658,14 @@ def main():
             wl = build_cfg2(ctx, torch, M, args.layers, args.seed)
         torch.cuda.synchronize()
         workload = f"cfg2: Qwen2.5-1.5B decode layer x{args.layers}, q4g256sf W4A8 GEMV, 7 projections (fused qkv, o, fused gate+up, down), M={M}"
-        dtype = "int8"
+        dtype = DT_W4A8
         cfg = {"workload": workload, "layers": args.layers, "M": M, "format": "q4g256sf", "activations": "W4A8 (int8, group 256)",
                "calls_per_step": wl.ncalls(), "weight_bytes_per_step": int(wl.nbytes()), "seed": args.seed}
     elif args.workload == "cfg1":
         with torch.cuda.stream(stream):
             wl = build_rotated(ctx, torch, 5, 4, 8960, 1536, M, args.seed, beglin_amd.ACT_F32)
         workload = f"cfg1: int4 g32 fp16-scale GEMV K=1536 N=8960, fp32 activations, M={M}, {wl.ncalls()} rotated copies"
-        dtype = "int8"
+        dtype = DT_F32ACT
         cfg = {"workload": workload, "M": M, "format": "q4g32h", "copies": wl.ncalls(), "seed": args.seed}
     elif args.workload == "cfg4":
         with torch.cuda.stream(stream):
@@ -618,7 +673,7 @@ def main():
         touched = [l[6] for l in wl.layers]
         workload = (f"cfg4: DeepSeek-V2-Lite routed MoE layer x{args.layers} (router + top-6 + experts + shared on "
                     f"the device), E=64+2 shared, hidden 2048, inter 1408, T={M}, per-expert precision from the seed")
-        dtype = "int8"
+        dtype = DT_F32ACT
         cfg = {"workload": workload, "T": M, "layers": args.layers, "experts_touched_per_layer": touched,
                "formats": "q4g32h | q8g64 | qNg64 n=7..15 per expert (fp32 activations)", "seed": args.seed,
                "bytes_per_step": int(wl.nbytes())}
@@ -627,7 +682,7 @@ def main():
         with torch.cuda.stream(stream):
             wl = build_rotated(ctx, torch, 4, args.bits, out, inn, M, args.seed, beglin_amd.ACT_F32)
         workload = f"cfg3: qNg64 n={args.bits} GEMV {out}x{inn} (Llama-3.1-8B MLP {args.shape}), fp32 activations, M={M}, {wl.ncalls()} rotated copies"
-        dtype = "int8"
+        dtype = DT_F32ACT
         cfg = {"workload": workload, "M": M, "format": f"qNg64 n={args.bits}", "copies": wl.ncalls(), "seed": args.seed}
     torch.cuda.synchronize()
 
@@ -639,6 +694,10 @@ def main():
     if args.workload == "cfg5":
         per_call = {"layer": {"us": round(step_ms * 1e3 / args.layers, 2), "GB/s": round(value, 1)}}
         roof = mfma_roofline(ctx, torch, stream, wl, M, max(3, args.steps // 10))
+        pr_ms = plain_read(ctx, torch, stream, wl, max(5, args.steps // 5))
+        roof["plain_read"] = {"us_per_step": round(pr_ms * 1e3, 2), "GB/s": round(wl.nbytes() / (pr_ms * 1e-3) / 1e9, 1),
+                              "step_over_plain": round(step_ms / pr_ms, 3),
+                              "how": "bgl_read_probe_dev over each call's tensors, 1024 x 256 threads, graph-timed"}
         cpu = None if args.no_cpu else cpu_baseline_cfg5(M, args.cpu_seconds, args.seed)
         finish(args, wl, ctx, graph, value, step_ms, wall, dtype, cfg, per_call, roof, cpu)
         return
@@ -688,14 +747,24 @@ def main():
             "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3), "prep_call_types": prep_tags,
             "bytes_per_launch": round(nbytes / launches)}
 
+    # the plain-read floor for the same bytes and launch count, measured in this run
+    pr_ms = plain_read(ctx, torch, stream, wl, max(5, args.steps // 5))
+    roof["plain_read"] = {"us_per_step": round(pr_ms * 1e3, 2), "us_per_launch": round(pr_ms * 1e3 / launches, 3),
+                          "GB/s": round(nbytes / (pr_ms * 1e-3) / 1e9, 1), "step_over_plain": round(step_ms / pr_ms, 3),
+                          "how": "bgl_read_probe_dev over each call's tensors, 1024 x 256 threads, graph-timed"}
+
     # HBM traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this
-    # same workload, scaled by a known-size copy (profiles/traffic.json)
+    # same workload, scaled by a known-size copy (profiles/traffic.json) -- only while the kernel
+    # sources it was measured on are the current ones
     if args.workload == "cfg2" and M == 1 and args.layers == 28:
         try:
             tr = json.load(open(os.path.join(ROOT, "profiles", "traffic.json")))["cfg2_M1"]
-            roof["traffic"] = tr["traffic_bytes_per_launch"]
-            roof["traffic_over_algorithmic"] = round(tr["traffic_bytes_per_launch"] / (nbytes / launches), 3)
-            roof["traffic_source"] = tr["summary"]
+            if tr.get("kernel_sources_sha16") == kernel_sources_sha16():
+                roof["traffic"] = tr["traffic_bytes_per_launch"]
+                roof["traffic_over_algorithmic"] = round(tr["traffic_bytes_per_launch"] / (nbytes / launches), 3)
+                roof["traffic_source"] = tr["summary"]
+            else:
+                roof["traffic_note"] = "profiles/traffic.json was measured on other kernel sources: not used"
         except (OSError, KeyError, ValueError):
             pass
 

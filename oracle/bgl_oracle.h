@@ -124,6 +124,10 @@ void or_pool_gemv_q4g64_sdot(or_pool *p, const uint8_t *packed, const float *sca
                              const float *x, const float *bias, float *y, int out, int in);
 void or_pool_gemv_f32(or_pool *p, int kind, int bits, const void *packed, const void *scales,
                       const float *x, const float *bias, float *y, int out, int in);
+void or_pool_moe_ffn_bucketed(or_pool *p, const or_expert *gate, const or_expert *up, const or_expert *down, int E,
+                              const or_expert *sh_gate, const or_expert *sh_up, const or_expert *sh_down,
+                              int H, int I, int Ish, int T, int K, const float *x,
+                              const int *top_idx, const float *top_w, float *out);
 
 #ifdef __cplusplus
 }

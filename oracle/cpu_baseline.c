@@ -22,7 +22,9 @@ typedef struct {
     int kind, bits, out, in;
     const void *packed, *scales; const uint8_t *sub;
     const int8_t *xq; const float *ascale; const float *x; const float *bias; float *y;
+    const or_expert *ex;      /* kind JOB_MOE: one expert matrix (moe_matvec_af_row per row) */
 } job_t;
+#define JOB_MOE (-1)
 
 struct or_pool {
     int nthreads, max_in;
@@ -83,6 +85,10 @@ static void run_range(or_pool *p, int wi) {
     if (r1 > j->out) r1 = j->out;
     if (r0 >= r1) return;
     int in = j->in;
+    if (j->kind == JOB_MOE) {
+        for (int r = r0; r < r1; r++) j->y[r] = (float)or_moe_row(j->ex, in, r, j->x);
+        return;
+    }
     for (int r = r0; r < r1; r++) {
         float b = j->bias ? j->bias[r] : 0.0f, dot;
         if (j->kind == 3)
@@ -173,7 +179,7 @@ static void go_and_wait(or_pool *p) {
 void or_pool_gemv_g256sf_sdot(or_pool *p, const uint8_t *packed, const float *wsuper, const uint8_t *sub,
                               const float *x, const float *bias, float *y, int out, int in) {
     or_quant_act_i8(x, in, 256, p->xq, p->ascale);
-    job_t j = {3, 0, out, in, packed, wsuper, sub, p->xq, p->ascale, x, bias, y};
+    job_t j = {3, 0, out, in, packed, wsuper, sub, p->xq, p->ascale, x, bias, y, NULL};
     p->job = j;
     go_and_wait(p);
 }
@@ -182,7 +188,7 @@ void or_pool_gemv_g256sf_sdot(or_pool *p, const uint8_t *packed, const float *ws
 void or_pool_gemv_q4g64_sdot(or_pool *p, const uint8_t *packed, const float *scales,
                              const float *x, const float *bias, float *y, int out, int in) {
     or_quant_act_i8(x, in, 64, p->xq, p->ascale);
-    job_t j = {1, 0, out, in, packed, scales, NULL, p->xq, p->ascale, x, bias, y};
+    job_t j = {1, 0, out, in, packed, scales, NULL, p->xq, p->ascale, x, bias, y, NULL};
     p->job = j;
     go_and_wait(p);
 }
@@ -190,7 +196,57 @@ void or_pool_gemv_q4g64_sdot(or_pool *p, const uint8_t *packed, const float *sca
 /* gemv_q4g64_mt / gemv_q8g64_mt / qng64_matvec_f32 fp32-activation rows through the pool. */
 void or_pool_gemv_f32(or_pool *p, int kind, int bits, const void *packed, const void *scales,
                       const float *x, const float *bias, float *y, int out, int in) {
-    job_t j = {kind, bits, out, in, packed, scales, NULL, NULL, NULL, x, bias, y};
+    job_t j = {kind, bits, out, in, packed, scales, NULL, NULL, NULL, x, bias, y, NULL};
     p->job = j;
     go_and_wait(p);
+}
+
+/* moe_matvec_af_mt (qwen_infer.c:3223-3457): one expert matvec, its rows in contiguous blocks over
+ * the pool, each row the double-accumulated moe_matvec_af_row. */
+static void pool_moe_matvec(or_pool *p, const or_expert *w, int out, int in, const float *x, float *y) {
+    job_t j;
+    memset(&j, 0, sizeof j);
+    j.kind = JOB_MOE; j.out = out; j.in = in; j.x = x; j.y = y; j.ex = w;
+    p->job = j;
+    go_and_wait(p);
+}
+
+/* moe_ffn_batched (qwen_infer.c:5238-5350) with routing supplied, every expert matvec through the
+ * pool: or_moe_ffn_bucketed's order (experts ascending, members in token order, then the shared
+ * experts), so the outputs are bit-identical to it. */
+void or_pool_moe_ffn_bucketed(or_pool *p, const or_expert *gate, const or_expert *up, const or_expert *down, int E,
+                              const or_expert *sh_gate, const or_expert *sh_up, const or_expert *sh_down,
+                              int H, int I, int Ish, int T, int K, const float *x,
+                              const int *top_idx, const float *top_w, float *out) {
+    int *cnt = (int *)calloc((size_t)E, sizeof(int));
+    int *mtok = (int *)malloc(sizeof(int) * (size_t)E * T);
+    float *mw = (float *)malloc(sizeof(float) * (size_t)E * T);
+    for (int b = 0; b < T; b++)
+        for (int k = 0; k < K; k++) {
+            int e = top_idx[(size_t)b * K + k];
+            mtok[(size_t)e * T + cnt[e]] = b; mw[(size_t)e * T + cnt[e]] = top_w[(size_t)b * K + k]; cnt[e]++;
+        }
+    for (size_t i = 0; i < (size_t)T * H; i++) out[i] = 0.0f;
+    int Imax = I > Ish ? I : Ish;
+    float *g = (float *)malloc(sizeof(float) * (size_t)Imax), *u = (float *)malloc(sizeof(float) * (size_t)Imax);
+    float *d = (float *)malloc(sizeof(float) * (size_t)H);
+    for (int e = 0; e < E; e++)
+        for (int m = 0; m < cnt[e]; m++) {
+            int b = mtok[(size_t)e * T + m];
+            float wgt = mw[(size_t)e * T + m];
+            pool_moe_matvec(p, &gate[e], I, H, x + (size_t)b * H, g);
+            pool_moe_matvec(p, &up[e], I, H, x + (size_t)b * H, u);
+            or_moe_swiglu_inplace(g, u, I);
+            pool_moe_matvec(p, &down[e], H, I, g, d);
+            for (int c = 0; c < H; c++) out[(size_t)b * H + c] += wgt * d[c];
+        }
+    if (sh_gate && sh_up && sh_down)
+        for (int b = 0; b < T; b++) {
+            pool_moe_matvec(p, sh_gate, Ish, H, x + (size_t)b * H, g);
+            pool_moe_matvec(p, sh_up, Ish, H, x + (size_t)b * H, u);
+            or_moe_swiglu_inplace(g, u, Ish);
+            pool_moe_matvec(p, sh_down, H, Ish, g, d);
+            for (int c = 0; c < H; c++) out[(size_t)b * H + c] += d[c];
+        }
+    free(cnt); free(mtok); free(mw); free(g); free(u); free(d);
 }

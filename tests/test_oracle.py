@@ -618,3 +618,31 @@ def test_moe_decode_dense_and_affine_fixed_points(oracle):
         af = moe_decode(oracle, aff, out, inn, r, range(inn))
         tol = np.repeat(s1[r], 64) * np.float32(2 ** -20)
         assert np.all(np.abs(af - sym) <= tol)
+
+
+def test_pool_moe_ffn_equals_bucketed(oracle):
+    """The CPU baseline's threaded MoE FFN (rows of every expert matvec over the pool) gives the
+    single-threaded bucketed FFN's outputs bit for bit (each row is one thread's sequential sum)."""
+    import ctypes as C
+    from oracle_ffi import _ptr, expert_array, moe_ffn
+    E, H, I, Ish, T, K = 6, 128, 64, 96, 5, 2
+    rng = np.random.default_rng(700)
+    def d(kind, o, i, s):
+        w = seeded_normal(s, (o, i), 0.02)
+        p, sc = oracle.quantize_q4g32h(w) if kind == 5 else oracle.quantize_qng64(w, 7)
+        return (kind, 4 if kind == 5 else 7, p, sc)
+    gate = [d(5 if e % 2 else 4, I, H, 710 + e) for e in range(E)]
+    up = [d(5 if e % 2 else 4, I, H, 720 + e) for e in range(E)]
+    down = [d(5 if e % 2 else 4, H, I, 730 + e) for e in range(E)]
+    shared = (d(5, Ish, H, 740), d(5, Ish, H, 741), d(5, H, Ish, 742))
+    x = seeded_normal(750, (T, H))
+    idx, w = oracle.route(seeded_normal(751, (T, E)), K)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    (ga, k1), (ua, k2), (da, k3), (sa, k4) = expert_array(gate), expert_array(up), expert_array(down), expert_array(list(shared))
+    out = np.zeros((T, H), np.float32)
+    pool = oracle.lib.or_pool_create(3, 1)
+    z = C.sizeof(sa[0])
+    oracle.lib.or_pool_moe_ffn_bucketed(C.c_void_p(pool), ga, ua, da, E, C.byref(sa, 0), C.byref(sa, z), C.byref(sa, 2 * z),
+                                        H, I, Ish, T, K, _ptr(x), _ptr(idx), _ptr(w), _ptr(out))
+    oracle.lib.or_pool_destroy(pool)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
