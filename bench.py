@@ -308,14 +308,47 @@ def plain_read(ctx, torch, stream, wl, steps):
     return ms
 
 
-def kernel_sources_sha16():
-    """Hash of the GEMV kernel sources: a committed counter reading is used only while it matches."""
+# The kernel sources behind each workload's dominant kernel (its file and the headers it includes).
+KERNEL_SOURCES = {
+    "cfg2": ("bgl_gemv.hip", "bgl_gemv_impl.h", "bgl_device.h", "bgl_kernels.h"),
+    "cfg1": ("bgl_gemv_x.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_device.h", "bgl_kernels.h"),
+    "cfg3": ("bgl_gemv_x.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_device.h", "bgl_kernels.h"),
+    "cfg4": ("bgl_moe_x.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_device.h", "bgl_kernels.h"),
+    "cfg5": ("bgl_mfma.hip", "bgl_device.h", "bgl_kernels.h"),
+}
+
+
+def kernel_sources_sha16(workload="cfg2"):
+    """Hash of a workload's kernel sources: a committed counter reading is used only while it matches."""
     import hashlib
     h = hashlib.sha256()
-    for f in ("bgl_gemv.hip", "bgl_gemv_impl.h", "bgl_device.h", "bgl_kernels.h"):
+    for f in KERNEL_SOURCES[workload]:
         with open(os.path.join(ROOT, "beglin_amd", "csrc", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()[:16]
+
+
+def traffic_key(args):
+    """The profiles/traffic.json entry measured on exactly this bench configuration."""
+    base = {"cfg3": f"cfg3_{args.shape}_n{args.bits}"}.get(args.workload, args.workload)
+    return f"{base}_M{args.M}_L{args.layers}" if args.workload in ("cfg2", "cfg4", "cfg5") else f"{base}_M{args.M}"
+
+
+def attach_traffic(roof, args, alg_per_launch):
+    """HBM traffic per launch of the dominant kernel from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes over this same configuration, scaled by a known-size copy -- used only while
+    the kernel sources it was measured on are the current ones."""
+    try:
+        tr = json.load(open(os.path.join(ROOT, "profiles", "traffic.json")))[traffic_key(args)]
+    except (OSError, KeyError, ValueError):
+        roof["traffic_note"] = f"no committed counter reading for {traffic_key(args)}"
+        return
+    if tr.get("kernel_sources_sha16") != kernel_sources_sha16(args.workload):
+        roof["traffic_note"] = "profiles/traffic.json was measured on other kernel sources: not used"
+        return
+    roof["traffic"] = tr["traffic_bytes_per_launch"]
+    roof["traffic_over_algorithmic"] = round(tr["traffic_bytes_per_launch"] / alg_per_launch, 3)
+    roof["traffic_source"] = tr["summary"]
 
 
 def time_prep(ctx, torch, stream, wl, steps, tags):
@@ -620,6 +653,9 @@ def main():
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB 5 times (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes) and exit")
+    ap.add_argument("--counter-steps", type=int, default=0, metavar="N",
+                    help="only build the workload and launch exactly N eager steps, no timing (a rocprofv3 --pmc "
+                         "pass over it then holds N steps' dispatches of the path's kernels and nothing else)")
     args = ap.parse_args()
     if args.copy_calib:
         copy_calib(args.copy_calib)
@@ -686,6 +722,15 @@ def main():
         cfg = {"workload": workload, "M": M, "format": f"qNg64 n={args.bits}", "copies": wl.ncalls(), "seed": args.seed}
     torch.cuda.synchronize()
 
+    if args.counter_steps:
+        with torch.cuda.stream(stream):
+            for _ in range(args.counter_steps):
+                wl.run()
+        torch.cuda.synchronize()
+        print(json.dumps({"counter_steps": args.counter_steps, "config": cfg, "calls_per_step": wl.ncalls(),
+                          "bytes_per_step": int(wl.nbytes())}), flush=True)
+        return
+
     step_ms, wall, graph = time_graph(torch, stream, wl.run, args.steps, args.warmup)
     nbytes = wl.nbytes()
     value = nbytes / (step_ms * 1e-3) / 1e9
@@ -694,6 +739,7 @@ def main():
     if args.workload == "cfg5":
         per_call = {"layer": {"us": round(step_ms * 1e3 / args.layers, 2), "GB/s": round(value, 1)}}
         roof = mfma_roofline(ctx, torch, stream, wl, M, max(3, args.steps // 10))
+        attach_traffic(roof, args, roof["bytes_per_launch"])
         pr_ms = plain_read(ctx, torch, stream, wl, max(5, args.steps // 5))
         roof["plain_read"] = {"us_per_step": round(pr_ms * 1e3, 2), "GB/s": round(wl.nbytes() / (pr_ms * 1e-3) / 1e9, 1),
                               "step_over_plain": round(step_ms / pr_ms, 3),
@@ -704,6 +750,7 @@ def main():
     if args.workload == "cfg4":
         per_call = {"moe_layer": {"us": round(step_ms * 1e3 / args.layers, 2), "GB/s": round(value, 1)}}
         roof = moe_roofline(ctx, torch, stream, wl, max(3, args.steps // 10))
+        attach_traffic(roof, args, roof["bytes_per_launch"])
         cpu = None if args.no_cpu else cpu_baseline_cfg4(wl, args.cpu_seconds, args.seed)
         finish(args, wl, ctx, graph, value, step_ms, wall, dtype, cfg, per_call, roof, cpu)
         return
@@ -753,20 +800,7 @@ def main():
                           "GB/s": round(nbytes / (pr_ms * 1e-3) / 1e9, 1), "step_over_plain": round(step_ms / pr_ms, 3),
                           "how": "bgl_read_probe_dev over each call's tensors, 1024 x 256 threads, graph-timed"}
 
-    # HBM traffic per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes over this
-    # same workload, scaled by a known-size copy (profiles/traffic.json) -- only while the kernel
-    # sources it was measured on are the current ones
-    if args.workload == "cfg2" and M == 1 and args.layers == 28:
-        try:
-            tr = json.load(open(os.path.join(ROOT, "profiles", "traffic.json")))["cfg2_M1"]
-            if tr.get("kernel_sources_sha16") == kernel_sources_sha16():
-                roof["traffic"] = tr["traffic_bytes_per_launch"]
-                roof["traffic_over_algorithmic"] = round(tr["traffic_bytes_per_launch"] / (nbytes / launches), 3)
-                roof["traffic_source"] = tr["summary"]
-            else:
-                roof["traffic_note"] = "profiles/traffic.json was measured on other kernel sources: not used"
-        except (OSError, KeyError, ValueError):
-            pass
+    attach_traffic(roof, args, nbytes / launches)
 
     cpu = None
     if not args.no_cpu:
