@@ -167,6 +167,9 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     c->x_fuse = xf ? (atoi(xf) != 0) : -1;
     const char *mm = getenv("BGL_MOE_MERGE");
     c->moe_merge = mm ? (atoi(mm) != 0) : -1;
+    const char *mcap = getenv("BGL_MOE_CAP");
+    c->moe_cap = mcap ? atoi(mcap) : 0;
+    if (c->moe_cap != 4 && c->moe_cap != 8) c->moe_cap = 0;
     *out = c;
     return 0;
 }

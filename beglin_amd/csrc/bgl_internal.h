@@ -36,6 +36,7 @@ struct bgl_ctx {
     bool no_moe_x = false;                // BGL_NO_MOE_X=1: MoE gathers through the prep kernel + k_moe_gemv
     int x_fuse = -1;                      // BGL_X_FUSE: 0 never / 1 always make the digits inside k_gemv_x; -1 by K
     int moe_merge = -1;                   // BGL_MOE_MERGE: 0 never / 1 always run the routed and shared gate+up in one launch; -1 by shape
+    int moe_cap = 0;                      // BGL_MOE_CAP: 4 / 8 token columns of records per k_moe_x chunk; 0 by LDS fit (tuning)
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
     int prep_act = -1, prep_gq = 0, prep_M = 0, prep_K = 0;   // what act_* currently hold
     const float *prep_x = nullptr;        // the raw fp32 columns they were made from (non-finite slow path)

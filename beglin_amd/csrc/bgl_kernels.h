@@ -188,6 +188,7 @@ struct MoeTask {
     const int *cpos;
     const int32_t *cidx;
     int ck;
+    int mbx;                     // k_moe_x: token columns of records the launch's LDS holds (4 or 8)
 };
 
 // ---- kernels (bgl_prep.hip) ----
@@ -221,13 +222,14 @@ int bgl_launch_gemv_x(const GemvLaunch &L, bool fuse, int nblocks, int TR, int n
 size_t bgl_gemv_x_lds(int K, int TR, int nw, bool fuse);
 // ---- bgl_moe_x.hip: the MoE gather over records made in the kernel ----
 bool bgl_moe_x_fmt(int fmt);
-size_t bgl_moe_x_lds(int K, int nw, int TR);
+size_t bgl_moe_x_lds(int K, int nw, int TR, int cap);
+int bgl_moe_x_cap(int K, int nw, int TR);
 void bgl_moe_x_shape(int K, long active_wgs, int tr_force, int nw_cap, int *TR, int *nw);
-int bgl_launch_moe_x(const MoeTask &Mt, int K, int TR, int nw, hipStream_t st);
+int bgl_launch_moe_x(const MoeTask &Mt, int K, int TR, int nw, int cap, hipStream_t st);
 // Two gathers over the same activation rows in one launch (workgroups [0, nb0) run t[0], the rest
 // t[1]); whole 64-row tiles; t[1] may be segmented (seg > 0 without off).
 struct MoePair {
     MoeTask t[2];
     int nb0;
 };
-int bgl_launch_moe_x2(const MoeTask &a, const MoeTask &b, int K, int nw, hipStream_t st);
+int bgl_launch_moe_x2(const MoeTask &a, const MoeTask &b, int K, int nw, int cap, hipStream_t st);

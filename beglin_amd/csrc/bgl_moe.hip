@@ -362,12 +362,20 @@ static bool task_wide(const bgl_tensor *stack, const MoeTask &Mt) {
     return !Mt.ta && (dense_fmt(Mt.da.fmt) || (Mt.swiglu && dense_fmt(Mt.db.fmt)));
 }
 
-// The shared experts' T columns are cut into segments of MOE_SHARED_SEG, one pseudo-expert each
-// (every one reads the same tensor), so the chunks run on separate workgroups instead of one after
-// another on each tile's workgroup; the tiles' rereads come from cache (two small experts).
-// Routed experts keep one workgroup per tile: a second reader of a large expert's tile would go to
-// HBM, while one workgroup walking its segment rereads the tile from L2.
-#define MOE_SHARED_SEG MOE_MB
+// The shared experts' T columns are cut into segments, one pseudo-expert each (every one reads
+// the same tensor), so the chunks run on separate workgroups instead of one after another on each
+// tile's workgroup.  Every segment reads the whole tensor, so segments are as long as one weight
+// pass serves: MOE_MB columns in k_moe_gemv; in k_moe_x 8 (two column groups) beyond 8 tokens and
+// 4 between 5 and 8 tokens, which keeps twice the workgroups where the tensors are small.
+// Routed experts keep one workgroup per tile, which walks its segment in chunks.
+static int shared_seg(int T, bool xpath) {
+    if (!xpath) return T > MOE_MB ? MOE_MB : 0;
+    return T > 8 ? 8 : T > 4 ? 4 : 0;
+}
+
+// Token columns of records one k_moe_x chunk holds: 8 where the launch's LDS allows (BGL_MOE_CAP
+// forces 4 or 8).
+static int moe_cap(const bgl_ctx *c, int K, int nw, int TR) { return c->moe_cap ? c->moe_cap : bgl_moe_x_cap(K, nw, TR); }
 
 static int moe_launch(bgl_ctx *c, const MoeTask &Mt, int units, bool wide) {
     int nw = units < c->max_waves ? units : c->max_waves;
@@ -394,7 +402,7 @@ static bool x_tensor_ok(const BglDevTensor &T) {
     return bgl_moe_x_fmt(T.fmt) && (size_t)T.ntiles * T.cpr * 1024 < (1ull << 31) && (size_t)T.ntiles * T.nunits * 512 < (1ull << 31);
 }
 static bool moe_x_ok(bgl_ctx *c, const bgl_tensor *sa, const bgl_tensor *sb, const MoeTask &Mt, int K) {
-    if (c->no_moe_x || bgl_moe_x_lds(K, 16, 64) > 160 * 1024 || bgl_moe_x_lds(K, 8, 16) > 160 * 1024) return false;
+    if (c->no_moe_x || bgl_moe_x_lds(K, 16, 64, 4) > 160 * 1024 || bgl_moe_x_lds(K, 8, 16, 4) > 160 * 1024) return false;
     for (const bgl_tensor *st : {sa, sb})
         if (st)
             for (const bgl_tensor *e : st->experts)
@@ -422,7 +430,7 @@ static int moe_run(bgl_ctx *c, MoeTask &Mt, const bgl_tensor *sa, const bgl_tens
         int tok = prof_begin(c, 1);
         int TR, nw;
         bgl_moe_x_shape(K, active_wgs, c->force_tr, c->x_waves, &TR, &nw);
-        int rc = bgl_launch_moe_x(Mt, K, TR, nw, c->stream);
+        int rc = bgl_launch_moe_x(Mt, K, TR, nw, moe_cap(c, K, nw, TR), c->stream);
         prof_end(c, tok);
         if (rc) return bgl_fail(BGL_E_ARG, "k_moe_x launch: in=%d", K);
         HIPCHK(hipGetLastError());
@@ -526,8 +534,8 @@ static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, con
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         Ms.da = sg->T; Ms.db = su->T; Ms.tpe = sg->T.ntiles; Ms.ncols = T;
-        Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
         Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
+        Ms.seg = shared_seg(T, moe_x_ok(c, nullptr, nullptr, Ms, H)); Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
     }
     // The shared gate+up joins the routed launch when that launch runs whole-tile workgroups
     // (BGL_MOE_MERGE=1 forces whole tiles, 0 keeps two launches).
@@ -542,7 +550,7 @@ static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, con
             Mr.a.xf = x_dev;
             Ms.a.xf = x_dev;
             int tok = prof_begin(c, 1);
-            rc = bgl_launch_moe_x2(Mr, Ms, H, nw, c->stream);
+            rc = bgl_launch_moe_x2(Mr, Ms, H, nw, moe_cap(c, H, nw, BGL_TILE), c->stream);
             prof_end(c, tok);
             if (rc) return bgl_fail(BGL_E_ARG, "k_moe_x2 launch: in=%d", H);
             HIPCHK(hipGetLastError());
@@ -561,8 +569,9 @@ static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, con
     if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         Ms.da = sd->T; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
-        Ms.seg = T > MOE_SHARED_SEG ? MOE_SHARED_SEG : 0; Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
-        if (moe_x_ok(c, nullptr, nullptr, Ms, Ish)) {      // the combine rides on the shared down's store
+        const bool sdx = moe_x_ok(c, nullptr, nullptr, Ms, Ish);
+        Ms.seg = shared_seg(T, sdx); Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
+        if (sdx) {      // the combine rides on the shared down's store
             Ms.cout = out_dev; Ms.cdown = dd; Ms.cw = w_dev; Ms.cpos = S.pos; Ms.cidx = idx_dev; Ms.ck = K;
             combined = true;
         }

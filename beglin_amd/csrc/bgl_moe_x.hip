@@ -3,7 +3,10 @@
 // of mlx_moe.cpp's gather_qmm), for experts in int4 g64, int4 g32 fp16-scale, int8 g64 or qNg64.
 //
 // A workgroup owns one 64-row tile of one expert (gate and up rows together in SwiGLU mode; lane =
-// row) and walks the expert's sorted segment in chunks of up to MB = 4 token columns.  Per chunk it
+// row) and walks the expert's sorted segment in chunks of up to 4 token columns, or up to 8 where
+// the launch's LDS holds 8 columns of records (MoeTask.mbx): then the waves form two column groups
+// of up to 4 columns each that take the same weight items in the same order, so the chunk's
+// weights come from HBM once and the second group's loads hit the L2.  Per chunk it
 // makes the columns' activation records (bgl_gemv_x.h) from the raw fp32 rows itself -- so a routed
 // FFN needs no activation-prep launches -- while its waves' first weight loads are in flight; then
 // the waves take the 64-groups in turn (each group once per tensor, two in flight): each lane
@@ -18,11 +21,17 @@
 
 bool bgl_moe_x_fmt(int fmt) { return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64; }
 
-// LDS: MB columns of records (K/64 rounded up to whole slots of 64/TR groups), the wave partials,
-// and one slot of level-1 records per wave (cold path).
-size_t bgl_moe_x_lds(int K, int nw, int TR) {
+// LDS: cap columns of records (K/64 rounded up to whole slots of 64/TR groups), the wave partials
+// (MX_MB columns per wave), and one slot of level-1 records per wave (cold path).
+size_t bgl_moe_x_lds(int K, int nw, int TR, int cap) {
     const int KQ = BGL_TILE / TR, S = (K / 64 + KQ - 1) / KQ;
-    return (size_t)MX_MB * S * KQ * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * TR * 4 + (size_t)nw * KQ * XREC_DW * 4;
+    return (size_t)cap * S * KQ * XREC_DW * 4 + (size_t)nw * 2 * MX_MB * TR * 4 + (size_t)nw * KQ * XREC_DW * 4;
+}
+
+// Record columns a launch's LDS holds: 8 where that fits the workgroups the launch keeps per CU
+// (two of 64 rows, one of 16 rows), else 4.
+int bgl_moe_x_cap(int K, int nw, int TR) {
+    return bgl_moe_x_lds(K, nw, TR, 2 * MX_MB) <= (TR == BGL_TILE ? 80 : 160) * 1024 ? 2 * MX_MB : MX_MB;
 }
 
 // out[t][c] = (((0 + w_a d_a) + w_b d_b) + ...) over t's experts in ascending expert id (then k), then
@@ -46,25 +55,30 @@ __device__ __forceinline__ void moe_x_combine(const MoeTask &Mt, int t, int c, f
     Mt.cout[(size_t)t * Mt.ystride + c] = acc + shared;
 }
 
+// mc columns from sorted position base; cgn column groups (1, or 2 with nw even and mc <= 2 MB):
+// group g = waves [g nwg, (g+1) nwg) takes columns [g mc0, g mc0 + mcg) -- mc0 = ceil(mc / cgn) --
+// over every item of the tile.
 template <int FMT, int NB, int MB, int TR>
 __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
-                                            int tile, int r0, int base, int mc, int *xl) {
+                                            int tile, int r0, int base, int mc, int cgn, int *xl) {
     constexpr int KQ = BGL_TILE / TR;              // groups per slot: lane = (row lane % TR, group lane / TR)
     const int nthr = blockDim.x, nw = nthr >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int K = Ta.K, G = K >> 6, S = (G + KQ - 1) / KQ, RC = S * KQ * XREC_DW, NPX = (K + 255) >> 8;
     const int r = lane % TR, kq = lane / TR;
+    const int nwg = nw / cgn, cg = wave / nwg, wv = wave - cg * nwg;
+    const int mc0 = (mc + cgn - 1) / cgn, cb = cg * mc0, mcg = cg ? mc - mc0 : mc0;
 
-    // ---- a wave's items: its slots wave, wave + nw, ... -- each once per tensor in SwiGLU mode
+    // ---- a wave's items: its slots wv, wv + nwg, ... -- each once per tensor in SwiGLU mode
     // (gate then up) -- MX_DEPTH in flight; the first ones go out ahead of the activation work.
     // Lanes whose group of the last slot lies past K read nothing there; their records are zero.
     const XRes Ra = x_res<FMT>(Ta, tile), Rb = x_res<FMT>(Tb, tile);
     const XLane xlane = x_lane<FMT, NB, KQ>(r0 + r, kq);
     XLane xlast = xlane;
     if (kq >= G - (S - 1) * KQ) xlast = XLane{X_OOB, X_OOB, X_OOB, X_OOB, X_OOB};
-    const int ns = (S - 1 - wave) / nw + 1, NI = glu ? 2 * ns : ns;     // nw <= S: every wave has a slot
+    const int ns = (S - 1 - wv) / nwg + 1, NI = glu ? 2 * ns : ns;     // nwg <= nw <= S: every wave has a slot
     auto item_load = [&](XRaw<FMT, NB> &rw, int j) {
-        const int sl = wave + (glu ? j >> 1 : j) * nw;
+        const int sl = wv + (glu ? j >> 1 : j) * nwg;
         x_load<FMT, NB, KQ>(rw, glu && (j & 1) ? Rb : Ra, sl == S - 1 ? xlast : xlane, sl, j < NI);
     };
     XRaw<FMT, NB> c[MX_DEPTH];
@@ -99,13 +113,13 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
             const int j = j0 + jj;
             if (j < NI) {
                 const bool up = glu && (j & 1);
-                const int *rec = xk + (wave + (glu ? j >> 1 : j) * nw) * (KQ * XREC_DW);
+                const int *rec = xk + (wv + (glu ? j >> 1 : j) * nwg) * (KQ * XREC_DW) + cb * RC;
                 const XDec<FMT, NB> d = x_decode<FMT, NB>(c[jj]);
                 // columns one loop iteration at a time (not unrolled: the scheduler would hoist every
                 // column's record reads, and their registers, to the front); the accumulator is
                 // picked by wave-uniform branches
 #pragma unroll 1
-                for (int m = 0; m < mc; m++) {
+                for (int m = 0; m < mcg; m++) {
                     const float v = x_dot<FMT, NB>(d, rec + m * RC);
 #pragma unroll
                     for (int q = 0; q < MB; q++) {
@@ -122,22 +136,22 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
     {
         int fl = 0;
         for (int i = 0; i < ns; i++)
-            for (int m = 0; m < mc; m++) fl |= xk[(wave + i * nw) * (KQ * XREC_DW) + m * RC + XREC_DSUM + 3];
+            for (int m = 0; m < mcg; m++) fl |= xk[(wv + i * nwg) * (KQ * XREC_DW) + (cb + m) * RC + XREC_DSUM + 3];
         if (__builtin_amdgcn_ballot_w64(fl != 0)) {
-            int *scr = xl + MX_MB * RC + nw * 2 * MX_MB * TR + wave * KQ * XREC_DW;   // this wave's level-1 records
+            int *scr = xl + Mt.mbx * RC + nw * 2 * MX_MB * TR + wave * KQ * XREC_DW;   // this wave's level-1 records
             const int *r1 = scr + kq * XREC_DW;
             for (int j = 0; j < NI; j++) {
-                const int sl = wave + (glu ? j >> 1 : j) * nw, gl = min(sl * KQ + kq, G - 1);
+                const int sl = wv + (glu ? j >> 1 : j) * nwg, gl = min(sl * KQ + kq, G - 1);
                 const bool up = glu && (j & 1);
-                const int *rec = xk + sl * (KQ * XREC_DW);
+                const int *rec = xk + sl * (KQ * XREC_DW) + cb * RC;
                 int f2 = 0;
-                for (int m = 0; m < mc; m++) f2 |= rec[m * RC + XREC_DSUM + 3];
+                for (int m = 0; m < mcg; m++) f2 |= rec[m * RC + XREC_DSUM + 3];
                 if (!__builtin_amdgcn_ballot_w64(f2 != 0)) continue;
 #pragma unroll 1
-                for (int m = 0; m < mc; m++) {
+                for (int m = 0; m < mcg; m++) {
                     const int f3 = rec[m * RC + XREC_DSUM + 3];
                     if (!__builtin_amdgcn_ballot_w64(f3 != 0)) continue;
-                    const int xrow_m = Mt.cols ? uni(Mt.cols)[base + m] : base + m;
+                    const int xrow_m = Mt.cols ? uni(Mt.cols)[base + cb + m] : base + cb + m;
                     const float *xr = Mt.a.xf + (size_t)xrow_m * K;
                     // the column's level-1 records first, then the weights: the two never hold
                     // registers at the same time
@@ -164,7 +178,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
         }
     }
 
-    // ---- row sums: over the KQ lanes of a row, then over the waves in order
+    // ---- row sums: over the KQ lanes of a row, then over the column group's waves in order
 #pragma unroll
     for (int m = 0; m < MB; m++) {
 #pragma unroll
@@ -173,7 +187,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
             accb[m] += __shfl_xor(accb[m], o);
         }
     }
-    float *red = reinterpret_cast<float *>(xl + MX_MB * RC);      // [wave][2][MB][TR]
+    float *red = reinterpret_cast<float *>(xl + Mt.mbx * RC);     // [wave][2][MB][TR]
     if (lane < TR) {
 #pragma unroll
         for (int m = 0; m < MB; m++) {
@@ -185,10 +199,11 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
     for (int t = threadIdx.x; t < mc * TR; t += nthr) {
         const int m = t / TR, rl = t % TR, row = tile * BGL_TILE + r0 + rl;
         if (row < Ta.N) {
-            float va = red[(0 * MB + m) * TR + rl], vb = red[(1 * MB + m) * TR + rl];
-            for (int w = 1; w < nw; w++) {
-                va += red[((w * 2 + 0) * MB + m) * TR + rl];
-                vb += red[((w * 2 + 1) * MB + m) * TR + rl];
+            const int g = m >= mc0, mm = m - g * mc0, w0 = g * nwg;
+            float va = red[((w0 * 2 + 0) * MB + mm) * TR + rl], vb = red[((w0 * 2 + 1) * MB + mm) * TR + rl];
+            for (int w = w0 + 1; w < w0 + nwg; w++) {
+                va += red[((w * 2 + 0) * MB + mm) * TR + rl];
+                vb += red[((w * 2 + 1) * MB + mm) * TR + rl];
             }
             const float out = glu ? (va / (1.0f + expf(-va))) * vb : va;
             const int yr = Mt.ymap ? Mt.ymap[base + m] : base + m;
@@ -203,11 +218,16 @@ template <int FMT, int NB, int TR>
 __device__ __forceinline__ void moe_x_tile(const MoeTask &Mt, const BglDevTensor &Ta, const BglDevTensor &Tb, bool glu,
                                            int tile, int r0, int seg0, int ncols, int *xl) {
     int c0 = 0;
+    if (Mt.mbx > MX_MB && !((blockDim.x >> 6) & 1))            // chunks of 5..8 columns: two column groups
+        for (; ncols - c0 > MX_MB; c0 += 2 * MX_MB) {
+            const int rem = ncols - c0;
+            moe_x_chunk<FMT, NB, MX_MB, TR>(Mt, Ta, Tb, glu, tile, r0, seg0 + c0, rem < 2 * MX_MB ? rem : 2 * MX_MB, 2, xl);
+        }
     for (; ncols - c0 >= 2; c0 += MX_MB) {
         const int rem = ncols - c0;
-        moe_x_chunk<FMT, NB, MX_MB, TR>(Mt, Ta, Tb, glu, tile, r0, seg0 + c0, rem < MX_MB ? rem : MX_MB, xl);
+        moe_x_chunk<FMT, NB, MX_MB, TR>(Mt, Ta, Tb, glu, tile, r0, seg0 + c0, rem < MX_MB ? rem : MX_MB, 1, xl);
     }
-    if (c0 < ncols) moe_x_chunk<FMT, NB, 1, TR>(Mt, Ta, Tb, glu, tile, r0, seg0 + c0, 1, xl);
+    if (c0 < ncols) moe_x_chunk<FMT, NB, 1, TR>(Mt, Ta, Tb, glu, tile, r0, seg0 + c0, 1, 1, xl);
 }
 
 // Expert record through the constant address space (scalar loads, wave-uniform addresses).
@@ -283,14 +303,15 @@ __global__ __launch_bounds__(NWMAX * BGL_TILE, 4) void k_moe_x2(MoePair P) {
     else moe_x_body<SEG1, BGL_TILE>(P.t[1], (int)blockIdx.x - P.nb0, xl);
 }
 
-int bgl_launch_moe_x2(const MoeTask &a, const MoeTask &b, int K, int nw, hipStream_t st) {
-    if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW) return -1;
+int bgl_launch_moe_x2(const MoeTask &a, const MoeTask &b, int K, int nw, int cap, hipStream_t st) {
+    if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW || (cap != MX_MB && cap != 2 * MX_MB)) return -1;
     if (a.seg > 0 && !a.off) return -1;                     // the first task is never segmented
     const bool seg1 = !b.off && b.seg > 0;
-    const size_t lds = bgl_moe_x_lds(K, nw, BGL_TILE);
+    const size_t lds = bgl_moe_x_lds(K, nw, BGL_TILE, cap);
     if (lds > 160 * 1024) return -1;
     MoePair P;
     P.t[0] = a; P.t[1] = b;
+    P.t[0].mbx = cap; P.t[1].mbx = cap;
     P.nb0 = a.E * a.tpe;
     const dim3 g(P.nb0 + b.E * b.tpe), bl(nw * BGL_TILE);
     if (nw <= 8) {
@@ -305,10 +326,12 @@ int bgl_launch_moe_x2(const MoeTask &a, const MoeTask &b, int K, int nw, hipStre
 
 // Mt.a.xf: the raw fp32 activation rows (row stride K = the tensors' in).  TR rows per workgroup
 // (64 or 16), nw waves (<= 16, at most one per slot of 64/TR groups).
-int bgl_launch_moe_x(const MoeTask &Mt, int K, int TR, int nw, hipStream_t st) {
-    if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW || (TR != 64 && TR != 16)) return -1;
-    const size_t lds = bgl_moe_x_lds(K, nw, TR);
+int bgl_launch_moe_x(const MoeTask &Mt0, int K, int TR, int nw, int cap, hipStream_t st) {
+    if (K < 64 || K % 64 || nw < 1 || nw > MX_MAXW || (TR != 64 && TR != 16) || (cap != MX_MB && cap != 2 * MX_MB)) return -1;
+    const size_t lds = bgl_moe_x_lds(K, nw, TR, cap);
     if (lds > 160 * 1024) return -1;
+    MoeTask Mt = Mt0;
+    Mt.mbx = cap;
     const dim3 g(Mt.E * Mt.tpe * (BGL_TILE / TR)), b(nw * BGL_TILE);
     const bool seg = !Mt.off && Mt.seg > 0;
 #define MX_GO(S_, W_, T_) hipLaunchKernelGGL((k_moe_x<S_, W_, T_>), g, b, lds, st, Mt)

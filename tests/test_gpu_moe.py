@@ -541,3 +541,31 @@ def test_moe_merged_gate_up_equals_two_launches(torch_dev, oracle, monkeypatch, 
     assert np.array_equal(np.asarray(outs[0]).view(np.uint32), np.asarray(outs[1]).view(np.uint32))
     ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
     assert relerr(outs[0], ref) <= TOL
+
+
+@pytest.mark.parametrize("T,tr", [(9, 64), (21, 64), (40, 64), (21, 16)])
+def test_moe_x_column_groups(torch_dev, oracle, monkeypatch, T, tr):
+    """Chunks of 5..8 token columns in one pass over the weights (two column groups of waves,
+    record capacity 8) against chunks of at most 4 (capacity 4) and the oracle: four experts so
+    segments run 2..20 columns (8-column chunks, then a 4-column or single last chunk), 4 waves
+    (two per group), whole tiles and 16-row workgroups, shared experts in segments of 8."""
+    import beglin_amd
+    torch = torch_dev
+    E, H, I, K, Ish = 4, 320, 256, 2, 256
+    say("moe_x column groups", T, tr)
+    fm = [(5, 0), (2, 0), (4, 7), (4, 15)]
+    gate, up, down, shared = moe_setup(oracle, 6600 + T, E, H, I, Ish, fm, down_fmts=fm[::-1], sh_fmt=(4, 12))
+    x = seeded_normal(6610 + T, (T, H))
+    idx, w = oracle.route(seeded_normal(6620 + T, (T, E)), K, True)
+    outs = []
+    for cap in ("8", "4"):
+        monkeypatch.setenv("BGL_MOE_CAP", cap)
+        monkeypatch.setenv("BGL_FORCE_TR", str(tr))
+        monkeypatch.setenv("BGL_X_WAVES", "4")
+        c = beglin_amd.Context(0)
+        outs.append(run_moe(c, torch, gate, up, down, shared, x, idx, w))
+        c.close()
+    for k in ("BGL_MOE_CAP", "BGL_FORCE_TR", "BGL_X_WAVES"):
+        monkeypatch.delenv(k, raising=False)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    assert relerr(outs[0], ref) <= TOL and relerr(outs[1], ref) <= TOL and relerr(outs[0], outs[1]) <= 2 * TOL
