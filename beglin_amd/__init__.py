@@ -158,6 +158,11 @@ class Context:
         B = (C.c_void_p * n)(*[(b.data_ptr() if b is not None else None) for b in (biases or [None] * n)])
         _check(lib().bgl_matmul_group_dev(self.h, n, W, act, _p(x_dev), B, Y, M), "bgl_matmul_group_dev")
 
+    def mlp(self, gate, up, down, x_dev, y_dev, act=ACT_F32, h_dev=None):
+        """y = W_down (silu(W_gate x) * (W_up x)) on the device (bgl_mlp_dev); h_dev receives h."""
+        M = 1 if x_dev.dim() == 1 else x_dev.shape[0]
+        _check(lib().bgl_mlp_dev(self.h, gate.h, up.h, down.h, act, _p(x_dev), _p(y_dev), M, _p(h_dev)), "bgl_mlp_dev")
+
     def read_probe(self, ts, nblocks=0, nthreads=0):
         """Plain streaming read of the tensors' device bytes (the memory floor for a call)."""
         W = (C.c_void_p * len(ts))(*[t.h.value for t in ts])
@@ -271,6 +276,12 @@ def layout_check(layout, blob):
     return rc, n.value
 
 
+def af_layout_check(layout, blob_bytes):
+    n = C.c_int()
+    rc = lib().bgl_af_layout_check(layout.encode(), blob_bytes, C.byref(n))
+    return rc, n.value
+
+
 def cache_valid(cache, layout, blob):
     return lib().bgl_model_cache_valid(cache.encode(), layout.encode(), blob.encode())
 
@@ -289,6 +300,10 @@ class Registry:
     def bind_af(self, blob, name, E, out, inn, ng, packed_off, scale_off, bias_off, bits):
         return lib().bgl_gpu_bind_af(blob.ctypes.data, blob.nbytes, name.encode(), E, out, inn, ng, packed_off,
                                      scale_off, bias_off, bits)
+
+    def load_layout_af(self, layout, blob):
+        """Binds every tensor of an AF layout manifest over blob (uint8 array); the count or -1."""
+        return lib().bgl_gpu_load_layout_af(layout.encode(), blob.ctypes.data, blob.nbytes)
 
     def binding_kind(self, name):
         b = C.c_int()

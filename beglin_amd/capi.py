@@ -40,6 +40,7 @@ SIGNATURES = [
     ("bgl_tensor_info", _I, [_P, C.POINTER(_I), C.POINTER(_I), C.POINTER(_I), C.POINTER(_I), C.POINTER(C.c_size_t)]),
     ("bgl_dequant_dev", _I, [_P, _P, _I, _I, _P]),
     ("bgl_matmul_dev", _I, [_P, _P, _I, _P, _P, _P, _I]),
+    ("bgl_mlp_dev", _I, [_P, _P, _P, _P, _I, _P, _P, _I, _P]),
     ("bgl_matmul_group_dev", _I, [_P, _I, C.POINTER(_P), _I, _P, C.POINTER(_P), C.POINTER(_P), _I]),
     ("bgl_matmul_group_noalloc_dev", _I, [_P, _I, C.POINTER(_P), _I, _P, C.POINTER(_P), C.POINTER(_P), _I]),
     ("bgl_read_probe_dev", _I, [_P, _I, C.POINTER(_P), _I, _I]),
@@ -71,6 +72,8 @@ SIGNATURES = [
     ("bgl_gpu_bind_router", _I, [C.c_char_p, _P, _P, _L, _L]),
     ("bgl_bind_qng64_mixed", _I, [_P, _P, _L, _P, _P, _P, _I, _I, C.POINTER(_P)]),
     ("bgl_int4_layout_check", _I, [C.c_char_p, C.c_char_p, C.POINTER(_I)]),
+    ("bgl_af_layout_check", _I, [C.c_char_p, _L, C.POINTER(_I)]),
+    ("bgl_gpu_load_layout_af", _I, [C.c_char_p, _P, _L]),
     ("bgl_model_load_int4", _I, [_P, C.c_char_p, C.c_char_p, C.POINTER(_P)]),
     ("bgl_model_count", _I, [_P]),
     ("bgl_model_find", _I, [_P, C.c_char_p, C.POINTER(_I), C.POINTER(_I), C.POINTER(_I), C.POINTER(_P), C.POINTER(_P)]),

@@ -90,7 +90,7 @@ static void dbuf_free(DevBuf &b) {
 size_t ctx_scratch(bgl_ctx *c, bool release) {
     DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->part, &c->hx, &c->hy, &c->hb,
                       &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_e, &c->moe_f, &c->moe_g, &c->moe_meta,
-                      &c->moe_route, &c->moe_scores};
+                      &c->moe_route, &c->moe_scores, &c->mlp};
     size_t total = 0;
     for (DevBuf *b : bufs) {
         total += b->bytes;

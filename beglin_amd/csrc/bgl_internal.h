@@ -45,6 +45,7 @@ struct bgl_ctx {
     DevBuf moe_a, moe_b, moe_c, moe_d, moe_e, moe_f, moe_g, moe_meta;   // MoE digits x2, fp32 h/down, bucket scratch
     DevBuf moe_route;                     // routing of bgl_moe_layer_dev: idx [T][K] + w [T][K]
     DevBuf moe_scores;                    // router scores [T][E]
+    DevBuf mlp;                           // bgl_mlp_dev: gate and up outputs [M][I] each, then h [M][I]
     std::vector<void *> retired;          // outgrown scratch, kept for captured graphs until destroy / epoch reset
     uint8_t *fixed_base = nullptr;        // set during bgl_matmul_group_noalloc_dev: scratch comes from here
     size_t fixed_cap = 0, fixed_used = 0;

@@ -12,8 +12,12 @@
 // device architecture and the device-layout version; a directory; each tensor's three device
 // buffers, 64-byte aligned.  A cache whose header does not match is not valid (the caller loads the
 // manifest again and rewrites it); a directory that points outside the file is an error.
+#include <ctype.h>
+#include <errno.h>
 #include <fcntl.h>
+#include <limits.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -64,62 +68,189 @@ struct Mapping {
     }
 };
 
-// load_int4's parse and checks (qwen_infer.c:558-609).  Like the reference's fscanf loop, parsing
-// stops at the first line that does not hold the seven leading fields.
+// ---- manifests
+// A manifest is a stream of whitespace-separated tokens holding one record per tensor: a name,
+// then fields of fixed meaning.  Line breaks carry no meaning, and a record that runs out of
+// tokens, or holds a non-integer where an integer belongs, ends the manifest quietly: the
+// engine's fscanf loops stop there too.
+class Tokens {
+    FILE *f_;
+    bool fail_ = false, long_ = false;
+public:
+    explicit Tokens(FILE *f) : f_(f) {}
+    // a token longer than its field allows ended the stream (an error, not a quiet end)
+    bool too_long() const { return long_; }
+    // the next token into buf (at most cap - 1 characters); false at the end of the stream or
+    // when the token is longer
+    bool word(char *buf, size_t cap) {
+        if (fail_) return false;
+        int ch;
+        do ch = fgetc(f_); while (ch != EOF && isspace(ch));
+        size_t n = 0;
+        while (ch != EOF && !isspace(ch)) {
+            if (n + 1 >= cap) { fail_ = long_ = true; return false; }
+            buf[n++] = (char)ch;
+            ch = fgetc(f_);
+        }
+        buf[n] = 0;
+        if (!n) fail_ = true;
+        return n > 0;
+    }
+    bool integer(long &v) {
+        char t[32], *end = nullptr;
+        if (!word(t, sizeof t)) return false;
+        errno = 0;
+        v = strtol(t, &end, 10);
+        if (*end || errno) { fail_ = true; return false; }
+        return true;
+    }
+};
+
+// The int4-mode manifest (load_int4, qwen_infer.c:551-609): "name kind doff out in ng soff", and
+// for q4g256sf an 8th field, the sub-code offset.  What each kind stores, as a table: the codes at
+// doff (bytes per value = num / den), fp32 scales [out][ng] at soff for the grouped kinds, u8
+// sub-codes [out][in/64] at soff2; `group` values per scale (0: f32, no groups, `in` 0 meaning a
+// vector of `out`); the byte alignment every offset must have.
+struct Int4Kind {
+    const char *tag;
+    int kind;                 // BGL_K_*, 0 for f32 (read in place from the blob)
+    int group;
+    int align;
+    int num, den;
+    bool sub;
+};
+const Int4Kind kInt4Kinds[] = {
+    {"q4g64", BGL_K_Q4G64, 64, 64, 1, 2, false},
+    {"q8g64", BGL_K_Q8G64, 64, 1, 1, 1, false},
+    {"q4g256sf", BGL_K_Q4G256SF, 256, 64, 1, 2, true},
+    {"f32", 0, 0, 1, 4, 1, false},
+};
+constexpr int kInt4MaxTensors = 512;
+
+// A plane [off, off + bytes) must lie inside the blob.
+int plane_in_blob(const char *layout, const char *nm, const char *what, long off, size_t bytes, size_t wb) {
+    if (off < 0) return bgl_fail(BGL_E_ARG, "%s: tensor %s: %s offset %ld is negative", layout, nm, what, off);
+    if ((size_t)off > wb || bytes > wb - (size_t)off)
+        return bgl_fail(BGL_E_ARG, "%s: tensor %s: %s bytes [%ld, %ld + %zu) reach past the %zu-byte blob", layout, nm, what, off,
+                        off, bytes, wb);
+    return 0;
+}
+
 int parse_int4(const char *layout, size_t wb, std::vector<Rec> &recs) {
     FILE *f = fopen(layout, "r");
-    if (!f) return bgl_fail(BGL_E_ARG, "layout_int4: cannot open %s", layout);
-    char nm[96], kind[16];
-    long doff, soff;
-    int out, in, ng;
+    if (!f) return bgl_fail(BGL_E_ARG, "int4 layout %s cannot be opened", layout);
+    Tokens tk(f);
     std::unordered_map<std::string, int> seen;
     int rc = 0;
-    while (!rc && fscanf(f, "%95s %15s %ld %d %d %d %ld", nm, kind, &doff, &out, &in, &ng, &soff) == 7) {
-        if (recs.size() >= 512) { rc = bgl_fail(BGL_E_ARG, ">512 tensors in layout_int4"); break; }
-        if (out < 0 || in < 0 || doff < 0) { rc = bgl_fail(BGL_E_ARG, "%s bad dims/off", nm); break; }
-        if (seen.count(nm)) { rc = bgl_fail(BGL_E_ARG, "duplicate tensor name in layout: %s", nm); break; }
-        seen[nm] = 1;
-        Rec r;
-        r.name = nm; r.out = out; r.in = in; r.ng = ng; r.doff = doff; r.soff = soff;
-        if (!strcmp(kind, "q4g256sf")) {
-            long soff2;
-            if (fscanf(f, " %ld", &soff2) != 1) { rc = bgl_fail(BGL_E_ARG, "%s q4g256sf missing soff2 (8th field)", nm); break; }
-            if (in % 256 != 0) { rc = bgl_fail(BGL_E_ARG, "%s in%%256!=0", nm); break; }
-            if (ng != in / 256) { rc = bgl_fail(BGL_E_ARG, "%s ng=%d != in/256=%d", nm, ng, in / 256); break; }
-            if (doff % 64 || soff % 64 || soff2 % 64) { rc = bgl_fail(BGL_E_ARG, "%s misaligned", nm); break; }
-            const size_t pb = (size_t)out * (in / 2), sb = (size_t)out * ng * 4, cb = (size_t)out * (in / 64);
-            if (soff < 0 || soff2 < 0 || (size_t)doff + pb > wb || (size_t)soff + sb > wb || (size_t)soff2 + cb > wb) {
-                rc = bgl_fail(BGL_E_ARG, "%s q4g256sf extent past blob (wb=%zu)", nm, wb);
-                break;
-            }
-            r.kind = BGL_K_Q4G256SF; r.soff2 = soff2;
-        } else if (!strcmp(kind, "q4g64")) {
-            if (in % 64 != 0) { rc = bgl_fail(BGL_E_ARG, "%s in%%64!=0", nm); break; }
-            if (ng != in / 64) { rc = bgl_fail(BGL_E_ARG, "%s ng=%d != in/64=%d", nm, ng, in / 64); break; }
-            if (doff % 64 || soff % 64) { rc = bgl_fail(BGL_E_ARG, "%s misaligned", nm); break; }
-            const size_t pb = (size_t)out * (in / 2), sb = (size_t)out * ng * 4;
-            if (soff < 0 || (size_t)doff + pb > wb || (size_t)soff + sb > wb) {
-                rc = bgl_fail(BGL_E_ARG, "%s q4 extent past blob (wb=%zu)", nm, wb);
-                break;
-            }
-            r.kind = BGL_K_Q4G64;
-        } else if (!strcmp(kind, "q8g64")) {
-            if (in % 64 != 0) { rc = bgl_fail(BGL_E_ARG, "%s in%%64!=0", nm); break; }
-            if (ng != in / 64) { rc = bgl_fail(BGL_E_ARG, "%s ng=%d != in/64=%d", nm, ng, in / 64); break; }
-            const size_t cb = (size_t)out * in, sb = (size_t)out * ng * 4;
-            if (soff < 0 || (size_t)doff + cb > wb || (size_t)soff + sb > wb) {
-                rc = bgl_fail(BGL_E_ARG, "%s q8 extent past blob (wb=%zu)", nm, wb);
-                break;
-            }
-            r.kind = BGL_K_Q8G64;
-        } else if (!strcmp(kind, "f32")) {
-            const size_t numel = in > 0 ? (size_t)out * in : (size_t)out;
-            if ((size_t)doff + numel * 4 > wb) { rc = bgl_fail(BGL_E_ARG, "%s f32 extent past blob (wb=%zu)", nm, wb); break; }
-            r.kind = 0;
-        } else {
-            rc = bgl_fail(BGL_E_ARG, "%s unknown kind '%s' in %s (recognized: q4g64 q8g64 q4g256sf f32)", nm, kind, layout);
+    for (;;) {
+        char nm[96], tag[16];
+        long doff, out, in, ng, soff;
+        if (!tk.word(nm, sizeof nm) || !tk.word(tag, sizeof tag) || !tk.integer(doff) || !tk.integer(out) ||
+            !tk.integer(in) || !tk.integer(ng) || !tk.integer(soff)) {
+            if (tk.too_long()) rc = bgl_fail(BGL_E_ARG, "%s: record %zu holds a token longer than its field", layout, recs.size() + 1);
             break;
         }
+        if (out > INT_MAX || in > INT_MAX || ng > INT_MAX || ng < INT_MIN) break;    // not an int: the record ends here
+        if ((int)recs.size() == kInt4MaxTensors) {
+            rc = bgl_fail(BGL_E_ARG, "%s: more than %d tensors", layout, kInt4MaxTensors);
+            break;
+        }
+        if (out < 0 || in < 0 || doff < 0) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: out=%ld in=%ld doff=%ld (none may be negative)", layout, nm, out, in, doff);
+            break;
+        }
+        if (!seen.emplace(nm, 1).second) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s is listed twice", layout, nm);
+            break;
+        }
+        const Int4Kind *k = nullptr;
+        for (const Int4Kind &c : kInt4Kinds)
+            if (!strcmp(c.tag, tag)) k = &c;
+        if (!k) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s has kind \"%s\"; the kinds are q4g64, q8g64, q4g256sf and f32", layout, nm, tag);
+            break;
+        }
+        long soff2 = 0;
+        if (k->sub && !tk.integer(soff2)) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s (%s) ends before its sub-code offset, the 8th field", layout, nm, tag);
+            break;
+        }
+        if (k->group) {
+            if (in % k->group) {
+                rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: in=%ld is not a whole number of %d-value groups", layout, nm, in, k->group);
+                break;
+            }
+            if (ng != in / k->group) {
+                rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: ng=%ld, but in / %d = %ld", layout, nm, ng, k->group, in / k->group);
+                break;
+            }
+        }
+        if (k->align > 1 && (doff % k->align || soff % k->align || (k->sub && soff2 % k->align))) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s (%s): every offset must be a multiple of %d bytes", layout, nm, tag, k->align);
+            break;
+        }
+        const size_t values = k->group || in > 0 ? (size_t)out * in : (size_t)out;
+        if ((rc = plane_in_blob(layout, nm, "code", doff, values * k->num / k->den, wb))) break;
+        if (k->group && (rc = plane_in_blob(layout, nm, "scale", soff, (size_t)out * ng * 4, wb))) break;
+        if (k->sub && (rc = plane_in_blob(layout, nm, "sub-code", soff2, (size_t)out * (in / 64), wb))) break;
+        Rec r;
+        r.name = nm; r.kind = k->kind; r.out = (int)out; r.in = (int)in; r.ng = (int)ng;
+        r.doff = doff; r.soff = soff; r.soff2 = soff2;
+        recs.push_back(r);
+    }
+    fclose(f);
+    return rc;
+}
+
+// The AF layout manifest (moe_load_layout_af, qwen_infer.c:2496-2515): "name E out in ng po pb so
+// bo" per tensor -- E experts of [out][in] int4 affine weights (nib * scale + bias, groups of 64)
+// over one blob: packed nibbles at po (pb bytes, E * out * in / 2 of them read), fp32 scales
+// [E][out][ng] at so and biases of the same shape at bo.
+struct AfRec {
+    std::string name;
+    long E, out, in, ng, po, pb, so, bo;
+};
+constexpr int kAfMaxTensors = 1024;
+
+int parse_af(const char *layout, size_t wb, std::vector<AfRec> &recs) {
+    FILE *f = fopen(layout, "r");
+    if (!f) return bgl_fail(BGL_E_ARG, "AF layout %s cannot be opened", layout);
+    Tokens tk(f);
+    std::unordered_map<std::string, int> seen;
+    int rc = 0;
+    for (;;) {
+        char nm[128];
+        AfRec r;
+        if (!tk.word(nm, sizeof nm) || !tk.integer(r.E) || !tk.integer(r.out) || !tk.integer(r.in) || !tk.integer(r.ng) ||
+            !tk.integer(r.po) || !tk.integer(r.pb) || !tk.integer(r.so) || !tk.integer(r.bo)) {
+            if (tk.too_long()) rc = bgl_fail(BGL_E_ARG, "%s: record %zu holds a token longer than its field", layout, recs.size() + 1);
+            break;
+        }
+        r.name = nm;
+        if ((int)recs.size() == kAfMaxTensors) {
+            rc = bgl_fail(BGL_E_ARG, "%s: more than %d tensors", layout, kAfMaxTensors);
+            break;
+        }
+        if (!seen.emplace(nm, 1).second) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s is listed twice", layout, nm);
+            break;
+        }
+        if (r.E < 1 || r.out < 1 || r.in < 64 || r.E > INT_MAX || r.out > INT_MAX || r.in > INT_MAX) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: E=%ld out=%ld in=%ld (each at least 1, in at least 64)", layout, nm, r.E, r.out, r.in);
+            break;
+        }
+        if (r.in % 64 || r.ng != r.in / 64) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: in=%ld, ng=%ld; the groups hold 64 values", layout, nm, r.in, r.ng);
+            break;
+        }
+        const size_t codes = (size_t)r.E * r.out * (r.in / 2), side = (size_t)r.E * r.out * r.ng * 4;
+        if (r.pb < 0 || (size_t)r.pb < codes) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: pb=%ld is less than its %zu bytes of codes", layout, nm, r.pb, codes);
+            break;
+        }
+        if ((rc = plane_in_blob(layout, nm, "code", r.po, codes, wb)) || (rc = plane_in_blob(layout, nm, "scale", r.so, side, wb)) ||
+            (rc = plane_in_blob(layout, nm, "bias", r.bo, side, wb)))
+            break;
         recs.push_back(r);
     }
     fclose(f);
@@ -333,6 +464,12 @@ extern "C" int bgl_model_load_cache(bgl_ctx *c, const char *cache_path, const ch
             size_t lb[3];
             BglDevTensor T;
             if (e.kind != BGL_K_Q4G64 && e.kind != BGL_K_Q8G64 && e.kind != BGL_K_Q4G256SF) { rc = bgl_fail(BGL_E_ARG, "%s: kind %d", e.name, e.kind); break; }
+            // the directory's shape is validated like a bind's before it sizes anything
+            if ((rc = check_wt(e.kind, e.kind == BGL_K_Q8G64 ? 8 : 4, e.out, e.in))) break;
+            if (e.ng != e.in / (e.kind == BGL_K_Q4G256SF ? 256 : 64)) {
+                rc = bgl_fail(BGL_E_ARG, "bgl_model_load_cache: %s: ng=%d does not match in=%d", e.name, e.ng, e.in);
+                break;
+            }
             device_layout(e.kind, e.kind == BGL_K_Q8G64 ? 8 : 4, e.out, e.in, T, lb);
             void *buf[3] = {nullptr, nullptr, nullptr};
             size_t total = 0;
@@ -365,4 +502,25 @@ extern "C" int bgl_model_load_cache(bgl_ctx *c, const char *cache_path, const ch
     }
     *out = m;
     return 0;
+}
+
+extern "C" int bgl_af_layout_check(const char *layout_path, long blob_bytes, int *n_tensors) {
+    if (!layout_path || blob_bytes < 0) return bgl_fail(BGL_E_ARG, "bgl_af_layout_check: NULL path or negative blob size");
+    std::vector<AfRec> recs;
+    int rc = parse_af(layout_path, (size_t)blob_bytes, recs);
+    if (rc) return rc;
+    if (n_tensors) *n_tensors = (int)recs.size();
+    return 0;
+}
+
+extern "C" int bgl_gpu_load_layout_af(const char *layout_path, const uint8_t *blob, long blob_bytes) {
+    if (!layout_path || !blob || blob_bytes <= 0) {
+        bgl_fail(BGL_E_ARG, "bgl_gpu_load_layout_af: NULL path or blob, or blob_bytes <= 0");
+        return -1;
+    }
+    std::vector<AfRec> recs;
+    if (parse_af(layout_path, (size_t)blob_bytes, recs)) return -1;
+    for (const AfRec &r : recs)
+        if (!bgl_gpu_bind_af(blob, blob_bytes, r.name.c_str(), r.E, r.out, r.in, r.ng, r.po, r.so, r.bo, 4)) return -1;
+    return (int)recs.size();
 }

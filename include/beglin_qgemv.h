@@ -113,6 +113,14 @@ int  bgl_matmul_dev(bgl_ctx *ctx, const bgl_tensor *w, int act, const float *x_d
  * qwen_infer.c:1276-1306) in ONE launch.  All must have the same `in` and kind; n <= 4. */
 int  bgl_matmul_group_dev(bgl_ctx *ctx, int n, const bgl_tensor *const *w, int act, const float *x_dev,
                           const float *const *bias_dev, float *const *y_dev, int M);
+/* The dense MLP block of forward_token (qwen_infer.c:1560-1573) on the device: g = W_gate x and
+ * u = W_up x in one fused launch, h = silu(g) * u (swiglu, qwen_infer.c:726-733: g / (1 + exp(-g)),
+ * then * u, in fp32; the exponential rounded once from double), y = W_down h.  gate / up [I][H],
+ * down [H][I], x_dev [M][H], y_dev [M][H]; act as bgl_matmul_dev (W4A8 quantizes x and h).  h_dev:
+ * optional [M][I] that receives h (NULL: it stays in the context's scratch).  No host round trip;
+ * capturable under the same scratch rule as the other *_dev calls. */
+int  bgl_mlp_dev(bgl_ctx *ctx, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down, int act,
+                 const float *x_dev, float *y_dev, int M, float *h_dev);
 /* bgl_matmul_group_dev that allocates nothing: no counterpart in the reference.  For callers that
  * cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc.  The same kernels and results as bgl_matmul_group_dev; the per-call
@@ -249,6 +257,18 @@ int bgl_gpu_reset_runtime_epoch(void);
  * 146-367).  Rebinding a name replaces it. */
 int bgl_gpu_bind_af(const uint8_t *blob, long blob_bytes, const char *name, long E, long out, long in, long ng,
                     long packed_off, long scale_off, long bias_off, int bits);           /* mlx_moe.h:48-50 */
+/* The AF layout manifest over an AF blob (moe_load_layout_af, qwen_infer.c:2496-2515): one record per
+ * tensor, "name E out in ng packed_off packed_bytes scale_off bias_off", whitespace-separated; every
+ * tensor is E experts of [out][in] int4 affine weights (bits = 4: nib * scale + bias, groups of 64).
+ * Each record is checked (in % 64 == 0 and ng == in/64; packed_bytes at least the E*out*in/2 code
+ * bytes; codes, scales [E][out][ng] and biases inside the blob; no duplicate names; at most 1024
+ * records; names under 128 characters) before anything is bound, then every tensor is bound by name
+ * through bgl_gpu_bind_af.  A record cut short ends the manifest, as the reference's fscanf loop
+ * ends.  Returns the number of tensors bound, or -1 (bgl_last_error() says why; on a device failure
+ * the tensors before it stay bound).  The reference exits where this returns -1. */
+int bgl_gpu_load_layout_af(const char *layout_path, const uint8_t *blob, long blob_bytes);
+/* The same parse and checks with no device work: 0 and the record count, or a BGL_E_* code. */
+int bgl_af_layout_check(const char *layout_path, long blob_bytes, int *n_tensors);
 /* 0 missing, 1 quantized (bits 2..6, 8), 2 dense (16/32), 3 qNg64 planes n=7, 9..15 (mlx_moe.h:57). */
 int bgl_gpu_binding_kind(const char *name, int *bits_out);
 int bgl_gpu_snapshot_binding(const char *name, uint64_t *snapshot_id);  /* mlx_moe.h:63 */

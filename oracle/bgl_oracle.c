@@ -675,6 +675,18 @@ void or_moe_swiglu_inplace(float *gate, const float *up, int n) {
     }
 }
 
+/* qwen_infer.c:726-733 (swiglu, the dense MLP's): out = (g / (1 + e)) * u, e = exp(-g), each step
+ * rounded to float as the reference's vDSP sequence rounds it (negate, vvexpf, +1, divide,
+ * multiply).  e is exp evaluated in double and rounded once: the correctly rounded expf in all but
+ * double-rounding cases, where the reference's vvexpf is only faithful -- the choice that makes h
+ * a function of g and u alone. */
+void or_swiglu(const float *g, const float *u, float *out, int n) {
+    for (int i = 0; i < n; i++) {
+        const float e = (float)exp(-(double)g[i]);
+        out[i] = (g[i] / (1.0f + e)) * u[i];
+    }
+}
+
 /* Mixed per-cell qNg64 (MixedQNg64Tensor, mlx_moe.cpp:87-93) decoded as the QT-4 GEMV kernel does
  * (mlx_moe.cpp:1708-1722): cell (r, g) has n = bits[cell] planes of 8 bytes at planes + offsets[cell];
  * element p's bit j is bit (p & 7) of byte j*8 + (p >> 3); value (u - 2^(n-1)) * scales[cell]. */

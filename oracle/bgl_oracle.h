@@ -102,6 +102,7 @@ void or_moe_softmax_full(float *x, int n);
 void or_moe_top_k_select(const float *scores, int n, int k, int *out_idx);
 void or_moe_topk_renorm(float *scores, const int *idx, int k);
 void or_moe_swiglu_inplace(float *gate, const float *up, int n);
+void or_swiglu(const float *g, const float *u, float *out, int n);
 void or_moe_route(const float *logits, int T, int E, int K, int renorm, int *top_idx, float *top_w);
 void or_moe_router_logits(const float *w, const float *bias, const float *x, int T, int E, int H, float *logits);
 void or_moe_ffn_bucketed(const or_expert *gate, const or_expert *up, const or_expert *down, int E,

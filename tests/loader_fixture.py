@@ -53,3 +53,30 @@ def build(oracle, d, tensors=None):
     with open(path, "wb") as f:
         f.write(bytes(blob))
     return layout, path, refs
+
+
+def build_af(d, tensors=None, seed=7):
+    """Writes d/layout_af.txt (moe_load_layout_af's record format, qwen_infer.c:2496-2515) over an AF
+    blob of int4 affine tensors: per tensor E x [out][in/2] code bytes, fp32 scales and biases
+    [E][out][in/64], each at a 64-byte aligned offset.  Returns (layout, blob uint8 array, records),
+    records[name] = (E, out, in, codes, scales, biases)."""
+    tensors = tensors or [("layers.0.mlp.experts.gate", 4, 64, 128), ("layers.0.mlp.experts.up", 4, 64, 128),
+                          ("layers.0.mlp.experts.down", 4, 128, 64), ("lm_head", 1, 96, 128)]
+    rng = np.random.default_rng(seed)
+    blob = bytearray()
+    lines, recs = [], {}
+    for name, E, out, inn in tensors:
+        ng = inn // 64
+        codes = rng.integers(0, 256, (E, out, inn // 2), dtype=np.uint8)
+        sc = (rng.random((E, out, ng), dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+        bi = (rng.standard_normal((E, out, ng), dtype=np.float32) * np.float32(0.04)).astype(np.float32)
+        po = _align(blob); blob.extend(codes.tobytes())
+        so = _align(blob); blob.extend(sc.tobytes())
+        bo = _align(blob); blob.extend(bi.tobytes())
+        lines.append(f"{name} {E} {out} {inn} {ng} {po} {codes.nbytes} {so} {bo}")
+        recs[name] = (E, out, inn, codes, sc, bi)
+    _align(blob)
+    layout = os.path.join(d, "layout_af.txt")
+    with open(layout, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    return layout, np.frombuffer(bytes(blob), np.uint8), recs

@@ -74,6 +74,13 @@ class Oracle:
     def __init__(self):
         self.lib = load_oracle()
 
+    # ---- the dense MLP's SwiGLU (or_swiglu) ----
+    def swiglu(self, g, u):
+        g = np.ascontiguousarray(g, np.float32); u = np.ascontiguousarray(u, np.float32)
+        h = np.zeros_like(g)
+        self.lib.or_swiglu(_ptr(g), _ptr(u), _ptr(h), g.size)
+        return h
+
     # ---- fp16 ----
     def f32_to_f16(self, f):
         return self.lib.or_f32_to_f16(C.c_float(f))

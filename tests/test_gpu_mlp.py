@@ -1,0 +1,149 @@
+"""GPU: the dense MLP block on the device (bgl_mlp_dev; forward_token's gate+up -> swiglu -> down,
+qwen_infer.c:1560-1573, swiglu :726-733) against the oracle chain, at Qwen2.5-1.5B (H 1536,
+I 8960) and Llama-3.1-8B (H 4096, I 14336) shapes.
+
+* W4A8 (q4g256sf for Qwen, q4g64 for Llama): gate and up are bit-exact GEMVs, the SwiGLU is the
+  same float function on both sides (exp rounded once from double), so h equals the oracle's
+  or_swiglu of the oracle's g and u bit for bit, and y equals the oracle's W4A8 down projection
+  of that h bit for bit.
+* fp32 activations (int4 g32 and qNg64 n=5 for Llama, q8g64 for Qwen): h within 1e-5 of the
+  oracle's (max-normalised), y within 1e-5 of the oracle's fp32 down projection of the device's
+  own h, and the whole chain within 1e-5 of the oracle's."""
+import sys
+
+import numpy as np
+import pytest
+
+from golden.fixtures import seeded_normal
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "gpu tests need a GPU"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ctx(torch_dev):
+    import beglin_amd
+    c = beglin_amd.Context(0)
+    yield c
+    c.sync()
+    c.close()
+
+
+def relerr(y, r):
+    y = np.asarray(y, np.float64); r = np.asarray(r, np.float64)
+    return float(np.max(np.abs(y - r)) / max(np.max(np.abs(r)), 1e-30))
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def qdev(ctx, torch, gen, kind, bits, out, inn):
+    w = torch.randn((out, inn), generator=gen, device="cuda") * 0.02
+    t, ref = ctx.quantize(kind, w, bits=bits, want_ref=True)
+    del w
+    return t, ref
+
+
+def run(ctx, torch, ts, x, act):
+    M, H = x.shape
+    I = ts[0].info()["out"]
+    y = torch.full((M, H), float("nan"), device="cuda")
+    h = torch.full((M, I), float("nan"), device="cuda")
+    ctx.mlp(ts[0], ts[1], ts[2], dev(torch, x), y, act=act, h_dev=h)
+    ctx.sync()
+    return y.cpu().numpy(), h.cpu().numpy()
+
+
+W4A8_CASES = [("qwen", 3, 1536, 8960, 1), ("qwen", 3, 1536, 8960, 4), ("llama", 1, 4096, 14336, 1)]
+
+
+@pytest.mark.parametrize("model,kind,H,I,M", W4A8_CASES)
+def test_mlp_w4a8_bitexact(ctx, torch_dev, oracle, model, kind, H, I, M):
+    import beglin_amd
+    torch = torch_dev
+    say("mlp w4a8", model, M)
+    gen = torch.Generator(device="cuda").manual_seed(700 + M + H)
+    shapes = ((I, H), (I, H), (H, I))
+    ts, refs = zip(*[qdev(ctx, torch, gen, kind, 4, o, i) for o, i in shapes])
+    x = seeded_normal(710 + M, (M, H))
+    y, h = run(ctx, torch, ts, x, beglin_amd.ACT_W4A8)
+    g = oracle.matmul_sdot(kind, refs[0][0], refs[0][1], x, sub=refs[0][2])
+    u = oracle.matmul_sdot(kind, refs[1][0], refs[1][1], x, sub=refs[1][2])
+    hr = oracle.swiglu(g, u)
+    assert np.array_equal(h.view(np.uint32), hr.view(np.uint32)), relerr(h, hr)
+    yr = oracle.matmul_sdot(kind, refs[2][0], refs[2][1], hr, sub=refs[2][2])
+    assert np.array_equal(y.view(np.uint32), yr.view(np.uint32)), relerr(y, yr)
+    for t in ts:
+        t.free()
+
+
+F32_CASES = [("llama", 5, 0, 4096, 14336, 1), ("llama", 5, 0, 4096, 14336, 32), ("llama", 4, 5, 4096, 14336, 3),
+             ("qwen", 2, 0, 1536, 8960, 1)]
+
+
+@pytest.mark.parametrize("model,kind,bits,H,I,M", F32_CASES)
+def test_mlp_f32(ctx, torch_dev, oracle, model, kind, bits, H, I, M):
+    import beglin_amd
+    torch = torch_dev
+    say("mlp f32", model, kind, bits, M)
+    gen = torch.Generator(device="cuda").manual_seed(800 + M + H + bits)
+    shapes = ((I, H), (I, H), (H, I))
+    ts, refs = zip(*[qdev(ctx, torch, gen, kind, bits, o, i) for o, i in shapes])
+    x = seeded_normal(810 + M, (M, H))
+    y, h = run(ctx, torch, ts, x, beglin_amd.ACT_F32)
+    g = oracle.gemm_f32(kind, refs[0][0], refs[0][1], x, bits=bits)
+    u = oracle.gemm_f32(kind, refs[1][0], refs[1][1], x, bits=bits)
+    hr = oracle.swiglu(g, u)
+    assert relerr(h, hr) <= TOL
+    assert relerr(y, oracle.gemm_f32(kind, refs[2][0], refs[2][1], h, bits=bits)) <= TOL
+    assert relerr(y, oracle.gemm_f32(kind, refs[2][0], refs[2][1], hr, bits=bits)) <= TOL
+    for t in ts:
+        t.free()
+
+
+def test_mlp_graph_replay_and_refusals(ctx, torch_dev, oracle):
+    """The block captured in a HIP graph replays to the eager result (no host round trip inside);
+    shapes that do not form an MLP are refused before anything is launched."""
+    import beglin_amd
+    torch = torch_dev
+    say("mlp graph + refusals")
+    s = torch.cuda.Stream()
+    c = beglin_amd.Context(0, stream=s.cuda_stream)
+    gen = torch.Generator(device="cuda").manual_seed(900)
+    H, I = 512, 1024
+    ts = [qdev(c, torch, gen, 5, 0, o, i)[0] for o, i in ((I, H), (I, H), (H, I))]
+    x = dev(torch, seeded_normal(901, (1, H)))
+    y = torch.zeros((1, H), device="cuda")
+    with torch.cuda.stream(s):
+        c.mlp(ts[0], ts[1], ts[2], x, y)
+    c.sync()
+    eager = y.cpu().numpy().copy()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        c.mlp(ts[0], ts[1], ts[2], x, y)
+    for r in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy(), eager), r
+    with pytest.raises(beglin_amd.BglError):
+        c.mlp(ts[0], ts[2], ts[2], x, y)                 # up is [H][I]: not an MLP
+    with pytest.raises(beglin_amd.BglError):
+        c.mlp(ts[0], ts[1], ts[0], x, y)                 # down is [I][H]
+    for t in ts:
+        t.free()
+    c.close()

@@ -403,3 +403,43 @@ def test_caller_quantized_sdot_dropins(lib, oracle, kind, M):
     ctx.sync()
     ctx.close()
     del C
+
+
+def test_af_layout_manifest_binds_and_multiplies(R, oracle, tmp_path):
+    """bgl_gpu_load_layout_af (moe_load_layout_af, qwen_infer.c:2496-2515): every record of the
+    manifest is bound as an int4 affine tensor under its name; each expert's product equals the
+    oracle's moe_matvec_af_row, the decode equals moe_decode_af bit for bit, and the named gather
+    and the routed SwiGLU FFN run over the loaded names."""
+    from loader_fixture import build_af
+    say("AF layout manifest")
+    layout, blob, recs = build_af(str(tmp_path), seed=11)
+    assert R.load_layout_af(layout, blob) == len(recs)
+    descs = {}
+    for name, (E, out, inn, codes, sc, bi) in recs.items():
+        assert R.binding_kind(name) == (1, 4), name
+        descs[name] = [(6, 4, codes[e], sc[e], bi[e]) for e in range(E)]
+        x = seeded_normal(1100 + E + out, (inn,))
+        for e in range(E):
+            ok, y = R.matvec_probe(name, e, x, out)
+            assert ok == 1
+            assert relerr(y, moe_matvec(oracle, descs[name][e], out, inn, x)) <= TOL, (name, e)
+        ok, got = R.dequant_probe(name, E - 1, out - 1, 0, inn)
+        assert ok == 1 and np.array_equal(got, moe_decode(oracle, descs[name][E - 1], out, inn, out - 1, range(inn)))
+    g, u, d = "layers.0.mlp.experts.gate", "layers.0.mlp.experts.up", "layers.0.mlp.experts.down"
+    T, K, H, I = 5, 2, 128, 64
+    x = seeded_normal(1200, (T, H))
+    idx, w = oracle.route(seeded_normal(1201, (T, 4)), K, True)
+    out = np.zeros((T, H), np.float32)
+    import ctypes as C
+    ok = R.L().bgl_gpu_moe_ffn(g.encode(), u.encode(), d.encode(), None, None, None, x.ctypes.data, T,
+                               np.ascontiguousarray(idx, np.int32).ctypes.data,
+                               np.ascontiguousarray(w, np.float32).ctypes.data, K, out.ctypes.data)
+    assert ok == 1, R.L().bgl_last_error().decode()
+    ref = moe_ffn(oracle, descs[g], descs[u], descs[d], None, H, I, x, idx, w)
+    assert relerr(out, ref) <= TOL
+    del C
+    # a manifest that fails its checks binds nothing and says why
+    bad = tmp_path / "bad_af.txt"
+    bad.write_text(open(layout).read().replace(" 4 64 128 2 ", " 4 64 128 3 ", 1))
+    assert R.load_layout_af(str(bad), blob) == -1
+    assert "ng" in R.L().bgl_last_error().decode()

@@ -81,3 +81,55 @@ def test_missing_files(model, tmp_path):
     layout, blob, _ = model
     assert check(str(tmp_path / "nope.txt"), blob)[0] < 0
     assert check(layout, str(tmp_path / "nope.bin"))[0] < 0
+
+
+# ---------------------------------------------------------------- the AF layout manifest
+def af_check(layout, blob):
+    import beglin_amd
+    return beglin_amd.af_layout_check(layout, blob.nbytes)
+
+
+def test_af_valid_layout(tmp_path):
+    from loader_fixture import build_af
+    layout, blob, recs = build_af(str(tmp_path))
+    assert af_check(layout, blob) == (0, len(recs))
+
+
+@pytest.mark.parametrize("case", ["ng", "in64", "E0", "out0", "pb_short", "po_past", "so_past", "bo_past", "neg_off",
+                                  "duplicate", "long_name"])
+def test_af_refusals(tmp_path, case):
+    from loader_fixture import build_af
+    layout, blob, _ = build_af(str(tmp_path))
+    wb = blob.nbytes
+
+    def field(i, j, v):
+        def ed(lines):
+            f = lines[i].split()
+            f[j] = str(v)
+            lines[i] = " ".join(f)
+            return lines
+        return ed
+
+    edits = {
+        "ng": field(0, 4, 3), "in64": lambda L: field(0, 3, 96)(field(0, 4, 1)(L)), "E0": field(1, 1, 0),
+        "out0": field(1, 2, 0), "pb_short": field(2, 6, 4 * 128 * 64 // 2 - 1), "po_past": field(3, 5, wb - 64),
+        "so_past": field(3, 7, wb - 64), "bo_past": field(3, 8, wb), "neg_off": field(0, 7, -64),
+        "duplicate": field(2, 0, "lm_head"), "long_name": field(1, 0, "x" * 128),
+    }
+    rewrite(layout, edits[case])
+    rc, _ = af_check(layout, blob)
+    assert rc < 0, case
+
+
+def test_af_limits_and_short_records(tmp_path):
+    from loader_fixture import build_af
+    layout, blob, recs = build_af(str(tmp_path))
+    rewrite(layout, lambda L: L[:2] + ["truncated 4 64"] + L[2:])       # the manifest ends at a short record
+    assert af_check(layout, blob) == (0, 2)
+    rec = open(layout).read().splitlines()[0].split()
+    for n, want in ((1024, (0, 1024)), (1025, None)):
+        with open(layout, "w") as f:
+            f.write("".join(" ".join([f"t{i}"] + rec[1:]) + "\n" for i in range(n)))
+        rc, cnt = af_check(layout, blob)
+        assert (rc, cnt) == want if want else rc < 0
+    assert af_check(str(tmp_path / "missing.txt"), blob)[0] < 0

@@ -646,3 +646,29 @@ def test_pool_moe_ffn_equals_bucketed(oracle):
                                         H, I, Ish, T, K, _ptr(x), _ptr(idx), _ptr(w), _ptr(out))
     oracle.lib.or_pool_destroy(pool)
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_swiglu_pins(oracle):
+    """or_swiglu (swiglu, qwen_infer.c:726-733): against numpy's float64 exp rounded once to float32,
+    then the same float steps (g / (1 + e)) * u; special values; and within 1 ulp of the float-exp
+    form the reference evaluates (moe_swiglu_inplace's expf)."""
+    rng = np.random.default_rng(77)
+    g = np.concatenate([rng.standard_normal(4000).astype(np.float32) * np.float32(4),
+                        np.array([0.0, -0.0, 88.0, -88.0, 104.0, -104.0, 1e-30, -1e-30, np.inf, -np.inf, np.nan], np.float32)])
+    u = rng.standard_normal(g.size).astype(np.float32)
+    u[-11:] = 1.5
+    with np.errstate(all="ignore"):
+        e = np.exp(-g.astype(np.float64)).astype(np.float32)
+        want = (g / (np.float32(1) + e)) * u
+    got = oracle.swiglu(g, u)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)) or np.array_equal(got, want, equal_nan=True)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert got[-11] == 0 and got[-9] == np.float32(88.0) * np.float32(1.5)      # silu(0) = 0; silu(88) ~ 88
+    assert np.isnan(got[-2]) and np.isnan(got[-1])                              # -inf / inf and NaN propagate
+    ref = np.array(g, np.float32)
+    gate = ref.copy()
+    import ctypes as C
+    oracle.lib.or_moe_swiglu_inplace(C.c_void_p(gate.ctypes.data), C.c_void_p(u.ctypes.data), g.size)  # float expf form
+    fin = np.isfinite(got) & np.isfinite(gate)
+    ulp = np.abs(got[fin].view(np.int32).astype(np.int64) - gate[fin].view(np.int32).astype(np.int64))
+    assert ulp.max() <= 2
