@@ -7,8 +7,8 @@ stream.  Every call goes through the HIP library; if it is not built, importing 
 import ctypes as C
 
 from . import capi
-from .capi import (ACT_F32, ACT_W4A8, K_F16, K_F32, K_Q4G32H, K_Q4G64, K_Q4G64A, K_Q4G256SF,  # noqa: F401
-                   K_Q8G64, K_QNG64)
+from .capi import (ACT_F32, ACT_W4A8, K_F16, K_F32, K_MXFP4, K_Q4G32H, K_Q4G64, K_Q4G64A,  # noqa: F401
+                   K_Q4G256SF, K_Q8G64, K_QNG64)
 
 _lib = None
 
@@ -98,7 +98,7 @@ class Context:
     # ---- binding ----
     def bind(self, kind, packed, scales, out, inn, bits=0, sub=None):
         """Bind host (numpy) buffers in the reference layout (sub: g256sf sub-codes or Q4G64A biases;
-        scales None for the dense kinds)."""
+        scales None for the dense kinds and MXFP4, whose blocks carry their exponents)."""
         w = capi.bgl_wt(kind, bits if kind == K_QNG64 else (8 if kind == K_Q8G64 else 4), out, inn,
                         packed.ctypes.data, scales.ctypes.data if scales is not None else None,
                         sub.ctypes.data if sub is not None else None)
@@ -193,6 +193,8 @@ class Context:
             out = pk.shape[0]
             if kind in (K_F16, K_F32):
                 inn = pk.shape[1]
+            elif kind == K_MXFP4:                # GGUF blocks of 32 values, 17 bytes each
+                inn = pk.reshape(out, -1).shape[1] // 17 * 32
             else:
                 inn = sc.shape[1] * (32 if kind == K_Q4G32H else 64)
             b = bits if kind == K_QNG64 else (8 if kind == K_Q8G64 else 4)

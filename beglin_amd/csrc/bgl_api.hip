@@ -250,7 +250,7 @@ extern "C" void *bgl_ctx_stream(bgl_ctx *c) { return c ? (void *)c->stream : nul
 // ------------------------------------------------------------------ tensors
 static int units_of(int kind, int in) {
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q8G64: case BGL_Q4G64A: case BGL_F16: case BGL_F32: return in / 64;
+    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q8G64: case BGL_Q4G64A: case BGL_F16: case BGL_F32: case BGL_MXFP4: return in / 64;
     case BGL_Q4G256SF: return in / 256;
     case BGL_QNG64: return (in / 64 + 1) / 2;
     default: return 0;
@@ -264,7 +264,8 @@ int check_wt(int kind, int bits, int out, int in) {
         if (in % 64) return bgl_fail(BGL_E_ARG, "in=%d %% 64 != 0", in);
         if (kind == BGL_QNG64 && (bits < 2 || bits > 15)) return bgl_fail(BGL_E_ARG, "qNg64 n=%d outside 2..15", bits);
         return 0;
-    case BGL_Q4G32H: case BGL_Q4G64A: case BGL_F16: case BGL_F32:
+    case BGL_Q4G32H: case BGL_Q4G64A: case BGL_F16: case BGL_F32: case BGL_MXFP4:
+        // MXFP4 blocks hold 32 values; the gather works in 64-groups (two blocks)
         if (in % 64) return bgl_fail(BGL_E_ARG, "kind %d: in=%d %% 64 != 0", kind, in);
         return 0;
     case BGL_Q4G256SF:
@@ -281,6 +282,7 @@ static size_t ref_packed_bytes(int kind, int bits, int out, int in) {
     case BGL_F16: return (size_t)out * in * 2;
     case BGL_F32: return (size_t)out * in * 4;
     case BGL_QNG64: return (size_t)out * (in / 64) * bits * 8;
+    case BGL_MXFP4: return (size_t)out * (in / 32) * 17;
     default: return 0;
     }
 }
@@ -347,7 +349,7 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     t->device_bytes = wbytes + s0bytes + (s1 ? (size_t)rows * T.nunits * 4 : 0);
     long nch = rows * T.cpr;
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q4G256SF: case BGL_Q4G64A:
+    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q4G256SF: case BGL_Q4G64A: case BGL_MXFP4:
         // g256sf is only read by the int8-activation kernels, which take its codes as signed nibbles
         hipLaunchKernelGGL(k_repack_nib, dim3(nblk(nch)), dim3(256), 0, c->stream, (const uint8_t *)dpk, out, in,
                            kind == BGL_Q4G256SF ? 0x88888888u : 0u, (uint8_t *)w);
@@ -362,8 +364,8 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     }
     long nu = rows * T.nunits;
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q8G64: case BGL_Q4G32H: case BGL_Q4G64A:
-        // Q4G32H: two fp16 per unit read as one u32; the others one fp32 per unit.
+    case BGL_Q4G64: case BGL_Q8G64: case BGL_Q4G32H: case BGL_Q4G64A: case BGL_MXFP4:
+        // Q4G32H: two fp16 per unit read as one u32; MXFP4: the two exponent bytes; the others one fp32.
         hipLaunchKernelGGL(k_repack_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsc, out, T.nunits, (uint32_t *)s0);
         if (has_s1)   // Q4G64A: the fp32 bias per unit
             hipLaunchKernelGGL(k_repack_u32, dim3(nblk(nu)), dim3(256), 0, c->stream, (const uint32_t *)dsub, out, T.nunits, (uint32_t *)s1);
@@ -382,11 +384,49 @@ static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const vo
     return 0;
 }
 
+// MXFP4 blocks [out][in/32][17] (exponent byte, then 16 bytes whose byte j holds value j in its
+// low nibble and value j+16 in its high nibble) -> codes [out][in/2] in the reference q4 order
+// (byte b: value 2b low, 2b+1 high) and one u32 per 64-unit with its two exponent bytes; then
+// the q4 repacks.
+__global__ void k_split_mxfp4(const uint8_t *__restrict__ blk, int out, int in, uint8_t *__restrict__ codes,
+                              uint32_t *__restrict__ ex) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x, nu = (long)out * (in / 64);
+    if (i >= nu) return;
+    const uint8_t *b = blk + i * 34;                 // two blocks per unit, consecutive within a row
+    uint8_t *d = codes + i * 32;
+    auto code = [&](int h, int p) {                  // value p (0..31) of block h
+        const uint8_t q = b[17 * h + 1 + (p & 15)];
+        return p < 16 ? q & 15 : q >> 4;
+    };
+    for (int h = 0; h < 2; h++)
+        for (int j = 0; j < 16; j++) d[16 * h + j] = (uint8_t)(code(h, 2 * j) | (code(h, 2 * j + 1) << 4));
+    ex[i] = (uint32_t)b[0] | ((uint32_t)b[17] << 8);
+}
+
+static int bind_mxfp4(bgl_ctx *c, const bgl_wt *w, bgl_tensor **out) {
+    HIPCHK(hipSetDevice(c->device));
+    const size_t pb = ref_packed_bytes(BGL_MXFP4, 4, w->out, w->in), nu = (size_t)w->out * (w->in / 64);
+    void *dblk = nullptr, *dcodes = nullptr, *dex = nullptr;
+    HIPCHK(hipMalloc(&dblk, pb));
+    HIPCHK(hipMalloc(&dcodes, nu * 32));
+    HIPCHK(hipMalloc(&dex, nu * 4));
+    HIPCHK(hipMemcpyAsync(dblk, w->packed, pb, hipMemcpyHostToDevice, c->stream));
+    hipLaunchKernelGGL(k_split_mxfp4, dim3(nblk((long)nu)), dim3(256), 0, c->stream, (const uint8_t *)dblk, w->out, w->in,
+                       (uint8_t *)dcodes, (uint32_t *)dex);
+    int rc = repack_into(c, BGL_MXFP4, 4, w->out, w->in, dcodes, dex, nullptr, out);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    (void)hipFree(dblk); (void)hipFree(dcodes); (void)hipFree(dex);
+    if (rc) return rc;
+    if (e != hipSuccess) return bgl_fail(BGL_E_HIP, "bind sync: %s", hipGetErrorString(e));
+    return 0;
+}
+
 extern "C" int bgl_bind(bgl_ctx *c, const bgl_wt *w, bgl_tensor **out) {
     if (!c || !w || !out || !w->packed) return bgl_fail(BGL_E_ARG, "bgl_bind: NULL argument");
     int rc = check_wt(w->kind, w->bits, w->out, w->in);
     if (rc) return rc;
     const bool dense = w->kind == BGL_F16 || w->kind == BGL_F32;
+    if (w->kind == BGL_MXFP4) return bind_mxfp4(c, w, out);
     if (!dense && !w->scales) return bgl_fail(BGL_E_ARG, "bgl_bind: kind %d needs scales", w->kind);
     if (w->kind == BGL_Q4G256SF && !w->sub) return bgl_fail(BGL_E_ARG, "bgl_bind: g256sf needs sub-codes");
     if (w->kind == BGL_Q4G64A && !w->sub) return bgl_fail(BGL_E_ARG, "bgl_bind: int4 affine needs biases (sub)");
@@ -470,7 +510,7 @@ extern "C" int bgl_quantize_dev(bgl_ctx *c, int kind, int bits, int qng64_encode
     if (!c || !w_dev || !t) return bgl_fail(BGL_E_ARG, "bgl_quantize_dev: NULL argument");
     int rc = check_wt(kind, bits, out, in);
     if (rc) return rc;
-    if (kind == BGL_Q4G64A || kind == BGL_F16 || kind == BGL_F32)
+    if (kind == BGL_Q4G64A || kind == BGL_F16 || kind == BGL_F32 || kind == BGL_MXFP4)
         return bgl_fail(BGL_E_UNSUPPORTED, "bgl_quantize_dev: kind %d has no packer here (bind its bytes with bgl_bind)", kind);
     if (kind == BGL_QNG64 && qng64_encoder && bits == 4)
         return bgl_fail(BGL_E_ARG, "qng64_quantize_f32 rejects n=4 (qng64_dense.c:9)");
@@ -828,7 +868,7 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
             return bgl_fail(BGL_E_ARG, "bgl_matmul_group_dev: fused tensors must share kind, bits and in");
     }
     const int kind = Ts[0].fmt;
-    if (kind == BGL_Q4G64A || kind == BGL_F16 || kind == BGL_F32)
+    if (kind == BGL_Q4G64A || kind == BGL_F16 || kind == BGL_F32 || kind == BGL_MXFP4)
         return bgl_fail(BGL_E_UNSUPPORTED, "kind %d runs in the MoE gather only (bgl_gather_matvec_dev / bgl_moe_ffn_dev)", kind);
     if (kind == BGL_Q4G256SF && act != BGL_ACT_W4A8)
         return bgl_fail(BGL_E_UNSUPPORTED, "K_Q4G256SF requires W4A8 activations -- no fp32-activation path exists for g256sf");
@@ -896,7 +936,7 @@ extern "C" int bgl_prep_act_dev(bgl_ctx *c, int act, int kind, const float *x_de
 extern "C" int bgl_matmul_prepped_dev(bgl_ctx *c, const bgl_tensor *w, int act, const float *bias_dev, float *y_dev, int M) {
     if (!c || !w || !y_dev || !w->experts.empty()) return bgl_fail(BGL_E_ARG, "bgl_matmul_prepped_dev: bad argument");
     const BglDevTensor &T = w->T;
-    if (T.fmt == BGL_Q4G64A || T.fmt == BGL_F16 || T.fmt == BGL_F32)
+    if (T.fmt == BGL_Q4G64A || T.fmt == BGL_F16 || T.fmt == BGL_F32 || T.fmt == BGL_MXFP4)
         return bgl_fail(BGL_E_UNSUPPORTED, "kind %d runs in the MoE gather only", T.fmt);
     if (c->prep_act != act || c->prep_K != T.K || c->prep_gq != act_group(T.fmt) || M > c->prep_M)
         return bgl_fail(BGL_E_ARG, "bgl_matmul_prepped_dev: no prepared activation matches (act %d, in %d, M %d)", act, T.K, M);

@@ -28,6 +28,7 @@
 #define BGL_Q4G64A BGL_K_Q4G64A
 #define BGL_F16 BGL_K_F16
 #define BGL_F32 BGL_K_F32
+#define BGL_MXFP4 BGL_K_MXFP4
 
 // fp32 activations as exact integers, per 64-group:
 //   level 0: X = rint(x * 2^(21-e)), e = exponent of the group's largest finite |x| (|X| <= 2^21),
@@ -106,6 +107,21 @@ __device__ __forceinline__ int nib_lo(uint32_t w) { return (int)(w & 0x0F0F0F0Fu
 __device__ __forceinline__ int nib_hi(uint32_t w) { return (int)((w >> 4) & 0x0F0F0F0Fu); }
 
 __device__ __forceinline__ uint4 ldg16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// MXFP4 (OCP microscaling FP4 in GGUF blocks of 32): an E2M1 nibble's value doubled -- 0, 1, 2, 3,
+// 4, 6, 8, 12 for codes 0..7 and the same negated for 8..15 -- times an E8M0 exponent byte b read
+// as 2^(b-128), i.e. the exponent halved to undo the doubling (gguf_quants.c:284-305).  Both
+// factors are exact, so every weight is an exact float.
+__device__ __forceinline__ float mx_scale(uint32_t b) { return __uint_as_float(b < 2u ? (0x00200000u << b) : (b - 1u) << 23); }
+// Four codes (one per byte, bits 0..3) -> their four doubled values as int8: magnitude and
+// negated magnitude by byte permutes over the low three bits, picked per byte by the fourth.
+__device__ __forceinline__ int mx_codes(uint32_t c) {
+    const uint32_t idx = c & 0x07070707u;
+    const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, idx);
+    const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, idx);
+    const uint32_t m = ((c >> 3) & 0x01010101u) * 0xFFu;
+    return (int)((neg & m) | (pos & ~m));
+}
 
 // qNg64 field decomposition: n = 8a + 4b + 2c + d; field widths in descending order occupy
 // consecutive bits of the biased code u = code + 2^(n-1) from bit 0 upwards.

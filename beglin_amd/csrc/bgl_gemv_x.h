@@ -37,6 +37,7 @@ __device__ __forceinline__ uint32_t x_and_or(uint32_t a, uint32_t m, uint32_t o)
 template <int FMT, int NB> struct XRaw;
 template <int NB> struct XRaw<BGL_Q4G64, NB> { uint4 c[2]; float s; };
 template <int NB> struct XRaw<BGL_Q4G32H, NB> { uint4 c[2]; uint32_t s; };
+template <int NB> struct XRaw<BGL_MXFP4, NB> { uint4 c[2]; uint32_t s; };
 template <int NB> struct XRaw<BGL_Q8G64, NB> { uint4 c[4]; float s; };
 template <int NB> struct XRaw<BGL_QNG64, NB> {
     static constexpr int H8 = (NB >> 3) & 1, H4 = (NB >> 2) & 1, H2 = (NB >> 1) & 1, H1 = NB & 1;
@@ -138,7 +139,7 @@ __device__ __forceinline__ void x_load(XRaw<FMT, NB> &r, const XRes &R, const XL
         for (int k = 0; k < CPU; k++) r.c[k] = ld(l.p8, wo + 1024u * k);
         sv = __builtin_amdgcn_raw_buffer_load_b32(S, l.s, R.stile + su * 256u, 0);
     }
-    if constexpr (FMT == BGL_Q4G32H) r.s = sv;
+    if constexpr (FMT == BGL_Q4G32H || FMT == BGL_MXFP4) r.s = sv;
     else r.s = __uint_as_float(sv);
 }
 
@@ -166,6 +167,7 @@ __device__ __forceinline__ XDig x_digit(const int *rec, int d) {
 template <int FMT, int NB> struct XDec;
 template <int NB> struct XDec<BGL_Q4G64, NB> { int lo[8], hi[8]; float s; };
 template <int NB> struct XDec<BGL_Q4G32H, NB> { int lo[8], hi[8]; float sa, sb; };
+template <int NB> struct XDec<BGL_MXFP4, NB> { int lo[8], hi[8]; float sa, sb; };   // codes as signed int8
 template <int NB> struct XDec<BGL_Q8G64, NB> { int w[16]; float s; };
 template <int NB> struct XDec<BGL_QNG64, NB> {
     static constexpr int H8 = (NB >> 3) & 1, H4 = (NB >> 2) & 1, H2 = (NB >> 1) & 1, H1 = NB & 1;
@@ -177,7 +179,13 @@ template <int NB> struct XDec<BGL_QNG64, NB> {
 template <int FMT, int NB>
 __device__ __forceinline__ XDec<FMT, NB> x_decode(const XRaw<FMT, NB> &r) {
     XDec<FMT, NB> d;
-    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H) {
+    if constexpr (FMT == BGL_MXFP4) {
+        const uint32_t raw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w};
+#pragma unroll
+        for (int q = 0; q < 8; q++) { d.lo[q] = mx_codes((uint32_t)nib_lo(raw[q])); d.hi[q] = mx_codes((uint32_t)nib_hi(raw[q])); }
+        d.sa = mx_scale(r.s & 255u);
+        d.sb = mx_scale((r.s >> 8) & 255u);
+    } else if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H) {
         const uint32_t raw[8] = {r.c[0].x, r.c[0].y, r.c[0].z, r.c[0].w, r.c[1].x, r.c[1].y, r.c[1].z, r.c[1].w};
 #pragma unroll
         for (int q = 0; q < 8; q++) { d.lo[q] = nib_lo(raw[q]); d.hi[q] = nib_hi(raw[q]); }
@@ -239,7 +247,7 @@ __device__ __forceinline__ XDec<FMT, NB> x_decode(const XRaw<FMT, NB> &r) {
 template <int FMT, int NB>
 __device__ __forceinline__ void x_ints(const XDec<FMT, NB> &w, const int *rec, const int4 &ds0, const int4 &ds1, int (&o)[6]) {
     // cold path only: one digit at a time (unrolled, the three digits' LDS reads are hoisted together)
-    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H) {
+    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H || FMT == BGL_MXFP4) {
         int ta[3], tb[3];
 #pragma unroll 1
         for (int d = 0; d < 3; d++) {
@@ -254,6 +262,8 @@ __device__ __forceinline__ void x_ints(const XDec<FMT, NB> &w, const int *rec, c
         if constexpr (FMT == BGL_Q4G64) {
             o[0] = ta[0] + tb[0] - 8 * (ds0.x + ds1.x); o[1] = ta[1] + tb[1] - 8 * (ds0.y + ds1.y);
             o[2] = ta[2] + tb[2] - 8 * (ds0.z + ds1.z);
+        } else if constexpr (FMT == BGL_MXFP4) {     // signed codes: no bias correction
+            o[0] = ta[0]; o[1] = ta[1]; o[2] = ta[2]; o[3] = tb[0]; o[4] = tb[1]; o[5] = tb[2];
         } else {
             o[0] = ta[0] - 8 * ds0.x; o[1] = ta[1] - 8 * ds0.y; o[2] = ta[2] - 8 * ds0.z;
             o[3] = tb[0] - 8 * ds1.x; o[4] = tb[1] - 8 * ds1.y; o[5] = tb[2] - 8 * ds1.z;
@@ -302,7 +312,7 @@ __device__ __forceinline__ float x_dot(const XDec<FMT, NB> &w, const int *rec) {
     const int4 ds0 = *reinterpret_cast<const int4 *>(rec + XREC_DSUM);
     const int4 ds1 = *reinterpret_cast<const int4 *>(rec + XREC_DSUM + 4);
     const float xs = *reinterpret_cast<const float *>(rec + XREC_SCALE);
-    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H) {
+    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H || FMT == BGL_MXFP4) {
         int ta[3], tb[3];
 #pragma unroll
         for (int d = 0; d < 3; d++) {
@@ -318,6 +328,8 @@ __device__ __forceinline__ float x_dot(const XDec<FMT, NB> &w, const int *rec) {
             const float V = fold_digits(ta[0] + tb[0] - 8 * (ds0.x + ds1.x), ta[1] + tb[1] - 8 * (ds0.y + ds1.y),
                                         ta[2] + tb[2] - 8 * (ds0.z + ds1.z));
             return w.s * (V * xs);
+        } else if constexpr (FMT == BGL_MXFP4) {
+            return w.sa * (fold_digits(ta[0], ta[1], ta[2]) * xs) + w.sb * (fold_digits(tb[0], tb[1], tb[2]) * xs);
         } else {
             const float Va = fold_digits(ta[0] - 8 * ds0.x, ta[1] - 8 * ds0.y, ta[2] - 8 * ds0.z);
             const float Vb = fold_digits(tb[0] - 8 * ds1.x, tb[1] - 8 * ds1.y, tb[2] - 8 * ds1.z);
@@ -372,7 +384,7 @@ __device__ __forceinline__ float x_fix(const XDec<FMT, NB> &w, const int *rec, c
         int p[6];
         x_ints<FMT, NB>(w, r1, e0, e1, p);
         const float rt = (fl & BGL_XF_L1) ? xs.y : 0.0f;      // other lanes' level-1 data is not theirs: 0
-        if constexpr (FMT == BGL_Q4G32H)
+        if constexpr (FMT == BGL_Q4G32H || FMT == BGL_MXFP4)
             t = w.sa * ((fold_digits(p[0], p[1], p[2]) * rt) * xs.x) + w.sb * ((fold_digits(p[3], p[4], p[5]) * rt) * xs.x);
         else
             t = w.s * ((fold_digits(p[0], p[1], p[2]) * rt) * xs.x);

@@ -9,6 +9,8 @@
 //           sub s), one load per unit; codes stored as signed nibbles (code ^ 8)
 //   Q8G64   64 elements, 4 chunks, s0 = fp32 scale
 //   QNG64   128 elements (a pair of 64-groups), n chunks, s0 = float2 (the two group scales)
+//   MXFP4   64 elements (two GGUF blocks), 2 chunks (Q4G64's nibble order), s0 = u32 holding the
+//           two E8M0 exponent bytes (low = first block)
 struct BglDevTensor {
     int fmt, bits, N, K, ntiles, cpr, nunits, cpu;   // cpu: chunks per unit
     const uint8_t *w;
@@ -58,7 +60,7 @@ __device__ __forceinline__ float w_at(const BglDevTensor &T, int r, int c) {
         const uint8_t *p = T.w + (((size_t)tile * T.cpr + c / per) * BGL_TILE + lane) * 16 + (c % per) * esz;
         if (T.fmt == BGL_F16) v = __half2float(__ushort_as_half(*reinterpret_cast<const unsigned short *>(p)));
         else v = *reinterpret_cast<const float *>(p);
-    } else if (T.fmt == BGL_Q4G64 || T.fmt == BGL_Q4G32H || T.fmt == BGL_Q4G256SF || T.fmt == BGL_Q4G64A) {
+    } else if (T.fmt == BGL_Q4G64 || T.fmt == BGL_Q4G32H || T.fmt == BGL_Q4G256SF || T.fmt == BGL_Q4G64A || T.fmt == BGL_MXFP4) {
         int chunk = c / 32, e = c % 32, j = e / 8, q = e % 8;
         const uint8_t *p = T.w + (((size_t)tile * T.cpr + chunk) * BGL_TILE + lane) * 16 + 4 * j;
         int nib = q < 4 ? (p[q] & 15) : (p[q - 4] >> 4);
@@ -75,6 +77,10 @@ __device__ __forceinline__ float w_at(const BglDevTensor &T, int r, int c) {
             uint32_t s2 = reinterpret_cast<const uint32_t *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
             uint16_t h = (uint16_t)(((c / 32) & 1) ? (s2 >> 16) : (s2 & 0xffff));
             v = (float)(nib - 8) * __half2float(__ushort_as_half(h));
+        } else if (T.fmt == BGL_MXFP4) {
+            // moe_decode_af's MXFP4 arm (qwen_infer.c:2584-2595): kvalues[nib] * e8m0_half(block byte)
+            uint32_t s2 = reinterpret_cast<const uint32_t *>(T.s0)[((size_t)tile * T.nunits + c / 64) * BGL_TILE + lane];
+            v = (float)(int8_t)(mx_codes((uint32_t)nib) & 255) * mx_scale((s2 >> (8 * ((c / 32) & 1))) & 255u);
         } else {
             size_t o = ((size_t)tile * T.nunits + c / 256) * BGL_TILE + lane;
             const uint2 wsub = reinterpret_cast<const uint2 *>(T.s0)[o];
@@ -101,7 +107,7 @@ __device__ __forceinline__ float w_at(const BglDevTensor &T, int r, int c) {
 template <int FMT, int NB>
 __device__ __forceinline__ float w_at_t(const BglDevTensor &T, int r, int c) {
     const uint32_t tile = (uint32_t)r / BGL_TILE, lane = (uint32_t)r % BGL_TILE;
-    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H || FMT == BGL_Q4G64A) {
+    if constexpr (FMT == BGL_Q4G64 || FMT == BGL_Q4G32H || FMT == BGL_Q4G64A || FMT == BGL_MXFP4) {
         const uint32_t e = (uint32_t)c % 32u, j = e / 8u, q = e % 8u;
         const uint8_t b = T.w[((tile * (uint32_t)T.cpr + (uint32_t)c / 32u) * BGL_TILE + lane) * 16u + 4u * j + (q & 3u)];
         const int nib = q < 4 ? (b & 15) : (b >> 4);
@@ -110,6 +116,9 @@ __device__ __forceinline__ float w_at_t(const BglDevTensor &T, int r, int c) {
             return __fadd_rn(__fmul_rn((float)nib, reinterpret_cast<const float *>(T.s0)[so]), reinterpret_cast<const float *>(T.s1)[so]);
         else if constexpr (FMT == BGL_Q4G64)
             return (float)(nib - 8) * reinterpret_cast<const float *>(T.s0)[so];
+        else if constexpr (FMT == BGL_MXFP4)
+            return (float)(int8_t)(mx_codes((uint32_t)nib) & 255) *
+                   mx_scale((reinterpret_cast<const uint32_t *>(T.s0)[so] >> (8u * (((uint32_t)c / 32u) & 1u))) & 255u);
         else {
             const uint32_t s2 = reinterpret_cast<const uint32_t *>(T.s0)[so];
             return (float)(nib - 8) * __half2float(__ushort_as_half((unsigned short)((((uint32_t)c / 32u) & 1u) ? (s2 >> 16) : (s2 & 0xffffu))));

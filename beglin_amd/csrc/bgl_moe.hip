@@ -436,6 +436,15 @@ static int moe_run(bgl_ctx *c, MoeTask &Mt, const bgl_tensor *sa, const bgl_tens
         HIPCHK(hipGetLastError());
         return 0;
     }
+    // k_moe_gemv has no MXFP4 arm: such a launch (an MXFP4 expert beside an AF int4 or dense one, or
+    // BGL_NO_MOE_X) is refused rather than run with that expert's tiles skipped
+    bool mx = !Mt.ta && (Mt.da.fmt == BGL_MXFP4 || (Mt.swiglu && Mt.db.fmt == BGL_MXFP4));
+    for (const bgl_tensor *st : {sa, sb})
+        if (st)
+            for (const bgl_tensor *e : st->experts) mx = mx || e->T.fmt == BGL_MXFP4;
+    if (mx)
+        return bgl_fail(BGL_E_UNSUPPORTED, "MXFP4 experts run in the in-kernel-digit gather only; this launch also holds "
+                        "AF int4 / dense experts (or BGL_NO_MOE_X is set)");
     if (memo.x != x_rows || memo.K != K) {
         int rc = moe_prep(c, slot, x_rows, nrows, K, memo.A);
         if (rc) return rc;

@@ -1,6 +1,7 @@
 // bgl_moe_x.hip -- the expert-sorted MoE gather GEMV over LDS activation records (the gate+up with
 // SwiGLU and down projections of moe_ffn_batched, qwen_infer.c:5238-5350, and the routed gather
-// of mlx_moe.cpp's gather_qmm), for experts in int4 g64, int4 g32 fp16-scale, int8 g64 or qNg64.
+// of mlx_moe.cpp's gather_qmm), for experts in int4 g64, int4 g32 fp16-scale, int8 g64, qNg64 or
+// MXFP4.
 //
 // A workgroup owns one 64-row tile of one expert (gate and up rows together in SwiGLU mode; lane =
 // row) and walks the expert's sorted segment in chunks of up to 4 token columns, or up to 8 where
@@ -19,7 +20,9 @@
 #define MX_DEPTH 2               // items (a group of one tensor) a wave keeps in flight
 #define MX_MAXW 16               // waves per workgroup (instances of 8 and 16)
 
-bool bgl_moe_x_fmt(int fmt) { return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64; }
+bool bgl_moe_x_fmt(int fmt) {
+    return fmt == BGL_Q4G64 || fmt == BGL_Q4G32H || fmt == BGL_Q8G64 || fmt == BGL_QNG64 || fmt == BGL_MXFP4;
+}
 
 // LDS: cap columns of records (K/64 rounded up to whole slots of 64/TR groups), the wave partials
 // (MX_MB columns per wave), and one slot of level-1 records per wave (cold path).
@@ -259,6 +262,7 @@ __device__ __forceinline__ void moe_x_body(const MoeTask &Mt, int bid, int *xl) 
     const BglDevTensor Tb = glu ? (Mt.tb ? mx_tensor(Mt.tb + e) : Mt.db) : Ta;
     switch (Ta.fmt) {
     case BGL_Q4G32H: moe_x_tile<BGL_Q4G32H, 0, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
+    case BGL_MXFP4: moe_x_tile<BGL_MXFP4, 0, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
     case BGL_Q4G64: moe_x_tile<BGL_Q4G64, 0, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
     case BGL_Q8G64: moe_x_tile<BGL_Q8G64, 0, TR>(Mt, Ta, Tb, glu, tile, r0, seg0, ncols, xl); break;
     case BGL_QNG64:

@@ -540,9 +540,34 @@ void or_matmul_sdot(int kind, const void *packed, const float *scales, const uin
  * columns left to right; the per-format weight value is the fp32 decode (q4 sym:
  * ((float)nib - 8.0f) * scale; int8: (float)code * scale; qNg64: (float)(u - 2^(n-1)) * scale).
  * Q4G32H has no MoE decoder in the reference; its value is dequant_row_q4_0's. */
+/* MXFP4 (gguf_quants.c:284-312): E2M1 values doubled, and the E8M0 exponent byte as 2^(b-128)
+ * (b < 2: the subnormal bit patterns 2^-128, 2^-127). */
+static const int8_t or_mx_values[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+float or_mx_scale(uint8_t b) {
+    uint32_t bits = b < 2 ? 0x00200000u << b : (uint32_t)(b - 1) << 23;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+int or_mx_value(int code) { return or_mx_values[code & 15]; }
+
 double or_moe_row(const or_expert *w, int in, long row, const float *x) {
     int ng = in / G64;
     double acc = 0.0;
+    if (w->kind == 9) {                        /* MXFP4 arm, qwen_infer.c:2702-2725 */
+        const long rb = (long)(in / 32) * 17;
+        const uint8_t *pr = (const uint8_t *)w->packed + (size_t)row * rb;
+        for (long b = 0; b < in / 32; b++) {
+            const uint8_t *blk = pr + b * 17;
+            float scale = or_mx_scale(blk[0]);
+            long c0 = b * 32;
+            for (int j = 0; j < 16; j++) {
+                float w0 = (float)or_mx_value(blk[1 + j] & 15) * scale, w1 = (float)or_mx_value(blk[1 + j] >> 4) * scale;
+                acc += (double)w0 * x[c0 + j] + (double)w1 * x[c0 + j + 16];
+            }
+        }
+        return acc;
+    }
     if (w->kind == 8) {                        /* bits==32 arm, qwen_infer.c:2674-2682 */
         const float *pr = (const float *)w->packed + (size_t)row * in;
         for (int c = 0; c < in; c++) acc += (double)pr[c] * x[c];
@@ -613,6 +638,11 @@ double or_moe_row(const or_expert *w, int in, long row, const float *x) {
 float or_moe_decode(const or_expert *w, int in, long row, long col) {
     int ng = in / G64;
     long g = col / G64;
+    if (w->kind == 9) {                        /* MXFP4 arm, qwen_infer.c:2584-2595 */
+        const uint8_t *blk = (const uint8_t *)w->packed + (size_t)row * (in / 32) * 17 + (size_t)(col / 32) * 17;
+        int p = (int)(col % 32), q = blk[1 + (p & 15)];
+        return (float)or_mx_value(p < 16 ? q & 15 : q >> 4) * or_mx_scale(blk[0]);
+    }
     if (w->kind == 8) return ((const float *)w->packed)[(size_t)row * in + col];
     if (w->kind == 7) return or_f16_to_f32(((const uint16_t *)w->packed)[(size_t)row * in + col]);
     if (w->kind == 2)

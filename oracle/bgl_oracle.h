@@ -88,7 +88,8 @@ void or_matmul_sdot(int kind, const void *packed, const float *scales, const uin
 
 /* ---------------- MoE ---------------- */
 typedef struct {
-    int kind;            /* 1 q4g64 (sym), 2 q8g64, 4 qNg64, 5 q4g32h, 6 int4 affine, 7 fp16, 8 fp32 */
+    int kind;            /* 1 q4g64 (sym), 2 q8g64, 4 qNg64, 5 q4g32h, 6 int4 affine, 7 fp16, 8 fp32,
+                            9 MXFP4 (GGUF blocks [out][in/32][17]) */
     int bits;            /* qNg64 n */
     const void *packed;
     const void *scales;  /* fp32, or fp16 bits for q4g32h; unused for 7 / 8 */
@@ -96,6 +97,8 @@ typedef struct {
 } or_expert;
 
 double or_moe_row(const or_expert *w, int in, long row, const float *x);
+float or_mx_scale(uint8_t b);
+int or_mx_value(int code);
 float or_moe_decode(const or_expert *w, int in, long row, long col);
 void or_moe_matvec(const or_expert *w, int out, int in, const float *x, float *y);
 void or_moe_softmax_full(float *x, int n);

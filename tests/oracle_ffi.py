@@ -330,3 +330,10 @@ def mixed_qng64_py_decode(planes, offsets, bits, scales, out, inn):
         r, g = divmod(cell, ng)
         w[r, g * 64:(g + 1) * 64] = code * scales[cell]
     return w
+
+
+def mxfp4_blocks(rng, out, inn, lo=116, hi=132):
+    """Random GGUF MXFP4 blocks [out][inn/32][17]: exponent bytes in [lo, hi), random nibbles."""
+    b = rng.integers(0, 256, (out, inn // 32, 17), dtype=np.uint8)
+    b[:, :, 0] = rng.integers(lo, hi, (out, inn // 32), dtype=np.uint8)
+    return b

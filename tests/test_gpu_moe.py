@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from golden.fixtures import gate9, seeded_normal
-from oracle_ffi import moe_ffn, moe_matvec
+from oracle_ffi import moe_decode, moe_ffn, moe_matvec, mxfp4_blocks
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -67,6 +67,9 @@ def desc(oracle, kind, bits, w):
         return (6, 4, pk, sc, bi)
     if kind == 7:
         return (7, 16, w.astype(np.float16).view(np.uint16), None)
+    if kind == 9:                                   # GGUF MXFP4 blocks: any bytes are valid
+        rng = np.random.default_rng(int(abs(w[0, 0]) * 1e9) % (2 ** 31))
+        return (9, 4, mxfp4_blocks(rng, w.shape[0], w.shape[1], 118, 124), None)
     if kind == 8:
         return (8, 32, np.ascontiguousarray(w), None)
     if kind == 1:
@@ -85,7 +88,7 @@ def dev(torch, a):
 
 
 FORMATS = [(5, 0), (1, 0), (2, 0), (4, 2), (4, 3), (4, 5), (4, 7), (4, 8), (4, 9), (4, 12), (4, 15), (6, 4), (7, 16),
-           (8, 32)]
+           (8, 32), (9, 4)]
 
 
 @pytest.mark.parametrize("kind,bits", FORMATS)
@@ -172,7 +175,10 @@ def moe_setup(oracle, seed, E, H, I, Ish, fmts, down_fmts=None, sh_fmt=(5, 0)):
 
 def bind_one(ctx, d):
     k, b, p, sc = d[:4]
-    inn = p.shape[1] if k in (7, 8) else sc.shape[1] * (32 if k == 5 else 64)
+    if k == 9:                                      # MXFP4: blocks of 32 values, 17 bytes each
+        inn = p.reshape(p.shape[0], -1).shape[1] // 17 * 32
+    else:
+        inn = p.shape[1] if k in (7, 8) else sc.shape[1] * (32 if k == 5 else 64)
     return ctx.bind(k, p, sc, p.shape[0], inn, bits=b, sub=d[4] if len(d) > 4 else None)
 
 
@@ -569,3 +575,84 @@ def test_moe_x_column_groups(torch_dev, oracle, monkeypatch, T, tr):
         monkeypatch.delenv(k, raising=False)
     ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
     assert relerr(outs[0], ref) <= TOL and relerr(outs[1], ref) <= TOL and relerr(outs[0], outs[1]) <= 2 * TOL
+
+
+# ---------------------------------------------------------------- MXFP4 experts (AF bits = 40)
+def test_mxfp4_decode_bitexact(ctx, torch_dev, oracle):
+    """moe_decode_af's MXFP4 arm (qwen_infer.c:2584-2595) from the device layout, every exponent
+    byte (the subnormal 0 / 1 and the overflowing 255 included) and every code: bit for bit."""
+    torch = torch_dev
+    import beglin_amd
+    say("mxfp4 decode")
+    out, inn = 72, 512
+    rng = np.random.default_rng(90)
+    blk = mxfp4_blocks(rng, out, inn, 0, 256)
+    blk[0, :, 0] = np.arange(16, dtype=np.uint8); blk[1, :, 0] = 255 - np.arange(16, dtype=np.uint8)
+    t = ctx.bind(beglin_amd.K_MXFP4, blk, None, out, inn)
+    y = torch.zeros((out, inn), dtype=torch.float32, device="cuda")
+    ctx.dequant(t, 0, out, y)
+    ctx.sync()
+    got = y.cpu().numpy()
+    desc_ = (9, 4, blk, None)
+    for r in range(out):
+        want = moe_decode(oracle, desc_, out, inn, r, range(inn))
+        assert np.array_equal(got[r].view(np.uint32), want.view(np.uint32)), r
+    t.free()
+
+
+@pytest.mark.parametrize("T", [1, 6, 21])
+def test_mxfp4_moe_ffn(ctx, torch_dev, oracle, T):
+    """The routed SwiGLU FFN with MXFP4 experts beside q4g32h and qNg64 ones (one gather launch
+    serves every format), shared experts in MXFP4, against the oracle's bucketed FFN."""
+    torch = torch_dev
+    say("mxfp4 moe ffn", T)
+    E, H, I, K, Ish = 6, 320, 192, 2, 128
+    fm = [(9, 4), (5, 0), (9, 4), (4, 7), (9, 4), (2, 0)]
+    gate, up, down, shared = moe_setup(oracle, 9100 + T, E, H, I, Ish, fm, sh_fmt=(9, 4))
+    x = seeded_normal(9110 + T, (T, H))
+    idx, w = oracle.route(seeded_normal(9120 + T, (T, E)), K, True)
+    got = run_moe(ctx, torch, gate, up, down, shared, x, idx, w)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    assert relerr(got, ref) <= TOL
+
+
+def test_mxfp4_gpt_oss_shape(ctx, torch_dev, oracle):
+    """GPT-OSS-20B's expert shape (hidden 2880 = 45 groups of 64, expert width 2880), 8 experts,
+    top-4 over 4 tokens."""
+    torch = torch_dev
+    say("mxfp4 gpt-oss shape")
+    E, H, I, K, T = 8, 2880, 2880, 4, 4
+    gate, up, down, _ = moe_setup(oracle, 9200, E, H, I, 0, [(9, 4)])
+    x = seeded_normal(9210, (T, H))
+    idx, w = oracle.route(seeded_normal(9220, (T, E)), K, True)
+    got = run_moe(ctx, torch, gate, up, down, None, x, idx, w)
+    ref = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
+    assert relerr(got, ref) <= TOL
+
+
+def test_mxfp4_refusals(torch_dev, oracle, monkeypatch):
+    """MXFP4 runs in the in-kernel-digit gather only: a dense GEMV on it, a gather forced onto the
+    prepared-digit kernel, and a launch that also holds an AF int4 expert are refused."""
+    import beglin_amd
+    torch = torch_dev
+    say("mxfp4 refusals")
+    E, H, I, K, T = 2, 256, 128, 1, 3
+    c = beglin_amd.Context(0)
+    blk = mxfp4_blocks(np.random.default_rng(93), 64, H, 118, 124)
+    t = c.bind(beglin_amd.K_MXFP4, blk, None, 64, H)
+    with pytest.raises(beglin_amd.BglError):
+        c.matmul(t, dev(torch, seeded_normal(94, (1, H))), torch.zeros((1, 64), device="cuda"))
+    t.free()
+    x = seeded_normal(95, (T, H))
+    idx, w = oracle.route(seeded_normal(96, (T, E)), K, True)
+    gate, up, down, _ = moe_setup(oracle, 9300, E, H, I, 0, [(9, 4), (6, 4)])
+    with pytest.raises(beglin_amd.BglError):
+        run_moe(c, torch, gate, up, down, None, x, idx, w)
+    c.close()
+    monkeypatch.setenv("BGL_NO_MOE_X", "1")
+    c = beglin_amd.Context(0)
+    gate, up, down, _ = moe_setup(oracle, 9400, E, H, I, 0, [(9, 4)])
+    with pytest.raises(beglin_amd.BglError):
+        run_moe(c, torch, gate, up, down, None, x, idx, w)
+    c.close()
+    monkeypatch.delenv("BGL_NO_MOE_X", raising=False)

@@ -672,3 +672,48 @@ def test_swiglu_pins(oracle):
     fin = np.isfinite(got) & np.isfinite(gate)
     ulp = np.abs(got[fin].view(np.int32).astype(np.int64) - gate[fin].view(np.int32).astype(np.int64))
     assert ulp.max() <= 2
+
+
+def test_mxfp4_decode_matches_reference(oracle, ref):
+    """The oracle's MXFP4 arms (moe_decode_af / moe_matvec_af_row, qwen_infer.c:2584-2595, :2702-2725)
+    against oracle/_ref's gguf_quants.c: every exponent byte 0..255 and every code, element by
+    element against gguf_dequant_row(MXFP4 = 39), and the row dot against the decoded row in double
+    (pairs j, j+16 summed per the reference's order)."""
+    from oracle_ffi import moe_decode, moe_matvec, mxfp4_blocks
+    ref.gguf_e8m0_to_fp32_half.restype = C.c_float
+    ref.gguf_e8m0_to_fp32_half.argtypes = [C.c_uint8]
+    ref.gguf_mxfp4_nibble.restype = C.c_int8
+    ref.gguf_mxfp4_nibble.argtypes = [C.c_int]
+    oracle.lib.or_mx_scale.restype = C.c_float
+    oracle.lib.or_mx_scale.argtypes = [C.c_uint8]
+    for b in range(256):
+        a, r = np.float32(oracle.lib.or_mx_scale(b)), np.float32(ref.gguf_e8m0_to_fp32_half(b))
+        assert a.view(np.uint32) == r.view(np.uint32), b
+    assert [oracle.lib.or_mx_value(c) for c in range(16)] == [ref.gguf_mxfp4_nibble(c) for c in range(16)]
+    rng = np.random.default_rng(40)
+    out, inn = 16, 256
+    blk = mxfp4_blocks(rng, out, inn, 0, 256)                 # every exponent byte, subnormal scales included
+    blk[0, :, 0] = np.arange(inn // 32, dtype=np.uint8)      # 0 and 1 (the subnormal patterns) for sure
+    blk[1, :, 0] = 255 - np.arange(inn // 32, dtype=np.uint8)
+    rd = np.zeros(out * inn, np.float32)
+    ref.gguf_dequant_row(39, _ptr(blk), _ptr(rd), C.c_int64(out * inn))       # GGML_TYPE_MXFP4 = 39
+    rd = rd.reshape(out, inn)
+    desc = (9, 4, blk, None)
+    for r in (0, 1, 7, 15):
+        got = moe_decode(oracle, desc, out, inn, r, range(inn))
+        assert np.array_equal(got.view(np.uint32), rd[r].view(np.uint32)), r
+    blk = mxfp4_blocks(rng, out, inn)
+    desc = (9, 4, blk, None)
+    rd = np.zeros(out * inn, np.float32)
+    ref.gguf_dequant_row(39, _ptr(blk), _ptr(rd), C.c_int64(out * inn))
+    rd = rd.reshape(out, inn)
+    x = rng.standard_normal(inn).astype(np.float32)
+    want = np.zeros(out, np.float64)
+    for r in range(out):
+        acc = 0.0
+        for b in range(inn // 32):
+            for j in range(16):
+                c0 = 32 * b
+                acc += float(rd[r, c0 + j]) * float(x[c0 + j]) + float(rd[r, c0 + j + 16]) * float(x[c0 + j + 16])
+        want[r] = acc
+    assert np.array_equal(moe_matvec(oracle, desc, out, inn, x), want.astype(np.float32))
