@@ -8,7 +8,7 @@ import ctypes as C
 
 from . import capi
 from .capi import (ACT_F32, ACT_W4A8, K_F16, K_F32, K_MXFP4, K_Q4G32H, K_Q4G64, K_Q4G64A,  # noqa: F401
-                   K_Q4G256SF, K_Q8G64, K_QNG64)
+                   K_Q4G256P, K_Q4G256SF, K_Q8G64, K_QNG64)
 
 _lib = None
 

@@ -11,7 +11,7 @@ LIB_PATH = os.environ.get("BGL_LIB") or os.path.join(HERE, "libbeglin_hip.so")
 
 # mirrors of the header's enums
 K_Q4G64, K_Q8G64, K_Q4G256SF, K_QNG64, K_Q4G32H = 1, 2, 3, 4, 5
-K_Q4G64A, K_F16, K_F32, K_MXFP4 = 6, 7, 8, 9
+K_Q4G64A, K_F16, K_F32, K_MXFP4, K_Q4G256P = 6, 7, 8, 9, 10
 ACT_F32, ACT_W4A8 = 0, 1
 
 _P = C.c_void_p

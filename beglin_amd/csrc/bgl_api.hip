@@ -268,8 +268,8 @@ int check_wt(int kind, int bits, int out, int in) {
         // MXFP4 blocks hold 32 values; the gather works in 64-groups (two blocks)
         if (in % 64) return bgl_fail(BGL_E_ARG, "kind %d: in=%d %% 64 != 0", kind, in);
         return 0;
-    case BGL_Q4G256SF:
-        if (in % 256) return bgl_fail(BGL_E_ARG, "g256sf in=%d %% 256 != 0", in);
+    case BGL_Q4G256SF: case BGL_K_Q4G256P:
+        if (in % 256) return bgl_fail(BGL_E_ARG, "g256 in=%d %% 256 != 0", in);
         return 0;
     default: return bgl_fail(BGL_E_UNSUPPORTED, "unknown weight kind %d", kind);
     }
@@ -277,7 +277,7 @@ int check_wt(int kind, int bits, int out, int in) {
 
 static size_t ref_packed_bytes(int kind, int bits, int out, int in) {
     switch (kind) {
-    case BGL_Q4G64: case BGL_Q4G256SF: case BGL_Q4G32H: case BGL_Q4G64A: return (size_t)out * in / 2;
+    case BGL_Q4G64: case BGL_Q4G256SF: case BGL_Q4G32H: case BGL_Q4G64A: case BGL_K_Q4G256P: return (size_t)out * in / 2;
     case BGL_Q8G64: return (size_t)out * in;
     case BGL_F16: return (size_t)out * in * 2;
     case BGL_F32: return (size_t)out * in * 4;
@@ -289,7 +289,7 @@ static size_t ref_packed_bytes(int kind, int bits, int out, int in) {
 static size_t ref_scale_bytes(int kind, int out, int in) {
     switch (kind) {
     case BGL_Q4G64: case BGL_Q8G64: case BGL_QNG64: case BGL_Q4G64A: return (size_t)out * (in / 64) * 4;
-    case BGL_Q4G256SF: return (size_t)out * (in / 256) * 4;
+    case BGL_Q4G256SF: case BGL_K_Q4G256P: return (size_t)out * (in / 256) * 4;
     case BGL_Q4G32H: return (size_t)out * (in / 32) * 2;
     default: return 0;
     }
@@ -304,6 +304,7 @@ void device_layout(int kind, int bits, int out, int in, BglDevTensor &T, size_t 
     T.fmt = kind;
     T.bits = kind == BGL_QNG64 ? bits : kind == BGL_Q8G64 ? 8 : kind == BGL_F16 ? 16 : kind == BGL_F32 ? 32 : 4;
     T.N = out; T.K = in; T.ntiles = (out + BGL_TILE - 1) / BGL_TILE;
+    T.gmul = kind == BGL_Q4G256SF ? 1.0f / 63.0f : 1.0f;
     T.nunits = units_of(kind, in);
     T.cpu = kind == BGL_Q4G256SF ? 8 : kind == BGL_Q8G64 ? 4 : kind == BGL_QNG64 ? bits : kind == BGL_F16 ? 8
           : kind == BGL_F32 ? 16 : 2;
@@ -421,12 +422,35 @@ static int bind_mxfp4(bgl_ctx *c, const bgl_wt *w, bgl_tensor **out) {
     return 0;
 }
 
+// The plain-g256 diagnostic (q4gemv_g256.h:102-130): q4 nibbles and one fp32 scale per 256 values,
+// bound as the g256sf layout with every sub-code 1 and the fold factor 1 instead of 1/63.
+static int bind_g256plain(bgl_ctx *c, const bgl_wt *w, bgl_tensor **out) {
+    if (!w->scales) return bgl_fail(BGL_E_ARG, "bgl_bind: plain g256 needs scales");
+    HIPCHK(hipSetDevice(c->device));
+    const size_t pb = (size_t)w->out * w->in / 2, sb = (size_t)w->out * (w->in / 256) * 4, nsub = (size_t)w->out * (w->in / 64);
+    void *dpk = nullptr, *dsc = nullptr, *dsub = nullptr;
+    HIPCHK(hipMalloc(&dpk, pb));
+    HIPCHK(hipMalloc(&dsc, sb));
+    HIPCHK(hipMalloc(&dsub, nsub));
+    HIPCHK(hipMemcpyAsync(dpk, w->packed, pb, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(hipMemcpyAsync(dsc, w->scales, sb, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(hipMemsetAsync(dsub, 1, nsub, c->stream));
+    int rc = repack_into(c, BGL_Q4G256SF, 4, w->out, w->in, dpk, dsc, (const uint8_t *)dsub, out);
+    hipError_t e = hipStreamSynchronize(c->stream);
+    (void)hipFree(dpk); (void)hipFree(dsc); (void)hipFree(dsub);
+    if (rc) return rc;
+    if (e != hipSuccess) return bgl_fail(BGL_E_HIP, "bind sync: %s", hipGetErrorString(e));
+    (*out)->T.gmul = 1.0f;
+    return 0;
+}
+
 extern "C" int bgl_bind(bgl_ctx *c, const bgl_wt *w, bgl_tensor **out) {
     if (!c || !w || !out || !w->packed) return bgl_fail(BGL_E_ARG, "bgl_bind: NULL argument");
     int rc = check_wt(w->kind, w->bits, w->out, w->in);
     if (rc) return rc;
     const bool dense = w->kind == BGL_F16 || w->kind == BGL_F32;
     if (w->kind == BGL_MXFP4) return bind_mxfp4(c, w, out);
+    if (w->kind == BGL_K_Q4G256P) return bind_g256plain(c, w, out);
     if (!dense && !w->scales) return bgl_fail(BGL_E_ARG, "bgl_bind: kind %d needs scales", w->kind);
     if (w->kind == BGL_Q4G256SF && !w->sub) return bgl_fail(BGL_E_ARG, "bgl_bind: g256sf needs sub-codes");
     if (w->kind == BGL_Q4G64A && !w->sub) return bgl_fail(BGL_E_ARG, "bgl_bind: int4 affine needs biases (sub)");
@@ -577,7 +601,7 @@ extern "C" int bgl_tensor_info(const bgl_tensor *t, int *kind, int *bits, int *o
         if (device_bytes) { size_t s = 0; for (auto *e : t->experts) s += e->device_bytes; *device_bytes = s; }
         return 0;
     }
-    if (kind) *kind = t->T.fmt;
+    if (kind) *kind = t->T.fmt == BGL_Q4G256SF && t->T.gmul == 1.0f ? BGL_K_Q4G256P : t->T.fmt;
     if (bits) *bits = t->T.bits;
     if (out) *out = t->T.N;
     if (in) *in = t->T.K;
@@ -864,7 +888,7 @@ extern "C" int bgl_matmul_group_dev(bgl_ctx *c, int n, const bgl_tensor *const *
     for (int i = 0; i < n; i++) {
         if (!w[i] || !w[i]->experts.empty() || !y_dev[i]) return bgl_fail(BGL_E_ARG, "bgl_matmul_group_dev: tensor %d invalid", i);
         Ts[i] = w[i]->T;
-        if (Ts[i].K != Ts[0].K || Ts[i].fmt != Ts[0].fmt || Ts[i].bits != Ts[0].bits)
+        if (Ts[i].K != Ts[0].K || Ts[i].fmt != Ts[0].fmt || Ts[i].bits != Ts[0].bits || Ts[i].gmul != Ts[0].gmul)
             return bgl_fail(BGL_E_ARG, "bgl_matmul_group_dev: fused tensors must share kind, bits and in");
     }
     const int kind = Ts[0].fmt;

@@ -383,10 +383,12 @@ __device__ __forceinline__ int unit_part(const RawPart<FMT, H> &r, const int8_t 
 }
 
 // The unit's fp32 term, exactly the reference's per-group expression (q4gemv_g256.h:154,
-// q4gemv.h:241): g256sf ((comb * wsuper) * (1/63)) * ascale; q4g64 / q8g64 (isum * wscale) * ascale.
+// q4gemv.h:241): g256sf ((comb * wsuper) * (1/63)) * ascale -- plain g256 (q4gemv_g256.h:125) has
+// sub-codes 1 and gm = 1, an exact multiply, so (isum * wscale) * ascale; q4g64 / q8g64
+// (isum * wscale) * ascale.
 template <int FMT>
-__device__ __forceinline__ float unit_float(int isum, float s, const float *asc, const int *xsum, int u) {
-    if constexpr (FMT == BGL_Q4G256SF) return __fmul_rn(__fmul_rn(__fmul_rn((float)(isum >> 4), s), C63), asc[u]);
+__device__ __forceinline__ float unit_float(int isum, float s, float gm, const float *asc, const int *xsum, int u) {
+    if constexpr (FMT == BGL_Q4G256SF) return __fmul_rn(__fmul_rn(__fmul_rn((float)(isum >> 4), s), gm), asc[u]);
     else if constexpr (FMT == BGL_Q4G64) return __fmul_rn(__fmul_rn((float)(isum - 8 * xsum[u]), s), asc[u]);
     else return __fmul_rn(__fmul_rn((float)isum, s), asc[u]);
 }
@@ -483,7 +485,7 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_gemv_q(GemvLaunch L) {
                 int p = unit_part<FMT, H>(c, xq + m * XQS, min(u, U - 1), h);
                 if constexpr (H == 2) p += __shfl_xor(p, TR);
                 if (h == 0 && u < U)
-                    tl[(m * U + u) * TR + r] = unit_float<FMT>(p, c.s, asc + m * (NGQ + 1), xsum + m * (K / 64 + 1), u);
+                    tl[(m * U + u) * TR + r] = unit_float<FMT>(p, c.s, T.gmul, asc + m * (NGQ + 1), xsum + m * (K / 64 + 1), u);
             }
         };
         for (;;) {

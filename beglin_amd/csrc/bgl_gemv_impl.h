@@ -62,7 +62,7 @@ __device__ __forceinline__ float fold_digits(int t0, int t1, int t2) {
 template <int FMT, int NB> struct Raw;
 template <int NB> struct Raw<BGL_Q4G64, NB> { uint4 c[2]; float s; };
 template <int NB> struct Raw<BGL_Q4G32H, NB> { uint4 c[2]; uint32_t s; };
-template <int NB> struct Raw<BGL_Q4G256SF, NB> { uint4 c[8]; float s; uint32_t sub; };
+template <int NB> struct Raw<BGL_Q4G256SF, NB> { uint4 c[8]; float s; uint32_t sub; float gm; };
 template <int NB> struct Raw<BGL_Q8G64, NB> { uint4 c[4]; float s; };
 template <int NB> struct Raw<BGL_QNG64, NB> { uint4 c[NB]; float2 s; };
 template <int NB> struct Raw<BGL_Q4G64A, NB> { uint4 c[2]; float s; float b; };
@@ -105,6 +105,7 @@ __device__ __forceinline__ void load_raw(Raw<FMT, NB> &r, const BglDevTensor &T,
         const bgl_u32x2 w = ((const BGL_GLOBAL bgl_u32x2 *)T.s0)[so];
         r.s = __uint_as_float(w.x);
         r.sub = w.y;
+        r.gm = T.gmul;
     } else r.s = ((const BGL_GLOBAL float *)T.s0)[so];
     }
 }
@@ -211,7 +212,7 @@ __device__ __forceinline__ void comp_g256sf(const Raw<BGL_Q4G256SF, NB> &r, int 
             }
             comb16 += isum16 * (int)((r.sub >> (8 * sg)) & 255u);
         }
-        float t = __fmul_rn(__fmul_rn(__fmul_rn((float)(comb16 >> 4), r.s), C63), uni(A.xs)[(size_t)am * (K >> 8) + u]);
+        float t = __fmul_rn(__fmul_rn(__fmul_rn((float)(comb16 >> 4), r.s), r.gm), uni(A.xs)[(size_t)am * (K >> 8) + u]);
         acc[m] = __fadd_rn(acc[m], t);
     }
 }

@@ -61,7 +61,7 @@ int bgl_last_code(void);             // the code of this thread's last bgl_fail 
 // The device layout's version: bump when any format's device bytes change, so caches of the
 // repacked layout written before the change are rejected.  (2: signed-nibble g256sf with one
 // 8-byte scale word per unit.)
-#define BGL_DEVICE_LAYOUT_VERSION 2
+#define BGL_DEVICE_LAYOUT_VERSION 3
 void device_layout(int kind, int bits, int out, int in, BglDevTensor &T, size_t bytes[3]);
 bgl_tensor *tensor_from_parts(const BglDevTensor &T, void *w, void *s0, void *s1, size_t device_bytes);
 // Profiling brackets: prof_begin returns a token (or -1 when profiling is off).

@@ -6,13 +6,15 @@
 //   Q4G64   64 elements, 2 chunks, s0 = fp32 scale
 //   Q4G32H  64 elements, 2 chunks, s0 = u32 holding the two fp16 group-32 scales (low = first)
 //   G256SF  256 elements, 8 chunks, s0 = u32x2 (x = fp32 wsuper bits, y = the 4 sub-codes, byte s =
-//           sub s), one load per unit; codes stored as signed nibbles (code ^ 8)
+//           sub s), one load per unit; codes stored as signed nibbles (code ^ 8).  The plain-g256
+//           diagnostic kind is this layout with every sub-code 1 and gmul 1 instead of 1/63.
 //   Q8G64   64 elements, 4 chunks, s0 = fp32 scale
 //   QNG64   128 elements (a pair of 64-groups), n chunks, s0 = float2 (the two group scales)
 //   MXFP4   64 elements (two GGUF blocks), 2 chunks (Q4G64's nibble order), s0 = u32 holding the
 //           two E8M0 exponent bytes (low = first block)
 struct BglDevTensor {
     int fmt, bits, N, K, ntiles, cpr, nunits, cpu;   // cpu: chunks per unit
+    float gmul;                                      // G256SF: the fold's factor, 1/63 (subfold) or 1 (plain g256)
     const uint8_t *w;
     const void *s0;
     const uint32_t *s1;
@@ -87,7 +89,7 @@ __device__ __forceinline__ float w_at(const BglDevTensor &T, int r, int c) {
             float ws = __uint_as_float(wsub.x);
             uint32_t sub4 = wsub.y;
             float sc = (float)((sub4 >> (8 * ((c / 64) & 3))) & 255);
-            v = (float)(nib - 8) * __fmul_rn(ws, __fdiv_rn(sc, 63.0f));
+            v = T.gmul == 1.0f ? (float)(nib - 8) * ws : (float)(nib - 8) * __fmul_rn(ws, __fdiv_rn(sc, 63.0f));
         }
     } else if (T.fmt == BGL_Q8G64) {
         const int8_t *p = reinterpret_cast<const int8_t *>(T.w) + (((size_t)tile * T.cpr + c / 16) * BGL_TILE + lane) * 16;

@@ -15,7 +15,8 @@
  *     8 BGL_K_F32 dense rows.  9 BGL_K_MXFP4 is the AF kind bits = MOE_BITS_GGUF_MXFP4 (40) of the CPU
  *     MoE path (moe_decode_af / moe_matvec_af_row, qwen_infer.c:2584-2595, :2702-2725): GGUF MXFP4
  *     blocks of 32, an E8M0 exponent byte then 16 bytes of E2M1 nibbles (gguf_quants.c:284-327).
- *     Kinds 6..9 run in the MoE gather only (fp32 activations).
+ *     Kinds 6..9 run in the MoE gather only (fp32 activations).  10 BGL_K_Q4G256P is the plain-g256
+ *     diagnostic of q4gemv_g256.h:102-130 (q4 nibbles, one fp32 scale per 256 values, W4A8 only).
  *   - *_dev entry points take DEVICE pointers and are asynchronous on the context's stream;
  *     host-pointer entry points (the drop-ins with the reference's exact argument lists) copy
  *     x in and y out and return after y is on the host.
@@ -38,7 +39,7 @@ extern "C" {
 #endif
 
 enum { BGL_K_Q4G64 = 1, BGL_K_Q8G64 = 2, BGL_K_Q4G256SF = 3, BGL_K_QNG64 = 4, BGL_K_Q4G32H = 5,
-       BGL_K_Q4G64A = 6, BGL_K_F16 = 7, BGL_K_F32 = 8, BGL_K_MXFP4 = 9 };
+       BGL_K_Q4G64A = 6, BGL_K_F16 = 7, BGL_K_F32 = 8, BGL_K_MXFP4 = 9, BGL_K_Q4G256P = 10 };
 enum { BGL_ACT_F32 = 0, BGL_ACT_W4A8 = 1 };
 enum { BGL_OK = 0, BGL_E_ARG = -1, BGL_E_UNSUPPORTED = -2, BGL_E_HIP = -3, BGL_E_NODEV = -4, BGL_E_NOMEM = -5,
        BGL_E_CAPTURE = -6 /* per-call scratch would have to grow inside a stream capture */ };
@@ -52,7 +53,7 @@ typedef struct bgl_tensor bgl_tensor;
  *           K_Q8G64 int8 codes [out][in]; K_QNG64 bit planes [out][in/64][n][8];
  *           F16 / F32: dense fp16 / fp32 rows [out][in]; MXFP4: the GGUF blocks [out][in/32][17].
  *   scales: fp32 [out][in/64] (K_Q4G64, K_Q8G64, K_QNG64, Q4G64A); fp32 wsuper [out][in/256]
- *           (K_Q4G256SF); fp16 bits [out][in/32] (Q4G32H); unused (may be NULL) for F16 / F32 / MXFP4.
+ *           (K_Q4G256SF; the plain scale for Q4G256P); fp16 bits [out][in/32] (Q4G32H); unused (may be NULL) for F16 / F32 / MXFP4.
  *   sub:    K_Q4G256SF: sub-codes u8 [out][in/64]; Q4G64A: fp32 biases [out][in/64] (read as bytes).
  *   bits:   K_QNG64 only: n in 2..15. */
 typedef struct {

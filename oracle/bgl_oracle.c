@@ -522,14 +522,41 @@ void or_gemm_g256sf_sdot(const uint8_t *packed, const float *wsuper, const uint8
     }
 }
 
+/* q4gemv_g256.h:102-130 (q4_dot_sdot_row_g256plain) and :196-220 (batched): the plain-g256
+ * diagnostic, one fp32 scale per 256 weights and no sub-codes: per 256 the exact int32 sum of
+ * (nib - 8) * xq, then acc += (float)sum * wscale256 * ascale256, left to right. */
+void or_gemm_g256plain_sdot(const uint8_t *packed, const float *wscale, const int8_t *xq, const float *ascale,
+                            const float *bias, float *y, int out, int in, int M) {
+    int ng256 = in / 256;
+    for (int r = 0; r < out; r++) {
+        const uint8_t *pr = packed + (size_t)r * (in / 2);
+        float b = bias ? bias[r] : 0.0f;
+        for (int m = 0; m < M; m++) {
+            const int8_t *xm = xq + (size_t)m * in;
+            const float *am = ascale + (size_t)m * ng256;
+            float acc = 0.0f;
+            for (int gs = 0; gs < ng256; gs++) {
+                int32_t sum = 0;
+                for (int c = gs * 256; c < gs * 256 + 256; c++) {
+                    int nib = (c & 1) ? (pr[c / 2] >> 4) : (pr[c / 2] & 0x0F);
+                    sum += (nib - 8) * (int32_t)xm[c];
+                }
+                acc += (float)sum * wscale[(size_t)r * ng256 + gs] * am[gs];
+            }
+            y[(size_t)m * out + r] = b + acc;
+        }
+    }
+}
+
 void or_matmul_sdot(int kind, const void *packed, const float *scales, const uint8_t *sub,
                     const float *x, const float *bias, float *y, int out, int in, int M) {
-    int gsize = (kind == 3) ? 256 : 64, ng = in / gsize;
+    int gsize = (kind == 3 || kind == 10) ? 256 : 64, ng = in / gsize;
     int8_t *xq = (int8_t *)malloc((size_t)M * in);
     float *as = (float *)malloc(sizeof(float) * (size_t)M * ng);
     for (int m = 0; m < M; m++) or_quant_act_i8(x + (size_t)m * in, in, gsize, xq + (size_t)m * in, as + (size_t)m * ng);
     if (kind == 1) or_gemm_q4g64_sdot((const uint8_t *)packed, scales, xq, as, bias, y, out, in, M);
     else if (kind == 2) or_gemm_q8g64_sdot((const int8_t *)packed, scales, xq, as, bias, y, out, in, M);
+    else if (kind == 10) or_gemm_g256plain_sdot((const uint8_t *)packed, scales, xq, as, bias, y, out, in, M);
     else or_gemm_g256sf_sdot((const uint8_t *)packed, scales, sub, xq, as, bias, y, out, in, M);
     free(xq); free(as);
 }

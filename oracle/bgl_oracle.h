@@ -82,7 +82,11 @@ void or_gemm_q8g64_sdot(const int8_t *codes, const float *wscale, const int8_t *
 void or_gemm_g256sf_sdot(const uint8_t *packed, const float *wsuper, const uint8_t *sub,
                          const int8_t *xq, const float *ascale, const float *bias, float *y,
                          int out, int in, int M);
-/* convenience: quantize each column of x then run the sdot GEMM (matmul_sdot, qwen_infer.c:1852-1900) */
+/* the plain-g256 diagnostic row (q4gemv_g256.h:102-130), unwired in the reference too */
+void or_gemm_g256plain_sdot(const uint8_t *packed, const float *wscale, const int8_t *xq, const float *ascale,
+                            const float *bias, float *y, int out, int in, int M);
+/* convenience: quantize each column of x then run the sdot GEMM (matmul_sdot, qwen_infer.c:1852-1900);
+ * kind 1 q4g64, 2 q8g64, 3 g256sf, 10 plain g256 */
 void or_matmul_sdot(int kind, const void *packed, const float *scales, const uint8_t *sub,
                     const float *x, const float *bias, float *y, int out, int in, int M);
 

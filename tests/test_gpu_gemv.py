@@ -380,3 +380,46 @@ def test_w4a8_batched_prep_equals_fused(torch_dev, oracle, monkeypatch, kind):
                 t.free(); c.close()
             assert np.array_equal(outs[0].view(np.uint32), ref.view(np.uint32)), (inn, M)
             assert np.array_equal(outs[1].view(np.uint32), ref.view(np.uint32)), (inn, M)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 13])
+@pytest.mark.parametrize("inn", [512, 8960])
+def test_g256plain_w4a8_bitexact(ctx, torch_dev, oracle, inn, M):
+    """The plain-g256 diagnostic kind (q4gemv_g256.h:102-130; bound as the g256sf layout with
+    sub-codes 1 and fold factor 1): W4A8 outputs bit-identical to the oracle's row at every M, the
+    fused and the up-front-quantized launches alike; decode = (nib - 8) * scale; the kind reads
+    back as 10; fusing it with a g256sf tensor is refused (the folds differ)."""
+    import beglin_amd
+    torch = torch_dev
+    out = 200
+    say("g256plain", inn, M)
+    rng = np.random.default_rng(1300 + inn + M)
+    pk = rng.integers(0, 256, (out, inn // 2), dtype=np.uint8)
+    ws = (rng.random((out, inn // 256), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = seeded_normal(1310 + M, (M, inn))
+    bias = seeded_normal(1320, (out,))
+    ref = oracle.matmul_sdot(10, pk, ws, x, bias=bias)
+    t = ctx.bind(beglin_amd.K_Q4G256P, pk, ws, out, inn)
+    assert t.info()["kind"] == beglin_amd.K_Q4G256P
+    y = torch.full((M, out), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.matmul(t, torch.from_numpy(x).cuda(), y, act=beglin_amd.ACT_W4A8, bias_dev=torch.from_numpy(bias).cuda())
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), relerr(got, ref)
+    if M == 1:
+        d = torch.zeros((out, inn), dtype=torch.float32, device="cuda")
+        ctx.dequant(t, 0, out, d)
+        torch.cuda.synchronize()
+        nib = np.empty((out, inn), np.float32)
+        nib[:, 0::2] = pk & 15
+        nib[:, 1::2] = pk >> 4
+        want = (nib - np.float32(8)) * np.repeat(ws, 256, axis=1)
+        assert np.array_equal(d.cpu().numpy().view(np.uint32), want.view(np.uint32))
+        with pytest.raises(beglin_amd.BglError):
+            ctx.matmul(t, torch.from_numpy(x).cuda(), y, act=beglin_amd.ACT_F32)        # W4A8 only
+        p2, s2, sub2 = oracle.quantize_g256sf(weights(1330, out, inn))
+        t2 = ctx.bind(3, p2, s2, out, inn, sub=sub2)
+        with pytest.raises(beglin_amd.BglError):
+            ctx.matmul_group([t, t2], torch.from_numpy(x).cuda(), [y, torch.zeros_like(y)], act=beglin_amd.ACT_W4A8)
+        t2.free()
+    t.free()

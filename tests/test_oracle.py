@@ -717,3 +717,32 @@ def test_mxfp4_decode_matches_reference(oracle, ref):
                 acc += float(rd[r, c0 + j]) * float(x[c0 + j]) + float(rd[r, c0 + j + 16]) * float(x[c0 + j + 16])
         want[r] = acc
     assert np.array_equal(moe_matvec(oracle, desc, out, inn, x), want.astype(np.float32))
+
+
+def test_g256plain_row_pins(oracle):
+    """or_gemm_g256plain_sdot (q4gemv_g256.h:102-130) at power-of-two weight and activation scales,
+    where every term (float)isum * ws * as is exact: the output then equals a float32 running sum,
+    in group order, of exact integer sums computed here from the nibbles (low = even column) and
+    the oracle's own int8 activation codes -- which pins the nibble order, the 256-groups and the
+    pairing of weight and activation groups; a dropped -8 or a group off by one fails it."""
+    rng = np.random.default_rng(33)
+    out, inn, M = 12, 1024, 3
+    pk = rng.integers(0, 256, (out, inn // 2), dtype=np.uint8)
+    ws = np.ldexp(np.float32(1), rng.integers(-12, -4, (out, inn // 256))).astype(np.float32)
+    x = rng.standard_normal((M, inn)).astype(np.float32)
+    xq, asc = oracle.quant_act_i8(x, 256)
+    asc = np.ldexp(np.float32(1), np.round(np.log2(asc)).astype(np.int32)).astype(np.float32)   # power-of-two
+    nib = np.empty((out, inn), np.int64)
+    nib[:, 0::2] = pk & 15
+    nib[:, 1::2] = pk >> 4
+    y = np.zeros((M, out), np.float32)
+    oracle.lib.or_gemm_g256plain_sdot(C.c_void_p(pk.ctypes.data), C.c_void_p(ws.ctypes.data),
+                                       C.c_void_p(np.ascontiguousarray(xq).ctypes.data), C.c_void_p(asc.ctypes.data),
+                                       None, C.c_void_p(y.ctypes.data), out, inn, M)
+    for m in range(M):
+        for r in range(out):
+            acc = np.float32(0)
+            for g in range(inn // 256):
+                s = int(np.sum((nib[r, g * 256:(g + 1) * 256] - 8) * xq[m, g * 256:(g + 1) * 256].astype(np.int64)))
+                acc = np.float32(acc + np.float32(s) * ws[r, g] * asc[m, g])
+            assert y[m, r] == acc, (m, r)
