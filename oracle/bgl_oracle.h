@@ -30,6 +30,15 @@
  *     independent Python bit-plane decode for random per-cell widths.
  *   - or_moe_route / _softmax_full / _top_k_select / _topk_renorm: brute force; or_moe_ffn_*:
  *     bucketed == naive and a dense float64 pipeline over decoded weights.
+ *   - or_mx_scale / or_mx_value and the MXFP4 arms of or_moe_decode / or_moe_row: bit for bit
+ *     against oracle/_ref's gguf_quants.c (every exponent byte, every code, gguf_dequant_row).
+ *   - or_gemm_g256plain_sdot: at power-of-two scales, where every term is exact, equal to a float32
+ *     running sum of integer sums computed independently from the nibbles.
+ *   - or_swiglu: numpy's float64 exp rounded once, then the float steps; special values; within
+ *     2 ulp of the reference's float-expf form.
+ *   - or_pool_* (the CPU baseline): equal to the single-threaded restatements they split.
+ * This file and its .c are test infrastructure: only tests/, smoke() and bench.py's CPU leg use
+ * them, as the checker, never as the thing measured or shipped.
  */
 #ifndef BGL_ORACLE_H
 #define BGL_ORACLE_H
