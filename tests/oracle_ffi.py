@@ -337,3 +337,23 @@ def mxfp4_blocks(rng, out, inn, lo=116, hi=132):
     b = rng.integers(0, 256, (out, inn // 32, 17), dtype=np.uint8)
     b[:, :, 0] = rng.integers(lo, hi, (out, inn // 32), dtype=np.uint8)
     return b
+
+
+MX_VALUES = np.array([0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12], np.float32)
+
+
+def mxfp4_quant(w):
+    """A GGUF MXFP4 encoding of float32 w [out][in] (in % 32 == 0): per 32-block the exponent byte b
+    with max|w| <= 12 * 2^(b-128), each value the nearest of the 16 doubled E2M1 codes.  Any valid
+    encoding serves the tests (parity is checked against the oracle's decode of the same blocks)."""
+    out, inn = w.shape
+    wb = w.reshape(out, inn // 32, 32).astype(np.float64)
+    mx = np.max(np.abs(wb), axis=2)
+    e = np.where(mx > 0, np.ceil(np.log2(np.maximum(mx, 1e-38) / 12.0)), -127).astype(np.int64) + 128
+    b = np.clip(e, 2, 254).astype(np.uint8)
+    scale = np.ldexp(1.0, b.astype(np.int64) - 128)[..., None]
+    codes = np.argmin(np.abs(wb[..., None] / scale[..., None] - MX_VALUES[None, None, None, :]), axis=3).astype(np.uint8)
+    blk = np.zeros((out, inn // 32, 17), np.uint8)
+    blk[:, :, 0] = b
+    blk[:, :, 1:] = codes[:, :, :16] | (codes[:, :, 16:] << 4)
+    return blk

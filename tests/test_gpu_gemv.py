@@ -423,3 +423,29 @@ def test_g256plain_w4a8_bitexact(ctx, torch_dev, oracle, inn, M):
             ctx.matmul_group([t, t2], torch.from_numpy(x).cuda(), [y, torch.zeros_like(y)], act=beglin_amd.ACT_W4A8)
         t2.free()
     t.free()
+
+
+@pytest.mark.parametrize("M", [1, 5])
+def test_g256plain_separate_quantization_path(torch_dev, oracle, monkeypatch, M):
+    """Plain g256 through the separate quantization kernel + the prepared-activation GEMV
+    (BGL_NO_FUSED_Q=1, whose fold takes the fold factor from the unit's record): bit-identical to
+    the oracle, as through the fused kernel."""
+    import beglin_amd
+    torch = torch_dev
+    say("g256plain separate", M)
+    out, inn = 136, 1536
+    rng = np.random.default_rng(1400 + M)
+    pk = rng.integers(0, 256, (out, inn // 2), dtype=np.uint8)
+    ws = (rng.random((out, inn // 256), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    x = seeded_normal(1410 + M, (M, inn))
+    ref = oracle.matmul_sdot(10, pk, ws, x)
+    monkeypatch.setenv("BGL_NO_FUSED_Q", "1")
+    c = beglin_amd.Context(0)
+    t = c.bind(beglin_amd.K_Q4G256P, pk, ws, out, inn)
+    y = torch.full((M, out), float("nan"), dtype=torch.float32, device="cuda")
+    c.matmul(t, torch.from_numpy(x).cuda(), y, act=beglin_amd.ACT_W4A8)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    t.free(); c.close()
+    monkeypatch.delenv("BGL_NO_FUSED_Q", raising=False)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), relerr(got, ref)

@@ -23,7 +23,7 @@ import numpy as np
 import pytest
 
 from golden.fixtures import seeded_normal
-from oracle_ffi import moe_ffn
+from oracle_ffi import moe_ffn, mxfp4_quant
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -235,6 +235,8 @@ def test_nonfinite_activations(torch_dev, oracle, monkeypatch, kind, bits, M, en
 def moe_descs(oracle, E, H, I, fmts, seed, wmul_h, wmul_i):
     def one(kind, bits, o, i, s, wm):
         w = (seeded_normal(s, (o, i), 0.02) * wm[None, :]).astype(np.float32)
+        if kind == 9:                                   # MXFP4 blocks (no scales array)
+            return (9, 4, mxfp4_quant(w), None)
         p, sc = quant(oracle, kind, w, bits)
         return (kind, bits, p, sc)
     gate = [one(*fmts[e % len(fmts)], I, H, seed + 3 * e, wmul_h) for e in range(E)]
@@ -294,5 +296,36 @@ def test_moe_nonfinite(torch_dev, oracle, monkeypatch, env):
     got = run_moe(c, torch, gate, up, down, x, idx, w)
     ref = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
     check_classes(got, ref, env)
+    assert np.all(np.isfinite(got[3:])) and relerr(got[3:], ref[3:]) <= TOL
+    c.close()
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_moe_outliers_mxfp4(torch_dev, oracle, monkeypatch, T):
+    """MXFP4 experts (beside int4 g32 and qNg64 ones) under the outlier patterns: their level-1 and
+    non-finite cold paths (signed codes, no -8 correction) against the oracle's MXFP4 row."""
+    torch = torch_dev
+    c = context(monkeypatch)
+    E, H, I, K = 8, 2048, 1408, 6
+    fm = [(9, 4), (5, 0), (9, 4), (4, 12)]
+    for i, pat in enumerate(["x1e4_w0.01", "x1e5_w0", "two_sizes_one_group"]):
+        say("moe outliers mxfp4", T, pat)
+        x, wmul = outlier_case(pat, H, T, 640 + i)
+        gate, up, down = moe_descs(oracle, E, H, I, fm, 650 + 40 * i, wmul, np.ones(I, np.float32))
+        idx, w = oracle.route(seeded_normal(660 + i, (T, E)), K, False)
+        got = run_moe(c, torch, gate, up, down, x, idx, w)
+        ref = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
+        e = relerr(got, ref)
+        print(f"  max-rel {e:.3e}")
+        assert e <= TOL, (pat, e)
+    x = seeded_normal(670, (5, H))
+    x[0, 10] = np.nan
+    x[1, 300] = np.inf
+    x[2, 7] = -np.inf
+    gate, up, down = moe_descs(oracle, E, H, I, fm, 680, np.ones(H, np.float32), np.ones(I, np.float32))
+    idx, w = oracle.route(seeded_normal(690, (5, E)), K, False)
+    got = run_moe(c, torch, gate, up, down, x, idx, w)
+    ref = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
+    check_classes(got, ref, {})
     assert np.all(np.isfinite(got[3:])) and relerr(got[3:], ref[3:]) <= TOL
     c.close()
