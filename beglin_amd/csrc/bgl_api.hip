@@ -73,6 +73,7 @@ int dbuf_reserve(bgl_ctx *c, DevBuf &b, size_t bytes, bool zero) {
         b.p = nullptr; b.bytes = 0;
     }
     size_t want = bytes + bytes / 4 + 4096;
+    HIPCHK(hipSetDevice(c->device));        // the context's device, whatever the calling thread had selected
     HIPCHK(hipMalloc(&b.p, want));
     b.bytes = want;
     if (zero) {

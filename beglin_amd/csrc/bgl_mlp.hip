@@ -47,10 +47,11 @@ extern "C" int bgl_mlp_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor 
         return bgl_fail(BGL_E_ARG, "bgl_mlp_dev: gate/up [%d x %d], up [%d x %d] and down [%d x %d] do not form an MLP", I, H,
                         up->T.N, up->T.K, down->T.N, down->T.K);
     const size_t n = (size_t)M * I;
+    // the scratch belongs to the context's device: select it before any allocation
+    HIPCHK(hipSetDevice(c->device));
     // g and u side by side, then h unless the caller keeps it
     if (dbuf_reserve(c, c->mlp, n * 4 * (h_dev ? 2 : 3), false)) return bgl_last_code();
     float *g = (float *)c->mlp.p, *u = g + n, *h = h_dev ? h_dev : u + n;
-    HIPCHK(hipSetDevice(c->device));
     const bgl_tensor *gu[2] = {gate, up};
     const float *nob[2] = {nullptr, nullptr};
     float *ys[2] = {g, u};
