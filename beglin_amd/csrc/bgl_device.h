@@ -79,6 +79,27 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return max(max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16)),
                max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48)));
 }
+// (value, index) maximum over the wave, ties to the lower index, in every lane.  The order is total
+// for non-NaN values, so any pairing gives the same winner: DPP within each row, then the four row
+// winners by readlane.
+__device__ __forceinline__ void arg_take(float &bv, int &bi, float ov, int oi) {
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+template <int CTRL>
+__device__ __forceinline__ void arg_dpp(float &bv, int &bi) { arg_take(bv, bi, dpp_f<CTRL>(bv), dpp_i<CTRL>(bi)); }
+__device__ __forceinline__ void wave_argmax(float &bv, int &bi) {
+    arg_dpp<0xB1>(bv, bi);
+    arg_dpp<0x4E>(bv, bi);
+    arg_dpp<0x141>(bv, bi);
+    arg_dpp<0x140>(bv, bi);
+    float v = rlane_f(bv, 0);
+    int i = __builtin_amdgcn_readlane(bi, 0);
+    arg_take(v, i, rlane_f(bv, 16), __builtin_amdgcn_readlane(bi, 16));
+    arg_take(v, i, rlane_f(bv, 32), __builtin_amdgcn_readlane(bi, 32));
+    arg_take(v, i, rlane_f(bv, 48), __builtin_amdgcn_readlane(bi, 48));
+    bv = v;
+    bi = i;
+}
 // returns the per-row (16-lane) sums in every lane of that row
 __device__ __forceinline__ int row_sum_i32(int v) {
     v += dpp_i<0xB1>(v);

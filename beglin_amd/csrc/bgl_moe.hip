@@ -662,7 +662,7 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ sc_t, 
         v[j] = e < E ? sc_t[e] : 0.0f;
         if (e < E) mx = fmaxf(mx, v[j]);
     }
-    for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = wave_max_f32(mx);
 #pragma unroll
     for (int j = 0; j < PL; j++) {
         const int e = lane + 64 * j;
@@ -699,11 +699,7 @@ __device__ __forceinline__ void route_topk_wave(const float *__restrict__ sc_t, 
             const int e = lane + 64 * j;
             if (e < E && !((used >> j) & 1u) && v[j] > bv) { bv = v[j]; bi = e; }
         }
-        for (int o = 32; o; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+        wave_argmax(bv, bi);                                  // DPP and readlane: no LDS round trips
         if ((bi & 63) == lane) used |= 1u << (bi >> 6);
         sel_w[k] = bv;
         sel_i[k] = bi;
