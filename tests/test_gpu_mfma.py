@@ -93,6 +93,25 @@ def test_mfma_parity(ctx, torch_dev, oracle, kind, bits, M):
         assert np.all(np.isfinite(got)) and e <= TOL, (out, inn, e)
 
 
+@pytest.mark.parametrize("kind,bits", [(2, 8), (5, 0)])
+@pytest.mark.parametrize("out,inn", [(198, 1024), (130, 256), (66, 2048)])
+@pytest.mark.parametrize("M", [17, 32])
+def test_mfma_ragged_rows(ctx, torch_dev, oracle, kind, bits, out, inn, M):
+    """Row counts that are not a multiple of 4: the last 16-byte run of each column is stored element
+    by element, and with out % 4 == 2 every odd column row of y (and of the K-split partials) starts
+    8 bytes off a 16-byte boundary, so the stores take the unaligned path; with and without a K
+    split, with a bias.  y starts as NaN, so an element the kernel skips fails the test."""
+    torch = torch_dev
+    say("mfma ragged", kind, out, inn, M)
+    w = weights(960 + out, out, inn)
+    pk, sc = quant(oracle, kind, w, bits)
+    x = seeded_normal(961 + M, (M, inn))
+    bias = seeded_normal(962, (out,))
+    got = run(ctx, torch, kind, bits, pk, sc, out, inn, x, bias)
+    ref = oracle.gemm_f32(kind, pk, sc, x, bias=bias, bits=bits)
+    assert np.all(np.isfinite(got)) and relerr(got, ref) <= TOL
+
+
 @pytest.mark.parametrize("M", [16, 17, 31, 32, 48, 64, 65])
 def test_mfma_column_tiles(ctx, torch_dev, oracle, M):
     """Every column-tile count 1..4 and a second 64-column launch, int8 weights."""
