@@ -243,7 +243,15 @@ int parse_af(const char *layout, size_t wb, std::vector<AfRec> &recs) {
             rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: in=%ld, ng=%ld; the groups hold 64 values", layout, nm, r.in, r.ng);
             break;
         }
-        const size_t codes = (size_t)r.E * r.out * (r.in / 2), side = (size_t)r.E * r.out * r.ng * 4;
+        // E * out * in can exceed 64 bits for fields within int range: such a tensor cannot lie in any blob
+        size_t rows = 0, vals = 0;
+        if (__builtin_mul_overflow((size_t)r.E, (size_t)r.out, &rows) || __builtin_mul_overflow(rows, (size_t)r.in, &vals) ||
+            vals > wb * 2) {
+            rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: E * out * in (%ld x %ld x %ld) is more than the blob's %zu bytes hold", layout,
+                          nm, r.E, r.out, r.in, wb);
+            break;
+        }
+        const size_t codes = vals / 2, side = rows * (size_t)r.ng * 4;
         if (r.pb < 0 || (size_t)r.pb < codes) {
             rc = bgl_fail(BGL_E_ARG, "%s: tensor %s: pb=%ld is less than its %zu bytes of codes", layout, nm, r.pb, codes);
             break;

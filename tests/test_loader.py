@@ -96,7 +96,7 @@ def test_af_valid_layout(tmp_path):
 
 
 @pytest.mark.parametrize("case", ["ng", "in64", "E0", "out0", "pb_short", "po_past", "so_past", "bo_past", "neg_off",
-                                  "duplicate", "long_name"])
+                                  "duplicate", "long_name", "huge"])
 def test_af_refusals(tmp_path, case):
     from loader_fixture import build_af
     layout, blob, _ = build_af(str(tmp_path))
@@ -115,6 +115,8 @@ def test_af_refusals(tmp_path, case):
         "out0": field(1, 2, 0), "pb_short": field(2, 6, 4 * 128 * 64 // 2 - 1), "po_past": field(3, 5, wb - 64),
         "so_past": field(3, 7, wb - 64), "bo_past": field(3, 8, wb), "neg_off": field(0, 7, -64),
         "duplicate": field(2, 0, "lm_head"), "long_name": field(1, 0, "x" * 128),
+        # E * out * in past 64 bits: refused before any size is formed from it
+        "huge": lambda L: field(0, 1, 2**31 - 1)(field(0, 2, 2**31 - 1)(field(0, 3, 2**31 - 64)(field(0, 4, (2**31 - 64) // 64)(L)))),
     }
     rewrite(layout, edits[case])
     rc, _ = af_check(layout, blob)
