@@ -244,6 +244,13 @@ extern "C" int bgl_gpu_bind_af(const uint8_t *blob, long blob_bytes, const char 
         bgl_fail(BGL_E_ARG, "bgl_gpu_bind_af: negative offset for a plane this width reads");
         return 0;
     }
+    // E * out * in values at most 2^40 (past any device's memory): every extent below then fits 64 bits
+    size_t rows = 0, vals = 0;
+    if (__builtin_mul_overflow((size_t)E, (size_t)out, &rows) || __builtin_mul_overflow(rows, (size_t)in, &vals) ||
+        vals > ((size_t)1 << 40)) {
+        bgl_fail(BGL_E_ARG, "bgl_gpu_bind_af: E * out * in (%ld x %ld x %ld) is more than 2^40 values", E, out, in);
+        return 0;
+    }
     size_t pb, sb;
     extents(E, out, in, ng, bits, &pb, &sb);
     if (blob_bytes > 0) {                  // bounds check when the caller states the blob size

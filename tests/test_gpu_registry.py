@@ -188,6 +188,9 @@ def test_dense_probe_bind_refusals_and_bounds(R, lib, oracle):
     assert R.bind_af(blob, "bad.ng", 1, 8, 128, 1, 0, 1024, -1, 8) == 0            # ng != in/64
     assert R.bind_af(blob, "bad.oob", 4, 256, 256, 4, 60000, 0, -1, 8) == 0       # past the blob
     assert R.bind_af(blob, "bad.nobias", 1, 8, 64, 1, 0, 1024, -1, 4) == 0         # affine needs biases
+    big = 2**31 - 64                                                                 # E * out * in past 64 bits
+    assert R.bind_af(blob, "bad.huge", 2**31 - 1, 2**31 - 1, big, big // 64, 0, 0, 0, 4) == 0
+    assert b"2^40" in lib.bgl_last_error()
     assert R.binding_kind("bad.oob") == (0, 0)
 
 
