@@ -9,7 +9,11 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libbeglin_hip.so")
-SOURCES = ["bgl_api.hip", "bgl_prep.hip", "bgl_gemv.hip", "bgl_gemv_x.hip", "bgl_moe.hip", "bgl_moe_x.hip", "bgl_registry.hip", "bgl_mfma.hip", "bgl_loader.hip", "bgl_mlp.hip"]
+# The MoE gather's kernel instances are one unit each (bgl_moe_x_i*.hip) so they compile in
+# parallel; the longest units come first.
+SOURCES = [f"bgl_moe_x_i{i}.hip" for i in range(10)] + [
+    "bgl_gemv.hip", "bgl_moe.hip", "bgl_mfma.hip", "bgl_gemv_x.hip", "bgl_api.hip", "bgl_prep.hip", "bgl_moe_x.hip",
+    "bgl_registry.hip", "bgl_loader.hip", "bgl_mlp.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
