@@ -546,10 +546,15 @@ static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, con
         Ms.y = shh; Ms.ystride = Ish; Ms.swiglu = 1;
         Ms.seg = shared_seg(T, moe_x_ok(c, nullptr, nullptr, Ms, H)); Ms.E = Ms.seg ? (T + Ms.seg - 1) / Ms.seg : 1;
     }
+    // Shared experts over >= BGL_MFMA_MIN_M tokens, in formats the matrix cores decode exactly, run
+    // as a dense MLP block on the matrix cores (bgl_mlp_dev: gate+up, SwiGLU, down) instead of in
+    // the gathers, whose exact-digit work grows with the token count; the combine adds their rows.
+    const bool shm = nsh && T >= BGL_MFMA_MIN_M && !c->no_mfma && bgl_mfma_ok(sg->T.fmt, sg->T.bits) &&
+                     bgl_mfma_ok(sd->T.fmt, sd->T.bits);
     // The shared gate+up joins the routed launch when that launch runs whole-tile workgroups
     // (BGL_MOE_MERGE=1 forces whole tiles, 0 keeps two launches).
     bool merged = false;
-    if (nsh && c->moe_merge != 0 && moe_x_ok(c, gate, up, Mr, H) && moe_x_ok(c, nullptr, nullptr, Ms, H)) {
+    if (nsh && !shm && c->moe_merge != 0 && moe_x_ok(c, gate, up, Mr, H) && moe_x_ok(c, nullptr, nullptr, Ms, H)) {
         int TR, nw;
         bgl_moe_x_shape(H, act_r * Mr.tpe + (long)Ms.E * Ms.tpe, c->moe_merge == 1 ? BGL_TILE : c->force_tr, c->x_waves, &TR,
                         &nw);
@@ -568,14 +573,17 @@ static int moe_ffn(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor *up, con
     }
     if (!merged) {
         if ((rc = moe_run(c, Mr, gate, up, units, 0, mx, x_dev, T, H, act_r * Mr.tpe))) return rc;
-        if (nsh && (rc = moe_run(c, Ms, nullptr, nullptr, sg->T.nunits, 0, mx, x_dev, T, H, (long)Ms.E * Ms.tpe))) return rc;
+        if (nsh && !shm && (rc = moe_run(c, Ms, nullptr, nullptr, sg->T.nunits, 0, mx, x_dev, T, H, (long)Ms.E * Ms.tpe)))
+            return rc;
     }
     memset(&Mr, 0, sizeof Mr);
     max_units(down, Mr.tpe, units);
     Mr.ta = (const BglDevTensor *)down->dev_table; Mr.E = E; Mr.off = S.off; Mr.y = dd; Mr.ystride = H;
     if ((rc = moe_run(c, Mr, down, nullptr, units, 1, mh, h, P, I, act_r * Mr.tpe))) return rc;
     bool combined = false;
-    if (nsh) {
+    if (shm) {
+        if ((rc = bgl_mlp_dev(c, sg, su, sd, BGL_ACT_F32, x_dev, sdd, T, shh))) return rc;
+    } else if (nsh) {
         memset(&Ms, 0, sizeof Ms);
         Ms.da = sd->T; Ms.tpe = sd->T.ntiles; Ms.ncols = T; Ms.y = sdd; Ms.ystride = H;
         const bool sdx = moe_x_ok(c, nullptr, nullptr, Ms, Ish);

@@ -519,6 +519,32 @@ def test_moe_x_matches_prep_path(torch_dev, oracle, monkeypatch, T, tr):
     assert relerr(outs[0], ref) <= TOL and relerr(outs[1], ref) <= TOL and relerr(outs[0], outs[1]) <= 2 * TOL
 
 
+@pytest.mark.parametrize("T,sh_fmt", [(16, (2, 0)), (21, (4, 10)), (64, (5, 0)), (40, (4, 12))])
+def test_moe_shared_on_matrix_cores(torch_dev, oracle, monkeypatch, T, sh_fmt):
+    """From 16 tokens on, shared experts in a format the matrix cores decode exactly (int8, int4 g32,
+    qNg64 n <= 10) run as a dense MLP block on the matrix cores (gate+up, SwiGLU, down) and the
+    combine adds their rows; n = 12 stays in the exact-digit gathers.  Both against the oracle's FFN
+    and against the gathers alone (BGL_NO_MFMA=1); hidden 320 (a partial pass of 256), shared width
+    320, routed experts in mixed formats."""
+    import beglin_amd
+    torch = torch_dev
+    E, H, I, K, Ish = 6, 320, 192, 2, 320
+    say("moe shared matrix cores", T, sh_fmt)
+    fm = [(5, 0), (2, 0), (4, 7), (4, 15)]
+    gate, up, down, shared = moe_setup(oracle, 6300 + T, E, H, I, Ish, fm, down_fmts=fm[::-1], sh_fmt=sh_fmt)
+    x = seeded_normal(6310 + T, (T, H))
+    idx, w = oracle.route(seeded_normal(6320 + T, (T, E)), K, True)
+    outs = []
+    for flag in ("0", "1"):
+        monkeypatch.setenv("BGL_NO_MFMA", flag)
+        c = beglin_amd.Context(0)
+        outs.append(run_moe(c, torch, gate, up, down, shared, x, idx, w))
+        c.close()
+    monkeypatch.delenv("BGL_NO_MFMA", raising=False)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    assert relerr(outs[0], ref) <= TOL and relerr(outs[1], ref) <= TOL and relerr(outs[0], outs[1]) <= 2 * TOL
+
+
 @pytest.mark.parametrize("T", [1, 3, 6, 13])
 def test_moe_merged_gate_up_equals_two_launches(torch_dev, oracle, monkeypatch, T):
     """The routed and the shared gate+up in one launch (k_moe_x2; past 4 tokens the shared columns
