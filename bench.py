@@ -313,7 +313,8 @@ KERNEL_SOURCES = {
     "cfg2": ("bgl_gemv.hip", "bgl_gemv_impl.h", "bgl_device.h", "bgl_kernels.h"),
     "cfg1": ("bgl_gemv_x.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_device.h", "bgl_kernels.h"),
     "cfg3": ("bgl_gemv_x.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_device.h", "bgl_kernels.h"),
-    "cfg4": ("bgl_moe_x.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_device.h", "bgl_kernels.h"),
+    "cfg4": ("bgl_moe_x.hip", "bgl_moe_x.h", "bgl_moe.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_mfma.hip", "bgl_mlp.hip",
+             "bgl_device.h", "bgl_kernels.h"),
     "cfg5": ("bgl_mfma.hip", "bgl_device.h", "bgl_kernels.h"),
 }
 
@@ -378,7 +379,8 @@ def moe_roofline(ctx, torch, stream, wl, reps):
     o_ms, o_n = ph["other"][0] / reps, ph["other"][1] // reps
     achieved = wl.nbytes() / (g_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_moe_x (bgl_moe_x.hip)",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_moe_x / k_moe_x2 gathers (bgl_moe_x.h); from 16 tokens the shared experts' k_gemm_mfma (bgl_mfma.hip)",
             "launches_per_step": g_n, "kernel_us_per_launch": round(g_ms * 1e3 / max(g_n, 1), 3),
             "bytes_per_launch": round(wl.nbytes() / max(g_n, 1)),
             "prep_us_per_step": round(p_ms * 1e3, 2), "prep_launches": p_n,
