@@ -399,15 +399,16 @@ def test_moe_layer_fused_router_ties_and_wide(ctx, torch_dev, oracle):
         t.free()
 
 
-@pytest.mark.parametrize("merge", ["auto", "1"])
-def test_moe_layer_graph_replays_match_eager(torch_dev, oracle, monkeypatch, merge):
+@pytest.mark.parametrize("merge,T", [("auto", 5), ("1", 5), ("auto", 20)])
+def test_moe_layer_graph_replays_match_eager(torch_dev, oracle, monkeypatch, merge, T):
     """The whole layer (router, top-K + bucketing, FFN, shared experts) replayed
     from a graph: every replay, with eager calls in between, equals the eager result bit for bit
-    (merge "1": the routed and shared gate+up in one launch, k_moe_x2)."""
+    (merge "1": the routed and shared gate+up in one launch, k_moe_x2; T = 20: the Q4G32H shared
+    experts run as the matrix-core MLP block)."""
     import beglin_amd
     torch = torch_dev
-    E, H, I, K, Ish, T = 16, 256, 128, 4, 128, 5
-    say("moe_layer graph", merge)
+    E, H, I, K, Ish = 16, 256, 128, 4, 128
+    say("moe_layer graph", merge, T)
     if merge == "auto":
         monkeypatch.delenv("BGL_MOE_MERGE", raising=False)
     else:
