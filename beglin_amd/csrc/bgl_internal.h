@@ -79,5 +79,7 @@ int run_gemv(bgl_ctx *c, int n, const BglDevTensor *Ts, int act, const GemvAct &
 // Batched fp32-activation GEMM on the matrix cores (bgl_mfma.hip): formats it takes, and the call.
 #define BGL_MFMA_MIN_M 16
 bool bgl_mfma_ok(int fmt, int bits);
+// glu_h (n == 2, a gate/up pair of one shape): the reduce launch also forms h = silu(gate) * up
+// into glu_h [M][N] (k_swiglu's arithmetic), so the caller needs no SwiGLU launch.
 int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
-                  float *const *y, const int *ystride);
+                  float *const *y, const int *ystride, float *glu_h = nullptr);

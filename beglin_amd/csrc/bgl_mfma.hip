@@ -658,6 +658,10 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
 // ==================================================================================== K-split reduce
 // y[m][n] = bias[n] + sum_s part[s][m][n], s in order, for every task of a launch with S > 1.  A
 // thread owns 4 consecutive n of one m and keeps MF_RED_BATCH partials in flight.
+// SwiGLU pair mode (glu_h set; tasks 0 and 1 are gate and up of one shape): a thread forms both
+// tasks' values at its (m, n) -- the split sums as above, or y as the GEMM stored it when the task
+// did not split -- and stores h = silu(g) * u (k_swiglu's arithmetic: exp in double, rounded once)
+// instead of g and u.
 #define MF_RED_BATCH 8
 struct MfmaReduceTask {
     const float *part;
@@ -668,22 +672,17 @@ struct MfmaReduceTask {
 struct MfmaReduce {
     MfmaReduceTask t[BGL_MAX_TASKS];
     int ntasks, M, nquads;
+    float *glu_h;            // SwiGLU pair mode: h [M][glu_stride]
+    int glu_stride;
 };
 
-__global__ __launch_bounds__(256) void k_mfma_reduce(MfmaReduce R) {
-    const int qd = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-    if (qd >= R.nquads) return;
-    int ti = 0;
-#pragma unroll
-    for (int i = 1; i < BGL_MAX_TASKS; i++)
-        if (i < R.ntasks && qd >= R.t[i].q0) ti = i;
-    const MfmaReduceTask &t = R.t[ti];
-    const int nq = (t.N + 3) >> 2, lq = qd - t.q0;
-    const int m = lq / nq, n = 4 * (lq % nq);
-    const size_t plane = (size_t)R.M * t.N;
+// bias[n] + sum_s part[s][m][n] for the 4 values n.. of row m, s in order
+__device__ __forceinline__ void mf_red_quad(const MfmaReduceTask &t, int M, int m, int n, float (&a)[4]) {
+    const size_t plane = (size_t)M * t.N;
     const float *p = t.part + (size_t)m * t.N + n;
     const bool vec = (t.N & 3) == 0;
-    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < 4; e++) a[e] = 0.0f;
     for (int s0 = 0; s0 < t.S; s0 += MF_RED_BATCH) {               // a batch of partials in flight, added in order
         float v[MF_RED_BATCH][4];
 #pragma unroll
@@ -706,9 +705,47 @@ __global__ __launch_bounds__(256) void k_mfma_reduce(MfmaReduce R) {
         }
     }
 #pragma unroll
+    for (int e = 0; e < 4; e++) a[e] = (t.bias && n + e < t.N ? t.bias[n + e] : 0.0f) + a[e];
+}
+
+__global__ __launch_bounds__(256) void k_mfma_reduce(MfmaReduce R) {
+    const int qd = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (qd >= R.nquads) return;
+    if (R.glu_h) {
+        const MfmaReduceTask &tg = R.t[0], &tu = R.t[1];
+        const int nq = (tg.N + 3) >> 2, m = qd / nq, n = 4 * (qd % nq);
+        float g[4], u[4];
+        if (tg.S > 1) mf_red_quad(tg, R.M, m, n, g);
+        else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) g[e] = n + e < tg.N ? tg.y[(size_t)m * tg.ystride + n + e] : 0.0f;
+        }
+        if (tu.S > 1) mf_red_quad(tu, R.M, m, n, u);
+        else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) u[e] = n + e < tu.N ? tu.y[(size_t)m * tu.ystride + n + e] : 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (n + e >= tg.N) break;
+            const float ex = (float)exp(-(double)g[e]);
+            R.glu_h[(size_t)m * R.glu_stride + n + e] = (g[e] / (1.0f + ex)) * u[e];
+        }
+        return;
+    }
+    int ti = 0;
+#pragma unroll
+    for (int i = 1; i < BGL_MAX_TASKS; i++)
+        if (i < R.ntasks && qd >= R.t[i].q0) ti = i;
+    const MfmaReduceTask &t = R.t[ti];
+    const int nq = (t.N + 3) >> 2, lq = qd - t.q0;
+    const int m = lq / nq, n = 4 * (lq % nq);
+    float a[4];
+    mf_red_quad(t, R.M, m, n, a);
+#pragma unroll
     for (int e = 0; e < 4; e++) {
         if (n + e >= t.N) break;
-        t.y[(size_t)m * t.ystride + n + e] = (t.bias ? t.bias[n + e] : 0.0f) + a[e];
+        t.y[(size_t)m * t.ystride + n + e] = a[e];
     }
 }
 
@@ -775,8 +812,10 @@ static double mf_weight_bytes(const BglDevTensor &T) {
 // width and K), M >= 1 columns (the caller routes M >= 16 here).  Columns go in launches of up to
 // 64: one fragment prep, one GEMM over every tensor, and one reduce when any tensor splits K.
 int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
-                  float *const *y, const int *ystride) {
+                  float *const *y, const int *ystride, float *glu_h) {
     const int K = Ts[0].K;
+    if (glu_h && (n != 2 || Ts[1].N != Ts[0].N))
+        return bgl_fail(BGL_E_ARG, "MFMA path: the SwiGLU pair needs two tensors of one shape");
     if (K % 64) return bgl_fail(BGL_E_ARG, "MFMA path: in=%d %% 64 != 0", K);
     if (n < 1 || n > BGL_MAX_TASKS) return bgl_fail(BGL_E_ARG, "MFMA path: %d tensors in a group (1..%d)", n, BGL_MAX_TASKS);
     for (int i = 0; i < n; i++) {
@@ -839,6 +878,18 @@ int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev,
                 nq += Mc * ((t.T.N + 3) / 4);
             }
             R.nquads = nq;
+        }
+        if (glu_h) {                    // SwiGLU pair: both tasks, split or not, one quad grid
+            for (int i = 0; i < 2; i++) {
+                const MfmaTask &t = L.t[i];
+                MfmaReduceTask &rt = R.t[i];
+                rt.part = S_[i] > 1 ? t.part : nullptr; rt.bias = t.bias; rt.y = t.y;
+                rt.N = t.T.N; rt.S = S_[i]; rt.ystride = t.ystride; rt.q0 = 0;
+            }
+            R.ntasks = 2;
+            R.glu_h = glu_h + (size_t)m0 * Ts[0].N;
+            R.glu_stride = Ts[0].N;
+            R.nquads = Mc * ((Ts[0].N + 3) / 4);
         }
         int tok = prof_begin(c, 1);
         if (launch_any(L, Ts[0].fmt, Ts[0].bits, CT, dim3(wgs), c->stream)) return bgl_fail(BGL_E_UNSUPPORTED, "MFMA path: format");

@@ -5,6 +5,9 @@
 //
 //   g, u = W_gate x, W_up x      bgl_matmul_group_dev over {gate, up} (one fused launch)
 //   h = silu(g) * u              k_swiglu: h = (g / (1 + exp(-g))) * u in fp32, exp rounded once
+//                                (>= 16 fp32 columns on the matrix cores: the GEMM's reduce launch
+//                                forms h with the same arithmetic, from the K-split sums or, for a
+//                                tensor whose K did not split, from the g / u the GEMM stored)
 //   y = W_down h                 bgl_matmul_dev (W4A8: h quantized to int8 as any activation)
 //
 // The exponential is evaluated in double and rounded once to float: a correctly rounded expf in
@@ -55,6 +58,14 @@ extern "C" int bgl_mlp_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor 
     const bgl_tensor *gu[2] = {gate, up};
     const float *nob[2] = {nullptr, nullptr};
     float *ys[2] = {g, u};
+    // M >= BGL_MFMA_MIN_M fp32 columns on the matrix cores: the K-split reduce forms h itself
+    if (act == BGL_ACT_F32 && M >= BGL_MFMA_MIN_M && !c->no_mfma && gate->T.fmt == up->T.fmt &&
+        gate->T.bits == up->T.bits && bgl_mfma_ok(gate->T.fmt, gate->T.bits)) {
+        const BglDevTensor Ts[2] = {gate->T, up->T};
+        int rc = run_gemm_mfma(c, 2, Ts, x_dev, M, nob, ys, nullptr, h);
+        if (rc) return rc;
+        return bgl_matmul_dev(c, down, act, h, nullptr, y_dev, M);
+    }
     int rc = bgl_matmul_group_dev(c, 2, gu, act, x_dev, nob, ys, M);
     if (rc) return rc;
     int tok = prof_begin(c, 2);

@@ -114,6 +114,36 @@ def test_mlp_f32(ctx, torch_dev, oracle, model, kind, bits, H, I, M):
         t.free()
 
 
+@pytest.mark.parametrize("H,I,M", [(512, 1024, 16), (4096, 14336, 32), (1536, 8960, 40)])
+def test_mlp_matrix_core_swiglu_in_reduce(ctx, torch_dev, oracle, H, I, M):
+    """From 16 fp32 columns the gate+up GEMM runs on the matrix cores and its reduce launch forms
+    h = silu(g) * u itself.  h must equal SwiGLU (the oracle's, which the GPU's k_swiglu matches bit
+    for bit) of the g and u that the same GEMM stores when asked for them, bit for bit: at a K that
+    does not split (512: the GEMM stores g and u, the reduce reads them) and at K-split shapes
+    (4096, 1536); the whole block to 1e-5 against the oracle."""
+    import beglin_amd
+    torch = torch_dev
+    say("mlp matrix-core swiglu", H, I, M)
+    gen = torch.Generator(device="cuda").manual_seed(950 + M + H)
+    shapes = ((I, H), (I, H), (H, I))
+    ts, refs = zip(*[qdev(ctx, torch, gen, 5, 0, o, i) for o, i in shapes])
+    x = seeded_normal(960 + M, (M, H))
+    y, h = run(ctx, torch, ts, x, beglin_amd.ACT_F32)
+    gd = torch.empty((M, I), device="cuda")
+    ud = torch.empty((M, I), device="cuda")
+    ctx.matmul_group([ts[0], ts[1]], dev(torch, x), [gd, ud], act=beglin_amd.ACT_F32)
+    ctx.sync()
+    hs = oracle.swiglu(gd.cpu().numpy(), ud.cpu().numpy())
+    assert np.array_equal(h.view(np.uint32), np.asarray(hs, np.float32).view(np.uint32))
+    g = oracle.gemm_f32(5, refs[0][0], refs[0][1], x)
+    u = oracle.gemm_f32(5, refs[1][0], refs[1][1], x)
+    hr = oracle.swiglu(g, u)
+    assert relerr(h, hr) <= TOL
+    assert relerr(y, oracle.gemm_f32(5, refs[2][0], refs[2][1], hr)) <= TOL
+    for t in ts:
+        t.free()
+
+
 def test_mlp_graph_replay_and_refusals(ctx, torch_dev, oracle):
     """The block captured in a HIP graph replays to the eager result (no host round trip inside);
     shapes that do not form an MLP are refused before anything is launched."""
