@@ -993,10 +993,12 @@ struct ReadSeg {
     const uint8_t *p;
     uint64_t n16;                       // 16-byte words
 };
+#define BGL_READ_PROBE_MAX_TENSORS 64   // a MoE gather launch's expert tensors (3 segments each)
 struct ReadProbe {
-    ReadSeg s[3 * BGL_MAX_TASKS];
+    ReadSeg s[3 * BGL_READ_PROBE_MAX_TENSORS];
     int nseg;
 };
+static_assert(sizeof(ReadProbe) <= 3584, "the read probe's segment list travels as a kernel argument (<= 4 KB)");
 __global__ __launch_bounds__(1024) void k_read_probe(ReadProbe P) {
     const uint64_t nt = (uint64_t)gridDim.x * blockDim.x, tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     uint32_t acc = 0;
@@ -1017,7 +1019,8 @@ __global__ __launch_bounds__(1024) void k_read_probe(ReadProbe P) {
 }
 
 extern "C" int bgl_read_probe_dev(bgl_ctx *c, int n, const bgl_tensor *const *w, int nblocks, int nthreads) {
-    if (!c || n < 1 || n > BGL_MAX_TASKS || !w) return bgl_fail(BGL_E_ARG, "bgl_read_probe_dev: bad argument");
+    if (!c || n < 1 || n > BGL_READ_PROBE_MAX_TENSORS || !w)
+        return bgl_fail(BGL_E_ARG, "bgl_read_probe_dev: bad argument (1 <= n <= %d tensors)", BGL_READ_PROBE_MAX_TENSORS);
     if (nblocks <= 0) nblocks = 1024;
     if (nthreads <= 0) nthreads = 256;
     if (nthreads > 1024 || nthreads % 64) return bgl_fail(BGL_E_ARG, "bgl_read_probe_dev: nthreads %d", nthreads);

@@ -211,16 +211,18 @@ class MoeWorkload:
         self.x = torch.randn((T, H), generator=gen, device="cuda")
         self.layers = []
         self.formats = []
+        self.probe_sets = []          # per layer: the single tensors each gather launch streams
         for _ in range(layers):
             fm = [CFG4_FORMATS[i] for i in rng.integers(0, len(CFG4_FORMATS), E)]
             shf = CFG4_FORMATS[int(rng.integers(0, len(CFG4_FORMATS)))]
-            stacks = []
+            stacks, handles = [], []
             for (o, i) in ((I, H), (I, H), (H, I)):
                 ts = []
                 for (k, b) in fm:
                     w = gen_weight(torch, gen, o, i)
                     ts.append(ctx.quantize(k, w, bits=b))
                     del w
+                handles.append([t.h.value for t in ts])        # the stack owns them; kept for the read probe
                 stacks.append(ctx.experts_from_tensors(ts))
             sh = []
             for (o, i) in ((Ish, H), (Ish, H), (H, Ish)):
@@ -240,11 +242,26 @@ class MoeWorkload:
             out = torch.empty((T, H), device="cuda")
             self.layers.append((stacks, tuple(sh), idx, w, out, nb, len(touched), rw))
             self.formats.append((fm, shf))
+            # the gather launches' tensors: routed gate+up (+ the shared gate+up, in the same launch
+            # below 16 tokens or where the shared experts stay in the gathers), routed down, shared down
+            view = lambda hs: [beglin_amd.Tensor(hs[e]) for e in touched]
+            shm = T >= 16 and (shf[0] in (5, 2) or (shf[0] == 4 and shf[1] <= 10))
+            gu = view(handles[0]) + view(handles[1])
+            sets = [gu, view(handles[2]), [sh[0], sh[1]], [sh[2]]] if shm else [gu + [sh[0], sh[1]], view(handles[2]), [sh[2]]]
+            self.probe_sets.append(sets)
 
     def run(self, tags=None):
         K = DSV2["K"]
         for stacks, sh, idx, w, out, _, _, rw in self.layers:
             self.ctx.moe_layer(rw, stacks[0], stacks[1], stacks[2], sh, self.x, K, out)
+
+    def read_probe(self):
+        """A plain read of exactly the weight bytes each gather launch streams, launch by launch
+        (bgl_read_probe_dev takes up to 64 tensors, so a launch of more becomes several)."""
+        for sets in self.probe_sets:
+            for ts in sets:
+                for i in range(0, len(ts), 64):
+                    self.ctx.read_probe(ts[i:i + 64])
 
     def nbytes(self, tags=None):
         return sum(l[5] for l in self.layers)
@@ -753,6 +770,12 @@ def main():
         per_call = {"moe_layer": {"us": round(step_ms * 1e3 / args.layers, 2), "GB/s": round(value, 1)}}
         roof = moe_roofline(ctx, torch, stream, wl, max(3, args.steps // 10))
         attach_traffic(roof, args, roof["bytes_per_launch"])
+        pr_ms, _, _ = time_graph(torch, stream, wl.read_probe, max(5, args.steps // 5), 3)
+        roof["plain_read"] = {"us_per_step": round(pr_ms * 1e3, 2), "GB/s": round(wl.nbytes() / (pr_ms * 1e-3) / 1e9, 1),
+                              "step_over_plain": round(step_ms / pr_ms, 3),
+                              "how": "bgl_read_probe_dev over the touched experts' and the shared experts' tensors of "
+                                     "each gather launch (launches of up to 64 tensors), 1024 x 256 threads, graph-timed; "
+                                     "router weights and activations not read"}
         cpu = None if args.no_cpu else cpu_baseline_cfg4(wl, args.cpu_seconds, args.seed)
         finish(args, wl, ctx, graph, value, step_ms, wall, dtype, cfg, per_call, roof, cpu)
         return

@@ -135,9 +135,10 @@ int  bgl_mlp_dev(bgl_ctx *ctx, const bgl_tensor *gate, const bgl_tensor *up, con
 #define BGL_NOALLOC_SCRATCH_BYTES (32u << 20)
 int  bgl_matmul_group_noalloc_dev(bgl_ctx *ctx, int n, const bgl_tensor *const *w, int act, const float *x_dev,
                                   const float *const *bias_dev, float *const *y_dev, int M);
-/* Streaming read of up to 4 bound tensors' device bytes (packed chunks, scales, biases) on the
- * context's stream: no counterpart in the reference -- a measurement aid that gives the plain-read
- * floor for exactly the bytes a GEMV call streams.  nblocks / nthreads <= 0: 1024 x 256. */
+/* Streaming read of up to 64 bound tensors' device bytes (packed chunks, scales, biases) on the
+ * context's stream, in one launch: no counterpart in the reference -- a measurement aid that gives
+ * the plain-read floor for exactly the bytes a GEMV call or a MoE gather launch streams.  The
+ * tensors are single (not expert stacks).  nblocks / nthreads <= 0: 1024 x 256. */
 int  bgl_read_probe_dev(bgl_ctx *ctx, int n, const bgl_tensor *const *w, int nblocks, int nthreads);
 /* Prepare activation operands once and reuse them for several GEMVs with the same input (the
  * caller-side quantization of matmul_sdot, qwen_infer.c:1870-1889, feeding gemm_qXg64_sdot_mt's
