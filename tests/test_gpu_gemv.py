@@ -449,3 +449,19 @@ def test_g256plain_separate_quantization_path(torch_dev, oracle, monkeypatch, M)
     t.free(); c.close()
     monkeypatch.delenv("BGL_NO_FUSED_Q", raising=False)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), relerr(got, ref)
+
+
+def test_read_probe_tensor_limits(ctx, torch_dev):
+    """The streaming-read probe (a measurement aid) takes 1-64 single tensors per launch, as a MoE
+    gather launch's expert tensors need; more is refused before anything is launched."""
+    import beglin_amd
+    torch = torch_dev
+    gen = torch.Generator(device="cuda").manual_seed(77)
+    ts = [ctx.quantize(beglin_amd.K_Q4G32H, torch.randn((64, 256), generator=gen, device="cuda") * 0.02) for _ in range(65)]
+    ctx.read_probe(ts[:64])
+    ctx.read_probe(ts[:1], nblocks=8, nthreads=64)
+    ctx.sync()
+    with pytest.raises(beglin_amd.BglError):
+        ctx.read_probe(ts)
+    for t in ts:
+        t.free()
