@@ -20,13 +20,19 @@ def lib():
     return _lib
 
 
+# BGL_E_* codes of include/beglin_qgemv.h
+E_ARG, E_UNSUPPORTED, E_HIP, E_NODEV, E_NOMEM, E_CAPTURE, E_TIMEOUT = -1, -2, -3, -4, -5, -6, -7
+
+
 class BglError(RuntimeError):
-    pass
+    def __init__(self, msg, code=0):
+        super().__init__(msg)
+        self.code = code
 
 
 def _check(rc, what):
     if rc != 0:
-        raise BglError(f"{what} failed ({rc}): {lib().bgl_last_error().decode(errors='replace')}")
+        raise BglError(f"{what} failed ({rc}): {lib().bgl_last_error().decode(errors='replace')}", rc)
 
 
 def _p(t):
@@ -83,6 +89,10 @@ class Context:
 
     def sync(self):
         _check(lib().bgl_synchronize(self.h), "bgl_synchronize")
+
+    def check(self):
+        """Synchronize, then raise if a bounded in-kernel wait gave up since the last check (bgl_ctx_check)."""
+        _check(lib().bgl_ctx_check(self.h), "bgl_ctx_check")
 
     # ---- profiling (QWEN_PROF analogue) ----
     def prof_enable(self, on=True):

@@ -31,6 +31,7 @@ SIGNATURES = [
     ("bgl_ctx_create", _I, [_I, _P, C.POINTER(_P)]),
     ("bgl_ctx_destroy", None, [_P]),
     ("bgl_synchronize", _I, [_P]),
+    ("bgl_ctx_check", _I, [_P]),
     ("bgl_ctx_stream", _P, [_P]),
     ("bgl_prof_enable", _I, [_P, _I]),
     ("bgl_prof_read", _I, [_P, C.POINTER(C.c_double), C.POINTER(_I), _I]),

@@ -91,16 +91,21 @@ static void dbuf_free(DevBuf &b) {
 size_t ctx_scratch(bgl_ctx *c, bool release) {
     DevBuf *bufs[] = {&c->act_w, &c->act_s, &c->act_sum, &c->part, &c->hx, &c->hy, &c->hb,
                       &c->moe_a, &c->moe_b, &c->moe_c, &c->moe_d, &c->moe_e, &c->moe_f, &c->moe_g, &c->moe_meta,
-                      &c->moe_route, &c->moe_scores, &c->mlp};
+                      &c->moe_route, &c->moe_scores, &c->mlp, &c->prep_xc};
     size_t total = 0;
     for (DevBuf *b : bufs) {
         total += b->bytes;
         if (release) dbuf_free(*b);
     }
+    for (auto &kv : c->mlp_sync) {
+        total += kv.second.bytes;
+        if (release) dbuf_free(kv.second);
+    }
+    if (release) c->mlp_sync.clear();
     if (release) {
         for (void *p : c->retired) (void)hipFree(p);
         c->retired.clear();
-        c->prep_act = -1; c->prep_M = 0; c->prep_K = 0;
+        c->prep_act = -1; c->prep_M = 0; c->prep_K = 0; c->prep_reuse = false; c->prep_x = nullptr;
     }
     return total;
 }
@@ -171,6 +176,18 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     const char *mcap = getenv("BGL_MOE_CAP");
     c->moe_cap = mcap ? atoi(mcap) : 0;
     if (c->moe_cap != 4 && c->moe_cap != 8) c->moe_cap = 0;
+    const char *nfm = getenv("BGL_NO_FUSED_MLP");
+    c->no_fused_mlp = nfm && atoi(nfm) != 0;
+    const char *ms = getenv("BGL_MLP_SPIN");
+    if (ms && atoi(ms) > 0) c->mlp_spin = atoi(ms);
+    const char *mwv = getenv("BGL_MLP_WAVES");
+    c->mlp_waves = mwv ? atoi(mwv) : 0;
+    if (c->mlp_waves < 0 || c->mlp_waves > 16) c->mlp_waves = 0;
+    const char *mtr = getenv("BGL_MLP_TRG");
+    c->mlp_trg = mtr ? atoi(mtr) : 0;
+    if (c->mlp_trg != 16 && c->mlp_trg != 32) c->mlp_trg = 0;
+    const char *mt = getenv("BGL_MLP_TEST_TIMEOUT");
+    c->mlp_test_timeout = mt && atoi(mt) > 0 ? atoi(mt) : 0;
     *out = c;
     return 0;
 }
@@ -329,6 +346,13 @@ bgl_tensor *tensor_from_parts(const BglDevTensor &T, void *w, void *s0, void *s1
 // Repack reference-layout device buffers into a new tensor.
 static int repack_into(bgl_ctx *c, int kind, int bits, int out, int in, const void *dpk, const void *dsc,
                        const uint8_t *dsub, bgl_tensor **res) {
+    switch (kind) {
+    case BGL_Q4G64: case BGL_Q4G32H: case BGL_Q4G256SF: case BGL_Q4G64A: case BGL_MXFP4:
+    case BGL_Q8G64: case BGL_F16: case BGL_F32: case BGL_QNG64:
+        break;
+    default:
+        return bgl_fail(BGL_E_ARG, "repack: kind %d has no device layout of its own", kind);
+    }
     bgl_tensor *t = new bgl_tensor();
     BglDevTensor &T = t->T;
     size_t lb[3];
@@ -535,7 +559,7 @@ extern "C" int bgl_quantize_dev(bgl_ctx *c, int kind, int bits, int qng64_encode
     if (!c || !w_dev || !t) return bgl_fail(BGL_E_ARG, "bgl_quantize_dev: NULL argument");
     int rc = check_wt(kind, bits, out, in);
     if (rc) return rc;
-    if (kind == BGL_Q4G64A || kind == BGL_F16 || kind == BGL_F32 || kind == BGL_MXFP4)
+    if (kind == BGL_Q4G64A || kind == BGL_F16 || kind == BGL_F32 || kind == BGL_MXFP4 || kind == BGL_K_Q4G256P)
         return bgl_fail(BGL_E_UNSUPPORTED, "bgl_quantize_dev: kind %d has no packer here (bind its bytes with bgl_bind)", kind);
     if (kind == BGL_QNG64 && qng64_encoder && bits == 4)
         return bgl_fail(BGL_E_ARG, "qng64_quantize_f32 rejects n=4 (qng64_dense.c:9)");
@@ -619,7 +643,8 @@ extern "C" int bgl_dequant_dev(bgl_ctx *c, const bgl_tensor *t, int row0, int nr
 }
 
 // ------------------------------------------------------------------ activation prep
-static int act_group(int kind) { return kind == BGL_Q4G256SF ? 256 : 64; }
+// g256sf and plain g256 (same device format, gmul = 1) quantize their activations per 256 values
+static int act_group(int kind) { return kind == BGL_Q4G256SF || kind == BGL_K_Q4G256P ? 256 : 64; }
 
 // The fp32-activation operands of M prepared columns of length K: k_act_x24 writes level 0 of all
 // M columns and then level 1 into each of the three buffers.
@@ -655,6 +680,7 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
     }
     HIPCHK(hipGetLastError());
     c->prep_act = act; c->prep_gq = gq; c->prep_M = M; c->prep_K = K; c->prep_x = x_dev;
+    c->prep_reuse = false;                 // a GEMV call's own operands: x_dev is the caller's, valid for that call only
     if (act == BGL_ACT_F32) {
         f32_act_ptrs(c->act_w.p, c->act_s.p, c->act_sum.p, M, K, x_dev, A);
     } else {
@@ -936,6 +962,7 @@ extern "C" int bgl_matmul_group_noalloc_dev(bgl_ctx *c, int n, const bgl_tensor 
     const DevBuf aw = c->act_w, as = c->act_s, asum = c->act_sum, part = c->part;
     const int pa = c->prep_act, pg = c->prep_gq, pm = c->prep_M, pk = c->prep_K;
     const float *px = c->prep_x;
+    const bool pr = c->prep_reuse;
     const bool prof = c->prof;
     c->act_w = c->act_s = c->act_sum = c->part = DevBuf{};
     c->fixed_base = base; c->fixed_cap = BGL_NOALLOC_SCRATCH_BYTES; c->fixed_used = 0;
@@ -943,7 +970,7 @@ extern "C" int bgl_matmul_group_noalloc_dev(bgl_ctx *c, int n, const bgl_tensor 
     const int rc = bgl_matmul_group_dev(c, n, w, act, x_dev, bias_dev, y_dev, M);
     c->fixed_base = nullptr; c->fixed_cap = 0; c->fixed_used = 0;
     c->act_w = aw; c->act_s = as; c->act_sum = asum; c->part = part;
-    c->prep_act = pa; c->prep_gq = pg; c->prep_M = pm; c->prep_K = pk; c->prep_x = px;
+    c->prep_act = pa; c->prep_gq = pg; c->prep_M = pm; c->prep_K = pk; c->prep_x = px; c->prep_reuse = pr;
     c->prof = prof;
     return rc;
 }
@@ -955,7 +982,20 @@ extern "C" int bgl_prep_act_dev(bgl_ctx *c, int act, int kind, const float *x_de
     if (in % 64 || in % gq) return bgl_fail(BGL_E_ARG, "bgl_prep_act_dev: in=%d not a multiple of the group", in);
     HIPCHK(hipSetDevice(c->device));
     GemvAct A;
-    return prep_act(c, act, gq, x_dev, M, in, A);
+    const float *src = x_dev;
+    if (act == BGL_ACT_F32) {
+        // The fp32 GEMVs read the raw columns again for groups holding NaN / +-Inf: keep a copy in the
+        // context, so x_dev may be reused or freed once this call is ordered on the stream.
+        const size_t xb = (size_t)M * in * sizeof(float);
+        if (dbuf_reserve(c, c->prep_xc, xb, false)) return bgl_last_code();
+        HIPCHK(hipMemcpyAsync(c->prep_xc.p, x_dev, xb, hipMemcpyDeviceToDevice, c->stream));
+        src = (const float *)c->prep_xc.p;
+    }
+    const int rc = prep_act(c, act, gq, src, M, in, A);
+    if (rc) return rc;
+    if (act != BGL_ACT_F32) c->prep_x = nullptr;
+    c->prep_reuse = true;
+    return 0;
 }
 
 extern "C" int bgl_matmul_prepped_dev(bgl_ctx *c, const bgl_tensor *w, int act, const float *bias_dev, float *y_dev, int M) {
@@ -963,8 +1003,10 @@ extern "C" int bgl_matmul_prepped_dev(bgl_ctx *c, const bgl_tensor *w, int act, 
     const BglDevTensor &T = w->T;
     if (T.fmt == BGL_Q4G64A || T.fmt == BGL_F16 || T.fmt == BGL_F32 || T.fmt == BGL_MXFP4)
         return bgl_fail(BGL_E_UNSUPPORTED, "kind %d runs in the MoE gather only", T.fmt);
-    if (c->prep_act != act || c->prep_K != T.K || c->prep_gq != act_group(T.fmt) || M > c->prep_M)
-        return bgl_fail(BGL_E_ARG, "bgl_matmul_prepped_dev: no prepared activation matches (act %d, in %d, M %d)", act, T.K, M);
+    const int kind = T.fmt == BGL_Q4G256SF && T.gmul == 1.0f ? BGL_K_Q4G256P : T.fmt;
+    if (!c->prep_reuse || c->prep_act != act || c->prep_K != T.K || c->prep_gq != act_group(kind) || M > c->prep_M)
+        return bgl_fail(BGL_E_ARG, "bgl_matmul_prepped_dev: no activation prepared by bgl_prep_act_dev matches (act %d, in %d, M %d)",
+                        act, T.K, M);
     if (T.fmt == BGL_Q4G256SF && act != BGL_ACT_W4A8)
         return bgl_fail(BGL_E_UNSUPPORTED, "K_Q4G256SF requires W4A8 activations -- no fp32-activation path exists for g256sf");
     HIPCHK(hipSetDevice(c->device));
@@ -1116,7 +1158,7 @@ static int host_call_i8(bgl_ctx *c, const bgl_wt &wt, const int8_t *xq, const fl
                        (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
     prof_end(c, tok);
     HIPCHK(hipGetLastError());
-    c->prep_act = BGL_ACT_W4A8; c->prep_gq = gq; c->prep_M = M; c->prep_K = K;
+    c->prep_act = BGL_ACT_W4A8; c->prep_gq = gq; c->prep_M = M; c->prep_K = K; c->prep_x = nullptr; c->prep_reuse = true;
     rc = bgl_matmul_prepped_dev(c, t, BGL_ACT_W4A8, bias ? (const float *)c->hb.p : nullptr, (float *)c->hy.p, M);
     if (rc) return rc;
     HIPCHK(hipMemcpyAsync(y, c->hy.p, yb, hipMemcpyDeviceToHost, c->stream));

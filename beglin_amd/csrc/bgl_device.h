@@ -31,22 +31,33 @@
 #define BGL_MXFP4 BGL_K_MXFP4
 
 // fp32 activations as exact integers, per 64-group:
-//   level 0: X = rint(x * 2^(21-e)), e = exponent of the group's largest finite |x| (|X| <= 2^21),
-//            as three balanced base-256 int8 digits X = d0 + 256*d1 + 65536*d2;
-//   level 1: only in groups where fewer than half of the nonzero elements lie within 2^6 of that
-//            maximum (an outlier would otherwise leave the rest of the group with few bits): the
-//            residual r = x * 2^(21-e) - X (exact) as X1 = rint(r * 2^(21-e1)), e1 = exponent of the
-//            group's largest |r|, in the same three digits.  x = (X + X1 * 2^(e1-21)) * 2^(e-21) to
-//            about 2^-44 of the group maximum.
+//   level 0: X = rint(x * 2^(22-e)), e = exponent of the group's largest finite |x| (|X| <= 2^22),
+//            as three balanced base-256 int8 digits X = d0 + 256*d1 + 65536*d2 (|d2| <= 64).  An
+//            element's error is at most 2^(e-23): relative to any |x| >= 2^(e-6), at most 2^-17.
+//   level 1: in groups holding at least BGL_X_SMALL_MAX nonzero elements below 2^(e-6), or more
+//            such small elements than elements at or above it (an outlier, or a cluster of large
+//            channels, would otherwise leave the small elements with few bits): the residual
+//            r = x * 2^(22-e) - X (exact) as X1 = rint(r * 2^(22-e1)), e1 = exponent of the group's
+//            largest |r|, in the same three digits.  x = (X + X1 * 2^(e1-22)) * 2^(e-22) to about
+//            2^-46 of the group maximum.
+//   So a level-0 group's dot product errs by at most 2^-17 * sum |w| * max(|x|, 2^(e-6)), where at
+//   most BGL_X_SMALL_MAX - 1 nonzero elements take the 2^(e-6) floor.
 // Non-finite elements (NaN, +-Inf) enter both levels as 0; the group is flagged and the GEMVs add
 // their products code * scale * x one element at a time, so NaN and +-Inf propagate as in IEEE
 // arithmetic.  Per column the prep kernel writes [group][digit][64 bytes] (48 dwords per group),
-// the power-of-two scale 2^(e-21) per group and the exact integer sum of the digits per
-// 32-element half-group; level 1 the same beside it, plus the ratio 2^(e1-21) (0 without level 1).
+// the power-of-two scale 2^(e-22) per group and the exact integer sum of the digits per
+// 32-element half-group; level 1 the same beside it, plus the ratio 2^(e1-22) (0 without level 1).
 #define BGL_XD_DW 48
 #define BGL_XF_L1 1            // group flags: the group has level-1 digits
 #define BGL_XF_NF 2            //              the group holds a non-finite element
-#define BGL_X_SPIKE_BITS 6     // level 1 when fewer than half the nonzero |x| are >= 2^(e-6)
+#define BGL_X_FRAC 22          // level-0 / level-1 fixed point: X = rint(x * 2^(BGL_X_FRAC - e))
+#define BGL_X_SPIKE_BITS 6     // "small": a nonzero |x| below 2^(e-6)
+#define BGL_X_SMALL_MAX 8      // level 1 from this many small elements (or more small than large)
+
+// The level-1 trigger from a group's count of small (nonzero, below 2^(e-6)) and large elements.
+__host__ __device__ __forceinline__ bool bgl_x_level1(int nsmall, int nlarge) {
+    return nsmall > nlarge || nsmall >= BGL_X_SMALL_MAX;
+}
 
 // Wave-uniform read-only operands (activations, column maps) are read through the constant address
 // space so the compiler emits scalar loads (s_load_dwordx16) and feeds v_dot4 from SGPRs.

@@ -398,7 +398,7 @@ __device__ __forceinline__ void comp_dense(const Raw<FMT, NB> &r, int K, int u, 
 
 // ======================================================================== flagged groups (cold path)
 // The terms the level-0 digits leave out, for the groups of unit u flagged in some column of the
-// launch: the level-1 residual s * ((V1 * 2^(e1-21)) * 2^(e-21)) and the non-finite products.  Run
+// launch: the level-1 residual s * ((V1 * 2^(e1-22)) * 2^(e-22)) and the non-finite products.  Run
 // after the main loop over units whose flags are set (the unit's weights are loaded again), so the
 // hot loop keeps its registers.
 template <int FMT, int NB>

@@ -4,9 +4,9 @@
 // the fp32 fold, and the in-kernel making of the records from raw fp32 values.
 //
 // A record (one per 64-group and activation column, 240 bytes in LDS): the three balanced int8
-// digits of X = rint(x * 2^(21-e)) (e = exponent of the group's largest finite |x|) as 48 dwords,
+// digits of X = rint(x * 2^(22-e)) (e = exponent of the group's largest finite |x|) as 48 dwords,
 // the digit sums of the two 32-element halves (the first half's 4th int holds the group's BGL_XF_*
-// flags), the scale 2^(e-21) and the level-1 ratio 2^(e1-21) -- k_act_x24's operands
+// flags), the scale 2^(e-22) and the level-1 ratio 2^(e1-22) -- k_act_x24's operands
 // (bgl_prep.hip), so every product is an exact int32 dot4 sum and fp32 only enters in the
 // per-group fold.  A group flagged BGL_XF_L1 also has a level-1 record (the residual's digits and
 // sums) at a fixed dword offset l1 from its level-0 record; its ratio is 0 otherwise, so a level-1
@@ -22,7 +22,7 @@
 
 #define XREC_DW 60            // LDS dwords per 64-group record
 #define XREC_DSUM 48          // digit sums of the two halves: [half][digit 0..2, flags / pad]
-#define XREC_SCALE 56         // 2^(e-21), then the level-1 ratio 2^(e1-21)
+#define XREC_SCALE 56         // 2^(e-22), then the level-1 ratio 2^(e1-22)
 #define X_PRE 4               // record pieces (16 bytes) per thread loaded ahead of the weights
 
 // (a & m) | o in one v_and_or_b32 (gfx9's three-operand encoding takes no literal constant and
@@ -306,7 +306,7 @@ struct XRow {
 };
 
 // The group's fp32 term against one record: the exact integer dot product per digit, folded as
-// s * ((t0 + 256 t1 + 65536 t2) * 2^(e-21)).
+// s * ((t0 + 256 t1 + 65536 t2) * 2^(e-22)).
 template <int FMT, int NB>
 __device__ __forceinline__ float x_dot(const XDec<FMT, NB> &w, const int *rec) {
     const int4 ds0 = *reinterpret_cast<const int4 *>(rec + XREC_DSUM);
@@ -371,7 +371,7 @@ __device__ __forceinline__ float x_dot(const XDec<FMT, NB> &w, const int *rec) {
 
 // The terms the level-0 digits leave out, for a lane's group flagged BGL_XF_L1 or BGL_XF_NF (0 for
 // the lanes of the wave whose groups are not): the level-1 residual
-// s * ((V1 * 2^(e1-21)) * 2^(e-21)) against the level-1 digits at r1 (48 dwords, LDS or global)
+// s * ((V1 * 2^(e1-22)) * 2^(e-22)) against the level-1 digits at r1 (48 dwords, LDS or global)
 // with their half sums e0 / e1, and the non-finite products.  Cold path: the GEMVs run it after
 // their main loop for the slots whose records carry flags, with the weights loaded again.
 template <int FMT, int NB>
@@ -398,11 +398,11 @@ __device__ __forceinline__ float x_group(const XRaw<FMT, NB> &r, const int *rec)
 
 // ---- fused activation digits (k_act_x24's arithmetic, bgl_prep.hip): one pass is 256 consecutive
 // values, lane l holding values 4l..4l+3 (one float4), a 16-lane row one 64-group g = 4p + l/16.
-// Per group e = exponent of the largest finite |x| (frexp), X = rint(x * 2^(21-e)) split into
+// Per group e = exponent of the largest finite |x| (frexp), X = rint(x * 2^(22-e)) split into
 // balanced int8 digits X = d0 + 256 d1 + 65536 d2; the record gets the digits, their sums per
-// 32-element half, the flags, 2^(e-21) and the level-1 ratio.  Groups with an outlier (fewer than
-// half the nonzero elements within 2^BGL_X_SPIKE_BITS of the max) also get the level-1 record of
-// the residual at rec + l1; non-finite elements count as 0 and flag the group.
+// 32-element half, the flags, 2^(e-22) and the level-1 ratio.  Groups that bgl_x_level1 selects
+// (many elements more than 2^BGL_X_SPIKE_BITS below the max) also get the level-1 record of the
+// residual at rec + l1; non-finite elements count as 0 and flag the group.
 template <int CTRL>
 __device__ __forceinline__ uint32_t x_dpp(uint32_t v) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false); }
 __device__ __forceinline__ uint32_t x_umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
@@ -418,7 +418,7 @@ __device__ __forceinline__ float4 x_pass_load(const float *x, int p, int lane, i
     return make_float4(t.x, t.y, t.z, t.w);
 }
 
-// Three balanced digits of 4 integers |X| <= 2^21, packed one byte per element, and their sums
+// Three balanced digits of 4 integers |X| <= 2^22, packed one byte per element, and their sums
 // over the lane's 8-lane half of the row (32 elements).
 struct XPack {
     uint32_t D[3];
@@ -457,13 +457,13 @@ __device__ __forceinline__ void x_store3(int *rec, int q, const XPack &p, int fl
 
 // A 16-lane row's 64-group (4 values per lane): non-finite values zeroed (rare: only when the
 // row's largest |x| bits are Inf/NaN), e = exponent of the largest finite |x| (frexp), whether the
-// group has an outlier, and the level-0 integers X = rint(x * 2^(21-e)) with their exact residuals.
+// group needs level 1, and the level-0 integers X = rint(x * 2^(22-e)) with their exact residuals.
 struct XStat {
     float mx;                  // the group's largest finite |x|
     int e, nnf;                // exponent of mx; non-finite values in the row
-    bool spiky;                // fewer than half the nonzero |x| are >= 2^(e - BGL_X_SPIKE_BITS)
+    bool spiky;                // bgl_x_level1 over the nonzero |x| below / at or above 2^(e - BGL_X_SPIKE_BITS)
     int X[4];
-    float r[4];                // x * 2^(21-e) - X, exact, |r| <= 1/2
+    float r[4];                // x * 2^(22-e) - X, exact, |r| <= 1/2
 };
 __device__ __forceinline__ XStat x_stat(const float4 &v) {
     XStat st;
@@ -488,10 +488,10 @@ __device__ __forceinline__ XStat x_stat(const float4 &v) {
 #pragma unroll
     for (int i = 0; i < 4; i++) cnt += (b[i] != 0u ? 256 : 0) + (b[i] >= thr ? 1 : 0);
     cnt = row_sum_i32(cnt);
-    st.spiky = 2 * (cnt & 255) < (cnt >> 8);
+    st.spiky = bgl_x_level1((cnt >> 8) - (cnt & 255), cnt & 255);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float xp = st.mx > 0.0f ? ldexpf(f[i], 21 - st.e) : 0.0f;   // power-of-two scaling: exact
+        const float xp = st.mx > 0.0f ? ldexpf(f[i], BGL_X_FRAC - st.e) : 0.0f;   // power-of-two scaling: exact
         const float Xf = rintf(xp);
         st.X[i] = (int)Xf;
         st.r[i] = xp - Xf;
@@ -508,8 +508,8 @@ __device__ __forceinline__ int x_resid_exp(const XStat &st, float &mr) {
     return e1;
 }
 
-// Pass p's level-0 records: digits, sums, flags, the scale 2^(e-21) and the level-1 ratio
-// 2^(e1-21) (0 unless the group has an outlier).  The level-1 digits themselves are made only where
+// Pass p's level-0 records: digits, sums, flags, the scale 2^(e-22) and the level-1 ratio
+// 2^(e1-22) (0 unless the group needs level 1).  The level-1 digits themselves are made only where
 // a GEMV needs them (x_pass_l1, cold path).
 __device__ __forceinline__ void x_pass_digits(const float4 &v, int p, int lane, int G, int *xl) {
     const int g = 4 * p + (lane >> 4), q = lane & 15;
@@ -520,12 +520,12 @@ __device__ __forceinline__ void x_pass_digits(const float4 &v, int p, int lane, 
     if (__builtin_amdgcn_ballot_w64(st.spiky)) {    // uniform branch: some row of the wave has an outlier
         float mr;
         const int e1 = x_resid_exp(st, mr);
-        if (st.spiky && mr > 0.0f) { ratio = ldexpf(1.0f, e1 - 21); flags |= BGL_XF_L1; }
+        if (st.spiky && mr > 0.0f) { ratio = ldexpf(1.0f, e1 - BGL_X_FRAC); flags |= BGL_XF_L1; }
     }
     if (g < G) {
         int *rec = xl + g * XREC_DW;
         x_store3(rec, q, P0, flags);
-        if (q == 0) *reinterpret_cast<float2 *>(rec + XREC_SCALE) = make_float2(st.mx > 0.0f ? ldexpf(1.0f, st.e - 21) : 0.0f, ratio);
+        if (q == 0) *reinterpret_cast<float2 *>(rec + XREC_SCALE) = make_float2(st.mx > 0.0f ? ldexpf(1.0f, st.e - BGL_X_FRAC) : 0.0f, ratio);
     }
 }
 
@@ -538,7 +538,7 @@ __device__ __forceinline__ void x_pass_l1(const float4 &v, int p, int lane, int 
     const int e1 = x_resid_exp(st, mr);
     int X1[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) X1[i] = mr > 0.0f ? (int)rintf(ldexpf(st.r[i], 21 - e1)) : 0;
+    for (int i = 0; i < 4; i++) X1[i] = mr > 0.0f ? (int)rintf(ldexpf(st.r[i], BGL_X_FRAC - e1)) : 0;
     const XPack P1 = x_pack3(X1);
     if (g >= g0 && g < g1) x_store3(dst + (g - g0) * XREC_DW, q, P1, 0);
 }

@@ -40,12 +40,20 @@ struct bgl_ctx {
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
     int prep_act = -1, prep_gq = 0, prep_M = 0, prep_K = 0;   // what act_* currently hold
     const float *prep_x = nullptr;        // the raw fp32 columns they were made from (non-finite slow path)
+    bool prep_reuse = false;              // act_* come from bgl_prep_act_dev (or a host drop-in): bgl_matmul_prepped_dev may use them
+    DevBuf prep_xc;                       // bgl_prep_act_dev's own copy of the fp32 columns (prep_x points here)
     DevBuf part;                          // K-split partial sums [ks][M][N]
     DevBuf hx, hy, hb;                    // staging for the host-pointer entry points
     DevBuf moe_a, moe_b, moe_c, moe_d, moe_e, moe_f, moe_g, moe_meta;   // MoE digits x2, fp32 h/down, bucket scratch
     DevBuf moe_route;                     // routing of bgl_moe_layer_dev: idx [T][K] + w [T][K]
     DevBuf moe_scores;                    // router scores [T][E]
     DevBuf mlp;                           // bgl_mlp_dev: gate and up outputs [M][I] each, then h [M][I]
+    std::unordered_map<uint64_t, DevBuf> mlp_sync;   // single-launch MLP, per shape (in << 32 | down workgroups): counters, generations, flag
+    int mlp_trg = 0;                      // BGL_MLP_TRG: rows of gate / up per single-launch MLP workgroup (tuning; 0 by shape)
+    bool no_fused_mlp = false;            // BGL_NO_FUSED_MLP=1: the MLP block as three launches at every M
+    int mlp_spin = 1 << 20;               // BGL_MLP_SPIN: polls of the single-launch MLP's bounded wait
+    int mlp_waves = 0;                    // BGL_MLP_WAVES: wavefronts per single-launch MLP workgroup (tuning; 0 by shape)
+    int mlp_test_timeout = 0;             // BGL_MLP_TEST_TIMEOUT=n: the next n such launches wait for a count never reached (tests of the give-up path)
     std::vector<void *> retired;          // outgrown scratch, kept for captured graphs until destroy / epoch reset
     uint8_t *fixed_base = nullptr;        // set during bgl_matmul_group_noalloc_dev: scratch comes from here
     size_t fixed_cap = 0, fixed_used = 0;
@@ -83,3 +91,7 @@ bool bgl_mfma_ok(int fmt, int bits);
 // into glu_h [M][N] (k_swiglu's arithmetic), so the caller needs no SwiGLU launch.
 int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
                   float *const *y, const int *ystride, float *glu_h = nullptr);
+// The dense MLP block at one W4A8 column in one launch (bgl_mlp_q.hip): the formats it takes, and the call.
+bool mlp_q_ok(bgl_ctx *c, const BglDevTensor &gate, const BglDevTensor &up, const BglDevTensor &down);
+int run_mlp_q(bgl_ctx *c, const BglDevTensor &gate, const BglDevTensor &up, const BglDevTensor &down, const float *x,
+              float *h, float *y);

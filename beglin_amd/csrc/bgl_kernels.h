@@ -154,11 +154,11 @@ struct GemvTask {
 // Activation operands (shared by every task of a launch; all tasks have the same K).
 struct GemvAct {
     const int *xw;            // W4A8: xq dwords [M][K/4];       F32: digits [M][K/64][48]
-    const float *xs;          // W4A8: ascale [M][K/gq];          F32: 2^(e-21) [M][K/64]
+    const float *xs;          // W4A8: ascale [M][K/gq];          F32: 2^(e-22) [M][K/64]
     const int *xsum;          // W4A8: sum xq per 64 [M][K/64];   F32: digit sums [M][K/32][4], the
                               //   4th int of a group's first half = its flags (BGL_XF_*)
     const int *xw1;           // F32 level 1 (groups flagged BGL_XF_L1): residual digits [M][K/64][48]
-    const float *xs1;         // F32 level 1: 2^(e1-21) relative to the level-0 scale, 0 without level 1 [M][K/64]
+    const float *xs1;         // F32 level 1: 2^(e1-22) relative to the level-0 scale, 0 without level 1 [M][K/64]
     const int *xsum1;         // F32 level 1: digit sums [M][K/32][4]
     const int *colmap;        // optional: column m of this launch reads activation row colmap[m]
     const float *xf;          // F32: the raw rows [M][K] (dense fp16 / fp32 weights and the non-finite

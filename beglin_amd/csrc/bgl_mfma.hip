@@ -826,8 +826,13 @@ int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev,
         if (wb >= 2147483648.0) return bgl_fail(BGL_E_UNSUPPORTED, "MFMA path: tensor %d holds >= 2 GiB (32-bit buffer offsets)", i);
     }
     const int KS = K / 32;
+    // The chunks run in stream order, so each reuses the same K-split partials.  In a no-alloc call
+    // the fixed array is handed out by a bump pointer: rewind it to this mark before every chunk,
+    // so the first (largest) chunk's reservation bounds the whole call.
+    const size_t fixed_mark = c->fixed_used;
     for (int m0 = 0; m0 < M; m0 += 16 * MF_MAXCT) {
         const int Mc = M - m0 < 16 * MF_MAXCT ? M - m0 : 16 * MF_MAXCT;
+        if (c->fixed_base) c->fixed_used = fixed_mark;
         const int CT = (Mc + 15) / 16;
         const int kpm = CT == 1 ? mf_kps_max(1) : CT == 2 ? mf_kps_max(2) : CT == 3 ? mf_kps_max(3) : mf_kps_max(4);
         MfmaLaunch L;

@@ -52,6 +52,15 @@ extern "C" int bgl_mlp_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor 
     const size_t n = (size_t)M * I;
     // the scratch belongs to the context's device: select it before any allocation
     HIPCHK(hipSetDevice(c->device));
+    // one W4A8 column: the whole block in one launch (bgl_mlp_q.hip)
+    if (act == BGL_ACT_W4A8 && M == 1 && !c->no_fused_mlp && !c->no_fused && mlp_q_ok(c, gate->T, up->T, down->T)) {
+        float *hq = h_dev;
+        if (!hq) {
+            if (dbuf_reserve(c, c->mlp, n * 4, false)) return bgl_last_code();
+            hq = (float *)c->mlp.p;
+        }
+        return run_mlp_q(c, gate->T, up->T, down->T, x_dev, hq, y_dev);
+    }
     // g and u side by side, then h unless the caller keeps it
     if (dbuf_reserve(c, c->mlp, n * 4 * (h_dev ? 2 : 3), false)) return bgl_last_code();
     float *g = (float *)c->mlp.p, *u = g + n, *h = h_dev ? h_dev : u + n;

@@ -13,6 +13,10 @@
 // q = sat8(trunc(x*inv +/- 0.5)).  One wave per (column, group); gsize is 64 or 256 (lane handles
 // gsize/64 elements, element l + 64*j).  Also writes the exact sum of xq per 64-subgroup (used for
 // the nibble bias correction) and xq itself as packed int8.
+// |x| is maximised on its bit pattern, where every NaN lies above +Inf and +Inf above every finite
+// value: that is the reference's FMAX (vmaxq_f32 / vmaxvq_f32), which carries a NaN into mx.  A group
+// whose maximum is NaN or +-Inf gets sc = NaN or +Inf and every code 0 (FCVTZS maps the NaN products
+// to 0; with inv = 0 the finite ones are +-0), so the fold's 0 * sc makes its outputs NaN.
 __global__ __launch_bounds__(256) void k_act_w4a8(const float *__restrict__ x, int M, int K, int gsize,
                                                   int8_t *__restrict__ xq, float *__restrict__ ascale,
                                                   int *__restrict__ xqsum64) {
@@ -22,13 +26,17 @@ __global__ __launch_bounds__(256) void k_act_w4a8(const float *__restrict__ x, i
     int m = wid / ng, g = wid % ng, per = gsize >> 6;
     const float *xp = x + (size_t)m * K + (size_t)g * gsize;
     float v[4];
-    float mx = 1e-8f;
-    for (int j = 0; j < per; j++) { v[j] = xp[lane + 64 * j]; mx = fmaxf(mx, fabsf(v[j])); }
-    mx = wave_max_f32(mx);
-    float sc = __fdiv_rn(mx, 127.0f), inv = __fdiv_rn(1.0f, sc);
+    uint32_t mb = __float_as_uint(1e-8f);                  // mx starts at 1e-8 (q4gemv.h:182)
+    for (int j = 0; j < per; j++) {
+        v[j] = xp[lane + 64 * j];
+        mb = max(mb, __float_as_uint(v[j]) & 0x7fffffffu);
+    }
+    mb = wave_max_u32(mb);
+    const bool nf = mb >= 0x7f800000u;                    // NaN or +-Inf in the group: every code 0
+    float sc = __fdiv_rn(__uint_as_float(mb), 127.0f), inv = __fdiv_rn(1.0f, sc);
     if (lane == 0) ascale[(size_t)m * ng + g] = sc;
     for (int j = 0; j < per; j++) {
-        float p = __fmul_rn(v[j], inv);
+        float p = nf ? 0.0f : __fmul_rn(v[j], inv);
         float t = __fadd_rn(p, p >= 0.0f ? 0.5f : -0.5f);
         int q;
         if (t >= 2147483647.0f) q = 2147483647;
@@ -43,13 +51,14 @@ __global__ __launch_bounds__(256) void k_act_w4a8(const float *__restrict__ x, i
 
 // ------------------------------------------------------------------ fp32 activation digits
 // One wave per (column, 64-group), lane = element.  Level 0: e = exponent of the group's largest
-// finite |x| (frexp), X = rint(x * 2^(21-e)), |X| <= 2^21, as X = d0 + 256*d1 + 65536*d2 with
-// balanced int8 digits.  Level 1 (groups with an outlier: fewer than half the nonzero elements
-// within 2^BGL_X_SPIKE_BITS of the max): the exact residual r = x * 2^(21-e) - X in the same form
-// relative to its own maximum, X1 = rint(r * 2^(21-e1)).  Non-finite elements count as 0 and flag
-// the group.  Each buffer holds level 0 for all M columns, then level 1:
+// finite |x| (frexp), X = rint(x * 2^(22-e)), |X| <= 2^22, as X = d0 + 256*d1 + 65536*d2 with
+// balanced int8 digits.  Level 1 (bgl_x_level1: groups with BGL_X_SMALL_MAX or more nonzero
+// elements below 2^(e-BGL_X_SPIKE_BITS), or more of them than elements above): the exact residual
+// r = x * 2^(22-e) - X in the same form relative to its own maximum, X1 = rint(r * 2^(22-e1)).
+// Non-finite elements count as 0 and flag the group.  Each buffer holds level 0 for all M columns,
+// then level 1:
 //   xd   [m][g][digit][64] bytes, then the level-1 digits;
-//   xs   [m][g] = 2^(e-21), then [m][g] = 2^(e1-21) (0 without level 1);
+//   xs   [m][g] = 2^(e-22), then [m][g] = 2^(e1-22) (0 without level 1);
 //   dsum [m][K/32][4] per-half digit sums (the 4th int: the group's BGL_XF_* flags), then level 1's.
 __device__ __forceinline__ int x_balanced3(int X, int &d0, int &d1) {
     d0 = (int)(int8_t)(X & 255);
@@ -75,7 +84,7 @@ __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, in
     const float thr = mx > 0.0f ? ldexpf(1.0f, e - BGL_X_SPIKE_BITS) : 0.0f;
     const int cnt = wave_sum_i32((ab != 0u && __uint_as_float(ab) >= thr ? 1 : 0) + (ab != 0u ? 256 : 0) + (nf ? 65536 : 0));
     const int nlarge = cnt & 255, nnz = (cnt >> 8) & 255, nnf = cnt >> 16;
-    const float xp = mx > 0.0f ? ldexpf(v, 21 - e) : 0.0f;  // power-of-two scaling: exact
+    const float xp = mx > 0.0f ? ldexpf(v, BGL_X_FRAC - e) : 0.0f;   // power-of-two scaling: exact
     const float Xf = rintf(xp);
     int d0, d1;
     int d2 = x_balanced3((int)Xf, d0, d1);
@@ -83,14 +92,14 @@ __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, in
     dst[lane] = (int8_t)d0; dst[64 + lane] = (int8_t)d1; dst[128 + lane] = (int8_t)d2;
     int flags = nnf ? BGL_XF_NF : 0;
     float ratio = 0.0f;
-    if (2 * nlarge < nnz) {                                // wave-uniform: one group per wave
+    if (bgl_x_level1(nnz - nlarge, nlarge)) {              // wave-uniform: one group per wave
         const float r = xp - Xf;                           // exact: xp and rint(xp) differ by <= 1/2
         const float mr = wave_max_f32(fabsf(r));
         if (mr > 0.0f) {
             int e1 = 0;
             frexpf(mr, &e1);
             int c0, c1;
-            const int c2 = x_balanced3((int)rintf(ldexpf(r, 21 - e1)), c0, c1);
+            const int c2 = x_balanced3((int)rintf(ldexpf(r, BGL_X_FRAC - e1)), c0, c1);
             int8_t *d1p = xd + ((size_t)M * ng + (size_t)m * ng + g) * 192;
             d1p[lane] = (int8_t)c0; d1p[64 + lane] = (int8_t)c1; d1p[128 + lane] = (int8_t)c2;
             const int2 t0 = half_sums_i32(c0), t1 = half_sums_i32(c1), t2 = half_sums_i32(c2);
@@ -99,12 +108,12 @@ __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, in
                 int *ds = dsum + ((size_t)M * (K >> 5) + (size_t)m * (K >> 5) + (size_t)g * 2 + h) * 4;
                 ds[0] = h ? t0.y : t0.x; ds[1] = h ? t1.y : t1.x; ds[2] = h ? t2.y : t2.x; ds[3] = 0;
             }
-            ratio = ldexpf(1.0f, e1 - 21);
+            ratio = ldexpf(1.0f, e1 - BGL_X_FRAC);
             flags |= BGL_XF_L1;
         }
     }
     if (lane == 0) {
-        xs[(size_t)m * ng + g] = (mx > 0.0f) ? ldexpf(1.0f, e - 21) : 0.0f;
+        xs[(size_t)m * ng + g] = (mx > 0.0f) ? ldexpf(1.0f, e - BGL_X_FRAC) : 0.0f;
         xs[(size_t)M * ng + (size_t)m * ng + g] = ratio;
     }
     int2 s0 = half_sums_i32(d0), s1 = half_sums_i32(d1), s2 = half_sums_i32(d2);

@@ -43,9 +43,10 @@ MALL_BYTES = 256 << 20
 
 
 def qwen_layer_shapes():
-    """(name, [(out, in), ...]) per call, in issue order."""
+    """(name, [(out, in), ...]) per call, in forward_token's issue order (qwen_infer.c:1276-1306,
+    1560-1573): the fused q/k/v projection, o, and the MLP block (gate, up, down)."""
     return [("qkv", [(1536, 1536), (256, 1536), (256, 1536)]), ("o", [(1536, 1536)]),
-            ("gate_up", [(8960, 1536), (8960, 1536)]), ("down", [(1536, 8960)])]
+            ("mlp", [(8960, 1536), (8960, 1536), (1536, 8960)])]
 
 
 def alg_bytes(kind, out, inn, bits, M):
@@ -76,7 +77,8 @@ ROTATE_BYTES = 512 << 20       # CPU legs cycle through weight copies of at leas
 
 # ------------------------------------------------------------------------------------- GPU side
 class Workload:
-    """A list of calls; each call = (tensors, x, ys, act, bytes)."""
+    """A list of calls; each call = (tensors, x, ys, act, bytes, tag).  Tag "mlp": the tensors are
+    (gate, up, down) of one MLP block (bgl_mlp_dev), ys its one output."""
 
     def __init__(self, ctx, torch):
         self.ctx, self.torch = ctx, torch
@@ -84,14 +86,17 @@ class Workload:
         self.tensors = []
 
     def add(self, group, x, act, nbytes, tag):
-        ys = [self.torch.empty((x.shape[0], t.info()["out"]), device="cuda") for t in group]
+        outs = [group[2]] if tag == "mlp" else group
+        ys = [self.torch.empty((x.shape[0], t.info()["out"]), device="cuda") for t in outs]
         self.calls.append((group, x, ys, act, nbytes, tag))
         self.tensors += group
 
     def run(self, tags=None):
         for group, x, ys, act, _, tag in self.calls:
             if tags is None or tag in tags:
-                if len(group) == 1:
+                if tag == "mlp":
+                    self.ctx.mlp(group[0], group[1], group[2], x, ys[0], act=act)
+                elif len(group) == 1:
                     self.ctx.matmul(group[0], x, ys[0], act=act)
                 else:
                     self.ctx.matmul_group(group, x, ys, act=act)
@@ -124,9 +129,13 @@ def build_cfg2(ctx, torch, M, layers, seed):
                 w = gen_weight(torch, gen, out, inn)
                 group.append(ctx.quantize(beglin_amd.K_Q4G256SF, w))
                 del w
-                nb += alg_bytes(3, out, inn, 4, M) - 4 * M * inn
-            nb += 4 * M * shapes[0][1]
-            wl.add(group, xs[shapes[0][1]], beglin_amd.ACT_W4A8, nb, tag)
+                nb += alg_bytes(3, out, inn, 4, M) - 4 * M * inn - 4 * M * out     # weight bytes
+            H = shapes[0][1]
+            if tag == "mlp":          # x and y, and h written once and read once (g and u stay on chip)
+                nb += 4 * M * H + 8 * M * shapes[0][0] + 4 * M * H
+            else:
+                nb += 4 * M * H + sum(4 * M * out for out, _ in shapes)
+            wl.add(group, xs[H], beglin_amd.ACT_W4A8, nb, tag)
     return wl
 
 
@@ -327,7 +336,7 @@ def plain_read(ctx, torch, stream, wl, steps):
 
 # The kernel sources behind each workload's dominant kernel (its file and the headers it includes).
 KERNEL_SOURCES = {
-    "cfg2": ("bgl_gemv.hip", "bgl_gemv_impl.h", "bgl_device.h", "bgl_kernels.h"),
+    "cfg2": ("bgl_mlp_q.hip", "bgl_gemv.hip", "bgl_gemv_q.h", "bgl_gemv_impl.h", "bgl_device.h", "bgl_kernels.h"),
     "cfg1": ("bgl_gemv_x.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_device.h", "bgl_kernels.h"),
     "cfg3": ("bgl_gemv_x.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_device.h", "bgl_kernels.h"),
     "cfg4": ("bgl_moe_x.hip", "bgl_moe_x.h", "bgl_moe.hip", "bgl_gemv_x.h", "bgl_prep.hip", "bgl_mfma.hip", "bgl_mlp.hip",
@@ -712,7 +721,8 @@ def main():
         with torch.cuda.stream(stream):
             wl = build_cfg2(ctx, torch, M, args.layers, args.seed)
         torch.cuda.synchronize()
-        workload = f"cfg2: Qwen2.5-1.5B decode layer x{args.layers}, q4g256sf W4A8 GEMV, 7 projections (fused qkv, o, fused gate+up, down), M={M}"
+        workload = (f"cfg2: Qwen2.5-1.5B decode layer x{args.layers}, q4g256sf W4A8 GEMV, 7 projections as forward_token "
+                    f"issues them (fused qkv, o, MLP block gate+up -> SwiGLU -> down), M={M}")
         dtype = DT_W4A8
         cfg = {"workload": workload, "layers": args.layers, "M": M, "format": "q4g256sf", "activations": "W4A8 (int8, group 256)",
                "calls_per_step": wl.ncalls(), "weight_bytes_per_step": int(wl.nbytes()), "seed": args.seed}
@@ -787,45 +797,66 @@ def main():
         n = wl.ncalls([tag])
         per_call[tag] = {"us": round(ms * 1e3 / n, 2), "GB/s": round(wl.nbytes([tag]) / (ms * 1e-3) / 1e9, 1)}
 
-    # The dominant kernel is the GEMV; where it is the only kernel of the step (W4A8 at M=1, the
-    # one-column fp32 GEMV over a short K) its average launch duration is the graph-timed step (HIP
-    # events on the context's stream around the timed replays) over the launches per step.  Call
-    # types whose path adds an activation-prep kernel have those timed the same way from a graph of
-    # the prep alone, subtracted from the step.
-    launches = wl.ncalls()
-    prep_ms = 0.0
-    # which call types launch an activation-prep kernel? (one profiled eager run of each counts
-    # them: the fused W4A8 kernel and the one-column fp32 GEMV over a short K make their operands
-    # themselves; several W4A8 columns over a long K and long fp32 K are quantized up front)
-    prep_tags = []
+    # Launches per call type, and which call types launch an activation-prep kernel: one profiled
+    # eager run of each.  (The fused W4A8 kernel and the one-column fp32 GEMV over a short K make
+    # their operands themselves; several W4A8 columns over a long K and long fp32 K are quantized
+    # up front.  The MLP block at one W4A8 column is one launch, otherwise three.)
+    prep_tags, launches_of = [], {}
     for tag in tags:
         ctx.prof_enable(True)
         ctx.prof_read()
         with torch.cuda.stream(stream):
             wl.run([tag])
         ctx.sync()
-        if ctx.prof_read()["prep"][1] > 0:
+        pr = ctx.prof_read()
+        if pr["prep"][1] > 0:
             prep_tags.append(tag)
+        launches_of[tag] = sum(v[1] for v in pr.values())
         ctx.prof_enable(False)
-    if prep_tags:
-        prep_ms = time_prep(ctx, torch, stream, wl, max(5, args.steps // 5), set(prep_tags))
-    k_ms = max(step_ms - prep_ms, 1e-6)
-    achieved = nbytes / (k_ms * 1e-3) / 1e9
-    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": ("k_gemv_q<fmt,TR,QP,MB> (bgl_gemv.hip)" if args.workload == "cfg2" else
-                       "k_gemv_x<fmt,n,TR,FUSE> (bgl_gemv_x.hip)" if M == 1 else "k_gemv<fmt,act,n,MB> (bgl_gemv.hip)"),
-            "launches_per_step": launches, "kernel_us_per_launch": round(k_ms * 1e3 / launches, 3),
-            "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3), "prep_call_types": prep_tags,
-            "bytes_per_launch": round(nbytes / launches)}
+    launches = sum(launches_of.values())
+    if args.workload == "cfg2" and launches_of.get("mlp") == wl.ncalls(["mlp"]):
+        # The dominant kernel is the single-launch MLP block (22 of the layer's 25 MB): its average
+        # launch duration is the graph of the step's MLP calls alone (HIP events on the context's
+        # stream around the timed replays) over their count.
+        n_m = wl.ncalls(["mlp"])
+        b_m = wl.nbytes(["mlp"]) / n_m
+        us_m = per_call["mlp"]["us"]
+        achieved = b_m / (us_m * 1e-6) / 1e9
+        others = {t: {"launches_per_step": launches_of[t], "us_per_launch": per_call[t]["us"]} for t in tags if t != "mlp"}
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "k_mlp_q<fmt,TRG,TRD> (bgl_mlp_q.hip): gate+up, SwiGLU and down of one MLP block in one launch",
+                "launches_per_step": n_m, "kernel_us_per_launch": round(us_m, 3), "bytes_per_launch": round(b_m),
+                "how": "graph of the step's MLP launches alone, HIP events on the context's stream",
+                "step_launches": launches, "other_kernels": {"k_gemv_q<fmt,TR,QP,MB> (bgl_gemv.hip)": others}}
+        dom_bytes = b_m
+    else:
+        # The dominant kernel is the GEMV; where it is the only kernel of the step (one-column
+        # fp32 GEMV over a short K) its average launch duration is the graph-timed step over the
+        # launches per step.  Call types whose path adds an activation-prep kernel have those timed
+        # the same way from a graph of the prep alone, subtracted from the step.
+        prep_ms = 0.0
+        if prep_tags:
+            prep_ms = time_prep(ctx, torch, stream, wl, max(5, args.steps // 5), set(prep_tags))
+        k_ms = max(step_ms - prep_ms, 1e-6)
+        achieved = nbytes / (k_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": ("k_gemv_q<fmt,TR,QP,MB> (bgl_gemv.hip) + k_swiglu (bgl_mlp.hip)" if args.workload == "cfg2" else
+                           "k_gemv_x<fmt,n,TR,FUSE> (bgl_gemv_x.hip)" if M == 1 else "k_gemv<fmt,act,n,MB> (bgl_gemv.hip)"),
+                "launches_per_step": launches, "kernel_us_per_launch": round(k_ms * 1e3 / launches, 3),
+                "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3), "prep_call_types": prep_tags,
+                "bytes_per_launch": round(nbytes / launches)}
+        dom_bytes = nbytes / launches
 
     # the plain-read floor for the same bytes and launch count, measured in this run
     pr_ms = plain_read(ctx, torch, stream, wl, max(5, args.steps // 5))
-    roof["plain_read"] = {"us_per_step": round(pr_ms * 1e3, 2), "us_per_launch": round(pr_ms * 1e3 / launches, 3),
+    roof["plain_read"] = {"us_per_step": round(pr_ms * 1e3, 2), "us_per_launch": round(pr_ms * 1e3 / wl.ncalls(), 3),
                           "GB/s": round(nbytes / (pr_ms * 1e-3) / 1e9, 1), "step_over_plain": round(step_ms / pr_ms, 3),
-                          "how": "bgl_read_probe_dev over each call's tensors, 1024 x 256 threads, graph-timed"}
+                          "how": "bgl_read_probe_dev over each call's tensors (one launch per call), 1024 x 256 threads, "
+                                 "graph-timed"}
 
-    attach_traffic(roof, args, nbytes / launches)
+    attach_traffic(roof, args, dom_bytes)
 
     cpu = None
     if not args.no_cpu:

@@ -42,7 +42,8 @@ enum { BGL_K_Q4G64 = 1, BGL_K_Q8G64 = 2, BGL_K_Q4G256SF = 3, BGL_K_QNG64 = 4, BG
        BGL_K_Q4G64A = 6, BGL_K_F16 = 7, BGL_K_F32 = 8, BGL_K_MXFP4 = 9, BGL_K_Q4G256P = 10 };
 enum { BGL_ACT_F32 = 0, BGL_ACT_W4A8 = 1 };
 enum { BGL_OK = 0, BGL_E_ARG = -1, BGL_E_UNSUPPORTED = -2, BGL_E_HIP = -3, BGL_E_NODEV = -4, BGL_E_NOMEM = -5,
-       BGL_E_CAPTURE = -6 /* per-call scratch would have to grow inside a stream capture */ };
+       BGL_E_CAPTURE = -6 /* per-call scratch would have to grow inside a stream capture */,
+       BGL_E_TIMEOUT = -7 /* a bounded wait inside a kernel gave up (bgl_ctx_check) */ };
 
 typedef struct bgl_ctx bgl_ctx;
 typedef struct bgl_tensor bgl_tensor;
@@ -69,6 +70,11 @@ const char *bgl_last_error(void);
 int  bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out);   /* q4pool_init+start (q4gemv.h:580-620); stream NULL = own stream */
 void bgl_ctx_destroy(bgl_ctx *ctx);                         /* q4pool_destroy (q4gemv.h:623-637) */
 int  bgl_synchronize(bgl_ctx *ctx);                         /* mlx_gpu_synchronize (mlx_moe.h:29) */
+/* Synchronize the context's stream, then report (and clear) a bounded in-kernel wait that gave up
+ * since the last check: BGL_E_TIMEOUT means the outputs of that call are invalid.  No counterpart in
+ * the reference (its CPU kernels never wait on each other); the single-launch MLP block of
+ * bgl_mlp_dev is the call that waits. */
+int  bgl_ctx_check(bgl_ctx *ctx);
 void *bgl_ctx_stream(bgl_ctx *ctx);                          /* the hipStream_t work is queued on */
 
 /* ---------------- profiling (the QWEN_PROF phase buckets, qwen_infer.c:1231, :1851-1895) ----------------
@@ -122,7 +128,11 @@ int  bgl_matmul_group_dev(bgl_ctx *ctx, int n, const bgl_tensor *const *w, int a
  * then * u, in fp32; the exponential rounded once from double), y = W_down h.  gate / up [I][H],
  * down [H][I], x_dev [M][H], y_dev [M][H]; act as bgl_matmul_dev (W4A8 quantizes x and h).  h_dev:
  * optional [M][I] that receives h (NULL: it stays in the context's scratch).  No host round trip;
- * capturable under the same scratch rule as the other *_dev calls. */
+ * capturable under the same scratch rule as the other *_dev calls.  One W4A8 column in q4g64,
+ * q8g64 or g256sf (plain g256 included) runs the whole block as ONE launch whose down-projection
+ * workgroups wait, bounded, for the gate+up workgroups (bgl_ctx_check reports a wait that gave up);
+ * the values are the three-launch path's, bit for bit.  Calls on one context run in its stream's
+ * order; two streams running this context's MLP calls at once would share its counters. */
 int  bgl_mlp_dev(bgl_ctx *ctx, const bgl_tensor *gate, const bgl_tensor *up, const bgl_tensor *down, int act,
                  const float *x_dev, float *y_dev, int M, float *h_dev);
 /* bgl_matmul_group_dev that allocates nothing: no counterpart in the reference.  For callers that

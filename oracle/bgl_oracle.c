@@ -416,25 +416,40 @@ void or_gemm_f32(int kind, int bits, const void *packed, const void *scales,
 
 /* ============================ W4A8 / W8A8 ============================ */
 
+/* AArch64 FMAX (vmaxq_f32 / vmaxvq_f32): a NaN operand gives NaN; otherwise the larger value. */
+static float or_fmax_nan(float a, float b) {
+    if (isnan(a) || isnan(b)) return NAN;
+    return a > b ? a : b;
+}
+
+/* AArch64 FCVTZS to int32 (vcvtq_s32_f32): toward zero, NaN -> 0, out of range saturates. */
+static int32_t or_fcvtzs(float t) {
+    if (isnan(t)) return 0;
+    if (t >= 2147483648.0f) return INT32_MAX;
+    if (t <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)t;
+}
+
 /* q4gemv.h:177-213 (q4_quant_act_i8) and q4gemv_g256.h:72-99 (q4_quant_act_i8_g256):
- * mx = max(1e-8, max|x|); sc = mx/127; inv = 1/sc; q = sat8(trunc(x*inv +/- 0.5))
- * (round half away from zero, saturating narrow through int16). */
+ * mx = FMAX(1e-8, |x|...); sc = mx/127; inv = 1/sc; q = sat8(FCVTZS(x*inv +/- 0.5))
+ * (round half away from zero, saturating narrow through int16).
+ * Non-finite groups follow the NEON instructions: FMAX carries a NaN into mx, so a group holding a
+ * NaN gets sc = NaN, inv = NaN, every x*inv NaN and every code FCVTZS(NaN) = 0; a group holding
+ * +-Inf (and no NaN) gets mx = +Inf, sc = +Inf, inv = 0, x*inv = +-0 (NaN at the Inf) and again
+ * every code 0.  The fold then multiplies 0 by a NaN or +Inf scale: every output row is NaN. */
 void or_quant_act_i8(const float *x, int in, int gsize, int8_t *xq, float *ascale) {
     int ng = in / gsize;
     for (int gi = 0; gi < ng; gi++) {
         const float *xp = x + (size_t)gi * gsize;
         float mx = 1e-8f;
-        for (int b = 0; b < gsize; b++) { float a = fabsf(xp[b]); if (a > mx) mx = a; }
+        for (int b = 0; b < gsize; b++) mx = or_fmax_nan(mx, fabsf(xp[b]));
         float sc = mx / 127.0f, inv = 1.0f / sc;
         ascale[gi] = sc;
         for (int b = 0; b < gsize; b++) {
             float p = xp[b] * inv;
-            float t = p + (p >= 0.0f ? 0.5f : -0.5f);
-            long q;
-            if (t >= 2147483647.0f) q = 2147483647L;
-            else if (t <= -2147483648.0f) q = -2147483647L - 1;
-            else q = (long)t;                                  /* vcvtq_s32_f32: toward zero */
-            if (q > 127) q = 127;
+            float t = p + (p >= 0.0f ? 0.5f : -0.5f);       /* vcgeq(NaN, 0) is false: NaN - 0.5 */
+            int32_t q = or_fcvtzs(t);
+            if (q > 127) q = 127;                             /* vqmovn_s32 then vqmovn_s16 */
             if (q < -128) q = -128;
             xq[(size_t)gi * gsize + b] = (int8_t)q;
         }

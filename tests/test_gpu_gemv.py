@@ -107,6 +107,76 @@ def test_w4a8_activation_codes_bit_exact(ctx, torch_dev, oracle, gsize):
     assert np.array_equal(ga.cpu().numpy().view(np.uint32), a.view(np.uint32))
 
 
+def nonfinite_columns(M, K, seed):
+    """M columns: column m % 4 == 0 carries a NaN, 1 a +Inf, 2 a -Inf (each in one group), 3 is
+    finite; the non-finite values sit at different offsets so both gsize 64 and 256 see them."""
+    x = seeded_normal(seed, (M, K))
+    for m in range(M):
+        j = (97 * m + 13) % K
+        if m % 4 == 0:
+            x[m, j] = np.nan
+        elif m % 4 == 1:
+            x[m, j] = np.inf
+        elif m % 4 == 2:
+            x[m, j] = -np.inf
+    return x
+
+
+def same_scales(got, want):
+    """Scales bit-exact where finite, NaN where the oracle's is NaN (the NaN payload is not part
+    of the reference's contract), +Inf where +Inf."""
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
+
+
+@pytest.mark.parametrize("gsize", [64, 256])
+def test_w4a8_activation_codes_nonfinite(ctx, torch_dev, oracle, gsize):
+    """k_act_w4a8 on NaN / +-Inf groups: every code 0, scale NaN or +Inf (FMAX / FCVTZS semantics
+    of q4gemv.h:182-206 and q4gemv_g256.h:76-96, restated by the oracle)."""
+    torch = torch_dev
+    say("quant_act nonfinite", gsize)
+    x = nonfinite_columns(8, 2048, 11)
+    xq, a = oracle.quant_act_i8(x, gsize)
+    gq = torch.empty((8, 2048), dtype=torch.int8, device="cuda")
+    ga = torch.empty((8, 2048 // gsize), dtype=torch.float32, device="cuda")
+    ctx.quant_act_i8(torch.from_numpy(x).cuda(), gsize, gq, ga)
+    torch.cuda.synchronize()
+    assert np.array_equal(gq.cpu().numpy(), xq)
+    same_scales(ga.cpu().numpy(), a)
+    assert np.isnan(a[0]).any() and np.isposinf(a[1]).any() and np.isposinf(a[2]).any()
+
+
+# (kind, K): q4g64, q8g64 and g256sf; M = 1 quantizes in the GEMV kernel, M = 8 over K = 8960
+# quantizes every column once up front (k_act_w4a8) and copies the codes
+@pytest.mark.parametrize("kind,inn,M", [(1, 1536, 1), (2, 1536, 1), (3, 1536, 1), (1, 8960, 8), (2, 8960, 8),
+                                        (3, 8960, 8), (3, 8960, 4), (3, 1536, 8)])
+def test_w4a8_nonfinite_outputs(ctx, torch_dev, oracle, kind, inn, M):
+    """A column with a NaN or +-Inf activation: every output row NaN, as in the reference (codes 0
+    times a NaN / +Inf scale); the finite columns are bit-exact."""
+    torch = torch_dev
+    out = 200
+    say("w4a8 nonfinite", kind, inn, M)
+    w = weights(700 + kind, out, inn)
+    pk, sc, sub = ref_quant(oracle, kind, w)
+    t = ctx.bind(kind, pk, sc, out, inn, sub=sub)
+    cols = [nonfinite_columns(4, inn, 12 + kind)[i] for i in range(4)]
+    for start in range(0, 4, M) if M == 1 else [0]:
+        x = np.stack([cols[(start + m) % 4] for m in range(M)]).astype(np.float32)
+        ref = oracle.matmul_sdot(kind, pk, sc, x, sub=sub)
+        y = torch.full((M, out), 7.0, dtype=torch.float32, device="cuda")
+        ctx.matmul(t, torch.from_numpy(x).cuda(), y, act=1)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), (start, np.isnan(got).sum(), np.isnan(ref).sum())
+        assert not np.isinf(ref).any() and not np.isinf(got).any()
+        fin = np.isfinite(ref)
+        assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+        for m in range(M):
+            assert np.isnan(ref[m]).all() == ((start + m) % 4 != 3)
+    t.free()
+
+
 GEMV_CASES = [
     (1, 0, 0, 1536), (1, 0, 1, 1536), (2, 0, 0, 1024), (2, 0, 1, 1024), (3, 0, 1, 1536), (5, 0, 0, 1536),
     (4, 2, 0, 1024), (4, 3, 0, 1024), (4, 4, 0, 1024), (4, 5, 0, 1408), (4, 7, 0, 1024), (4, 8, 0, 1024),
@@ -328,27 +398,60 @@ def test_graph_replays_match_eager(ctx, torch_dev, oracle):
     c2.close()
 
 
-def test_prepped_activation_reuse(ctx, torch_dev, oracle):
-    """Prepare once, run two GEMVs (gemm_qXg64_sdot_mt's caller-quantized activations)."""
+@pytest.mark.parametrize("nonfinite", [False, True])
+def test_prepped_activation_reuse(ctx, torch_dev, oracle, nonfinite):
+    """Prepare once, run two GEMVs (gemm_qXg64_sdot_mt's caller-quantized activations), for fp32
+    and W4A8 activations, g256sf and plain g256 included.  The prepared operands belong to the
+    context: x is overwritten (with NaN) after the prep, and the GEMVs still see the prepared x --
+    also the NaN / Inf elements of x the fp32 GEMVs read again.  Operands that a GEMV call prepared
+    for itself are not offered to a prepped call."""
+    import beglin_amd
     torch = torch_dev
-    say("prepped reuse")
+    say("prepped reuse", nonfinite)
     inn = 2048
     x = seeded_normal(1200, (3, inn))
-    xd = torch.from_numpy(x).cuda()
-    for act, kind in ((0, 1), (1, 1), (0, 2)):
+    if nonfinite:
+        x[0, 5] = np.nan
+        x[1, 700] = np.inf
+        x[2, 1900] = -np.inf
+    for act, kind in ((0, 1), (1, 1), (0, 2), (1, 3), (1, beglin_amd.K_Q4G256P)):
         ts, refs = [], []
         for i, out in enumerate((96, 160)):
-            pk, sc, sub = ref_quant(oracle, kind, weights(1201 + i, out, inn), 0)
-            ts.append(ctx.bind(kind, pk, sc, out, inn))
-            refs.append(oracle.gemm_f32(kind, pk, sc, x) if act == 0 else oracle.matmul_sdot(kind, pk, sc, x))
+            if kind == beglin_amd.K_Q4G256P:
+                rng = np.random.default_rng(1205 + i)
+                pk = rng.integers(0, 256, (out, inn // 2), dtype=np.uint8)
+                sc = (rng.random((out, inn // 256), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+                sub = None
+            else:
+                pk, sc, sub = ref_quant(oracle, kind, weights(1201 + i, out, inn), 0)
+            ts.append(ctx.bind(kind, pk, sc, out, inn, sub=sub))
+            refs.append(oracle.gemm_f32(kind, pk, sc, x) if act == 0 else oracle.matmul_sdot(kind, pk, sc, x, sub=sub))
+        xd = torch.from_numpy(x).cuda()
         ctx.prep_only(xd, act, ts[0])
+        xd.fill_(float("nan"))                                 # the caller reuses its buffer
         for t, ref in zip(ts, refs):
             y = torch.empty((3, t.info()["out"]), device="cuda")
             ctx.matmul_prepped(t, y, act=act, M=3)
             torch.cuda.synchronize()
-            assert relerr(y.cpu().numpy(), ref) <= TOL
+            got = y.cpu().numpy()
+            for f in (np.isnan, np.isposinf, np.isneginf):
+                assert np.array_equal(f(got), f(ref)), (act, kind, f.__name__)
+            fin = np.isfinite(ref)
+            if fin.any():                                  # (prepared operands run k_gemv's wave order)
+                assert relerr(got[fin], ref[fin]) <= TOL
         for t in ts:
             t.free()
+    # a context whose operands only a GEMV call prepared has nothing a prepped call may reuse
+    c2 = beglin_amd.Context(0)
+    pk, sc, _ = ref_quant(oracle, 1, weights(1209, 96, inn), 0)
+    t = c2.bind(1, pk, sc, 96, inn)
+    y = torch.empty((3, 96), device="cuda")
+    c2.matmul(t, torch.from_numpy(seeded_normal(1208, (3, inn))).cuda(), y, act=1)
+    with pytest.raises(beglin_amd.BglError):
+        c2.matmul_prepped(t, y, act=1, M=3)
+    c2.sync()
+    t.free()
+    c2.close()
 
 
 @pytest.mark.parametrize("kind", [1, 2, 3])

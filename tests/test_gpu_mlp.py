@@ -8,7 +8,12 @@ I 8960) and Llama-3.1-8B (H 4096, I 14336) shapes.
   of that h bit for bit.
 * fp32 activations (int4 g32 and qNg64 n=5 for Llama, q8g64 for Qwen): h within 1e-5 of the
   oracle's (max-normalised), y within 1e-5 of the oracle's fp32 down projection of the device's
-  own h, and the whole chain within 1e-5 of the oracle's."""
+  own h, and the whole chain within 1e-5 of the oracle's.
+* One W4A8 column runs the block as a single launch (bgl_mlp_q.hip: the down-projection workgroups
+  wait, bounded, for the gate+up workgroups' h): h and y bit-identical to the three-launch path
+  (BGL_NO_FUSED_MLP=1) and to the oracle, call after call and across graph replays; a wait forced
+  to give up is reported by bgl_ctx_check while every kernel exits normally, and the next call is
+  exact again."""
 import sys
 
 import numpy as np
@@ -174,6 +179,153 @@ def test_mlp_graph_replay_and_refusals(ctx, torch_dev, oracle):
         c.mlp(ts[0], ts[2], ts[2], x, y)                 # up is [H][I]: not an MLP
     with pytest.raises(beglin_amd.BglError):
         c.mlp(ts[0], ts[1], ts[0], x, y)                 # down is [I][H]
+    for t in ts:
+        t.free()
+    c.close()
+
+
+def bind_mlp(c, torch, oracle, kind, H, I, seed):
+    """gate, up, down bound from the oracle's packer bytes (plain g256: random codes and scales)."""
+    import beglin_amd
+    ts, refs = [], []
+    for i, (o, inn) in enumerate(((I, H), (I, H), (H, I))):
+        if kind == beglin_amd.K_Q4G256P:
+            rng = np.random.default_rng(seed + i)
+            pk = rng.integers(0, 256, (o, inn // 2), dtype=np.uint8)
+            sc = (rng.random((o, inn // 256), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+            sub = None
+        else:
+            w = seeded_normal(seed + i, (o, inn), 0.02)
+            if kind == 1:
+                pk, sc = oracle.quantize_q4g64(w); sub = None
+            elif kind == 2:
+                pk, sc = oracle.quantize_q8g64(w); sub = None
+            else:
+                pk, sc, sub = oracle.quantize_g256sf(w)
+        ts.append(c.bind(kind, pk, sc, o, inn, sub=sub))
+        refs.append((pk, sc, sub))
+    return ts, refs
+
+
+def mlp_ref(oracle, kind, refs, x):
+    g = oracle.matmul_sdot(kind, refs[0][0], refs[0][1], x, sub=refs[0][2])
+    u = oracle.matmul_sdot(kind, refs[1][0], refs[1][1], x, sub=refs[1][2])
+    h = oracle.swiglu(g, u)
+    return oracle.matmul_sdot(kind, refs[2][0], refs[2][1], h, sub=refs[2][2]), h
+
+
+def same_bits(a, b):
+    return np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a[~np.isnan(a)].view(np.uint32),
+                                                                       b[~np.isnan(b)].view(np.uint32))
+
+
+@pytest.mark.parametrize("kind,H,I", [(3, 1536, 8960), (1, 1536, 8960), (2, 1024, 3072), (10, 512, 2816),
+                                      (3, 4096, 14336)])
+def test_mlp_single_launch_equals_three_launches(torch_dev, oracle, monkeypatch, kind, H, I):
+    """Five calls in a row on one context (the counters return to 0 after every launch), x with a
+    NaN in the fourth call: y and h bit-identical to the oracle and to the three-launch path."""
+    import beglin_amd
+    torch = torch_dev
+    say("mlp single launch", kind, H, I)
+    monkeypatch.delenv("BGL_NO_FUSED_MLP", raising=False)
+    c1 = beglin_amd.Context(0)
+    monkeypatch.setenv("BGL_NO_FUSED_MLP", "1")
+    c3 = beglin_amd.Context(0)
+    monkeypatch.delenv("BGL_NO_FUSED_MLP")
+    ts1, refs = bind_mlp(c1, torch, oracle, kind, H, I, 1500 + kind)
+    ts3, _ = bind_mlp(c3, torch, oracle, kind, H, I, 1500 + kind)
+    for call in range(5):
+        x = seeded_normal(1510 + call, (1, H))
+        if call == 3:
+            x[0, 17] = np.nan
+        ys, hs = [], []
+        for c, ts in ((c1, ts1), (c3, ts3)):
+            y = torch.full((1, H), 7.0, device="cuda")
+            h = torch.full((1, I), 7.0, device="cuda")
+            c.mlp(ts[0], ts[1], ts[2], dev(torch, x), y, act=beglin_amd.ACT_W4A8, h_dev=h)
+            c.check()
+            ys.append(y.cpu().numpy()); hs.append(h.cpu().numpy())
+        yr, hr = mlp_ref(oracle, kind, refs, x)
+        assert same_bits(hs[0], hr) and same_bits(hs[1], hr), (call, relerr(hs[0], hr))
+        assert same_bits(ys[0], yr) and same_bits(ys[1], yr), (call, relerr(ys[0], yr))
+        assert np.isnan(yr).all() == (call == 3)
+    for t in ts1 + ts3:
+        t.free()
+    c1.close(); c3.close()
+
+
+def test_mlp_single_launch_graph_replay(torch_dev, oracle):
+    """Three MLP blocks (three layers' weights, chained: each block's y feeds the next) captured in
+    one graph: every replay, with the program's own eager work in between, equals the eager run."""
+    import beglin_amd
+    torch = torch_dev
+    say("mlp single launch graph")
+    s = torch.cuda.Stream()
+    c = beglin_amd.Context(0, stream=s.cuda_stream)
+    H, I = 1536, 8960
+    layers = [bind_mlp(c, torch, oracle, 3, H, I, 1600 + 10 * l)[0] for l in range(3)]
+    x = dev(torch, seeded_normal(1650, (1, H)))
+    ys = [torch.zeros((1, H), device="cuda") for _ in range(3)]
+
+    def step():
+        src = x
+        for ts, y in zip(layers, ys):
+            c.mlp(ts[0], ts[1], ts[2], src, y, act=beglin_amd.ACT_W4A8)
+            src = y
+
+    with torch.cuda.stream(s):
+        step()
+    c.check()
+    eager = [y.cpu().numpy().copy() for y in ys]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        step()
+    for r in range(4):
+        for y in ys:
+            y.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        c.check()
+        for y, e in zip(ys, eager):
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), e.view(np.uint32)), r
+        with torch.cuda.stream(s):                        # eager work between the replays
+            step()
+        c.check()
+    for ts in layers:
+        for t in ts:
+            t.free()
+    c.close()
+
+
+def test_mlp_bounded_wait_gives_up(torch_dev, oracle, monkeypatch):
+    """The down-projection workgroups' wait is bounded: forced from the host to wait for a count
+    that is never reached (BGL_MLP_TEST_TIMEOUT=1, a short BGL_MLP_SPIN), every workgroup still
+    exits, bgl_ctx_check reports BGL_E_TIMEOUT, and the next call on the same context -- whose
+    counters the timed-out launch returned to 0 -- is bit-exact again."""
+    import beglin_amd
+    torch = torch_dev
+    say("mlp bounded wait")
+    monkeypatch.setenv("BGL_MLP_TEST_TIMEOUT", "1")
+    monkeypatch.setenv("BGL_MLP_SPIN", "64")
+    c = beglin_amd.Context(0)
+    monkeypatch.delenv("BGL_MLP_TEST_TIMEOUT")
+    monkeypatch.delenv("BGL_MLP_SPIN")
+    H, I = 1536, 8960
+    ts, refs = bind_mlp(c, torch, oracle, 3, H, I, 1700)
+    x = seeded_normal(1710, (1, H))
+    y = torch.zeros((1, H), device="cuda")
+    c.mlp(ts[0], ts[1], ts[2], dev(torch, x), y, act=beglin_amd.ACT_W4A8)
+    with pytest.raises(beglin_amd.BglError) as ei:
+        c.check()
+    assert ei.value.code == beglin_amd.E_TIMEOUT
+    c.check()                                             # the flag was cleared
+    yr, _ = mlp_ref(oracle, 3, refs, x)
+    for _ in range(2):
+        y.zero_()
+        c.mlp(ts[0], ts[1], ts[2], dev(torch, x), y, act=beglin_amd.ACT_W4A8)
+        c.check()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), yr.view(np.uint32))
     for t in ts:
         t.free()
     c.close()

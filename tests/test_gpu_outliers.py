@@ -7,7 +7,9 @@ element; a group whose other elements lie far below that element (an outlier, a 
 activation" channel) also carries a level-1 residual, so the small elements keep their precision.
 These tests put such outliers where they hurt most: channels x1e3..x1e5 whose weight columns are
 x0.01 or zero (the outlier then adds little to y while its group's other elements carry the
-result), two outliers of different size in one group, all-zero and subnormal groups.
+result), clusters of 33 or 40 large channels per group with zero weight columns (y then comes
+from each group's small minority), two outliers of different size in one group, all-zero and
+subnormal groups.
 
 Non-finite policy (matches the reference's IEEE arithmetic): a NaN activation makes every output of
 its column NaN; +-Inf gives +-Inf where every product with it has that sign, NaN where a weight at
@@ -81,6 +83,11 @@ def outlier_case(name, K, M, seed):
         g = 64 * int(rng.integers(0, K // 64))
         x[:, g + 3] = np.float32(1e5); wmul[g + 3] = 0.0
         x[:, g + 40] *= np.float32(1e3)
+    elif name.startswith("maj"):                                    # "maj<count>_x<mult>": a cluster of large channels
+        nbig, mul = name[3:].split("_x")
+        for g0 in range(0, K, 64):
+            ch = g0 + rng.choice(64, int(nbig), replace=False)
+            x[:, ch] *= np.float32(float(mul)); wmul[ch] = 0.0
     elif name == "zeros_subnormals":
         x[:, :64] = 0.0
         if K >= 256:
@@ -93,6 +100,10 @@ def outlier_case(name, K, M, seed):
 
 
 PATTERNS = ["x1e3_w0.01", "x1e4_w0.01", "x1e5_w0", "two_sizes_one_group", "zeros_subnormals"]
+# Most of every group's channels large (x1e2 .. x1e4) with zero weight columns, so y comes from the
+# group's small elements alone: every level-0 element then errs by up to 2^-23 of its group's large
+# maximum, and the groups need their level-1 residual (bgl_x_level1: 8 or more small elements).
+MAJORITY = [f"maj{n}_x{m}" for n in (33, 40) for m in ("1e2", "1e3", "1e4")]
 
 
 def make_weights(oracle, kind, bits, N, K, wmul, seed):
@@ -140,6 +151,32 @@ def test_gemv_x_outliers(torch_dev, oracle, monkeypatch, kind, bits, N, K, fuse)
         got = run_dense(c, torch, kind, bits, pk, sc, N, K, x)
         ref = oracle.gemm_f32(kind, pk, sc, x, bits=bits)
         e = relerr(got, ref)
+        print(f"  max-rel {e:.3e}")
+        assert np.all(np.isfinite(got)) and e <= TOL, (pat, e)
+    c.close()
+
+
+# cfg1 (Q4G32H 8960x1536), cfg3 gate n = 2 / 15 and cfg3 down n = 7
+MAJ_DENSE = [(5, 0, 8960, 1536), (4, 2, 14336, 4096), (4, 15, 14336, 4096), (4, 7, 4096, 14336)]
+
+
+@pytest.mark.parametrize("kind,bits,N,K", MAJ_DENSE)
+@pytest.mark.parametrize("M,env", [(1, {}), (1, {"BGL_X_FUSE": 0}), (4, {}), (32, {})])
+def test_dense_majority_outliers(torch_dev, oracle, monkeypatch, kind, bits, N, K, M, env):
+    """33 or 40 of every group's 64 channels at x1e2 .. x1e4 with zero weight columns: k_gemv_x
+    (digits made in the kernel, or by the prep kernel), k_gemv at M = 4 and the matrix cores (or,
+    for qNg64 n > 10, k_gemv) at M = 32, all to the 1e-5 bar."""
+    torch = torch_dev
+    c = context(monkeypatch, **env)
+    if M > 4:
+        N = min(N, 2048)          # the pattern lies along K; fewer rows keep the CPU oracle to seconds
+    for i, pat in enumerate(MAJORITY):
+        say("majority outliers", kind, bits, N, K, M, env, pat)
+        x, wmul = outlier_case(pat, K, M, 800 + i)
+        pk, sc = make_weights(oracle, kind, bits, N, K, wmul, 820 + i)
+        got = run_dense(c, torch, kind, bits, pk, sc, N, K, x)
+        ref = oracle.gemm_f32(kind, pk, sc, x, bits=bits)
+        e = max(relerr(got[m], ref[m]) for m in range(M))
         print(f"  max-rel {e:.3e}")
         assert np.all(np.isfinite(got)) and e <= TOL, (pat, e)
     c.close()
@@ -270,6 +307,29 @@ def test_moe_outliers(torch_dev, oracle, monkeypatch, env, T):
         x, wmul = outlier_case(pat, H, T, 600 + i)
         gate, up, down = moe_descs(oracle, E, H, I, fm, 610 + 40 * i, wmul, np.ones(I, np.float32))
         idx, w = oracle.route(seeded_normal(620 + i, (T, E)), K, False)
+        got = run_moe(c, torch, gate, up, down, x, idx, w)
+        ref = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
+        e = relerr(got, ref)
+        print(f"  max-rel {e:.3e}")
+        assert e <= TOL, (pat, e)
+    c.close()
+
+
+@pytest.mark.parametrize("env", [{}, {"BGL_NO_MOE_X": 1}])
+@pytest.mark.parametrize("T", [1, 8])
+def test_moe_majority_outliers(torch_dev, oracle, monkeypatch, env, T):
+    """The routed FFN at DeepSeek-V2-Lite's expert shape (k_moe_x, and k_moe_gemv over prepared
+    digits) with 33 or 40 of every group's 64 hidden channels at x1e2 .. x1e4 and zero gate/up
+    columns there."""
+    torch = torch_dev
+    c = context(monkeypatch, **env)
+    E, H, I, K = 12, 2048, 1408, 6
+    fm = [(5, 0), (2, 0), (4, 7), (4, 12), (1, 0), (4, 15)]
+    for i, pat in enumerate(MAJORITY):
+        say("moe majority outliers", env, T, pat)
+        x, wmul = outlier_case(pat, H, T, 840 + i)
+        gate, up, down = moe_descs(oracle, E, H, I, fm, 850 + 40 * i, wmul, np.ones(I, np.float32))
+        idx, w = oracle.route(seeded_normal(860 + i, (T, E)), K, False)
         got = run_moe(c, torch, gate, up, down, x, idx, w)
         ref = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
         e = relerr(got, ref)

@@ -279,6 +279,46 @@ def test_quant_act_rounding_and_floor(oracle):
     assert np.array_equal(a, mx / np.float32(127.0))
 
 
+@pytest.mark.parametrize("gs", [64, 256])
+def test_quant_act_nonfinite_groups(oracle, gs):
+    """q4gemv.h:182-206 / q4gemv_g256.h:76-96 on NaN and +-Inf, by the AArch64 instruction
+    definitions: FMAX (vmaxq_f32, vmaxvq_f32) returns NaN when an operand is NaN, FCVTZS
+    (vcvtq_s32_f32) maps NaN to 0.  A NaN group: mx = NaN, sc = NaN, every code 0.  A +-Inf group:
+    mx = +Inf, sc = +Inf, inv = 0, x*inv = +-0 (NaN at the Inf): every code 0.  Groups without a
+    non-finite value are untouched, and the fold's 0 * NaN / 0 * Inf makes every output row NaN."""
+    x = seeded_normal(17, (4 * gs,))
+    clean_q, clean_a = oracle.quant_act_i8(x, gs)
+    x[1] = np.nan                                        # group 0: one NaN
+    x[gs + 5] = np.inf                                   # group 1: +Inf
+    x[2 * gs + 7] = -np.inf                              # group 2: -Inf and a NaN
+    x[2 * gs + 9] = np.nan
+    xq, a = oracle.quant_act_i8(x, gs)
+    assert np.isnan(a[0]) and not xq[:gs].any()
+    assert a[1] == np.float32(np.inf) and not xq[gs:2 * gs].any()
+    assert np.isnan(a[2]) and not xq[2 * gs:3 * gs].any()
+    assert a[3] == clean_a[3] and np.array_equal(xq[3 * gs:], clean_q[3 * gs:])
+    # -Inf alone: FMAX over |x| gives +Inf, the same as +Inf
+    y = seeded_normal(18, (gs,)); y[3] = -np.inf
+    yq, ya = oracle.quant_act_i8(y, gs)
+    assert ya[0] == np.float32(np.inf) and not yq.any()
+    # the largest finite values quantize normally: the max maps to +-127
+    big = seeded_normal(19, (gs,)); big[0] = np.float32(3.0e38); big[1] = np.float32(-3.0e38)
+    bq, ba = oracle.quant_act_i8(big, gs)
+    assert np.isfinite(ba[0]) and bq[0] == 127 and bq[1] == -127
+    # through the fold: every output row of a column with a non-finite group is NaN, the other
+    # column is finite
+    out, inn = 16, 4 * gs
+    w = _weights(91, out, inn)
+    kind = 3 if gs == 256 else 1
+    if kind == 1:
+        p, s = oracle.quantize_q4g64(w); sub = None
+    else:
+        p, s, sub = oracle.quantize_g256sf(w)
+    xm = np.stack([x, seeded_normal(20, (inn,))]).astype(np.float32)
+    ym = oracle.matmul_sdot(kind, p, s, xm, sub=sub)
+    assert np.isnan(ym[0]).all() and np.isfinite(ym[1]).all()
+
+
 @pytest.mark.parametrize("kind", [1, 2, 3])
 def test_sdot_gemm_equals_dequantized_product(oracle, kind):
     """Identity: the W4A8/W8A8 result equals the fp32 product of the decoded weights with the

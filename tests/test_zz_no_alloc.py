@@ -44,6 +44,9 @@ CASES = [
     ("fp32 prepared digits + K-split", 4, 6, 0, [(96, 8192)], 12, 3),
     ("fp32 fused group, prepared digits", 5, 0, 0, [(512, 6144), (256, 6144)], 6, 2),
     ("fp32 matrix cores, K-split", 5, 0, 0, [(1024, 14336)], 32, 17),
+    # M > 64 runs as chunks of 64 columns; each chunk's 16.8 MB of K-split partials reuses one
+    # slice of the fixed array (four chunks of fresh slices would exceed it)
+    ("fp32 matrix cores, 64-column chunks", 5, 0, 0, [(8192, 4096)], 256, 130),
     ("W4A8 g256sf, columns quantized up front", 3, 4, 1, [(1536, 8960)], 8, 4),
 ]
 
