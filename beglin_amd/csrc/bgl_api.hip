@@ -675,7 +675,7 @@ int prep_act(bgl_ctx *c, int act, int gq, const float *x_dev, int M, int K, Gemv
             return bgl_last_code();
         int tok = prof_begin(c, 0);
         hipLaunchKernelGGL(k_act_w4a8, dim3(nblk((long)M * (K / gq) * 64)), dim3(256), 0, c->stream, x_dev, M, K, gq,
-                           (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p);
+                           (int8_t *)c->act_w.p, (float *)c->act_s.p, (int *)c->act_sum.p, c->prep_u, c->prep_h);
         prof_end(c, tok);
     }
     HIPCHK(hipGetLastError());
@@ -697,7 +697,7 @@ extern "C" int bgl_quant_act_i8_dev(bgl_ctx *c, const float *x_dev, int M, int i
     if ((gsize != 64 && gsize != 256) || in % gsize) return bgl_fail(BGL_E_ARG, "bgl_quant_act_i8_dev: in=%d gsize=%d", in, gsize);
     if (dbuf_reserve(c, c->act_sum, (size_t)M * (in / 64) * 4, false)) return bgl_last_code();
     hipLaunchKernelGGL(k_act_w4a8, dim3(nblk((long)M * (in / gsize) * 64)), dim3(256), 0, c->stream, x_dev, M, in, gsize, xq_dev,
-                       ascale_dev, (int *)c->act_sum.p);
+                       ascale_dev, (int *)c->act_sum.p, (const float *)nullptr, (float *)nullptr);
     HIPCHK(hipGetLastError());
     return 0;
 }
@@ -867,7 +867,7 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
         memset(&L, 0, sizeof L);
         int blocks = 0;
         fill_tasks(L, n, Ts, bias, y, nullptr, blocks);
-        L.x = x_dev;
+        L.x = c->prep_h ? c->prep_h : x_dev;     // a SwiGLU column: h, which the prep launch wrote
         if (prep && MB > 1) L.a = A;
         L.m0 = m0;
         L.mcols = mc;
@@ -897,6 +897,28 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
         HIPCHK(hipGetLastError());
     }
     return 0;
+}
+
+// The MLP block's down projection at M > 1 W4A8 columns when its columns are quantized up front:
+// that one launch also forms h = SwiGLU(g, u) (k_act_w4a8 with u), writing h, so the block needs
+// no SwiGLU launch.  Returns 1 (nothing launched) where the down projection would not quantize up
+// front; the caller then runs the SwiGLU itself.
+int run_down_swiglu_w4a8(bgl_ctx *c, const BglDevTensor &down, const float *g, const float *u, float *h, int M, float *y) {
+    if (c->no_fused || M < 2) return 1;
+    const int kind = down.fmt, K = down.K;
+    if (kind != BGL_Q4G256SF && kind != BGL_Q4G64 && kind != BGL_Q8G64) return 1;
+    const int mbmax = q_mb_max(kind, K);
+    if (mbmax < 2) return 1;
+    const int passes = std::min(M, mbmax) * ((K + 255) / 256);
+    if (!(c->q_prep == 1 || (c->q_prep < 0 && passes >= BGL_Q_PREP_MIN_PASSES))) return 1;
+    c->prep_u = u;
+    c->prep_h = h;
+    const float *nob[1] = {nullptr};
+    float *ys[1] = {y};
+    const int rc = run_gemv_q(c, 1, &down, g, M, nob, ys);
+    c->prep_u = nullptr;
+    c->prep_h = nullptr;
+    return rc;
 }
 
 static bool fused_q_ok(bgl_ctx *c, int kind, int K, int M) {

@@ -40,6 +40,8 @@ struct bgl_ctx {
     DevBuf act_w, act_s, act_sum;         // activation operands of the current call
     int prep_act = -1, prep_gq = 0, prep_M = 0, prep_K = 0;   // what act_* currently hold
     const float *prep_x = nullptr;        // the raw fp32 columns they were made from (non-finite slow path)
+    const float *prep_u = nullptr;        // set around run_down_swiglu_w4a8: the prep launch forms h = SwiGLU(x, prep_u)
+    float *prep_h = nullptr;              //   into prep_h
     bool prep_reuse = false;              // act_* come from bgl_prep_act_dev (or a host drop-in): bgl_matmul_prepped_dev may use them
     DevBuf prep_xc;                       // bgl_prep_act_dev's own copy of the fp32 columns (prep_x points here)
     DevBuf part;                          // K-split partial sums [ks][M][N]
@@ -92,6 +94,7 @@ bool bgl_mfma_ok(int fmt, int bits);
 int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
                   float *const *y, const int *ystride, float *glu_h = nullptr);
 // The dense MLP block at one W4A8 column in one launch (bgl_mlp_q.hip): the formats it takes, and the call.
+int run_down_swiglu_w4a8(bgl_ctx *c, const BglDevTensor &down, const float *g, const float *u, float *h, int M, float *y);
 bool mlp_q_ok(bgl_ctx *c, const BglDevTensor &gate, const BglDevTensor &up, const BglDevTensor &down);
 int run_mlp_q(bgl_ctx *c, const BglDevTensor &gate, const BglDevTensor &up, const BglDevTensor &down, const float *x,
               float *h, float *y);

@@ -203,7 +203,8 @@ struct MoeTask {
 };
 
 // ---- kernels (bgl_prep.hip) ----
-__global__ void k_act_w4a8(const float *x, int M, int K, int gsize, int8_t *xq, float *ascale, int *xqsum64);
+__global__ void k_act_w4a8(const float *x, int M, int K, int gsize, int8_t *xq, float *ascale, int *xqsum64, const float *u,
+                           float *h);
 __global__ void k_act_x24(const float *x, int M, int K, int8_t *xd, float *xs, int *dsum);
 __global__ void k_act_import_i8(const int8_t *xq, const float *ascale, int M, int K, int gq, int split, int8_t *xw,
                                 float *xs, int *xsum64);

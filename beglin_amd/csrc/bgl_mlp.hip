@@ -5,6 +5,8 @@
 //
 //   g, u = W_gate x, W_up x      bgl_matmul_group_dev over {gate, up} (one fused launch)
 //   h = silu(g) * u              k_swiglu: h = (g / (1 + exp(-g))) * u in fp32, exp rounded once
+//                                (several W4A8 columns whose down projection quantizes them up front:
+//                                that quantization launch forms h itself, so no k_swiglu launch)
 //                                (>= 16 fp32 columns on the matrix cores: the GEMM's reduce launch
 //                                forms h with the same arithmetic, from the K-split sums or, for a
 //                                tensor whose K did not split, from the g / u the GEMM stored)
@@ -77,6 +79,11 @@ extern "C" int bgl_mlp_dev(bgl_ctx *c, const bgl_tensor *gate, const bgl_tensor 
     }
     int rc = bgl_matmul_group_dev(c, 2, gu, act, x_dev, nob, ys, M);
     if (rc) return rc;
+    // several W4A8 columns whose down projection quantizes them up front: that launch forms h too
+    if (act == BGL_ACT_W4A8) {
+        rc = run_down_swiglu_w4a8(c, down->T, g, u, h, M, y_dev);
+        if (rc <= 0) return rc;
+    }
     int tok = prof_begin(c, 2);
     hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, c->stream, g, u, h, (long)n);
     prof_end(c, tok);

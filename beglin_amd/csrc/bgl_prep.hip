@@ -17,18 +17,32 @@
 // value: that is the reference's FMAX (vmaxq_f32 / vmaxvq_f32), which carries a NaN into mx.  A group
 // whose maximum is NaN or +-Inf gets sc = NaN or +Inf and every code 0 (FCVTZS maps the NaN products
 // to 0; with inv = 0 the finite ones are +-0), so the fold's 0 * sc makes its outputs NaN.
+// u != null: the column is h = silu(x) * u of the MLP block (swiglu, qwen_infer.c:726-733, the
+// arithmetic of k_swiglu in bgl_mlp.hip: x / (1 + exp(-x)) * u, the exponential rounded once from
+// double), formed here and also written to h, so the SwiGLU costs no launch of its own.
 __global__ __launch_bounds__(256) void k_act_w4a8(const float *__restrict__ x, int M, int K, int gsize,
                                                   int8_t *__restrict__ xq, float *__restrict__ ascale,
-                                                  int *__restrict__ xqsum64) {
+                                                  int *__restrict__ xqsum64, const float *__restrict__ u,
+                                                  float *__restrict__ h) {
     int wid = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     int ng = K / gsize;
     if (wid >= M * ng) return;
     int m = wid / ng, g = wid % ng, per = gsize >> 6;
-    const float *xp = x + (size_t)m * K + (size_t)g * gsize;
+    const size_t o = (size_t)m * K + (size_t)g * gsize;
+    const float *xp = x + o;
     float v[4];
     uint32_t mb = __float_as_uint(1e-8f);                  // mx starts at 1e-8 (q4gemv.h:182)
-    for (int j = 0; j < per; j++) {
-        v[j] = xp[lane + 64 * j];
+    // all four slots unconditionally (per < 4 repeats the last element, which leaves the maximum
+    // unchanged), so the SwiGLU exponentials of a lane overlap
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int jj = j < per ? j : per - 1;
+        v[j] = xp[lane + 64 * jj];
+        if (u) {
+            const float e = (float)exp(-(double)v[j]);
+            v[j] = __fmul_rn(__fdiv_rn(v[j], __fadd_rn(1.0f, e)), u[o + lane + 64 * jj]);
+            if (j < per) h[o + lane + 64 * j] = v[j];
+        }
         mb = max(mb, __float_as_uint(v[j]) & 0x7fffffffu);
     }
     mb = wave_max_u32(mb);

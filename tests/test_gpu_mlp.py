@@ -72,7 +72,10 @@ def run(ctx, torch, ts, x, act):
     return y.cpu().numpy(), h.cpu().numpy()
 
 
-W4A8_CASES = [("qwen", 3, 1536, 8960, 1), ("qwen", 3, 1536, 8960, 4), ("llama", 1, 4096, 14336, 1)]
+# M = 4 and 5: the down projection quantizes its columns up front and that launch forms h too (the
+# 5th column runs a one-column launch over that h)
+W4A8_CASES = [("qwen", 3, 1536, 8960, 1), ("qwen", 3, 1536, 8960, 4), ("qwen", 3, 1536, 8960, 5),
+              ("llama", 1, 4096, 14336, 1), ("llama", 1, 4096, 14336, 8)]
 
 
 @pytest.mark.parametrize("model,kind,H,I,M", W4A8_CASES)

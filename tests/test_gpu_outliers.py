@@ -161,25 +161,33 @@ MAJ_DENSE = [(5, 0, 8960, 1536), (4, 2, 14336, 4096), (4, 15, 14336, 4096), (4, 
 
 
 @pytest.mark.parametrize("kind,bits,N,K", MAJ_DENSE)
-@pytest.mark.parametrize("M,env", [(1, {}), (1, {"BGL_X_FUSE": 0}), (4, {}), (32, {})])
-def test_dense_majority_outliers(torch_dev, oracle, monkeypatch, kind, bits, N, K, M, env):
+def test_dense_majority_outliers(torch_dev, oracle, monkeypatch, kind, bits, N, K):
     """33 or 40 of every group's 64 channels at x1e2 .. x1e4 with zero weight columns: k_gemv_x
-    (digits made in the kernel, or by the prep kernel), k_gemv at M = 4 and the matrix cores (or,
-    for qNg64 n > 10, k_gemv) at M = 32, all to the 1e-5 bar."""
+    (digits made in the kernel, and by the prep kernel) at M = 1, k_gemv at M = 4 and the matrix
+    cores (or, for qNg64 n > 10, k_gemv) at M = 32 on the first 2048 rows, all to the 1e-5 bar.
+    The weights of a pattern are quantized once and serve every configuration."""
     torch = torch_dev
-    c = context(monkeypatch, **env)
-    if M > 4:
-        N = min(N, 2048)          # the pattern lies along K; fewer rows keep the CPU oracle to seconds
+    ctxs = {"fused": context(monkeypatch), "prep": context(monkeypatch, BGL_X_FUSE=0)}
+    monkeypatch.delenv("BGL_X_FUSE", raising=False)
+    NR = min(N, 2048)                                   # rows of the 32-column run
     for i, pat in enumerate(MAJORITY):
-        say("majority outliers", kind, bits, N, K, M, env, pat)
-        x, wmul = outlier_case(pat, K, M, 800 + i)
+        x, wmul = outlier_case(pat, K, 32, 800 + i)
         pk, sc = make_weights(oracle, kind, bits, N, K, wmul, 820 + i)
-        got = run_dense(c, torch, kind, bits, pk, sc, N, K, x)
-        ref = oracle.gemm_f32(kind, pk, sc, x, bits=bits)
-        e = max(relerr(got[m], ref[m]) for m in range(M))
+        ref14 = oracle.gemm_f32(kind, pk, sc, x[:4], bits=bits)
+        ref32 = oracle.gemm_f32(kind, pk[:NR], sc[:NR], x, bits=bits)
+        for name, c, M in (("fused", ctxs["fused"], 1), ("prep", ctxs["prep"], 1), ("fused", ctxs["fused"], 4)):
+            say("majority outliers", kind, bits, N, K, M, name, pat)
+            got = run_dense(c, torch, kind, bits, pk, sc, N, K, x[:M])
+            e = max(relerr(got[m], ref14[m]) for m in range(M))
+            print(f"  max-rel {e:.3e}")
+            assert np.all(np.isfinite(got)) and e <= TOL, (pat, name, M, e)
+        say("majority outliers", kind, bits, NR, K, 32, pat)
+        got = run_dense(ctxs["fused"], torch, kind, bits, pk[:NR], sc[:NR], NR, K, x)
+        e = max(relerr(got[m], ref32[m]) for m in range(32))
         print(f"  max-rel {e:.3e}")
-        assert np.all(np.isfinite(got)) and e <= TOL, (pat, e)
-    c.close()
+        assert np.all(np.isfinite(got)) and e <= TOL, (pat, 32, e)
+    for c in ctxs.values():
+        c.close()
 
 
 @pytest.mark.parametrize("kind,bits", [(5, 0), (4, 3), (2, 0), (1, 0)])
@@ -315,27 +323,31 @@ def test_moe_outliers(torch_dev, oracle, monkeypatch, env, T):
     c.close()
 
 
-@pytest.mark.parametrize("env", [{}, {"BGL_NO_MOE_X": 1}])
-@pytest.mark.parametrize("T", [1, 8])
-def test_moe_majority_outliers(torch_dev, oracle, monkeypatch, env, T):
+def test_moe_majority_outliers(torch_dev, oracle, monkeypatch):
     """The routed FFN at DeepSeek-V2-Lite's expert shape (k_moe_x, and k_moe_gemv over prepared
     digits) with 33 or 40 of every group's 64 hidden channels at x1e2 .. x1e4 and zero gate/up
-    columns there."""
+    columns there, at T = 1 and 8.  The experts of a pattern are quantized once."""
     torch = torch_dev
-    c = context(monkeypatch, **env)
+    cx = context(monkeypatch)
+    cg = context(monkeypatch, BGL_NO_MOE_X=1)
+    monkeypatch.delenv("BGL_NO_MOE_X", raising=False)
     E, H, I, K = 12, 2048, 1408, 6
     fm = [(5, 0), (2, 0), (4, 7), (4, 12), (1, 0), (4, 15)]
     for i, pat in enumerate(MAJORITY):
-        say("moe majority outliers", env, T, pat)
-        x, wmul = outlier_case(pat, H, T, 840 + i)
+        x8, wmul = outlier_case(pat, H, 8, 840 + i)
         gate, up, down = moe_descs(oracle, E, H, I, fm, 850 + 40 * i, wmul, np.ones(I, np.float32))
-        idx, w = oracle.route(seeded_normal(860 + i, (T, E)), K, False)
-        got = run_moe(c, torch, gate, up, down, x, idx, w)
-        ref = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
-        e = relerr(got, ref)
-        print(f"  max-rel {e:.3e}")
-        assert e <= TOL, (pat, e)
-    c.close()
+        for T in (1, 8):
+            x = np.ascontiguousarray(x8[:T])
+            idx, w = oracle.route(seeded_normal(860 + i + T, (T, E)), K, False)
+            ref = moe_ffn(oracle, gate, up, down, None, H, I, x, idx, w)
+            for name, c in (("moe_x", cx), ("moe_gemv", cg)):
+                say("moe majority outliers", name, T, pat)
+                got = run_moe(c, torch, gate, up, down, x, idx, w)
+                e = relerr(got, ref)
+                print(f"  max-rel {e:.3e}")
+                assert e <= TOL, (pat, name, T, e)
+    cx.close()
+    cg.close()
 
 
 @pytest.mark.parametrize("env", [{}, {"BGL_NO_MOE_X": 1}])
