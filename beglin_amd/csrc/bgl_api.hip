@@ -183,9 +183,12 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     const char *mwv = getenv("BGL_MLP_WAVES");
     c->mlp_waves = mwv ? atoi(mwv) : 0;
     if (c->mlp_waves < 0 || c->mlp_waves > 16) c->mlp_waves = 0;
-    const char *mtr = getenv("BGL_MLP_TRG");
-    c->mlp_trg = mtr ? atoi(mtr) : 0;
-    if (c->mlp_trg != 16 && c->mlp_trg != 32) c->mlp_trg = 0;
+    const char *mdl = getenv("BGL_MLP_DELAY");
+    c->mlp_delay = mdl ? atoi(mdl) : -1;
+    if (c->mlp_delay < -1 || c->mlp_delay > 100000) c->mlp_delay = -1;
+    const char *mgu = getenv("BGL_MLP_GU");
+    c->mlp_gu = mgu ? atoi(mgu) : 0;
+    if (c->mlp_gu < 0 || c->mlp_gu > 4096) c->mlp_gu = 0;
     const char *mt = getenv("BGL_MLP_TEST_TIMEOUT");
     c->mlp_test_timeout = mt && atoi(mt) > 0 ? atoi(mt) : 0;
     *out = c;

@@ -75,7 +75,7 @@ __device__ __forceinline__ uint32_t quant_byte(float x, float inv, bool nf) {
 
 // Quantizes QP passes into LDS.  The MB columns of a launch are one run of passes: pass p is values
 // 256*(p % NP) .. +255 of column p / NP (NP passes per column, NPT = MB*NP in all); pass i of the
-// call is p0 + i*nw, lane l holding values 4l..4l+3 of it in v[i].  The passes are processed in
+// call is pp[i], lane l holding values 4l..4l+3 of it in v[i].  The passes are processed in
 // lockstep so their dependency chains interleave.  Column m's operands live at xq + m*XQS,
 // asc + m*(NGQ+1), xsum + m*(K/64+1); passes past NPT and lanes past K store into each region's dummy
 // slot.  |x| is maximised on its bit pattern (the same order as the float values for non-NaN inputs).
@@ -83,8 +83,8 @@ __device__ __forceinline__ uint32_t quant_byte(float x, float inv, bool nf) {
 // division pair serves every pass (lane i computes pass i's scale and reciprocal).  GQ=64: one pass
 // is four groups, one per 16-lane row.
 template <int FMT, int QP, int MB>
-__device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int nw, int K, int NP, int NPT, int NGQ, int U,
-                                             int lane, int8_t *xq, float *asc, int *xsum) {
+__device__ __forceinline__ void quant_passes_at(const float4 (&v)[QP], const int (&pp)[QP], int K, int NP, int NPT, int NGQ,
+                                                int U, int lane, int8_t *xq, float *asc, int *xsum) {
     using QU = QUnit<FMT>;
     const int XQS = (U + 1) * QU::STRIDE;
     uint32_t m[QP];
@@ -104,7 +104,7 @@ __device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int 
     bool ok[QP];
 #pragma unroll
     for (int i = 0; i < QP; i++) {
-        const int p = p0 + i * nw;
+        const int p = pp[i];
         if constexpr (MB == 1) {                       // one column: passes past K land past K
             col[i] = 0;
             e[i] = 256 * p + 4 * lane;
@@ -133,7 +133,9 @@ __device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int 
 #pragma unroll
         for (int i = 0; i < QP; i++) inv[i] = rlane_f(iv, i);
         if (lane < QP) {
-            const int p = p0 + lane * nw;
+            int p = pp[0];
+#pragma unroll
+            for (int i = 1; i < QP; i++) p = lane == i ? pp[i] : p;
             if constexpr (MB == 1) {
                 asc[256 * p < K ? p : NGQ] = sc;
             } else {
@@ -177,6 +179,16 @@ __device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int 
             for (int i = 0; i < QP; i++) xsum[col[i] * (K / 64 + 1) + (ok[i] ? e[i] / 64 : K / 64)] = sm[i];
         }
     }
+}
+
+// passes p0, p0 + nw, p0 + 2 nw, ...
+template <int FMT, int QP, int MB>
+__device__ __forceinline__ void quant_passes(const float4 (&v)[QP], int p0, int nw, int K, int NP, int NPT, int NGQ, int U,
+                                             int lane, int8_t *xq, float *asc, int *xsum) {
+    int pp[QP];
+#pragma unroll
+    for (int i = 0; i < QP; i++) pp[i] = p0 + i * nw;
+    quant_passes_at<FMT, QP, MB>(v, pp, K, NP, NPT, NGQ, U, lane, xq, asc, xsum);
 }
 
 // x values of QP passes (see quant_passes); addresses are clamped, so every load is valid.

@@ -51,9 +51,10 @@ struct bgl_ctx {
     DevBuf moe_scores;                    // router scores [T][E]
     DevBuf mlp;                           // bgl_mlp_dev: gate and up outputs [M][I] each, then h [M][I]
     std::unordered_map<uint64_t, DevBuf> mlp_sync;   // single-launch MLP, per shape (in << 32 | down workgroups): counters, generations, flag
-    int mlp_trg = 0;                      // BGL_MLP_TRG: rows of gate / up per single-launch MLP workgroup (tuning; 0 by shape)
+    int mlp_gu = 0;                       // BGL_MLP_GU: gate+up workgroups of the single-launch MLP (tuning; 0 by shape)
     bool no_fused_mlp = false;            // BGL_NO_FUSED_MLP=1: the MLP block as three launches at every M
     int mlp_spin = 1 << 20;               // BGL_MLP_SPIN: polls of the single-launch MLP's bounded wait
+    int mlp_delay = -1;                   // BGL_MLP_DELAY: ns the single-launch MLP's down waves wait before loading their weights (tuning; -1 by shape)
     int mlp_waves = 0;                    // BGL_MLP_WAVES: wavefronts per single-launch MLP workgroup (tuning; 0 by shape)
     int mlp_test_timeout = 0;             // BGL_MLP_TEST_TIMEOUT=n: the next n such launches wait for a count never reached (tests of the give-up path)
     std::vector<void *> retired;          // outgrown scratch, kept for captured graphs until destroy / epoch reset

@@ -2,36 +2,38 @@
 // at one W4A8 column in a single launch: g = W_gate x and u = W_up x, h = silu(g) * u (swiglu,
 // qwen_infer.c:726-733), y = W_down h.
 //
-// The grid holds two roles.  Workgroups [0, ngu) each own TRG rows of BOTH gate and up (the same
-// rows), quantize x into LDS (the reference's q4_quant_act_i8 / _g256, bit for bit), run the units
-// of the two tensors, fold each row in the reference's group order (q4gemv.h:241,
-// q4gemv_g256.h:154) and form h for their rows.  Workgroups [ngu, ngu + nd) each own 8 rows of
-// down.  Each of their waves loads ALL its weight units at once (the weights do not depend on h),
-// then waits only for the 256-value groups of h its own units read, quantizes exactly those
-// (every unit's codes are made by the wave that uses them, so no workgroup barrier comes between
-// the quantization and the dot products) and runs its units; a last barrier and the fold follow.
-// So the down projection's weight stream overlaps the gate+up work, the block is one launch instead
-// of three (gate+up, SwiGLU, down), and a down wave starts as soon as its part of h exists.  Every
-// value is the one the three-launch path computes: g, u and y bit for bit, h with the same
-// arithmetic.
+// The grid holds two roles.  Workgroups [0, ngu) run gate+up: each quantizes x into LDS once (the
+// reference's q4_quant_act_i8 / _g256, bit for bit), and each of its waves then runs one item of 8
+// rows of BOTH gate and up (the same rows): the units of the two tensors, the fold of each row in
+// the reference's group order (q4gemv.h:241, q4gemv_g256.h:154) and h for its rows.  With one item
+// per wave, a CU's share of the gate+up bytes is at most its waves' items (a whole-workgroup row
+// slice of 32 rows left some CUs with two slices and the launch waiting on them).  Workgroups
+// [ngu, ngu + nd) each own 8 rows of down.  Each of their waves first waits a fixed delay (about
+// the time the gate+up weights take to stream, so that the gate+up role's x and weights are not
+// queued behind the down weights), then loads ALL its weight units at once (they do not depend on
+// h), then loads the 256-value groups of h its own units read until they are complete: as soon as
+// the groups of one of its unit iterations are, it quantizes exactly those (every unit's codes are
+// made by the wave that uses them, so no workgroup barrier comes between the quantization and the
+// dot products) and runs that iteration's units.  A last barrier and the fold follow.  So the
+// block is one launch instead of three (gate+up, SwiGLU, down), the down weights stream while
+// gate+up computes, and when the last h rows land only their iteration is left.  Every value is
+// the one the three-launch path computes: g, u and y bit for bit, h with the same arithmetic.
 //
 // Publishing h across workgroups (which run on different XCDs, each with its own L2): h is written
 // and read with device-scope (sc1) buffer accesses, which the L2s do not hold stale, so no cache
 // maintenance is needed, and the data carries its own "not yet" mark.  h has two buffers, used in
 // turn by successive launches of one shape; a slot of the buffer a launch reads holds a sentinel (a
 // signalling-NaN bit pattern, which no arithmetic produces: every NaN an operation returns is
-// quiet) until its gate+up workgroup stores the value, and that workgroup also puts the sentinel
-// back into its rows of the other buffer for the next launch.  A producer stores its rows and moves
-// on: no wait for the stores to complete, no atomic read-modify-write.  One wave of each down
-// workgroup polls a sample of rows, then each wave loads its groups of h and checks that no
-// sentinel is left, reloading while one is.  Each workgroup keeps its own count of the launches it
-// has run on this shape (which buffer is current is its parity; every workgroup of a launch has the
-// same count), read at its start and stored +1 at its end, so graph replays need no memset.  The
-// wait is bounded: after `spin` polls a wave gives up, sets the host-visible flag and finishes with
-// whatever h holds (bgl_ctx_check reports it); the buffers stay consistent because every producer
-// resets its rows of the other buffer in every launch.  No workgroup waits on one that is not yet
-// running: the gate+up workgroups have the lower ids, so the dispatcher starts every one of them
-// before any down workgroup, and they wait on nothing.
+// quiet) until its gate+up wave stores the value, and that wave also puts the sentinel back into
+// its rows of the other buffer for the next launch.  A producer stores its rows and moves on: no
+// wait for the stores to complete, no atomic read-modify-write.  Each workgroup keeps its own
+// count of the launches it has run on this shape (which buffer is current is its parity; every
+// workgroup of a launch has the same count), read at its start and stored +1 at its end, so graph
+// replays need no memset.  The wait is bounded: after `spin` rounds a wave gives up, sets the
+// host-visible flag and finishes with whatever h holds (bgl_ctx_check reports it); the buffers
+// stay consistent because every producer resets its rows of the other buffer in every launch.  No
+// workgroup waits on one that is not yet running: the gate+up workgroups have the lower ids, so
+// the dispatcher starts every one of them before any down workgroup, and they wait on nothing.
 #include <string.h>
 
 #include <algorithm>
@@ -51,6 +53,8 @@
 // nd ints].
 #define MLP_TRD 8             // rows of down per workgroup
 #define MLP_MAXQ 8            // 256-value passes of h a down wave may quantize (its units' groups)
+#define MLP_MAXW 12           // waves per workgroup; at most 168 VGPRs (3 waves per SIMD), so a CU
+                              // holds a gate+up and a down workgroup of 6 waves together
 #define MLP_EMPTY 0x7F800001u // the sentinel of an h slot not yet written (a signalling NaN)
 
 struct MlpQLaunch {
@@ -64,6 +68,7 @@ struct MlpQLaunch {
     int ngu, nd;                   // workgroups of each role
     int never;                     // 1: the down waves' wait is never satisfied (tests of the give-up path)
     int spin;                      // polls before a down wave gives up
+    int delay;                     // 10 ns ticks a down wave waits before it loads its weights (0: none)
 };
 
 // buffer-resource word 3 for raw 32-bit accesses, and the cache-policy bit that makes a buffer
@@ -125,77 +130,98 @@ __device__ __forceinline__ void mlp_xload(float4 (&v)[QP], const float *x, int p
     }
 }
 
-template <int FMT, int TRG, int NIT>
-__global__ __launch_bounds__(MAXW * BGL_TILE) void k_mlp_q(MlpQLaunch L) {
+template <int FMT, int GP, int NIT>
+__global__ __launch_bounds__(MLP_MAXW * BGL_TILE, 4) void k_mlp_q(MlpQLaunch L) {
     extern __shared__ __align__(16) unsigned char lds[];
     using QU = QUnit<FMT>;
     const int nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if ((int)blockIdx.x < L.ngu) {
-        // ------------------------------------------------------------ gate + up: TRG rows of each
-        constexpr int SUBS = BGL_TILE / TRG, KQ = BGL_TILE / TRG, H = TRG <= 32 ? 2 : 1, UPI = KQ / H;
-        const int b = blockIdx.x, tile = b / SUBS, r0 = (b % SUBS) * TRG;
+        // ------------------------------------------------------------ gate + up: items of 8 rows
+        // An item is 8 consecutive rows of BOTH gate and up; a wave runs whole items (item k = rows
+        // 8k .. 8k+7), the workgroup only shares the quantized x.  Lane l: row l % 8 and, of each
+        // unit iteration's UPI = 4 units, unit (l / 8) / 2 (two lanes share a unit, half its chunks
+        // each); unit v < U is gate's unit v, v >= U up's unit v - U (the same shape and layout).
+        // The unit iterations are loaded GP at a time: GP >= 3 means every iteration of an item in
+        // one group (the host picks it only then), else the next group loads while one computes.
+        constexpr int TRI = MLP_TRD, IPT = BGL_TILE / TRI, KQ = BGL_TILE / TRI, H = 2, UPI = KQ / H;
+        const int b = blockIdx.x;
         const BglDevTensor &T = L.gate;
         const int K = T.K, U = T.nunits, U2 = 2 * U, NGQ = K / QU::GQ, NP = (K + 255) / 256;
+        const int NG = ((U2 + UPI - 1) / UPI + GP - 1) / GP;
+        const int nitems = (T.N + TRI - 1) / TRI;
         const unsigned gen = (unsigned)L.gen_gu[b];          // this shape's launches so far: its parity picks the buffer
         int8_t *xq = reinterpret_cast<int8_t *>(lds);
         float *asc = reinterpret_cast<float *>(lds + (size_t)(U + 1) * QU::STRIDE);
         int *xsum = reinterpret_cast<int *>(asc + NGQ + 1);
-        float *tl = reinterpret_cast<float *>(xsum + K / 64 + 1);
-        const int nwl = min(nw, (U2 + UPI - 1) / UPI);
-        const int r = lane % TRG, j = lane / TRG, kq = j / H, hh = j % H, rr = r0 + r;
-        // unit v < U is gate's unit v, v >= U up's unit v - U (the same shape and layout)
-        auto load = [&](RawPart<FMT, H> &c, int v) {
-            BglDevTensor Tv = L.gate;
-            if (v >= U) { Tv.w = L.up.w; Tv.s0 = L.up.s0; }
-            load_part<FMT, H>(c, Tv, tile, rr, v >= U ? v - U : v, hh);
-        };
-        // x loads first, then the first weight units: vector loads retire in order, so the
-        // quantization waits only for x while the weight bytes are in flight
-        float4 v[2];
-        mlp_xload<2, false>(v, L.x, wave, nw, K, lane);
-        RawPart<FMT, H> c0, c1;
-        int ub = wave * UPI;
-        load(c0, min(ub + kq, U2 - 1));                 // unconditional (clamped): no wait merges paths
-        __builtin_amdgcn_sched_barrier(0);
-        if (wave < NP) quant_passes<FMT, 2, 1>(v, wave, nw, K, NP, 1, NGQ, U, lane, xq, asc, xsum);
-        for (int p0 = wave + 2 * nw; p0 < NP; p0 += 2 * nw) {
-            mlp_xload<2, false>(v, L.x, p0, nw, K, lane);
-            quant_passes<FMT, 2, 1>(v, p0, nw, K, NP, 1, NGQ, U, lane, xq, asc, xsum);
-        }
-        __syncthreads();
-        if (wave < nwl) {
-            auto emit = [&](const RawPart<FMT, H> &c, int v) {
-                const int vc = min(v, U2 - 1), u = vc >= U ? vc - U : vc;
-                int p = unit_part<FMT, H>(c, xq, u, hh);
-                if constexpr (H == 2) p += __shfl_xor(p, TRG);
-                if (hh == 0 && v < U2) tl[v * TRG + r] = unit_float<FMT>(p, c.s, T.gmul, asc, xsum, u);
-            };
-            for (;;) {
-                const int un = ub + nwl * UPI, v = ub + kq;
-                if (un >= U2) {
-                    emit(c0, v);
-                    break;
-                }
-                load(c1, min(un + kq, U2 - 1));
-                emit(c0, v);
-                c0 = c1;
-                ub = un;
+        float *tw = reinterpret_cast<float *>(xsum + K / 64 + 1) + (size_t)wave * U2 * TRI;   // this wave's terms [v][8]
+        const int r = lane % TRI, j = lane / TRI, kq = j / H, hh = j % H;
+        auto ld = [&](RawPart<FMT, H>(&c)[GP], int item, int g) {
+            const int tile = item / IPT, rr = (item % IPT) * TRI + r;
+#pragma unroll
+            for (int i = 0; i < GP; i++) {
+                const int v = min((g * GP + i) * UPI + kq, U2 - 1);
+                BglDevTensor Tv = L.gate;
+                if (v >= U) { Tv.w = L.up.w; Tv.s0 = L.up.s0; }
+                load_part<FMT, H>(c[i], Tv, tile, rr, v >= U ? v - U : v, hh);
             }
+        };
+        auto em = [&](const RawPart<FMT, H>(&c)[GP], int g) {
+#pragma unroll
+            for (int i = 0; i < GP; i++) {
+                const int v = (g * GP + i) * UPI + kq, vc = min(v, U2 - 1), u = vc >= U ? vc - U : vc;
+                int p = unit_part<FMT, H>(c[i], xq, u, hh);
+                p += __shfl_xor(p, TRI);
+                if (hh == 0 && v < U2) tw[v * TRI + r] = unit_float<FMT>(p, c[i].s, T.gmul, asc, xsum, u);
+            }
+        };
+        // x loads first, then the first item's first weight units: vector loads retire in order, so
+        // the quantization waits only for x while the weight bytes are in flight.  Both unconditional
+        // (a wave without an item loads the last one's), so no wait merges paths.
+        const int item = b + wave * L.ngu;                  // ngu * nw >= items: one item per wave at most
+        float4 xv[2];
+        mlp_xload<2, false>(xv, L.x, wave, nw, K, lane);
+        constexpr bool ONE = GP >= 3;
+        RawPart<FMT, H> ca[GP], cb[ONE ? 1 : GP];
+        ld(ca, min(item, nitems - 1), 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (wave < NP) quant_passes<FMT, 2, 1>(xv, wave, nw, K, NP, 1, NGQ, U, lane, xq, asc, xsum);
+        for (int p0 = wave + 2 * nw; p0 < NP; p0 += 2 * nw) {
+            mlp_xload<2, false>(xv, L.x, p0, nw, K, lane);
+            quant_passes<FMT, 2, 1>(xv, p0, nw, K, NP, 1, NGQ, U, lane, xq, asc, xsum);
         }
         __syncthreads();
-        if (threadIdx.x < TRG) {
-            const int row = tile * BGL_TILE + r0 + threadIdx.x;
-            if (row < T.N) {
-                const float g = mlp_fold<TRG>(tl + threadIdx.x, U), u = mlp_fold<TRG>(tl + U * TRG + threadIdx.x, U);
+        const __amdgpu_buffer_rsrc_t HB = mlp_rsrc(L.hb, 2 * T.N);
+        if (item < nitems) {
+            if constexpr (ONE) {
+                em(ca, 0);
+            } else {
+                for (int g = 0;; g++) {
+                    if (g + 1 >= NG) {
+                        em(ca, g);
+                        break;
+                    }
+                    ld(cb, item, g + 1);
+                    em(ca, g);
+#pragma unroll
+                    for (int i = 0; i < GP; i++) ca[i] = cb[i];
+                }
+            }
+            // the terms were written by this wave's lanes: LDS operations of a wave are in order
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int row = item * TRI + lane;
+            if (lane < TRI && row < T.N) {
+                const float g = mlp_fold<TRI>(tw + lane, U), u = mlp_fold<TRI>(tw + U * TRI + lane, U);
                 const float hv = mlp_swiglu(g, u);
                 // the value into this launch's buffer, the sentinel back into the other one's row
-                const __amdgpu_buffer_rsrc_t HB = mlp_rsrc(L.hb, 2 * T.N);
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(hv), HB, ((gen & 1u) * T.N + row) * 4, 0, MLP_SC1);
                 __builtin_amdgcn_raw_buffer_store_b32(MLP_EMPTY, HB, ((~gen & 1u) * T.N + row) * 4, 0, MLP_SC1);
                 if (L.hout) L.hout[row] = hv;
             }
         }
+        __syncthreads();                                       // every wave has read gen
         if (threadIdx.x == 0) L.gen_gu[b] = (int)(gen + 1u);   // read by this workgroup's next launch only
         return;
     }
@@ -215,79 +241,59 @@ __global__ __launch_bounds__(MAXW * BGL_TILE) void k_mlp_q(MlpQLaunch L) {
     int *xsum = reinterpret_cast<int *>(asc + NGQ + 1);
     float *tl = reinterpret_cast<float *>(xsum + K / 64 + 1);
     const int r = lane % TRD, j = lane / TRD, kq = j / H, hh = j % H, rr = r0 + r;
-    // every wave takes part in the wait below (its barrier); waves past nwl hold no units
-    __shared__ int wait_polls;
     const unsigned gen = (unsigned)L.gen_d[d];                   // this shape's launches so far
     const float *hc = L.hb + (size_t)(gen & 1u) * K;
-    {
-        // every weight unit of this wave, before anything depends on h
+    if (wave < nwl) {
+        // First `delay` (about the time the gate+up weights take to stream), so that the gate+up
+        // role's x and weights are not queued behind these, then every weight unit of this wave,
+        // before anything depends on h.
+        if (L.delay > 0) {
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            while (__builtin_amdgcn_s_memrealtime() - t0 < (uint64_t)L.delay) __builtin_amdgcn_s_sleep(8);
+        }
         RawPart<FMT, H> cw[NIT];
-        if (wave < nwl) {
 #pragma unroll
-            for (int it = 0; it < NIT; it++) load_part<FMT, H>(cw[it], T, tile, rr, min((it * nwl + wave) * UPI + kq, U - 1), hh);
-        }
-        // wait (bounded) until h is written.  Wave 0 alone polls (the other waves wait at the
-        // barrier), cheaply: the last row of 64 gate+up workgroups spread over all of them (the
-        // highest id included; 64 different cache lines, so no line is a hot spot), two polls in
-        // flight.  A sampled row does not vouch for the unsampled workgroups, nor for its own
-        // workgroup's other rows (separate stores), so every wave then loads its groups and checks
-        // that no sentinel is left, reloading while one is.
-        int s = 0;
-        if (wave == 0) {
-            const __amdgpu_buffer_rsrc_t HC = mlp_rsrc(hc, K);
-            constexpr int SUBSG = BGL_TILE / TRG;
-            const int pb = (int)(((long)(lane + 1) * L.ngu) / 64) - 1;          // workgroup sampled by this lane
-            const int prow = pb < 0 ? 0 : (pb / SUBSG) * BGL_TILE + (pb % SUBSG) * TRG + TRG - 1;
-            bool ok = false;
-            uint32_t prev = __builtin_amdgcn_raw_buffer_load_b32(HC, prow * 4, 0, MLP_SC1);
-            for (; s < L.spin && !ok; s++) {
-                __builtin_amdgcn_s_sleep(4);
-                const uint32_t next = __builtin_amdgcn_raw_buffer_load_b32(HC, prow * 4, 0, MLP_SC1);
-                ok = __builtin_amdgcn_ballot_w64(pb >= 0 && prev == MLP_EMPTY) == 0 && !L.never;
-                prev = next;
-            }
-            if (lane == 0) wait_polls = s;
-        }
-        __syncthreads();
-        s = wait_polls;
-        bool ok = s < L.spin;
-        if (wave < nwl) {
-        // the wave's passes of h in one round (again while a sentinel is left), then their codes into LDS
-        float4 hv[NIT][PPI];
-        for (;;) {
-#pragma unroll
-            for (int it = 0; it < NIT; it++) mlp_xload<PPI, true>(hv[it], hc, (it * nwl + wave) * PPI, 1, K, lane);
-            bool fill = false;
-#pragma unroll
-            for (int it = 0; it < NIT; it++)
-#pragma unroll
-                for (int k = 0; k < PPI; k++)
-                    if (it * nwl + wave < UIT && (it * nwl + wave) * PPI + k < NP)
-                        fill |= __float_as_uint(hv[it][k].x) == MLP_EMPTY || __float_as_uint(hv[it][k].y) == MLP_EMPTY ||
-                                __float_as_uint(hv[it][k].z) == MLP_EMPTY || __float_as_uint(hv[it][k].w) == MLP_EMPTY;
-            if (__builtin_amdgcn_ballot_w64(fill) == 0 && ok) break;
-            if (++s >= L.spin) {
-                ok = false;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-        if (!ok && lane == 0) __hip_atomic_store(L.flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int it = 0; it < NIT; it++) load_part<FMT, H>(cw[it], T, tile, rr, min((it * nwl + wave) * UPI + kq, U - 1), hh);
+        // The wave's passes of h, loaded again while any is incomplete (a sentinel left): an
+        // iteration's PPI passes are quantized into LDS and its dot products run as soon as all of
+        // them are complete, so once the last gate+up rows land only their iteration remains.  The
+        // wait is bounded: after `spin` rounds one more round runs with whatever h holds and the
+        // flag is set.  ipend: iterations still to do (wave-uniform).
+        uint32_t ipend = 0u;
 #pragma unroll
         for (int it = 0; it < NIT; it++)
-            if (it * nwl + wave < UIT) quant_passes<FMT, PPI, 1>(hv[it], (it * nwl + wave) * PPI, 1, K, NP, 1, NGQ, U, lane, xq, asc, xsum);
-        // the codes this wave reads were written by this wave: LDS operations of a wave are in order
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (it * nwl + wave < UIT) ipend |= 1u << it;
+        bool ok = true;
+        for (int s = 0;;) {
 #pragma unroll
-        for (int it = 0; it < NIT; it++) {
-            const int u = (it * nwl + wave) * UPI + kq;
-            int p = unit_part<FMT, H>(cw[it], xq, min(u, U - 1), hh);
-            p += __shfl_xor(p, TRD);
-            if (hh == 0 && u < U) tl[u * TRD + r] = unit_float<FMT>(p, cw[it].s, T.gmul, asc, xsum, u);
+            for (int it = 0; it < NIT; it++) {
+                if (!(ipend >> it & 1u)) continue;
+                const int p0 = (it * nwl + wave) * PPI;
+                float4 hv[PPI];
+                mlp_xload<PPI, true>(hv, hc, p0, 1, K, lane);
+                bool e = false;
+#pragma unroll
+                for (int k = 0; k < PPI; k++)
+                    if (p0 + k < NP)
+                        e |= __float_as_uint(hv[k].x) == MLP_EMPTY || __float_as_uint(hv[k].y) == MLP_EMPTY ||
+                             __float_as_uint(hv[k].z) == MLP_EMPTY || __float_as_uint(hv[k].w) == MLP_EMPTY;
+                if ((__builtin_amdgcn_ballot_w64(e) != 0 || L.never) && ok) continue;
+                quant_passes<FMT, PPI, 1>(hv, p0, 1, K, NP, 1, NGQ, U, lane, xq, asc, xsum);
+                // the codes this wave reads were written by this wave: LDS operations of a wave are in order
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int u = (it * nwl + wave) * UPI + kq;
+                int p = unit_part<FMT, H>(cw[it], xq, min(u, U - 1), hh);
+                p += __shfl_xor(p, TRD);
+                if (hh == 0 && u < U) tl[u * TRD + r] = unit_float<FMT>(p, cw[it].s, T.gmul, asc, xsum, u);
+                ipend &= ~(1u << it);
+            }
+            if (ipend == 0u) break;
+            if (++s >= L.spin) ok = false;
+            else __builtin_amdgcn_s_sleep(2);
         }
-        }
+        if (!ok && lane == 0) __hip_atomic_store(L.flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (threadIdx.x < TRD) {
@@ -303,61 +309,55 @@ static size_t mlp_role_lds(int fmt, int K, int U, int nterm, int TR) {
     return (size_t)(U + 1) * (ELEMS + 16) + 4 * (size_t)(K / GQ + 1) + 4 * (size_t)(K / 64 + 1) + 4 * (size_t)nterm * TR;
 }
 
-template <int FMT, int TRG>
+template <int FMT, int GP>
 static int mlp_launch_nit(int NIT, const MlpQLaunch &L, dim3 g, dim3 b, size_t lds, hipStream_t st) {
     switch (NIT) {
-    case 1: hipLaunchKernelGGL((k_mlp_q<FMT, TRG, 1>), g, b, lds, st, L); return 0;
-    case 2: hipLaunchKernelGGL((k_mlp_q<FMT, TRG, 2>), g, b, lds, st, L); return 0;
+    case 1: hipLaunchKernelGGL((k_mlp_q<FMT, GP, 1>), g, b, lds, st, L); return 0;
+    case 2: hipLaunchKernelGGL((k_mlp_q<FMT, GP, 2>), g, b, lds, st, L); return 0;
     default: break;
     }
     if constexpr (FMT != BGL_Q4G256SF) {              // one pass per iteration: up to 8 iterations
         switch (NIT) {
-        case 4: hipLaunchKernelGGL((k_mlp_q<FMT, TRG, 4>), g, b, lds, st, L); return 0;
-        case 8: hipLaunchKernelGGL((k_mlp_q<FMT, TRG, 8>), g, b, lds, st, L); return 0;
+        case 4: hipLaunchKernelGGL((k_mlp_q<FMT, GP, 4>), g, b, lds, st, L); return 0;
+        case 8: hipLaunchKernelGGL((k_mlp_q<FMT, GP, 8>), g, b, lds, st, L); return 0;
         default: break;
         }
     }
     return -1;
 }
 
-template <int FMT>
-static int mlp_launch_trg(int TRG, int NIT, const MlpQLaunch &L, dim3 g, dim3 b, size_t lds, hipStream_t st) {
-    switch (TRG) {
-    case 16: return mlp_launch_nit<FMT, 16>(NIT, L, g, b, lds, st);
-    case 32: return mlp_launch_nit<FMT, 32>(NIT, L, g, b, lds, st);
-    default: return -1;
-    }
-}
-
-// The launch shape of one MLP: rows of gate / up per workgroup, waves per workgroup (the fewest
-// from 6 up that keep every down wave at <= MLP_MAXQ passes of h), wave iterations per down wave
-// (the instantiated 1, 2, 4 or 8 >= what the shape needs) and the workgroup counts.  False if
-// the shape cannot run in one launch.
+// The launch shape of one MLP: waves per workgroup (the fewest from 6 up that keep every down wave
+// at <= MLP_MAXQ passes of h), wave iterations per down wave (the instantiated 1, 2, 4 or 8 >= what
+// the shape needs), the gate+up workgroups (one 8-row item per wave: Qwen2.5-1.5B's 1120 items in
+// 187 workgroups of 6 waves) and the down workgroups (8 rows each).  False if the shape cannot run
+// in one launch.
 struct MlpShape {
-    int TRG, nw, NIT, ngu, nd;
+    int nw, NIT, ngu, nd;
 };
 static bool mlp_shape(bgl_ctx *c, const BglDevTensor &gate, const BglDevTensor &down, MlpShape &s) {
     const int ppi = gate.fmt == BGL_Q4G256SF ? 4 : 1;
     const int U = down.nunits, UIT = (U + 3) / 4;
-    // 32 rows of gate and of up per workgroup from 128 row tiles (Qwen2.5-1.5B's 140: 280 workgroups,
-    // 12.7 against 13.1-15 us per block with 16 rows), else 16
-    s.TRG = c->mlp_trg ? c->mlp_trg : gate.ntiles >= 128 ? 32 : 16;
-    s.ngu = gate.ntiles * (BGL_TILE / s.TRG);
+    const int nitems = (gate.N + MLP_TRD - 1) / MLP_TRD;
     s.nd = down.ntiles * (BGL_TILE / MLP_TRD);
-    // the fewest waves from 6 up (more waves per workgroup cost the gate+up role time and keep the
-    // two roles from all being resident at once)
     int nw0 = c->mlp_waves ? c->mlp_waves : 6;
-    for (int nw = nw0; nw <= 16; nw++) {
+    for (int nw = nw0; nw <= MLP_MAXW; nw++) {
         const int nwl = std::min(nw, UIT), nit = (UIT + nwl - 1) / nwl;
         const int NIT = nit <= 1 ? 1 : nit <= 2 ? 2 : nit <= 4 ? 4 : 8;
         if (nit <= NIT && NIT * ppi <= MLP_MAXQ) {      // every wave iteration covered, <= MLP_MAXQ passes
             s.nw = nw;
             s.NIT = NIT;
+            s.ngu = std::max(c->mlp_gu, (nitems + nw - 1) / nw);
             return nw <= c->max_waves;
         }
         if (c->mlp_waves) break;
     }
     return false;
+}
+
+// LDS of the single-launch kernel: the larger of the two roles'
+static size_t mlp_lds(const BglDevTensor &gate, const BglDevTensor &down, const MlpShape &s) {
+    return std::max(mlp_role_lds(gate.fmt, gate.K, gate.nunits, 2 * gate.nunits, MLP_TRD * s.nw),
+                    mlp_role_lds(down.fmt, down.K, down.nunits, down.nunits, MLP_TRD));
 }
 
 bool mlp_q_ok(bgl_ctx *c, const BglDevTensor &g, const BglDevTensor &u, const BglDevTensor &d) {
@@ -367,8 +367,7 @@ bool mlp_q_ok(bgl_ctx *c, const BglDevTensor &g, const BglDevTensor &u, const Bg
     if (g.K % 256 || d.K % 256) return false;              // whole 256-value groups of x and of h
     MlpShape s;
     if (!mlp_shape(c, g, d, s)) return false;
-    const size_t lds = std::max(mlp_role_lds(f, g.K, g.nunits, 2 * g.nunits, s.TRG), mlp_role_lds(f, d.K, d.nunits, d.nunits, MLP_TRD));
-    return lds <= 65536;
+    return mlp_lds(g, d, s) <= 65536;
 }
 
 // One column through the single-launch block.  Shapes as bgl_mlp_dev checked them, and mlp_q_ok.
@@ -400,19 +399,29 @@ int run_mlp_q(bgl_ctx *c, const BglDevTensor &gate, const BglDevTensor &up, cons
     L.never = c->mlp_test_timeout > 0 ? 1 : 0;                  // a test's launch whose wait must give up
     if (c->mlp_test_timeout > 0) c->mlp_test_timeout--;
     L.spin = c->mlp_spin;
+    // the down waves' delay: the time the gate+up weight bytes take at 5 TB/s, about what a
+    // streaming read sustains here (5000 bytes per ns; Qwen2.5-1.5B: 14.6 MB, 2.9 us: 10.9 us per
+    // block against 12.7 at 2.0 us and 11.3 at 3.5 us), in 10 ns ticks
+    const long gu_bytes = (long)2 * gate.ntiles * BGL_TILE * gate.nunits * (long)(gate.fmt == BGL_Q4G256SF ? 136 : gate.fmt == BGL_Q4G64 ? 36 : 68);
+    L.delay = (c->mlp_delay >= 0 ? c->mlp_delay : (int)std::min(gu_bytes / 5000, 100000L)) / 10;
     const int fmt = gate.fmt;
-    const size_t lds = std::max(mlp_role_lds(fmt, gate.K, gate.nunits, 2 * gate.nunits, s.TRG),
-                                mlp_role_lds(fmt, down.K, down.nunits, down.nunits, MLP_TRD));
+    const size_t lds = mlp_lds(gate, down, s);
     const dim3 g(L.ngu + L.nd), b(s.nw * BGL_TILE);
     int tok = prof_begin(c, 1);
     int rc;
+    // unit iterations of a gate+up item loaded per group: all of them when they are <= 3 (g256sf at
+    // K <= 1536: Qwen2.5-1.5B's 12 units of gate+up), else 2 at a time, double-buffered
+    const int git = (2 * gate.nunits + 3) / 4;
     switch (fmt) {
-    case BGL_Q4G256SF: rc = mlp_launch_trg<BGL_Q4G256SF>(s.TRG, s.NIT, L, g, b, lds, c->stream); break;
-    case BGL_Q4G64: rc = mlp_launch_trg<BGL_Q4G64>(s.TRG, s.NIT, L, g, b, lds, c->stream); break;
-    default: rc = mlp_launch_trg<BGL_Q8G64>(s.TRG, s.NIT, L, g, b, lds, c->stream); break;
+    case BGL_Q4G256SF:
+        rc = git <= 3 ? mlp_launch_nit<BGL_Q4G256SF, 3>(s.NIT, L, g, b, lds, c->stream)
+                      : mlp_launch_nit<BGL_Q4G256SF, 2>(s.NIT, L, g, b, lds, c->stream);
+        break;
+    case BGL_Q4G64: rc = mlp_launch_nit<BGL_Q4G64, 2>(s.NIT, L, g, b, lds, c->stream); break;
+    default: rc = mlp_launch_nit<BGL_Q8G64, 2>(s.NIT, L, g, b, lds, c->stream); break;
     }
     prof_end(c, tok);
-    if (rc) return bgl_fail(BGL_E_UNSUPPORTED, "single-launch MLP: no kernel for TRG %d, %d iterations", s.TRG, s.NIT);
+    if (rc) return bgl_fail(BGL_E_UNSUPPORTED, "single-launch MLP: no kernel for %d iterations", s.NIT);
     HIPCHK(hipGetLastError());
     return 0;
 }

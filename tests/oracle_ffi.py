@@ -1,6 +1,7 @@
 """ctypes bindings for the CPU oracle (oracle/liboracle.so) and the reference build
 (oracle/_ref/libbeglin_ref.so).  Test infrastructure: only tests/, __graft_entry__.smoke()
 and bench.py's cpu_baseline leg use this module."""
+import concurrent.futures
 import ctypes as C
 import os
 
@@ -301,7 +302,24 @@ def moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w, naive=False):
     T, K = idx.shape
     out = np.zeros((T, H), np.float32)
     fn = oracle.lib.or_moe_ffn_naive if naive else oracle.lib.or_moe_ffn_bucketed
-    fn(ga, ua, da, E, sg, su, sd, H, I, Ish, T, K, _ptr(x), _ptr(idx), _ptr(w), _ptr(out))
+    # Every token's output depends on its own routing only (each adds its experts' terms in expert
+    # order, then the shared experts'), so token chunks run on threads (ctypes drops the GIL).
+    nth = max(1, min(16, os.cpu_count() or 1, T // 4))
+    bounds = [(T * i // nth, T * (i + 1) // nth) for i in range(nth)]
+
+    def run(b):
+        t0, t1 = b
+        if t1 > t0:
+            xs, ids, ws = x[t0:t1], idx[t0:t1], w[t0:t1]
+            o = np.zeros((t1 - t0, H), np.float32)
+            fn(ga, ua, da, E, sg, su, sd, H, I, Ish, t1 - t0, K, _ptr(xs), _ptr(ids), _ptr(ws), _ptr(o))
+            out[t0:t1] = o
+
+    if nth == 1:
+        run((0, T))
+    else:
+        with concurrent.futures.ThreadPoolExecutor(nth) as ex:
+            list(ex.map(run, bounds))
     return out
 
 
