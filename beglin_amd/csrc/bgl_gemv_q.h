@@ -226,17 +226,17 @@ __device__ __forceinline__ int unit_part(const RawPart<FMT, H> &r, const int8_t 
         int comb16 = 0;
 #pragma unroll
         for (int sg = 0; sg < CP / 2; sg++) {
-            int isum16 = 0;
+            int ia = 0, ib = 0;                        // two independent dot chains; exact int32 sums
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 const uint4 c = r.c[2 * sg + k];
                 const int4 xa = x4[sg * 4 + 2 * k], xb = x4[sg * 4 + 2 * k + 1];
-                isum16 = dot4(snib_lo16(c.x), xa.x, isum16); isum16 = dot4(snib_hi16(c.x), xa.y, isum16);
-                isum16 = dot4(snib_lo16(c.y), xa.z, isum16); isum16 = dot4(snib_hi16(c.y), xa.w, isum16);
-                isum16 = dot4(snib_lo16(c.z), xb.x, isum16); isum16 = dot4(snib_hi16(c.z), xb.y, isum16);
-                isum16 = dot4(snib_lo16(c.w), xb.z, isum16); isum16 = dot4(snib_hi16(c.w), xb.w, isum16);
+                ia = dot4(snib_lo16(c.x), xa.x, ia); ib = dot4(snib_hi16(c.x), xa.y, ib);
+                ia = dot4(snib_lo16(c.y), xa.z, ia); ib = dot4(snib_hi16(c.y), xa.w, ib);
+                ia = dot4(snib_lo16(c.z), xb.x, ia); ib = dot4(snib_hi16(c.z), xb.y, ib);
+                ia = dot4(snib_lo16(c.w), xb.z, ia); ib = dot4(snib_hi16(c.w), xb.w, ib);
             }
-            comb16 += isum16 * (int)((r.sub >> (8 * sg)) & 255u);
+            comb16 += (ia + ib) * (int)((r.sub >> (8 * sg)) & 255u);
         }
         return comb16;
     } else if constexpr (FMT == BGL_Q4G64) {

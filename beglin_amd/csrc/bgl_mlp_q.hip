@@ -107,11 +107,15 @@ __device__ __forceinline__ float mlp_fold(const float *tr, int U) {
         for (int i = 0; i < 16; i++) t[i] = n[i];
     }
     const int R = U - U16;
+    // the tail: every load unconditional (clamped to a real term), the adds selected, so no
+    // branch per term
 #pragma unroll
-    for (int i = 0; i < 16; i++) t[i] = i < R ? tr[(U16 + i) * TR] : 0.0f;
+    for (int i = 0; i < 16; i++) t[i] = tr[max(U16 + min(i, R - 1), 0) * TR];
 #pragma unroll
-    for (int i = 0; i < 16; i++)
-        if (i < R) acc = __fadd_rn(acc, t[i]);
+    for (int i = 0; i < 16; i++) {
+        const float s = __fadd_rn(acc, t[i]);
+        acc = i < R ? s : acc;
+    }
     return acc;
 }
 
