@@ -13,7 +13,7 @@ LIB = os.path.join(HERE, "libbeglin_hip.so")
 # parallel; the longest units come first.
 SOURCES = [f"bgl_moe_x_i{i}.hip" for i in range(10)] + [
     "bgl_gemv.hip", "bgl_moe.hip", "bgl_mfma.hip", "bgl_gemv_x.hip", "bgl_api.hip", "bgl_prep.hip", "bgl_moe_x.hip",
-    "bgl_registry.hip", "bgl_loader.hip", "bgl_mlp.hip", "bgl_mlp_q.hip"]
+    "bgl_registry.hip", "bgl_loader.hip", "bgl_mlp.hip", "bgl_mlp_q.hip", "bgl_gemv_qm.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",

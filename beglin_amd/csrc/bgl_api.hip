@@ -186,6 +186,13 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     const char *mdl = getenv("BGL_MLP_DELAY");
     c->mlp_delay = mdl ? atoi(mdl) : -1;
     if (c->mlp_delay < -1 || c->mlp_delay > 100000) c->mlp_delay = -1;
+    const char *nqm = getenv("BGL_NO_QMFMA");
+    c->no_qmfma = nqm && atoi(nqm) != 0;
+    const char *qrb = getenv("BGL_QM_RB");
+    c->qm_rb = qrb ? atoi(qrb) : 0;
+    const char *qs = getenv("BGL_QM_S");
+    c->qm_s = qs ? atoi(qs) : 0;
+    if (c->qm_s < 0 || c->qm_s > 16) c->qm_s = 0;
     const char *mgu = getenv("BGL_MLP_GU");
     c->mlp_gu = mgu ? atoi(mgu) : 0;
     if (c->mlp_gu < 0 || c->mlp_gu > 4096) c->mlp_gu = 0;
@@ -849,9 +856,41 @@ static int q_mb_max(int kind, int K) {
 // W4A8 with the quantization fused in, M columns in launches of up to 8 -- fewer where the
 // columns' codes would not fit LDS (each launch streams the weights once for its columns; every
 // column's arithmetic is the one-column kernel's).
+// Launch shape of the matrix-core W4A8 kernel (k_gemv_qm): RB 16-row blocks and S unit slices per
+// workgroup.  With the columns quantized in the kernel, the row blocks of one tile share that work
+// (4 blocks while that still leaves >= 256 workgroups) and 8 waves split it; with prepared codes a
+// workgroup is one block with up to 8 slices.
+static void qm_shape(bgl_ctx *c, int nrb, int U, bool prep, int &RB, int &S) {
+    RB = prep ? 1 : (nrb / 4 >= 256 ? 4 : nrb / 2 >= 256 ? 2 : 1);
+    S = prep ? std::min(U, 16) : RB == 1 ? 12 : 8 / RB;
+    if (prep) return;
+    if (c->qm_rb == 1 || c->qm_rb == 2 || c->qm_rb == 4) RB = c->qm_rb;
+    if (c->qm_s > 0) S = std::min(c->qm_s, 16 / RB);
+}
+
+#define QM_MIN_COLS 5
+
+static bool qm_ok(bgl_ctx *c, int kind, int K) {
+    if (c->no_qmfma) return false;
+    if (kind == BGL_Q4G256SF) return K % 256 == 0;
+    return (kind == BGL_Q4G64 || kind == BGL_Q8G64) && K % 64 == 0;
+}
+
 static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev, int M, const float *const *bias,
                       float *const *y) {
-    const int mbmax = q_mb_max(Ts[0].fmt, Ts[0].K);
+    // 5..16 columns: the matrix-core kernel (one MFMA column per activation column), where its
+    // terms (and, quantizing in the kernel, the columns' codes) fit LDS.  (Qwen2.5-1.5B g256sf cfg2
+    // step: 8 columns 1.239 -> 1.115 ms; at 4 columns the dot4 kernel stays ahead, 0.957 against
+    // 0.983 ms.)
+    bool qm = M >= QM_MIN_COLS && qm_ok(c, Ts[0].fmt, Ts[0].K);
+    if (qm) {
+        const int pass16 = std::min(M, 16) * ((Ts[0].K + 255) / 256);
+        const bool p16 = c->q_prep == 1 || (c->q_prep < 0 && pass16 >= BGL_Q_PREP_MIN_PASSES);
+        const bool fit_nq = bgl_gemv_qm_lds(Ts[0].fmt, Ts[0].K, std::min(M, 16), 1, false) <= BGL_GEMV_Q_LDS_MAX;
+        qm = bgl_gemv_qm_lds(Ts[0].fmt, Ts[0].K, std::min(M, 16), 1, true) <= BGL_GEMV_Q_LDS_MAX && (p16 || fit_nq || c->q_prep != 0);
+    }
+    const int mbq = q_mb_max(Ts[0].fmt, Ts[0].K);            // columns per dot4 launch
+    const int mbmax = qm ? 16 : mbq;
     // Several columns over a long K: one k_act_w4a8 launch quantizes them all (the same codes)
     // instead of every workgroup quantizing every column of its launch.  (Measured on Qwen2.5-1.5B
     // g256sf: the down projection, 4 x 35 and 8 x 35 passes per workgroup, 10.95 -> 9.57 and
@@ -859,20 +898,43 @@ static int run_gemv_q(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_
     GemvAct A;
     memset(&A, 0, sizeof A);
     const int passes = std::min(M, mbmax) * ((Ts[0].K + 255) / 256);
-    const bool prep = M > 1 && (c->q_prep == 1 || (c->q_prep < 0 && passes >= BGL_Q_PREP_MIN_PASSES));
+    bool prep = M > 1 && (c->q_prep == 1 || (c->q_prep < 0 && passes >= BGL_Q_PREP_MIN_PASSES));
+    if (qm && !prep && bgl_gemv_qm_lds(Ts[0].fmt, Ts[0].K, std::min(M, 16), 1, false) > BGL_GEMV_Q_LDS_MAX) prep = true;
     if (prep) {
         int rc = prep_act(c, BGL_ACT_W4A8, act_group(Ts[0].fmt), x_dev, M, Ts[0].K, A);
         if (rc) return rc;
     }
-    for (int m0 = 0; m0 < M; m0 += mbmax) {
-        const int mc = std::min(mbmax, M - m0), MB = q_mb(mc);
+    for (int m0 = 0; m0 < M;) {
+        const bool qml = qm && M - m0 >= QM_MIN_COLS;
+        const int mc = std::min(qml ? 16 : mbq, M - m0), MB = q_mb(mc);
+        m0 += mc;
+        if (qml) {
+            GemvLaunch L;
+            memset(&L, 0, sizeof L);
+            int blocks = 0;
+            fill_tasks(L, n, Ts, bias, y, nullptr, blocks);
+            L.x = c->prep_h ? c->prep_h : x_dev;
+            if (prep) L.a = A;
+            L.m0 = m0 - mc;
+            L.mcols = mc;
+            int RB, S;
+            qm_shape(c, blocks * 4, Ts[0].nunits, prep, RB, S);
+            while (RB > 1 && bgl_gemv_qm_lds(Ts[0].fmt, Ts[0].K, mc, RB, prep) > BGL_GEMV_Q_LDS_MAX) RB >>= 1;
+            for (int i = 0; i < n; i++) L.t[i].blk0 *= 4 / RB;
+            int tok = prof_begin(c, 1);
+            int rc = bgl_launch_gemv_qm(L, blocks * (4 / RB), RB, S, prep, c->stream);
+            prof_end(c, tok);
+            if (rc) return bgl_fail(BGL_E_UNSUPPORTED, "matrix-core W4A8 path: kind %d", Ts[0].fmt);
+            HIPCHK(hipGetLastError());
+            continue;
+        }
         GemvLaunch L;
         memset(&L, 0, sizeof L);
         int blocks = 0;
         fill_tasks(L, n, Ts, bias, y, nullptr, blocks);
         L.x = c->prep_h ? c->prep_h : x_dev;     // a SwiGLU column: h, which the prep launch wrote
         if (prep && MB > 1) L.a = A;
-        L.m0 = m0;
+        L.m0 = m0 - mc;
         L.mcols = mc;
         // Rows per workgroup: split 64-row tiles until the launch has >= 512 workgroups (8 rows at
         // the least), so the weight stream is spread over every CU.  Waves: ceil(passes / 4), at

@@ -51,6 +51,8 @@ struct bgl_ctx {
     DevBuf moe_scores;                    // router scores [T][E]
     DevBuf mlp;                           // bgl_mlp_dev: gate and up outputs [M][I] each, then h [M][I]
     std::unordered_map<uint64_t, DevBuf> mlp_sync;   // single-launch MLP, per shape (in << 32 | down workgroups): counters, generations, flag
+    bool no_qmfma = false;                // BGL_NO_QMFMA=1: W4A8 at 2..16 columns through the dot4 kernel (k_gemv_q)
+    int qm_rb = 0, qm_s = 0;              // BGL_QM_RB / BGL_QM_S: k_gemv_qm row blocks / unit slices per workgroup (tuning; 0 by shape)
     int mlp_gu = 0;                       // BGL_MLP_GU: gate+up workgroups of the single-launch MLP (tuning; 0 by shape)
     bool no_fused_mlp = false;            // BGL_NO_FUSED_MLP=1: the MLP block as three launches at every M
     int mlp_spin = 1 << 20;               // BGL_MLP_SPIN: polls of the single-launch MLP's bounded wait

@@ -228,6 +228,10 @@ __global__ void k_splitk_reduce(const float *part, int ks, int M, int N, const f
 // ---- host-side launchers (bgl_gemv.hip) ----
 int bgl_launch_gemv(int act, int MB, const GemvLaunch &L, int nblocks, int nw, hipStream_t st);
 int bgl_launch_gemv_q(const GemvLaunch &L, int ntiles, int TR, int nw, int MB, hipStream_t st);
+// bgl_gemv_qm.hip: W4A8 at 2..16 columns on the matrix cores; nblk workgroups of RB 16-row blocks
+// and S unit slices; prep: L.a holds prepared codes
+int bgl_launch_gemv_qm(const GemvLaunch &L, int nblk, int RB, int S, bool prep, hipStream_t st);
+size_t bgl_gemv_qm_lds(int fmt, int K, int MC, int RB, bool prep);
 size_t bgl_gemv_q_lds(int fmt, int K, int TR, int MB);
 // ---- bgl_gemv_x.hip: one-column fp32-activation GEMV over prepared digits ----
 int bgl_launch_gemv_x(const GemvLaunch &L, bool fuse, int nblocks, int TR, int nw, hipStream_t st);
