@@ -52,7 +52,7 @@
 #define BGL_XF_NF 2            //              the group holds a non-finite element
 #define BGL_X_FRAC 22          // level-0 / level-1 fixed point: X = rint(x * 2^(BGL_X_FRAC - e))
 #define BGL_X_SPIKE_BITS 6     // "small": a nonzero |x| below 2^(e-6)
-#define BGL_X_SMALL_MAX 8      // level 1 from this many small elements (or more small than large)
+#define BGL_X_SMALL_MAX 22     // level 1 from this many small elements (or more small than large)
 
 // The level-1 trigger from a group's count of small (nonzero, below 2^(e-6)) and large elements.
 __host__ __device__ __forceinline__ bool bgl_x_level1(int nsmall, int nlarge) {
