@@ -139,14 +139,16 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
                 int f2 = 0;
                 for (int m = 0; m < mcg; m++) f2 |= rec[m * RC + XREC_DSUM + 3];
                 if (!__builtin_amdgcn_ballot_w64(f2 != 0)) continue;
+                // the item's weights once for all its flagged columns, loaded first so their latency
+                // runs under the first column's level-1 records
+                XRaw<FMT, NB> rf;
+                x_load<FMT, NB, KQ>(rf, up ? Rb : Ra, sl == S - 1 ? xlast : xlane, sl, true);
 #pragma unroll 1
                 for (int m = 0; m < mcg; m++) {
                     const int f3 = rec[m * RC + XREC_DSUM + 3];
                     if (!__builtin_amdgcn_ballot_w64(f3 != 0)) continue;
                     const int xrow_m = Mt.cols ? uni(Mt.cols)[base + cb + m] : base + cb + m;
                     const float *xr = Mt.a.xf + (size_t)xrow_m * K;
-                    // the column's level-1 records first, then the weights: the two never hold
-                    // registers at the same time
                     if (__builtin_amdgcn_ballot_w64(f3 & BGL_XF_L1)) {
                         __builtin_amdgcn_wave_barrier();      // the previous column's reads of scr are done
                         const int g0 = sl * KQ, g1 = min(g0 + KQ, G);
@@ -155,8 +157,6 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
                         __builtin_amdgcn_wave_barrier();
                         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                     }
-                    XRaw<FMT, NB> rf;
-                    x_load<FMT, NB, KQ>(rf, up ? Rb : Ra, sl == S - 1 ? xlast : xlane, sl, true);
                     const XRow xrow{up ? &Tb : &Ta, tile * BGL_TILE + r0 + r, xr};
                     const float v = x_fix<FMT, NB>(x_decode<FMT, NB>(rf), rec + m * RC, r1, *reinterpret_cast<const int4 *>(r1 + XREC_DSUM),
                                                    *reinterpret_cast<const int4 *>(r1 + XREC_DSUM + 4), xrow, gl);
