@@ -206,6 +206,16 @@ def wbytes(kind, out, inn, bits):
     return alg_bytes(kind, out, inn, bits, 0)
 
 
+def shared_on_matrix_cores(kind, bits, T):
+    """Whether bgl_moe_layer_dev runs the shared experts as a dense block on the matrix cores (the
+    library's rule, bgl_moe.hip `shm`: >= BGL_MFMA_MIN_M = 16 tokens, BGL_NO_MFMA unset, and a kind
+    bgl_mfma_ok accepts: Q4G64, Q4G32H, Q8G64, or qNg64 with 2 <= n <= MF_MAXN = 10)."""
+    import beglin_amd
+    if T < 16 or os.environ.get("BGL_NO_MFMA", "0") not in ("", "0"):
+        return False
+    return kind in (beglin_amd.K_Q4G64, beglin_amd.K_Q4G32H, beglin_amd.K_Q8G64) or (kind == beglin_amd.K_QNG64 and 2 <= bits <= 10)
+
+
 class MoeWorkload:
     """`layers` routed MoE layers, each run whole on the device (bgl_moe_layer_dev: router, sort,
     gate/up/SwiGLU, down, combine, shared experts); layer = (stacks, shared, idx, w, out, bytes
@@ -221,6 +231,7 @@ class MoeWorkload:
         self.layers = []
         self.formats = []
         self.probe_sets = []          # per layer: the single tensors each gather launch streams
+        self.shm = []                 # per layer: the shared experts run on the matrix cores (not in the gathers)
         for _ in range(layers):
             fm = [CFG4_FORMATS[i] for i in rng.integers(0, len(CFG4_FORMATS), E)]
             shf = CFG4_FORMATS[int(rng.integers(0, len(CFG4_FORMATS)))]
@@ -254,7 +265,8 @@ class MoeWorkload:
             # the gather launches' tensors: routed gate+up (+ the shared gate+up, in the same launch
             # below 16 tokens or where the shared experts stay in the gathers), routed down, shared down
             view = lambda hs: [beglin_amd.Tensor(hs[e]) for e in touched]
-            shm = T >= 16 and (shf[0] in (5, 2) or (shf[0] == 4 and shf[1] <= 10))
+            shm = shared_on_matrix_cores(shf[0], shf[1], T)
+            self.shm.append(shm)
             gu = view(handles[0]) + view(handles[1])
             sets = [gu, view(handles[2]), [sh[0], sh[1]], [sh[2]]] if shm else [gu + [sh[0], sh[1]], view(handles[2]), [sh[2]]]
             self.probe_sets.append(sets)
@@ -785,7 +797,8 @@ def main():
                               "step_over_plain": round(step_ms / pr_ms, 3),
                               "how": "bgl_read_probe_dev over the touched experts' and the shared experts' tensors of "
                                      "each gather launch (launches of up to 64 tensors), 1024 x 256 threads, graph-timed; "
-                                     "router weights and activations not read"}
+                                     "router weights and activations not read",
+                              "shared_on_matrix_cores_per_layer": [bool(v) for v in wl.shm]}
         cpu = None if args.no_cpu else cpu_baseline_cfg4(wl, args.cpu_seconds, args.seed)
         finish(args, wl, ctx, graph, value, step_ms, wall, dtype, cfg, per_call, roof, cpu)
         return
