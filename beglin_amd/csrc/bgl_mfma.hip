@@ -3,8 +3,8 @@
 //
 // Numerics.  Weight codes are exact in fp16 (int4 and int8 codes, qNg64 codes for n <= 10), so
 // the decode is exact.  Each activation column is scaled by a power of two so its largest
-// magnitude lies in [2^13, 2^14), then split as hi = fp16(x'), lo = fp16(x' - hi): hi + lo holds
-// x' to about 2^-22 of the column maximum.  v_mfma_f32_16x16x32_f16 multiplies exactly and
+// magnitude lies in [2^13, 2^14), then split as hi = fp16(x') and lo = fp16(x' - hi), both rounded
+// toward zero (x' - hi is exact in fp32): hi + lo holds x' to about 2^-21 of the column maximum.  v_mfma_f32_16x16x32_f16 multiplies exactly and
 // accumulates in fp32; each quantization group's partial sum is folded with its fp32 scale (one
 // FMA per output per group) and the column factor 2^-(14-e) is applied at the end.
 //
@@ -308,12 +308,12 @@ template <int FMT, int NB> constexpr int a_words() {
 // K-steps of weights a wave keeps in flight: a ring of depth/2 K-step pairs, Planes::WORDS
 // registers each.
 template <int FMT, int NB> constexpr int ring_depth() { return Planes<FMT, NB>::WORDS <= 4 ? 16 : Planes<FMT, NB>::WORDS <= 8 ? 8 : 4; }
-// LDS bytes per staged K-step: activation fragments (CT x hi/lo x 1 KB) + the 4 tiles' scale
-// words in the device layout (512 B for every format).
-constexpr int mf_step_lds(int CT) { return CT * 2048 + 512; }
-// K-steps one workgroup stages (its split's whole K range): as many as fit 144 KB, a multiple of
+// LDS bytes per staged K-step: activation fragments (CT x hi/lo x 1 KB, + 16 B of row padding) +
+// the 4 tiles' scale words in the device layout (512 B for every format).
+constexpr int mf_step_lds(int CT) { return CT * 2048 + 16 + 512; }
+// K-steps one workgroup stages (its split's whole K range): as many as fit 152 KB, a multiple of
 // 16 (every ring depth divides it).
-constexpr int mf_kps_max(int CT) { return (147456 / mf_step_lds(CT)) / 16 * 16; }
+constexpr int mf_kps_max(int CT) { return (155648 / mf_step_lds(CT)) / 16 * 16; }
 
 // Sum of code * scale * x over the non-finite x[k], k in [k0, k1), for weight row n (the rare path
 // of a column that holds NaN or +-Inf).
@@ -337,13 +337,14 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
     constexpr int SCW = scale_bytes<FMT>();
     constexpr int SPG = SPU / GPU;                                 // K-steps per scale group
     constexpr int BST = CT * 2 * 64;                               // activation uint4 per K-step
+    constexpr int XS = BST + 1;                                    // their row stride in the stage
     constexpr int UMAX = KPM / SPU;                                // staged units (max)
     constexpr int SUT = 64 * SCW / 16;                             // scale uint4 per tile and unit
     // ring depth: halved with two slices (each wave runs half the split, and 16 waves share the
     // registers); at least 4 so that a unit's groups keep their parity pattern
     constexpr int D = KW == 1 || ring_depth<FMT, NB>() == 4 ? ring_depth<FMT, NB>() : ring_depth<FMT, NB>() / 2;
     static_assert(KPM % D == 0 && KPM % SPU == 0 && D % SPU == 0, "staged range must hold whole rings and units");
-    __shared__ uint4 xs[KPM * BST];                                // [step][CT][hi/lo][64 lanes]
+    __shared__ uint4 xs[KPM * XS];                                 // [step][CT][hi/lo][64 lanes], rows XS apart
     __shared__ uint4 ss[MF_TILES * UMAX * SUT];                    // [tile][unit][64 rows] scale words
 
     const int ti = mf_task(L);
@@ -390,17 +391,28 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
             xv[ci][j][1] = make_float4(__uint_as_float(b[0]), __uint_as_float(b[1]), __uint_as_float(b[2]), __uint_as_float(b[3]));
         }
 
-    // ---- the 4 tiles' scales of the split: LDS (scale units past it are zeroed) ----
-    {
-        const int nsu = nu * SUT;                                  // scale uint4 per tile in this split
-        for (int e = threadIdx.x; e < MF_TILES * nsu; e += NT) {
-            const int st = e / nsu, rem = e % nsu, uu = rem / SUT;
-            const int tc = min(tile0 + st, T.ntiles - 1), uc = min(u0 + uu, T.nunits - 1);
-            const mf_u4 g = __builtin_amdgcn_raw_buffer_load_b128(
-                rsc, ((uint32_t)tc * T.nunits + uc) * (64 * SCW) + (uint32_t)(rem % SUT) * 16u, 0, 0);
-            ss[(st * UMAX + uu) * SUT + rem % SUT] = uu * SPU < ns ? make_uint4(g[0], g[1], g[2], g[3]) : make_uint4(0, 0, 0, 0);
-        }
-    }
+    // ---- the 4 tiles' scales of the split: loaded now (a fixed count per thread, clamped), put
+    // into LDS after the conversion below, so that nothing waits for them before the weights are
+    // requested ----
+    // (up to 32 columns, where that is one per thread; other shapes stage them here, before the
+    // weights, as holding them through the conversion made the compiler spill in their main loops)
+    constexpr int SLT = (MF_TILES * UMAX * SUT + NT - 1) / NT;     // scale uint4 per thread (max)
+    constexpr bool EARLY = SLT == 1 && CT <= 2;
+    const int nsu = nu * SUT;                                      // scale uint4 per tile in this split
+    auto scale_ld = [&](int e) -> mf_u4 {
+        e = min(e, MF_TILES * nsu - 1);                            // clamped: every load is real
+        const int st = e / nsu, rem = e % nsu, uu = rem / SUT;
+        const int tc = min(tile0 + st, T.ntiles - 1), uc = min(u0 + uu, T.nunits - 1);
+        return __builtin_amdgcn_raw_buffer_load_b128(rsc, ((uint32_t)tc * T.nunits + uc) * (64 * SCW) + (uint32_t)(rem % SUT) * 16u, 0, 0);
+    };
+    auto scale_st = [&](int e, const mf_u4 &g) {
+        const int st = e / nsu, rem = e % nsu, uu = rem / SUT;
+        ss[(st * UMAX + uu) * SUT + rem % SUT] = uu * SPU < ns ? make_uint4(g[0], g[1], g[2], g[3]) : make_uint4(0, 0, 0, 0);
+    };
+    mf_u4 sreg;
+    if constexpr (EARLY) sreg = scale_ld((int)threadIdx.x);
+    else
+        for (int e = threadIdx.x; e < MF_TILES * nsu; e += NT) scale_st(e, scale_ld(e));
 
     // ---- the weight ring: local K-step s lives in slot (s - ls0) % D until it is computed ----
     const int tile_c = min(tile, T.ntiles - 1);                    // waves past the tensor read a real tile
@@ -411,12 +423,15 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
         const int sc = min(s0 + s, KS - 2);                        // past the split: reread, multiplied by zeros
         ld_pair<FMT, NB>(slot, rw, ao, tchunk, sc);
     };
+    // the activation and scale loads go out first: the conversion below waits for them by the
+    // in-order load counter, which would also wait for any weight load issued before them
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d < D / 2; d++) load_w(ring[d], ls0 + 2 * d);
 
     // ---- activation fragments: each column is scaled by a power of two so its largest magnitude
-    // over the split lies in [2^13, 2^14), then split into hi = fp16(x'), lo = fp16(x' - hi) in the
-    // MFMA operand order; the split's column factor 2^(e-14) is applied to its partial sums ----
+    // over the split lies in [2^13, 2^14), then split into hi = fp16(x') and lo = fp16(x' - hi) in
+    // the MFMA operand order; the split's column factor 2^(e-14) is applied to its partial sums ----
     // Non-finite values (NaN, +-Inf) enter the fragments as 0 and flag the column; the store adds
     // their products code * scale * x one element at a time (IEEE propagation, as the reference's
     // fp32-product sums).
@@ -472,22 +487,29 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
             const bool ok = m < L.M && g < 4 * ns;
             const float4 a = xv[ci][j][0], b = xv[ci][j][1];
             const float v8[8] = {a.x, a.z, a.y, a.w, b.x, b.z, b.y, b.w};   // element order {0,2,1,3,4,6,5,7}
-            _Float16 hi[8], lo[8];
+            // hi = fp16(x') rounded toward zero, two at a time; x' - hi is exact in fp32 (hi is x'
+            // cut to 11 bits); lo = fp16 of that, toward zero
+            uint32_t H[4], Lo[4];
 #pragma unroll
-            for (int p = 0; p < 8; p++) {
-                const float v = ok ? v8[p] * sc : 0.0f;            // power-of-two scaling: exact
-                const _Float16 hh = (_Float16)v;
-                hi[p] = hh;
-                lo[p] = (_Float16)(v - (float)hh);
+            for (int k = 0; k < 4; k++) {
+                const float v0 = v8[2 * k] * sc, v1 = v8[2 * k + 1] * sc;   // power-of-two scaling: exact
+                const mf_h2 hh = __builtin_bit_cast(mf_h2, __builtin_amdgcn_cvt_pkrtz(v0, v1));
+                const float r0 = v0 - (float)hh[0], r1 = v1 - (float)hh[1];
+                const uint32_t hw = __builtin_bit_cast(uint32_t, hh);
+                const uint32_t lw = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+                H[k] = ok ? hw : 0u;                               // K-steps past the split: zero fragments
+                Lo[k] = ok ? lw : 0u;
             }
-            uint4 H, Lo;
-            memcpy(&H, hi, 16);
-            memcpy(&Lo, lo, 16);
-            uint4 *d = xs + ((g >> 2) * CT + ct) * 128 + ml + 16 * (g & 3);
-            d[0] = H;
-            d[64] = Lo;
+            // step rows are XS = BST + 1 uint4 apart: the lanes of one store hold 16 steps of one
+            // column, which then fall on 16 different bank groups instead of one
+            uint4 *d = xs + (g >> 2) * XS + ct * 128 + ml + 16 * (g & 3);
+            d[0] = make_uint4(H[0], H[1], H[2], H[3]);
+            d[64] = make_uint4(Lo[0], Lo[1], Lo[2], Lo[3]);
         }
     }
+    // the scales, into LDS (scale units past the split are zeroed)
+    if constexpr (EARLY)
+        if ((int)threadIdx.x < MF_TILES * nsu) scale_st((int)threadIdx.x, sreg);
     __syncthreads();
 
     mf_f4 acc[MF_RBW][CT];
@@ -529,7 +551,7 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
     // Activation fragments of local step s (clamped into the staged range).
     struct BF { mf_h8 h[CT], l[CT]; };
     auto load_b = [&](int s) -> BF {
-        const uint4 *p = xs + min(s, nsr - 1) * BST + lane;
+        const uint4 *p = xs + min(s, nsr - 1) * XS + lane;
         BF r;
 #pragma unroll
         for (int c = 0; c < CT; c++) {
@@ -757,14 +779,16 @@ bool bgl_mfma_ok(int fmt, int bits) {
 
 // Two K-slices (16 waves, <= 128 VGPRs) where that instance compiles without private memory --
 // which instances fit depends on the register allocator, so it is read from the code object --
-// else one slice (8 waves, <= 256 VGPRs).
+// else one slice (8 waves, <= 256 VGPRs), unless that one needs even more private memory.
 template <int FMT, int NB, int CT>
 static void launch_ct(const MfmaLaunch &L, dim3 grid, hipStream_t st) {
     static int kw2 = -1;
     if (kw2 < 0) {
-        hipFuncAttributes a;
-        kw2 = hipFuncGetAttributes(&a, reinterpret_cast<const void *>(&k_gemm_mfma<FMT, NB, CT, 2>)) == hipSuccess &&
-              a.localSizeBytes == 0;
+        hipFuncAttributes a2, a1;
+        const bool ok2 = hipFuncGetAttributes(&a2, reinterpret_cast<const void *>(&k_gemm_mfma<FMT, NB, CT, 2>)) == hipSuccess;
+        const bool ok1 = hipFuncGetAttributes(&a1, reinterpret_cast<const void *>(&k_gemm_mfma<FMT, NB, CT, 1>)) == hipSuccess;
+        // two slices unless they need private memory and one slice needs less
+        kw2 = ok2 && (a2.localSizeBytes == 0 || !ok1 || a2.localSizeBytes <= a1.localSizeBytes);
     }
     if (kw2) hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, CT, 2>), grid, dim3(MF_WAVES * 2 * 64), 0, st, L);
     else hipLaunchKernelGGL((k_gemm_mfma<FMT, NB, CT, 1>), grid, dim3(MF_WAVES * 64), 0, st, L);

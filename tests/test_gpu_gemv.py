@@ -485,6 +485,41 @@ def test_w4a8_batched_prep_equals_fused(torch_dev, oracle, monkeypatch, kind):
             assert np.array_equal(outs[1].view(np.uint32), ref.view(np.uint32)), (inn, M)
 
 
+@pytest.mark.parametrize("kind,inn", [(1, 1536), (2, 1024), (3, 1536), (3, 8960), (1, 8960)])
+def test_w4a8_matrix_cores_equal_dot4(torch_dev, oracle, monkeypatch, kind, inn):
+    """W4A8 at 5..16 columns on the matrix cores (k_gemv_qm) against the dot4 kernel
+    (BGL_NO_QMFMA=1) and the oracle, bit for bit: column counts that fill one launch, leave a
+    partial one, and leave a 1-4 column remainder for the dot4 kernel (17, 21); a fused group of two
+    tensors with biases; columns quantized in the kernel and up front (BGL_Q_PREP=1)."""
+    import beglin_amd
+    torch = torch_dev
+    outs_n = (200, 72)
+    ws = [weights(1400 + kind + inn + j, o, inn) for j, o in enumerate(outs_n)]
+    refq = [ref_quant(oracle, kind, w, 0) for w in ws]
+    biases = [seeded_normal(1410 + j, (o,)) for j, o in enumerate(outs_n)]
+    for M in (5, 8, 16, 17, 21):
+        say("w4a8 matrix cores", kind, inn, M)
+        x = seeded_normal(1420 + M, (M, inn))
+        refs = [oracle.matmul_sdot(kind, pk, sc, x, bias=bias, sub=sub) for (pk, sc, sub), bias in zip(refq, biases)]
+        for flags in ({}, {"BGL_Q_PREP": "1"}, {"BGL_NO_QMFMA": "1"}):
+            for k in ("BGL_Q_PREP", "BGL_NO_QMFMA"):
+                monkeypatch.delenv(k, raising=False)
+            for k, v in flags.items():
+                monkeypatch.setenv(k, v)
+            c = beglin_amd.Context(0)
+            ts = [c.bind(kind, pk, sc, o, inn, sub=sub) for (pk, sc, sub), o in zip(refq, outs_n)]
+            ys = [torch.full((M, o), float("nan"), dtype=torch.float32, device="cuda") for o in outs_n]
+            c.matmul_group(ts, torch.from_numpy(x).cuda(), ys, act=beglin_amd.ACT_W4A8,
+                           biases=[torch.from_numpy(b).cuda() for b in biases])
+            torch.cuda.synchronize()
+            for y, ref in zip(ys, refs):
+                got = y.cpu().numpy()
+                assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (kind, inn, M, flags, relerr(got, ref))
+            for t in ts:
+                t.free()
+            c.close()
+
+
 @pytest.mark.parametrize("M", [1, 3, 8, 13])
 @pytest.mark.parametrize("inn", [512, 8960])
 def test_g256plain_w4a8_bitexact(ctx, torch_dev, oracle, inn, M):
