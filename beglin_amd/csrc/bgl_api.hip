@@ -193,6 +193,11 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     const char *qs = getenv("BGL_QM_S");
     c->qm_s = qs ? atoi(qs) : 0;
     if (c->qm_s < 0 || c->qm_s > 16) c->qm_s = 0;
+    const char *qprb = getenv("BGL_QM_PRB");
+    c->qm_prb = qprb ? atoi(qprb) : 0;
+    const char *qps = getenv("BGL_QM_PS");
+    c->qm_ps = qps ? atoi(qps) : 0;
+    if (c->qm_ps < 0 || c->qm_ps > 16) c->qm_ps = 0;
     const char *mgu = getenv("BGL_MLP_GU");
     c->mlp_gu = mgu ? atoi(mgu) : 0;
     if (c->mlp_gu < 0 || c->mlp_gu > 4096) c->mlp_gu = 0;
@@ -863,9 +868,9 @@ static int q_mb_max(int kind, int K) {
 static void qm_shape(bgl_ctx *c, int nrb, int U, bool prep, int &RB, int &S) {
     RB = prep ? 1 : (nrb / 4 >= 256 ? 4 : nrb / 2 >= 256 ? 2 : 1);
     S = prep ? std::min(U, 16) : RB == 1 ? 12 : 8 / RB;
-    if (prep) return;
-    if (c->qm_rb == 1 || c->qm_rb == 2 || c->qm_rb == 4) RB = c->qm_rb;
-    if (c->qm_s > 0) S = std::min(c->qm_s, 16 / RB);
+    const int rb = prep ? c->qm_prb : c->qm_rb, s = prep ? c->qm_ps : c->qm_s;
+    if (rb == 1 || rb == 2 || rb == 4) RB = rb;
+    if (s > 0) S = std::min(s, 16 / RB);
 }
 
 #define QM_MIN_COLS 5

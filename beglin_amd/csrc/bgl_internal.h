@@ -53,6 +53,7 @@ struct bgl_ctx {
     std::unordered_map<uint64_t, DevBuf> mlp_sync;   // single-launch MLP, per shape (in << 32 | down workgroups): counters, generations, flag
     bool no_qmfma = false;                // BGL_NO_QMFMA=1: W4A8 at 2..16 columns through the dot4 kernel (k_gemv_q)
     int qm_rb = 0, qm_s = 0;              // BGL_QM_RB / BGL_QM_S: k_gemv_qm row blocks / unit slices per workgroup (tuning; 0 by shape)
+    int qm_prb = 0, qm_ps = 0;            // BGL_QM_PRB / BGL_QM_PS: the same for its launches over prepared codes
     int mlp_gu = 0;                       // BGL_MLP_GU: gate+up workgroups of the single-launch MLP (tuning; 0 by shape)
     bool no_fused_mlp = false;            // BGL_NO_FUSED_MLP=1: the MLP block as three launches at every M
     int mlp_spin = 1 << 20;               // BGL_MLP_SPIN: polls of the single-launch MLP's bounded wait
