@@ -20,7 +20,7 @@
 // Work split.  A workgroup owns 4 consecutive 64-row weight tiles (256 rows) over one K range (a
 // split) and has KW K-slices of 8 waves; in a slice two waves share a tile (two 16-row blocks
 // each).  The split's activation fragments and the 4 tiles' scales are staged in LDS once (up to
-// 144 KB, which bounds the split's length), then each wave streams its own weights with no further
+// 152 KB, which bounds the split's length), then each wave streams its own weights with no further
 // barrier: a register ring keeps the next K-steps' loads in flight.  Splits are sized so the grid
 // fills the chip; k_mfma_reduce adds their fp32 partials in split order (deterministic; no
 // atomics).  All tensors of a group (same format and K, one activation) run in one launch and one
