@@ -143,6 +143,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
                 // runs under the first column's level-1 records
                 XRaw<FMT, NB> rf;
                 x_load<FMT, NB, KQ>(rf, up ? Rb : Ra, sl == S - 1 ? xlast : xlane, sl, true);
+                const XDec<FMT, NB> df = x_decode<FMT, NB>(rf);   // decoded once for all its flagged columns
 #pragma unroll 1
                 for (int m = 0; m < mcg; m++) {
                     const int f3 = rec[m * RC + XREC_DSUM + 3];
@@ -158,7 +159,7 @@ __device__ __forceinline__ void moe_x_chunk(const MoeTask &Mt, const BglDevTenso
                         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                     }
                     const XRow xrow{up ? &Tb : &Ta, tile * BGL_TILE + r0 + r, xr};
-                    const float v = x_fix<FMT, NB>(x_decode<FMT, NB>(rf), rec + m * RC, r1, *reinterpret_cast<const int4 *>(r1 + XREC_DSUM),
+                    const float v = x_fix<FMT, NB>(df, rec + m * RC, r1, *reinterpret_cast<const int4 *>(r1 + XREC_DSUM),
                                                    *reinterpret_cast<const int4 *>(r1 + XREC_DSUM + 4), xrow, gl);
 #pragma unroll
                     for (int q = 0; q < MB; q++) {
