@@ -603,3 +603,40 @@ def test_read_probe_tensor_limits(ctx, torch_dev):
         ctx.read_probe(ts)
     for t in ts:
         t.free()
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_w4a8_random_shapes(torch_dev, oracle, case):
+    """Seeded random W4A8 shapes, bit for bit against the oracle: kinds 1-3, ragged row counts
+    (tiles and 16-row blocks partly filled), K of 1-40 groups, 1-20 columns (the dot4 kernel below
+    5 columns, the matrix cores from 5, a dot4 remainder past 16), fused groups of 1-3 tensors
+    with and without biases."""
+    import beglin_amd
+    torch = torch_dev
+    rng = np.random.default_rng(3100 + case)
+    kind = int(rng.integers(1, 4))
+    gq = 256 if kind == 3 else 64
+    inn = gq * int(rng.integers(1, 11 if kind == 3 else 41))
+    M = int(rng.integers(1, 21))
+    ntens = int(rng.integers(1, 4))
+    outs = [int(rng.integers(1, 300)) for _ in range(ntens)]
+    with_bias = bool(rng.integers(0, 2))
+    say("w4a8 random", case, kind, inn, M, outs, with_bias)
+    c = beglin_amd.Context(0)
+    ts, refs, ys, bds = [], [], [], []
+    x = seeded_normal(3200 + case, (M, inn))
+    for j, o in enumerate(outs):
+        pk, sc, sub = ref_quant(oracle, kind, weights(3300 + 7 * case + j, o, inn), 0)
+        b = seeded_normal(3400 + 7 * case + j, (o,)) if with_bias else None
+        ts.append(c.bind(kind, pk, sc, o, inn, sub=sub))
+        refs.append(oracle.matmul_sdot(kind, pk, sc, x, bias=b, sub=sub))
+        ys.append(torch.full((M, o), float("nan"), dtype=torch.float32, device="cuda"))
+        bds.append(torch.from_numpy(b).cuda() if b is not None else None)
+    c.matmul_group(ts, torch.from_numpy(x).cuda(), ys, act=beglin_amd.ACT_W4A8, biases=bds if with_bias else None)
+    torch.cuda.synchronize()
+    for y, ref in zip(ys, refs):
+        got = y.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (case, kind, inn, M, outs, relerr(got, ref))
+    for t in ts:
+        t.free()
+    c.close()

@@ -219,3 +219,26 @@ def test_mfma_graph_replays_match_eager(torch_dev, oracle):
     assert relerr(eager, oracle.gemm_f32(4, pk, sc, x.cpu().numpy(), bits=5)) <= TOL
     t.free()
     gc.close()
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_f32_random_shapes(ctx, torch_dev, oracle, case):
+    """Seeded random fp32-activation shapes against the oracle (<= 1e-5): int4 g64, int8 g64,
+    Q4G32H and qNg64 n = 2..15, ragged row counts, K of 1-48 groups, 1-70 columns (the one-column
+    kernel, the dot4 column chunks below 16, the matrix cores from 16 where the format takes them,
+    launches of 64 columns past that), with and without bias."""
+    torch = torch_dev
+    rng = np.random.default_rng(3500 + case)
+    kind = int(rng.choice([1, 2, 4, 5]))
+    bits = int(rng.integers(2, 16)) if kind == 4 else 0
+    inn = 64 * int(rng.integers(1, 49))
+    out = int(rng.integers(1, 400))
+    M = int(rng.integers(1, 71))
+    with_bias = bool(rng.integers(0, 2))
+    say("f32 random", case, kind, bits, inn, out, M, with_bias)
+    pk, sc = quant(oracle, kind, weights(3600 + case, out, inn), bits)
+    x = seeded_normal(3700 + case, (M, inn))
+    bias = seeded_normal(3800 + case, (out,)) if with_bias else None
+    got = run(ctx, torch, kind, bits, pk, sc, out, inn, x, bias=bias)
+    ref = oracle.gemm_f32(kind, pk, sc, x, bias=bias, bits=bits)
+    assert relerr(got, ref) <= TOL, (case, kind, bits, inn, out, M, relerr(got, ref))
