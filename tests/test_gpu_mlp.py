@@ -257,6 +257,38 @@ def test_mlp_single_launch_equals_three_launches(torch_dev, oracle, monkeypatch,
     c1.close(); c3.close()
 
 
+@pytest.mark.parametrize("case", range(8))
+def test_mlp_single_launch_random_shapes(torch_dev, oracle, case):
+    """Seeded random block shapes through the single-launch MLP (q4g64, q8g64, g256sf; hidden and
+    intermediate sizes in whole 256-value groups, rows that leave items and down workgroups partly
+    filled), two calls in a row: y and h bit-identical to the oracle."""
+    import beglin_amd
+    torch = torch_dev
+    rng = np.random.default_rng(1800 + case)
+    kind = int(rng.integers(1, 4))
+    H = 256 * int(rng.integers(1, 13))
+    I = 256 * int(rng.integers(1, 41))
+    say("mlp single launch random", case, kind, H, I)
+    c = beglin_amd.Context(0)
+    ts, refs = bind_mlp(c, torch, oracle, kind, H, I, 1810 + 3 * case)
+    for call in range(2):
+        x = seeded_normal(1820 + 2 * case + call, (1, H))
+        y = torch.full((1, H), 7.0, device="cuda")
+        h = torch.full((1, I), 7.0, device="cuda")
+        c.prof_enable(True)
+        c.prof_read()
+        c.mlp(ts[0], ts[1], ts[2], dev(torch, x), y, act=beglin_amd.ACT_W4A8, h_dev=h)
+        c.check()
+        assert sum(v[1] for v in c.prof_read().values()) == 1, (case, H, I)   # the single launch ran
+        c.prof_enable(False)
+        yr, hr = mlp_ref(oracle, kind, refs, x)
+        assert same_bits(h.cpu().numpy(), hr), (case, kind, H, I, call)
+        assert same_bits(y.cpu().numpy(), yr), (case, kind, H, I, call)
+    for t in ts:
+        t.free()
+    c.close()
+
+
 def test_mlp_single_launch_graph_replay(torch_dev, oracle):
     """Three MLP blocks (three layers' weights, chained: each block's y feeds the next) captured in
     one graph: every replay, with the program's own eager work in between, equals the eager run."""
