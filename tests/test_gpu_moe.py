@@ -683,3 +683,31 @@ def test_mxfp4_refusals(torch_dev, oracle, monkeypatch):
         run_moe(c, torch, gate, up, down, None, x, idx, w)
     c.close()
     monkeypatch.delenv("BGL_NO_MOE_X", raising=False)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_moe_ffn_random_configs(ctx, torch_dev, oracle, case):
+    """Seeded random routed FFN configurations against the oracle (<= 1e-5): expert count, top-K,
+    token count (1..70: the in-kernel gathers, their 8-column chunks and the matrix-core shared
+    experts from 16 tokens), hidden / expert sizes in whole 64-groups, a per-expert mix of the
+    gather formats (int4 g32 / g64, int8, qNg64 n = 2..15, MXFP4), shared experts or none, with
+    and without renormalised weights."""
+    torch = torch_dev
+    rng = np.random.default_rng(4200 + case)
+    E = int(rng.integers(4, 33))
+    K = int(rng.integers(1, min(E, 8) + 1))
+    T = int(rng.integers(1, 71))
+    H = 64 * int(rng.integers(2, 9))
+    I = 64 * int(rng.integers(2, 9))
+    Ish = 64 * int(rng.integers(0, 5))
+    pool = [(5, 0), (1, 0), (2, 0), (9, 40)] + [(4, n) for n in range(2, 16)]
+    fm = [pool[int(i)] for i in rng.integers(0, len(pool), size=int(rng.integers(1, 5)))]
+    sh_fmt = pool[int(rng.integers(0, 3))]
+    renorm = bool(rng.integers(0, 2))
+    say("moe_ffn random", case, E, K, T, H, I, Ish, fm, sh_fmt, renorm)
+    gate, up, down, shared = moe_setup(oracle, 4300 + 11 * case, E, H, I, Ish, fm, sh_fmt=sh_fmt)
+    x = seeded_normal(4400 + case, (T, H))
+    idx, w = oracle.route(seeded_normal(4500 + case, (T, E)), K, renorm)
+    got = run_moe(ctx, torch, gate, up, down, shared, x, idx, w)
+    ref = moe_ffn(oracle, gate, up, down, shared, H, I, x, idx, w)
+    assert relerr(got, ref) <= TOL, (case, relerr(got, ref))
