@@ -640,3 +640,36 @@ def test_w4a8_random_shapes(torch_dev, oracle, case):
     for t in ts:
         t.free()
     c.close()
+
+
+@pytest.mark.parametrize("kind", [1, 2, 3])
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_w4a8_extreme_columns(torch_dev, oracle, kind, M):
+    """W4A8 columns at the edges of fp32, bit for bit against the oracle: all zeros (scale 0),
+    negative zeros, subnormals only, values near 1e30, and a mix of 1e-38 and 1e30 in one group;
+    on the dot4 kernel (1 column) and the matrix cores (5, 16)."""
+    import beglin_amd
+    torch = torch_dev
+    inn, out = 1024, 136
+    say("w4a8 extreme", kind, M)
+    pk, sc, sub = ref_quant(oracle, kind, weights(3900 + kind, out, inn), 0)
+    x = seeded_normal(3910 + M, (M, inn))
+    pats = [np.zeros(inn, np.float32), -np.zeros(inn, np.float32),
+            (seeded_normal(3920, (inn,)) * np.float32(1e-40)).astype(np.float32),
+            (seeded_normal(3921, (inn,)) * np.float32(1e30)).astype(np.float32),
+            np.where(np.arange(inn) % 3 == 0, np.float32(1e30), np.float32(1e-38)).astype(np.float32)]
+    # one column: every pattern in turn; several: the patterns in the first columns, normal ones after
+    xs = [p[None, :].copy() for p in pats] if M == 1 else [np.concatenate([np.stack(pats), x[len(pats):]])]
+    c = beglin_amd.Context(0)
+    t = c.bind(kind, pk, sc, out, inn, sub=sub)
+    for xi in xs:
+        ref = oracle.matmul_sdot(kind, pk, sc, xi, sub=sub)
+        y = torch.full((M, out), float("nan"), dtype=torch.float32, device="cuda")
+        c.matmul(t, torch.from_numpy(xi).cuda(), y, act=beglin_amd.ACT_W4A8)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), (kind, M)
+        ok = ~np.isnan(ref)
+        assert np.array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32)), (kind, M, relerr(got, ref))
+    t.free()
+    c.close()
