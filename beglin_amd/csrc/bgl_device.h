@@ -32,7 +32,7 @@
 
 // fp32 activations as exact integers, per 64-group:
 //   level 0: X = rint(x * 2^(22-e)), e = exponent of the group's largest finite |x| (|X| <= 2^22),
-//            as three balanced base-256 int8 digits X = d0 + 256*d1 + 65536*d2 (|d2| <= 64).  An
+//            at least -127 (an all-subnormal group then has X = x * 2^149, exact), as three balanced base-256 int8 digits X = d0 + 256*d1 + 65536*d2 (|d2| <= 64).  An
 //            element's error is at most 2^(e-23): relative to any |x| >= 2^(e-6), at most 2^-17.
 //   level 1: in groups holding at least BGL_X_SMALL_MAX nonzero elements below 2^(e-6), or more
 //            such small elements than elements at or above it (an outlier, or a cluster of large
@@ -51,6 +51,8 @@
 #define BGL_XF_L1 1            // group flags: the group has level-1 digits
 #define BGL_XF_NF 2            //              the group holds a non-finite element
 #define BGL_X_FRAC 22          // level-0 / level-1 fixed point: X = rint(x * 2^(BGL_X_FRAC - e))
+#define BGL_X_EMIN (BGL_X_FRAC - 149)   // e is at least this, so the scale 2^(e-22) is >= 2^-149, a float;
+                                  // groups below it (|x| < 2^-128, subnormal) get X = x * 2^149 exactly
 #define BGL_X_SPIKE_BITS 6     // "small": a nonzero |x| below 2^(e-6)
 #define BGL_X_SMALL_MAX 22     // level 1 from this many small elements (or more small than large)
 

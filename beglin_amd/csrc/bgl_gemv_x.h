@@ -483,6 +483,7 @@ __device__ __forceinline__ XStat x_stat(const float4 &v) {
     st.mx = __uint_as_float(mb);
     st.e = 0;
     if (st.mx > 0.0f) frexpf(st.mx, &st.e);
+    st.e = max(st.e, BGL_X_EMIN);
     const uint32_t thr = st.mx > 0.0f ? __float_as_uint(ldexpf(1.0f, st.e - BGL_X_SPIKE_BITS)) : 0u;
     int cnt = 0;
 #pragma unroll

@@ -435,7 +435,7 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
     // Non-finite values (NaN, +-Inf) enter the fragments as 0 and flag the column; the store adds
     // their products code * scale * x one element at a time (IEEE propagation, as the reference's
     // fp32-product sums).
-    __shared__ float cinv[16 * MF_MAXCT];
+    __shared__ int cex[16 * MF_MAXCT];
     __shared__ int cnf[16 * MF_MAXCT];
 #pragma unroll
     for (int ci = 0; ci < CPW; ci++) {
@@ -477,8 +477,10 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
         const float mx = __uint_as_float(mb);
         int e = 0;
         if (mx > 0.0f) frexpf(mx, &e);                             // mx in [2^(e-1), 2^e)
-        const float sc = mx > 0.0f ? ldexpf(1.0f, 14 - e) : 1.0f;
-        if (lane == 0) cinv[m] = mx > 0.0f ? ldexpf(1.0f, e - 14) : 1.0f;
+        // x' = x * 2^(14-e), applied to each value (the factor alone leaves fp32's range for
+        // e < -113, columns whose largest |x| is below 2^-114); the sums are unscaled by 2^(e-14)
+        const int sh = mx > 0.0f ? 14 - e : 0;
+        if (lane == 0) cex[m] = -sh;
         const int ct = m >> 4, ml = m & 15;
 #pragma unroll
         for (int j = 0; j < SPL; j++) {
@@ -492,7 +494,7 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
             uint32_t H[4], Lo[4];
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const float v0 = v8[2 * k] * sc, v1 = v8[2 * k + 1] * sc;   // power-of-two scaling: exact
+                const float v0 = ldexpf(v8[2 * k], sh), v1 = ldexpf(v8[2 * k + 1], sh);   // power-of-two scaling: exact
                 const mf_h2 hh = __builtin_bit_cast(mf_h2, __builtin_amdgcn_cvt_pkrtz(v0, v1));
                 const float r0 = v0 - (float)hh[0], r1 = v1 - (float)hh[1];
                 const uint32_t hw = __builtin_bit_cast(uint32_t, hh);
@@ -657,11 +659,11 @@ __global__ __launch_bounds__(MF_WAVES * KW * 64) void k_gemm_mfma(MfmaLaunch L) 
             const float4 b = *reinterpret_cast<const float4 *>(ob + (16 * CT + m) * OBR + sw);
             o[0] += b.x; o[1] += b.y; o[2] += b.z; o[3] += b.w;
         }
-        const float ci = cinv[m];
+        const int ce = cex[m];
         float *dst = (S > 1 ? tk.part + ((size_t)split * L.M + m) * T.N : tk.y + (size_t)m * tk.ystride) + n;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            o[e] = o[e] * ci;
+            o[e] = ldexpf(o[e], ce);
             if (n + e < T.N) {
                 if (cnf[m]) o[e] += mf_nonfinite<FMT, NB>(T, n + e, L.x + (size_t)m * T.K, 32 * s0, min(32 * (s0 + ns), T.K));
                 if (S == 1 && tk.bias) o[e] += tk.bias[n + e];

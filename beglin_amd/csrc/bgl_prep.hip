@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void k_act_w4a8(const float *__restrict__ x, i
 
 // ------------------------------------------------------------------ fp32 activation digits
 // One wave per (column, 64-group), lane = element.  Level 0: e = exponent of the group's largest
-// finite |x| (frexp), X = rint(x * 2^(22-e)), |X| <= 2^22, as X = d0 + 256*d1 + 65536*d2 with
+// finite |x| (frexp, at least BGL_X_EMIN), X = rint(x * 2^(22-e)), |X| <= 2^22, as X = d0 + 256*d1 + 65536*d2 with
 // balanced int8 digits.  Level 1 (bgl_x_level1: groups with BGL_X_SMALL_MAX or more nonzero
 // elements below 2^(e-BGL_X_SPIKE_BITS), or more of them than elements above): the exact residual
 // r = x * 2^(22-e) - X in the same form relative to its own maximum, X1 = rint(r * 2^(22-e1)).
@@ -95,6 +95,7 @@ __global__ __launch_bounds__(256) void k_act_x24(const float *__restrict__ x, in
     float mx = wave_max_f32(__uint_as_float(ab));
     int e = 0;
     if (mx > 0.0f) frexpf(mx, &e);
+    e = max(e, BGL_X_EMIN);
     const float thr = mx > 0.0f ? ldexpf(1.0f, e - BGL_X_SPIKE_BITS) : 0.0f;
     const int cnt = wave_sum_i32((ab != 0u && __uint_as_float(ab) >= thr ? 1 : 0) + (ab != 0u ? 256 : 0) + (nf ? 65536 : 0));
     const int nlarge = cnt & 255, nnz = (cnt >> 8) & 255, nnf = cnt >> 16;

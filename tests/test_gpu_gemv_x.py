@@ -234,3 +234,46 @@ def test_gemv_x_fused_digits_equal_prepared(torch_dev, oracle, monkeypatch, kind
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (out, inn)
         assert relerr(a, oracle.gemm_f32(kind, pk, sc, x, bits=bits)[0]) <= TOL
     cf.close(); cp.close()
+
+
+@pytest.mark.parametrize("mode", ["fused", "prep", "tile"])
+def test_gemv_x_subnormal_columns(torch_dev, oracle, monkeypatch, mode):
+    """Activation columns at the bottom of fp32 through the exact-digit paths (digits made in the
+    GEMV, by the prep kernel, and the tile kernel at M = 1 and M = 4): a column of subnormals only
+    (every 64-group below 2^-128, where the group scale 2^(e-22) would be below fp32's range), one
+    of groups just above and just below 2^-128, and one near 1e-36.  Outputs within 1e-5 of the
+    oracle's relative to the column's largest, or, where they are themselves subnormal, within a
+    few subnormal spacings; and never all zero."""
+    torch = torch_dev
+    env = {"fused": {"BGL_X_FUSE": 1}, "prep": {"BGL_X_FUSE": 0}, "tile": {"BGL_NO_GEMV_X": 1}}[mode]
+    c = context(monkeypatch, **env)
+    out, inn = 136, 1024
+    tiny = np.float32(2.0 ** -149)
+    for kind, bits in [(1, 0), (5, 0), (2, 0), (4, 7)]:
+        pk, sc = quant(oracle, kind, weights(4700 + kind + bits, out, inn), bits)
+        base = seeded_normal(4710, (4, inn))
+        x = np.empty((4, inn), np.float32)
+        x[0] = base[0] * np.float32(1e-40)                              # subnormal only
+        x[1] = np.where(np.arange(inn) // 64 % 2 == 0, base[1] * np.float32(1e-38),
+                        base[1] * np.float32(1e-40)).astype(np.float32)  # groups above / below 2^-128
+        x[2] = base[2] * np.float32(1e-36)
+        x[3] = np.round(base[3] * 1000) * tiny                           # small integer multiples of 2^-149
+        for M in (1, 4):
+            if mode != "tile" and M > 1:
+                continue
+            say("gemv_x subnormal", mode, kind, bits, M)
+            t = c.bind(kind, pk, sc, out, inn, bits=bits)
+            for m0 in range(0, 4, M):
+                xc = np.ascontiguousarray(x[m0:m0 + M])
+                y = torch.full((M, out), float("nan"), dtype=torch.float32, device="cuda")
+                c.matmul(t, torch.from_numpy(xc).cuda(), y)
+                torch.cuda.synchronize()
+                got = y.cpu().numpy()
+                ref = oracle.gemm_f32(kind, pk, sc, xc, bits=bits)
+                for j in range(M):
+                    g, r = got[j].astype(np.float64), ref[j]
+                    err = np.abs(g - r)
+                    ok = np.all((err <= TOL * np.max(np.abs(r))) | (err <= 16 * float(tiny)))
+                    assert np.all(np.isfinite(g)) and ok and np.any(g != 0.0), (kind, bits, M, m0 + j, float(np.max(err)))
+            t.free()
+    c.close()

@@ -242,3 +242,29 @@ def test_f32_random_shapes(ctx, torch_dev, oracle, case):
     got = run(ctx, torch, kind, bits, pk, sc, out, inn, x, bias=bias)
     ref = oracle.gemm_f32(kind, pk, sc, x, bias=bias, bits=bits)
     assert relerr(got, ref) <= TOL, (case, kind, bits, inn, out, M, relerr(got, ref))
+
+
+@pytest.mark.parametrize("kind,bits", [(5, 0), (2, 0), (4, 7)])
+def test_mfma_tiny_and_huge_columns(ctx, torch_dev, oracle, kind, bits):
+    """Columns whose largest |x| is far from 1 on the matrix cores: 1e-36 and 1e-39 (the column's
+    power-of-two scale 2^(14-e) is then beyond fp32's range as a factor), subnormals only, 1e36,
+    and all zeros; every output finite and, column by column, within 1e-5 of the oracle's (the
+    subnormal column's outputs within a few subnormal spacings)."""
+    torch = torch_dev
+    out, inn, M = 160, 1024, 20
+    say("mfma tiny / huge", kind, bits)
+    pk, sc = quant(oracle, kind, weights(4600 + kind, out, inn), bits)
+    x = seeded_normal(4610, (M, inn))
+    x[0] *= np.float32(1e-36)
+    x[1] *= np.float32(1e-39)
+    x[2] = (seeded_normal(4611, (inn,)) * np.float32(1e-41)).astype(np.float32)
+    x[3] *= np.float32(1e36)
+    x[4] = 0.0
+    got = run(ctx, torch, kind, bits, pk, sc, out, inn, x)
+    ref = oracle.gemm_f32(kind, pk, sc, x, bits=bits)
+    assert np.all(np.isfinite(got)), [m for m in range(M) if not np.all(np.isfinite(got[m]))]
+    for m in (0, 1, 3) + tuple(range(5, M)):
+        assert relerr(got[m], ref[m]) <= TOL, (m, relerr(got[m], ref[m]))
+    # outputs ~1e-41 are subnormal (spacing 2^-149): a few spacings of absolute error
+    assert np.max(np.abs(got[2].astype(np.float64) - ref[2])) <= 16 * 2.0 ** -149
+    assert np.max(np.abs(ref[2])) > 0.0 and np.all(got[4] == 0.0)
