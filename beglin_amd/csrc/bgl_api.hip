@@ -153,6 +153,9 @@ extern "C" int bgl_ctx_create(int device, void *hip_stream, bgl_ctx **out) {
     if (c->max_waves < 1 || c->max_waves > 16) c->max_waves = 16;
     const char *mb = getenv("BGL_MIN_BLOCKS");
     c->min_blocks = mb ? atoi(mb) : 256;
+    const char *pc = getenv("BGL_MF_PCAP");
+    c->mf_pcap = pc ? (float)atof(pc) : 1.0f;
+    if (!(c->mf_pcap >= 0.0f && c->mf_pcap <= 64.0f)) c->mf_pcap = 1.0f;
     const char *ft = getenv("BGL_FORCE_TR");
     c->force_tr = ft ? atoi(ft) : 0;
     if (c->force_tr != 0 && c->force_tr != 8 && c->force_tr != 16 && c->force_tr != 32 && c->force_tr != 64) c->force_tr = 0;

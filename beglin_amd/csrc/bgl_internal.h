@@ -29,6 +29,7 @@ struct bgl_ctx {
     bool no_fused = false;                // BGL_NO_FUSED_Q=1: W4A8 M=1 through the separate prep kernel
     bool no_mfma = false;                 // BGL_NO_MFMA=1: fp32-activation M >= 16 through the dot4 kernels
     int min_blocks = 256;                 // fused W4A8: split tiles until at least this many workgroups
+    float mf_pcap = 1.0f;                 // matrix-core K split: partials (written + read) at most this x the weight bytes
     int force_tr = 0;                     // BGL_FORCE_TR: fixed rows per workgroup (tuning)
     bool no_gemv_x = false;               // BGL_NO_GEMV_X=1: fp32-activation M=1 through the tile kernel (k_gemv)
     int x_waves = 0;                      // BGL_X_WAVES: wavefronts per k_gemv_x workgroup (tuning)

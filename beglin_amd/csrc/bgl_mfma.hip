@@ -872,10 +872,12 @@ int run_gemm_mfma(bgl_ctx *c, int n, const BglDevTensor *Ts, const float *x_dev,
             const int wgr = (T.ntiles + MF_TILES - 1) / MF_TILES;
             // A split's K range must fit the workgroup's LDS (kpm steps); beyond that, split K until
             // the grid has ~min_blocks workgroups while the partials (written and read back once
-            // each) stay under half the weight bytes.
+            // each) stay under mf_pcap x the weight bytes (1 by default: at 0.5 the 4096 x 4096
+            // qNg64 n=5 tensors of a 32-column launch ran 64 workgroups, 19.3 us, against 128 and
+            // 15.0 us; finer splits than 16 K-steps measured no faster).
             const int smin = (KS + kpm - 1) / kpm;
             int S = (c->min_blocks + wgr - 1) / wgr;
-            const int capS = (int)(0.5 * mf_weight_bytes(T) / (8.0 * Mc * T.N));
+            const int capS = (int)(c->mf_pcap * mf_weight_bytes(T) / (8.0 * Mc * T.N));
             if (S > capS) S = capS;
             if (S < smin) S = smin;
             if (S < 1) S = 1;
