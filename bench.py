@@ -814,7 +814,7 @@ def main():
     # eager run of each.  (The fused W4A8 kernel and the one-column fp32 GEMV over a short K make
     # their operands themselves; several W4A8 columns over a long K and long fp32 K are quantized
     # up front.  The MLP block at one W4A8 column is one launch, otherwise three.)
-    prep_tags, launches_of = [], {}
+    prep_tags, launches_of, kern_of = [], {}, {}
     for tag in tags:
         ctx.prof_enable(True)
         ctx.prof_read()
@@ -825,6 +825,7 @@ def main():
         if pr["prep"][1] > 0:
             prep_tags.append(tag)
         launches_of[tag] = sum(v[1] for v in pr.values())
+        kern_of[tag] = pr["gemv"][1] + pr["other"][1]          # the launches after any prep kernel
         ctx.prof_enable(False)
     launches = sum(launches_of.values())
     if args.workload == "cfg2" and launches_of.get("mlp") == wl.ncalls(["mlp"]):
@@ -852,15 +853,17 @@ def main():
         if prep_tags:
             prep_ms = time_prep(ctx, torch, stream, wl, max(5, args.steps // 5), set(prep_tags))
         k_ms = max(step_ms - prep_ms, 1e-6)
+        klaunches = max(sum(kern_of.values()), 1)              # prep launches are timed apart
         achieved = nbytes / (k_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                 "kernel": ("k_gemv_q<fmt,TR,QP,MB> (bgl_gemv.hip) + k_swiglu (bgl_mlp.hip)" if args.workload == "cfg2" else
                            "k_gemv_x<fmt,n,TR,FUSE> (bgl_gemv_x.hip)" if M == 1 else "k_gemv<fmt,act,n,MB> (bgl_gemv.hip)"),
-                "launches_per_step": launches, "kernel_us_per_launch": round(k_ms * 1e3 / launches, 3),
-                "prep_us_per_launch": round(prep_ms * 1e3 / launches, 3), "prep_call_types": prep_tags,
-                "bytes_per_launch": round(nbytes / launches)}
-        dom_bytes = nbytes / launches
+                "launches_per_step": klaunches, "kernel_us_per_launch": round(k_ms * 1e3 / klaunches, 3),
+                "prep_launches_per_step": launches - klaunches,
+                "prep_us_per_launch": round(prep_ms * 1e3 / max(launches - klaunches, 1), 3), "prep_call_types": prep_tags,
+                "bytes_per_launch": round(nbytes / klaunches)}
+        dom_bytes = nbytes / klaunches
 
     # the plain-read floor for the same bytes and launch count, measured in this run
     pr_ms = plain_read(ctx, torch, stream, wl, max(5, args.steps // 5))
